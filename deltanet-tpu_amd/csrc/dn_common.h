@@ -1,0 +1,148 @@
+// Shared device helpers for the gfx950 delta-rule kernels.
+//
+// Fragment convention used by every MFMA in this library
+// ------------------------------------------------------
+// All matrix products are 16x16 output tiles reduced over 32-wide k slabs.
+// A lane l of a 64-wide wavefront owns index (l & 15) of the tile's row (A
+// operand) or column (B operand) and 8 k values of the slab, chosen by its
+// lane group q = l >> 4 through the permutation
+//
+//     pi(q, e) = 4q + e          (e = 0..3)
+//     pi(q, e) = 16 + 4q + e-4   (e = 4..7)
+//
+// With this permutation the 16x16 fp32 accumulator tile (lane l holds column
+// l&15, rows 4q..4q+3) of two vertically stacked tiles IS a B-operand
+// fragment of the next product, so chained products (U - W*S, M*Vnew,
+// ke^T*Vnew ...) need no LDS round trip.  The same fragment feeds
+//   * v_mfma_f32_16x16x32_bf16 (one instruction, 8 bf16 per lane), or
+//   * 8 x v_mfma_f32_16x16x4_f32 (step e uses k slot q <-> pi(q, e)),
+// so the bf16 and fp32 precisions share all indexing code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dn {
+
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I32 = 3, DT_I64 = 4 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ int pi_k(int q, int e) { return (e < 4) ? (4 * q + e) : (12 + 4 * q + e); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// scalar loads with a run-time element type (gates, segment ids)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ld_f(const void* p, int64_t i, int dt) {
+  if (dt == DT_BF16) return (float)((const bf16*)p)[i];
+  if (dt == DT_F16) return (float)((const f16*)p)[i];
+  return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ int64_t ld_i(const void* p, int64_t i, int dt) {
+  if (dt == DT_I64) return ((const int64_t*)p)[i];
+  return (int64_t)((const int32_t*)p)[i];
+}
+
+template <class T> __device__ __forceinline__ float to_f(T x) { return (float)x; }
+
+template <class T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ f16 from_f<f16>(float x) { return (f16)x; }
+
+// round a float through T and back (models storing into a T tensor)
+template <class T> __device__ __forceinline__ float round_as(float x) { return (float)from_f<T>(x); }
+
+// 4 contiguous elements -> floats
+template <class T> __device__ __forceinline__ void ld4(const T* p, float* o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = to_f(p[i]);
+}
+template <> __device__ __forceinline__ void ld4<float>(const float* p, float* o) {
+  float4 x = *reinterpret_cast<const float4*>(p);
+  o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+}
+template <> __device__ __forceinline__ void ld4<bf16>(const bf16* p, float* o) {
+  bf16x4 x = *reinterpret_cast<const bf16x4*>(p);
+  o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
+}
+
+template <class T> __device__ __forceinline__ void st4(T* p, const float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = from_f<T>(v[i]);
+}
+template <> __device__ __forceinline__ void st4<float>(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ void st4<bf16>(bf16* p, const float* v) {
+  bf16x4 x;
+  x[0] = (bf16)v[0]; x[1] = (bf16)v[1]; x[2] = (bf16)v[2]; x[3] = (bf16)v[3];
+  *reinterpret_cast<bf16x4*>(p) = x;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA fragments
+// ---------------------------------------------------------------------------
+template <bool BF> struct Frag;
+template <> struct Frag<true> { bf16x8 v; };
+template <> struct Frag<false> { float v[8]; };
+
+template <bool BF> __device__ __forceinline__ Frag<BF> make_frag(const float* x);
+template <> __device__ __forceinline__ Frag<true> make_frag<true>(const float* x) {
+  Frag<true> f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f.v[e] = (bf16)x[e];
+  return f;
+}
+template <> __device__ __forceinline__ Frag<false> make_frag<false>(const float* x) {
+  Frag<false> f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f.v[e] = x[e];
+  return f;
+}
+
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<true>& a, const Frag<true>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<false>& a, const Frag<false>& b) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], acc, 0, 0, 0);
+}
+
+// Fragment from a row-major row pointer at the slab start (k0 already added):
+// elements rowp[4q..4q+3] and rowp[16+4q..16+4q+3].
+template <bool BF, class T> __device__ __forceinline__ Frag<BF> frag_row(const T* rowp, int q) {
+  float x[8];
+  ld4<T>(rowp + 4 * q, x);
+  ld4<T>(rowp + 16 + 4 * q, x + 4);
+  return make_frag<BF>(x);
+}
+
+// Fragment from a column of row-major storage: elements colp[pi(q,e) * stride].
+template <bool BF, class T>
+__device__ __forceinline__ Frag<BF> frag_col(const T* colp, int64_t stride, int q) {
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = to_f(colp[(int64_t)pi_k(q, e) * stride]);
+  return make_frag<BF>(x);
+}
+
+// Two stacked accumulator tiles (rows 0-15 and 16-31 of a slab) as a fragment.
+template <bool BF> __device__ __forceinline__ Frag<BF> frag_from_acc(const f32x4& c0, const f32x4& c1) {
+  float x[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  return make_frag<BF>(x);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+}  // namespace dn

@@ -1,0 +1,260 @@
+// Single-token GDN-2 decode step on gfx950: a pure HBM stream of the
+// (B, Hv, K, V) state.  One workgroup of 512 lanes owns one (batch, value
+// head) 128x128 state: it reads the state once with 16-byte loads, keeps it in
+// VGPRs, and writes the updated state once.
+//
+// Reference: gdn2_decode_step (maelie-labs/deltanet-tpu v0.3.0,
+// src/deltanet_tpu/gdn2.py:2289-2490):
+//   g <- min(g, 0) (+ guard clamps)                 gdn2.py:2393-2402
+//   S <- 0 where reset                              gdn2.py:2404-2412
+//   q, k repeated to value heads (hv // G)          gdn2.py:2414-2448
+//   q <- scale q / sqrt(|q|^2 + 1e-6) (if l2norm)   gdn2.py:2434-2438
+//   Sd = e^g (rows) * S ; e = Sd^T (b k) ; vn = w v - e
+//   S' = Sd + k vn^T ; o = S'^T q                   gdn2.py:2471-2478
+//   cap |S'|_F at tau (guard), cast to state dtype  gdn2.py:2484-2489
+// The read-out uses o_j = sum_i q_i d_i S_ij + (q.k) vn_j, which equals
+// S'^T q exactly in real arithmetic and needs only the single pass over S.
+#include <string>
+
+#include "dn_common.h"
+#include "dn_host.h"
+
+namespace dn {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const char* msg) {
+  g_last_error = msg ? msg : "";
+  return code;
+}
+
+struct DP {
+  int B, Hk, Hv, G;
+  const void *q, *k, *v;
+  int qk_dt, v_dt;
+  const void* g; int g_dt, g_h, g_c;
+  const void* b; int b_dt, b_h, b_c;
+  const void* w; int w_dt, w_h, w_c;
+  const void* sin;
+  void* sout;
+  const uint8_t* reset;
+  void* out;
+  float scale; int l2norm, guard; float tau;
+};
+
+__device__ __forceinline__ int dgate_head(int H, int Hk, int Hv, int hv, int G) {
+  if (H == 1) return 0;
+  return (H == Hv) ? hv : hv / G;
+}
+
+// sum over the 512 lanes of the workgroup; `buf` holds 8 floats
+__device__ __forceinline__ float block_sum512(float x, float* buf) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) buf[w] = x;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t += buf[i];
+  return t;
+}
+
+template <class TS> __device__ __forceinline__ void ld_row4(const TS* p, float* o) { ld4<TS>(p, o); }
+
+template <class TSin, class TSout>
+__global__ __launch_bounds__(512) void k_decode(const DP p) {
+  constexpr int K = 128, V = 128;
+  __shared__ float qn[K], kn[K], dd[K], bt[K], vn[V];
+  __shared__ float red[2][16][V];
+  __shared__ float rbuf[8];
+
+  const int tid = threadIdx.x;
+  const int cg = tid & 31, rg = tid >> 5;
+  const int bh = blockIdx.x;
+  const int bb = bh / p.Hv, hv = bh % p.Hv;
+  const int hk = hv / p.G;
+  const bool rst = p.reset != nullptr && p.reset[bb] != 0;
+  const int64_t sbase = (int64_t)bh * K * V;
+
+  // issue the state loads first: 8 rows x 4 columns per lane
+  float S[8][4];
+  const TSin* sp = (const TSin*)p.sin + sbase;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (!rst) {
+      ld_row4<TSin>(sp + (int64_t)(8 * rg + r) * V + 4 * cg, S[r]);
+    } else {
+      S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
+    }
+  }
+
+  // q / k normalisation (lanes 0-127: q, 128-255: k), gates
+  float x = 0.f;
+  if (tid < 256) {
+    const int i = tid & 127;
+    const void* src = tid < 128 ? p.q : p.k;
+    x = ld_f(src, ((int64_t)bb * p.Hk + hk) * K + i, p.qk_dt);
+  }
+  float sq = x * x;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+  if ((tid & 63) == 0 && tid < 256) rbuf[tid >> 6] = sq;
+  __syncthreads();
+  if (tid < 256) {
+    const int i = tid & 127;
+    const float ss = tid < 128 ? rbuf[0] + rbuf[1] : rbuf[2] + rbuf[3];
+    float y;
+    if (p.l2norm) {
+      y = x / sqrtf(ss + 1e-6f);
+      if (tid < 128) y *= p.scale;
+    } else {
+      y = tid < 128 ? x * p.scale : x;
+    }
+    if (tid < 128) qn[i] = y; else kn[i] = y;
+  }
+  __syncthreads();
+  if (tid < K) {
+    const int i = tid;
+    const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
+    const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
+    float gv = ld_f(p.g, ((int64_t)bb * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
+    float bv = ld_f(p.b, ((int64_t)bb * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
+    gv = fminf(gv, 0.f);
+    if (p.guard) { bv = fmaxf(bv, 0.f); gv = fminf(gv, -1e-6f); }
+    dd[i] = __expf(gv);
+    bt[i] = bv * kn[i];
+  }
+  float qk_part = (tid < K) ? qn[tid] * kn[tid] : 0.f;
+  const float qk = block_sum512(qk_part, rbuf);
+
+  // partial column sums over this lane's 8 rows
+  float pa[4] = {0.f, 0.f, 0.f, 0.f}, pc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int i = 8 * rg + r;
+    const float di = dd[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      S[r][j] *= di;
+      pa[j] += bt[i] * S[r][j];
+      pc[j] += qn[i] * S[r][j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    red[0][rg][4 * cg + j] = pa[j];
+    red[1][rg][4 * cg + j] = pc[j];
+  }
+  __syncthreads();
+  if (tid < V) {
+    const int j = tid;
+    float A = 0.f, Cc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { A += red[0][r][j]; Cc += red[1][r][j]; }
+    const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+    const float wv = ld_f(p.w, ((int64_t)bb * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : j), p.w_dt);
+    const float vv = ld_f(p.v, ((int64_t)bb * p.Hv + hv) * V + j, p.v_dt);
+    const float nv = wv * vv - A;
+    vn[j] = nv;
+    const float o = Cc + qk * nv;
+    const int64_t oi = (int64_t)bh * V + j;
+    if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)o;
+    else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)o;
+    else ((float*)p.out)[oi] = o;
+  }
+  __syncthreads();
+  float ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float ki = kn[8 * rg + r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      S[r][j] += ki * vn[4 * cg + j];
+      ss += S[r][j] * S[r][j];
+    }
+  }
+  float fac = 1.f;
+  if (p.guard) {
+    const float tot = block_sum512(ss, rbuf);
+    fac = fminf(1.f, p.tau / sqrtf(tot + 1e-6f));
+  }
+  TSout* op = (TSout*)p.sout + sbase;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    float y[4] = {S[r][0] * fac, S[r][1] * fac, S[r][2] * fac, S[r][3] * fac};
+    st4<TSout>(op + (int64_t)(8 * rg + r) * V + 4 * cg, y);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_frob_cap(float* S, int64_t per, float tau) {
+  __shared__ float buf[4];
+  float* m = S + (int64_t)blockIdx.x * per;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < per; i += 256) ss += m[i] * m[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = buf[0] + buf[1] + buf[2] + buf[3];
+  const float fac = fminf(1.f, tau / sqrtf(tot + 1e-6f));
+  for (int64_t i = threadIdx.x; i < per; i += 256) m[i] *= fac;
+}
+
+}  // namespace dn
+
+using namespace dn;
+
+extern "C" const char* dn_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int dn_abi_version(void) { return DN_ABI_VERSION; }
+
+extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
+  if (a == nullptr) return set_error(DN_E_INVALID, "null args");
+  if (a->abi_version != DN_ABI_VERSION) return set_error(DN_E_ABI, "dn_decode_args built for another ABI version");
+  if (a->K != 128 || a->V != 128) return set_error(DN_E_INVALID, "K and V must both be 128");
+  if (a->B <= 0 || a->Hk <= 0 || a->Hv <= 0 || a->Hv % a->Hk) return set_error(DN_E_INVALID, "bad head counts");
+  if (!a->q || !a->k || !a->v || !a->g || !a->b || !a->w || !a->state_in || !a->state_out || !a->out)
+    return set_error(DN_E_INVALID, "missing tensor pointer");
+  auto gate_ok = [&](int H, int Cc, int dt) {
+    return (H == 1 || H == a->Hk || H == a->Hv) && (Cc == 1 || Cc == 128) && dt >= DN_F32 && dt <= DN_F16;
+  };
+  if (!gate_ok(a->g_heads, a->g_chans, a->g_dtype) || !gate_ok(a->b_heads, a->b_chans, a->b_dtype) ||
+      !gate_ok(a->w_heads, a->w_chans, a->w_dtype))
+    return set_error(DN_E_INVALID, "gate shape/dtype not supported");
+  const bool in_ok = a->state_in_dtype == DN_F32 || a->state_in_dtype == DN_BF16;
+  const bool out_ok = a->state_out_dtype == DN_F32 || a->state_out_dtype == DN_BF16;
+  if (!in_ok || !out_ok) return set_error(DN_E_INVALID, "state dtype must be f32 or bf16");
+  if (a->state_in == a->state_out && a->state_in_dtype != a->state_out_dtype)
+    return set_error(DN_E_INVALID, "in-place state update needs equal dtypes");
+  DP p{};
+  p.B = a->B; p.Hk = a->Hk; p.Hv = a->Hv; p.G = a->Hv / a->Hk;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.qk_dt = a->qk_dtype; p.v_dt = a->v_dtype;
+  p.g = a->g; p.g_dt = a->g_dtype; p.g_h = a->g_heads; p.g_c = a->g_chans;
+  p.b = a->b; p.b_dt = a->b_dtype; p.b_h = a->b_heads; p.b_c = a->b_chans;
+  p.w = a->w; p.w_dt = a->w_dtype; p.w_h = a->w_heads; p.w_c = a->w_chans;
+  p.sin = a->state_in; p.sout = a->state_out; p.reset = a->reset; p.out = a->out;
+  p.scale = a->scale; p.l2norm = a->qk_l2norm; p.guard = a->stability_guard; p.tau = a->stability_tau;
+  const dim3 grid((unsigned)(a->B * a->Hv));
+  hipStream_t st = (hipStream_t)stream;
+  const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
+  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(512), 0, st, p);
+  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(512), 0, st, p);
+  else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(512), 0, st, p);
+  else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(512), 0, st, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
+  return DN_OK;
+}
+
+extern "C" int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, float tau, void* stream) {
+  if (state == nullptr || nmat <= 0 || rows <= 0 || cols <= 0) return set_error(DN_E_INVALID, "bad cap arguments");
+  if (!(tau > 0.f)) return set_error(DN_E_INVALID, "tau must be positive");
+  hipLaunchKernelGGL(k_frob_cap, dim3((unsigned)nmat), dim3(256), 0, (hipStream_t)stream, state, (int64_t)rows * cols, tau);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
+  return DN_OK;
+}

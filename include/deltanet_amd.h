@@ -1,0 +1,135 @@
+/*
+ * deltanet_amd.h -- C ABI of the MI355X (gfx950) delta-rule recurrence core.
+ *
+ * Drop-in boundary for the forward path of maelie-labs/deltanet-tpu v0.3.0.
+ * In the reference the two device boundaries of chunk_gdn2 are Pallas calls
+ * inside a jax.custom_vjp (src/deltanet_tpu/gdn2.py:1262-1276 prepass,
+ * 1331-1347 sequential state/output pass, both launched by
+ * _chunked_recurrence_fwd gdn2.py:1176-1389) and the decode step is one XLA
+ * fusion (gdn2.py:2471-2478).  Each entry point below is what an XLA-FFI
+ * custom call (jax.ffi.ffi_call) or a ctypes / torch host binding would bind
+ * in their place.  Everything is plain C: device pointers, sizes, flags and an
+ * opaque HIP stream.  The library never allocates device memory for a call:
+ * scratch comes in through the `workspace` argument, whose size the caller
+ * asks for first.
+ *
+ * Tensor layouts (all row-major / C-contiguous, element strides implied):
+ *   q, k   (B, L, Hk, K)         v, out (B, L, Hv, V)
+ *   g, b   (B, L, Hx, Cx)        w      (B, L, Hx, Cx)
+ *          Hx in {1, Hk, Hv}; Cx in {1, K} for g/b and {1, V} for w.
+ *          A gate with Hx == Hk is shared by the G = Hv/Hk value heads of a
+ *          key head (value head hv reads head hv / G); Hx == 1 is shared by
+ *          all heads; Cx == 1 is one scalar per head.
+ *   seg    (B, L) or (L,) int32 / int64 segment (document) ids, or NULL.
+ *   state  (B, Hv, K, V) float32 (prefill) / float32 or bfloat16 (decode).
+ *
+ * Return value of every call: 0 on success, a negative DN_E* code otherwise;
+ * dn_last_error() gives the message of the calling thread's last failure.
+ */
+#ifndef DELTANET_AMD_H_
+#define DELTANET_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DN_ABI_VERSION 1
+
+/* element types */
+enum { DN_F32 = 0, DN_BF16 = 1, DN_F16 = 2, DN_I32 = 3, DN_I64 = 4 };
+
+/* error codes */
+enum {
+  DN_OK = 0,
+  DN_E_INVALID = -1,   /* bad shape / dtype / flag combination            */
+  DN_E_WORKSPACE = -2, /* workspace missing or smaller than required      */
+  DN_E_LAUNCH = -3,    /* HIP launch / runtime error                      */
+  DN_E_ABI = -4        /* args struct built against another ABI version   */
+};
+
+/* Arguments of one chunked prefill call (chunk_gdn2 forward, is_inference).
+ * Mirrors the static flags and operands of the reference's inference op
+ * (_get_inference_custom_vjp, gdn2.py:1392-1443) plus the wrapper-level
+ * semantics it performs before launching (gdn2.py:1970-2125), which this
+ * library applies inside its kernels instead of as extra HBM passes. */
+typedef struct dn_prefill_args {
+  int32_t abi_version;          /* must be DN_ABI_VERSION                      */
+  int32_t B, L, Hk, Hv, K, V;   /* tensor dims; K == V == 128 (gdn2.py:1897)   */
+  int32_t t0, nt;               /* token range [t0, t0+nt) of this call; t0 is a
+                                   multiple of 128 (streaming prefill block)   */
+  const void* q;                /* (B,L,Hk,K)                                   */
+  const void* k;                /* (B,L,Hk,K)                                   */
+  const void* v;                /* (B,L,Hv,V)                                   */
+  int32_t qk_dtype, v_dtype;    /* DN_F32 / DN_BF16 / DN_F16                    */
+  const void* g; int32_t g_dtype, g_heads, g_chans;
+  const void* b; int32_t b_dtype, b_heads, b_chans;
+  const void* w; int32_t w_dtype, w_heads, w_chans;
+  const void* seg;              /* NULL or segment ids                          */
+  int32_t seg_dtype;            /* DN_I32 / DN_I64                              */
+  int32_t seg_batched;          /* 1: seg is (B,L); 0: seg is (L,) shared       */
+  const float* init_state;      /* NULL or (B,Hv,K,V) f32; may alias final_state */
+  const int32_t* init_seg;      /* NULL or (B,) initial_state_segment_id         */
+  void* out;                    /* (B,L,Hv,V) of v_dtype                         */
+  float* final_state;           /* NULL or (B,Hv,K,V) f32                        */
+  float scale;                  /* query scale (1/sqrt(K) by default)            */
+  int32_t qk_l2norm;            /* L2-normalise q and k                          */
+  int32_t fuse_prologue;        /* raw g/b/w: g=-exp(min(g,5)), b,w=sigmoid      */
+  int32_t stability_guard;      /* clamps b>=0, g<=-1e-6 (not the state cap)     */
+  int32_t precision;            /* 0 = "bf16", 1 = "fp32"                        */
+  int32_t gates_at_hv;          /* 1: execute per value head (g or b has Hv heads) */
+  int32_t block_tokens;         /* internal token block (multiple of 128), 0=auto */
+} dn_prefill_args;
+
+/* Bytes of device workspace dn_prefill_fwd needs for these arguments. */
+size_t dn_prefill_workspace_size(const dn_prefill_args* a);
+
+/* Chunked WY prefill: replaces the prepass + sequential state pallas_calls of
+ * _chunked_recurrence_fwd (gdn2.py:1262-1276, 1331-1347) and the wrapper work
+ * around them (gate broadcast, segment canonicalisation, padding, q/k L2-norm,
+ * value-head fusion; gdn2.py:1970-2125, 2198-2238).  Enqueues on `stream`
+ * (a hipStream_t; NULL = default stream); never synchronises. */
+int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Arguments of one single-token decode step (gdn2_decode_step, gdn2.py:2289-2490). */
+typedef struct dn_decode_args {
+  int32_t abi_version;
+  int32_t B, Hk, Hv, K, V;      /* K == V == 128                                 */
+  const void* q;                /* (B,Hk,K)                                      */
+  const void* k;                /* (B,Hk,K)                                      */
+  const void* v;                /* (B,Hv,V)                                      */
+  int32_t qk_dtype, v_dtype;
+  const void* g; int32_t g_dtype, g_heads, g_chans;   /* (B,Hx,Cx) */
+  const void* b; int32_t b_dtype, b_heads, b_chans;
+  const void* w; int32_t w_dtype, w_heads, w_chans;
+  const void* state_in;  int32_t state_in_dtype;      /* (B,Hv,K,V) f32 / bf16  */
+  void* state_out;       int32_t state_out_dtype;     /* may alias state_in      */
+  const uint8_t* reset;         /* NULL or (B,) : clear the state first          */
+  void* out;                    /* (B,Hv,V) of v_dtype                            */
+  float scale;
+  int32_t qk_l2norm;
+  int32_t stability_guard;      /* clamps + Frobenius cap of the new state        */
+  float stability_tau;
+} dn_decode_args;
+
+/* Decode step: replaces the XLA fusion of gdn2.py:2393-2489 (upcast, clamp,
+ * reset, GQA repeat, L2-norm, decay/erase/write/readout, cap, state cast). */
+int dn_decode_step(const dn_decode_args* a, void* stream);
+
+/* In-place Frobenius cap S <- S * min(1, tau / sqrt(||S||_F^2 + 1e-6)) of
+ * `nmat` consecutive (rows x cols) float32 matrices (the stability_guard cap of
+ * gdn2.py:2180-2188 / 2224-2226 / 2236-2238). */
+int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, float tau, void* stream);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* dn_last_error(void);
+
+/* DN_ABI_VERSION the library was built with. */
+int dn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DELTANET_AMD_H_ */

@@ -1,0 +1,82 @@
+"""The C-ABI library loads and exports every entry point include/deltanet_amd.h
+declares, and the ctypes mirrors of the argument structs have the C layout
+(compiled here with gcc from the header).  No compute calls: CPU-only."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from deltanet_tpu_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "deltanet_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT\s+(dn_[a-z0-9_]+)\b", out))
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, f"missing exports: {missing}"
+    lib = _lib.load_library()
+    assert lib.dn_abi_version() == _lib.DN_ABI_VERSION
+    assert lib.dn_last_error() == b""
+
+
+def test_struct_layout_matches_header(tmp_path):
+    fields = {
+        "dn_prefill_args": _lib.PrefillArgs,
+        "dn_decode_args": _lib.DecodeArgs,
+    }
+    src = ['#include <stdio.h>', '#include <stddef.h>', '#include "deltanet_amd.h"', "int main(void){"]
+    for cname, cls in fields.items():
+        src.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            src.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    src.append("return 0;}")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(c), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, got):
+        parts = line.split()
+        cls = fields[parts[0]]
+        if parts[1] == "size":
+            assert ctypes.sizeof(cls) == int(parts[2]), line
+        else:
+            assert getattr(cls, parts[1]).offset == int(parts[2]), line
+
+
+def test_invalid_args_rejected_without_gpu():
+    """Argument checking happens before any HIP call, so it runs on the CPU."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _lib.load_library()
+    a = _lib.PrefillArgs()
+    a.abi_version = _lib.DN_ABI_VERSION
+    a.B, a.L, a.Hk, a.Hv, a.K, a.V = 1, 128, 2, 4, 64, 64
+    assert lib.dn_prefill_workspace_size(ctypes.byref(a)) == 0
+    rc = lib.dn_prefill_fwd(ctypes.byref(a), None, 0, None)
+    assert rc == -1 and b"128" in lib.dn_last_error()
+    a.abi_version = 99
+    assert lib.dn_prefill_fwd(ctypes.byref(a), None, 0, None) == -4
+    d = _lib.DecodeArgs()
+    d.abi_version = _lib.DN_ABI_VERSION
+    d.B, d.Hk, d.Hv, d.K, d.V = 1, 2, 3, 128, 128
+    assert lib.dn_decode_step(ctypes.byref(d), None) == -1
+    assert lib.dn_state_frob_cap(None, 1, 128, 128, 1.0, None) == -1

@@ -1,0 +1,157 @@
+"""BASELINE.json configurations at their full sizes on the GPU, checked against
+the oracle (the C restatement for the long ones, on a subset of heads/batch rows
+where the full problem is too large for a CPU check -- heads and batch rows are
+independent chains, so a slice is an exact sub-problem)."""
+
+import numpy as np
+import pytest
+import torch
+
+from deltanet_tpu_amd import chunk_gdn, chunk_gdn2, gdn2_decode_step
+from oracle import gdn_oracle as O
+from tests._util import sig
+from tests.gpu_common import as_np, check, oracle_prefill, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def geometric_segments(rng, B, L, mean, lo=16):
+    seg = np.zeros((B, L), np.int32)
+    for b in range(B):
+        t, d = 0, 0
+        while t < L:
+            n = int(np.clip(rng.geometric(1.0 / mean), lo, L))
+            seg[b, t:t + n] = d
+            t += n
+            d += 1
+    return seg
+
+
+def test_config1_shape_rejected_like_reference():
+    # K = V = 64 and chunk_size = 64 are rejected by the reference API
+    # (gdn2.py:1869-1870, 1897-1898); the drop-in keeps that contract.
+    z = lambda *s: torch.zeros(*s, device="cuda:0")
+    with pytest.raises(ValueError, match="Unsupported head dimensions"):
+        chunk_gdn2(z(1, 256, 2, 64), z(1, 256, 2, 64), z(1, 256, 4, 64), z(1, 256, 2, 64), z(1, 256, 2, 64),
+                   z(1, 256, 4, 64))
+
+
+def test_config1_at_supported_head_dim():
+    # config 1 with K = V = 128 (the only size the reference API accepts), fp32
+    rng = np.random.default_rng(1000)
+    B, L, Hk, Hv = 1, 256, 2, 4
+    q, k, v = rng.standard_normal((B, L, Hk, 128)), rng.standard_normal((B, L, Hk, 128)), rng.standard_normal((B, L, Hv, 128))
+    b = sig(0.39 * rng.standard_normal((B, L, Hk, 128)))
+    w = sig(0.39 * rng.standard_normal((B, L, Hv, 128)))
+    g = -np.exp(0.39 * rng.standard_normal((B, L, Hk, 128)) - 1)
+    seg = (np.arange(L) >= L // 2).astype(np.int32)[None]
+    T = to_dev
+    out, st = chunk_gdn2(T(q), T(k), T(v), T(g), T(b), T(w), segment_ids=T(seg, torch.int32), output_final_state=True,
+                         precision="fp32", qk_l2norm=True, is_inference=True)
+    ro, rs = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg, output_final_state=True, qk_l2norm=True)
+    check(out, ro, st, rs, "fp32", "fp32", "config1@K128")
+
+
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_config2_gdn2_prefill(precision):
+    rng = np.random.default_rng(2000)
+    B, L, Hk, Hv = 1, 2048, 12, 24
+    bfr = lambda x: O.bf16_round(x).astype(np.float64)
+    q, k, v = (bfr(rng.standard_normal(s)) for s in ((B, L, Hk, 128), (B, L, Hk, 128), (B, L, Hv, 128)))
+    b = sig(0.39 * rng.standard_normal((B, L, Hk, 128))).astype(np.float32)
+    w = sig(0.39 * rng.standard_normal((B, L, Hv, 128))).astype(np.float32)
+    g = (-np.exp(0.39 * rng.standard_normal((B, L, Hk, 128)) - 1)).astype(np.float32)
+    seg = (np.arange(L) >= 1024).astype(np.int32)[None]
+    out, st = chunk_gdn2(to_dev(q, torch.bfloat16), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16),
+                         to_dev(g), to_dev(b), to_dev(w), segment_ids=to_dev(seg, torch.int32),
+                         output_final_state=True, precision=precision, qk_l2norm=True, is_inference=True)
+    torch.cuda.synchronize()
+    ro, rs = oracle_prefill(q, k, v, g, b, w, segment_ids=seg, qk_l2norm=True, qk_dtype="bf16", use_c=True)
+    check(out, ro, st, rs, precision, "bf16", f"config2 {precision}")
+
+
+def test_config3_gdn_packed_documents():
+    rng = np.random.default_rng(3000)
+    B, L, Hk, Hv = 4, 8192, 16, 32
+    q = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    k = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    v = rng.standard_normal((B, L, Hv, 128)).astype(np.float32)
+    A_log = rng.uniform(np.log(1), np.log(16), Hv)
+    a = rng.standard_normal((B, L, Hv))
+    g = (-np.exp(A_log) * np.log1p(np.exp(a))).astype(np.float32)
+    beta = sig(rng.standard_normal((B, L, Hv))).astype(np.float32)
+    seg = geometric_segments(rng, B, L, 1024)
+    tb = lambda x: to_dev(x, torch.bfloat16)
+    out, st = chunk_gdn(tb(q), tb(k), tb(v), to_dev(g), to_dev(beta), segment_ids=to_dev(seg, torch.int32),
+                        output_final_state=True, qk_l2norm=True, is_inference=True, precision="bf16")
+    torch.cuda.synchronize()
+    # oracle on batch rows {0, 3} and key heads {0, 15} (value heads {0,1,30,31})
+    rows, hks = [0, 3], [0, 15]
+    hvs = [h * 2 + j for h in hks for j in range(2)]
+    bfr = lambda x: O.bf16_round(x).astype(np.float64)
+    ro, rs = oracle_prefill(bfr(q[rows][:, :, hks]), bfr(k[rows][:, :, hks]), bfr(v[rows][:, :, hvs]),
+                            g[rows][:, :, hvs], beta[rows][:, :, hvs], beta[rows][:, :, hvs],
+                            segment_ids=seg[rows], qk_l2norm=True, qk_dtype="bf16", use_c=True)
+    o = out[rows][:, :, hvs]
+    s = st[rows][:, hvs]
+    check(o, ro, s, rs, "bf16", "bf16", "config3 (rows 0,3; heads 0,15)")
+
+
+@pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
+def test_config4_decode_trajectory(state_dtype):
+    rng = np.random.default_rng(4000)
+    B, Hk, Hv, steps = 256, 16, 32, 64
+    rows = [0, 77, 255]
+    S0 = (0.02 * rng.standard_normal((B, Hv, 128, 128))).astype(np.float32)
+    st = to_dev(S0)
+    if state_dtype == "bfloat16":
+        st = st.to(torch.bfloat16)
+    ref = S0[rows].astype(np.float64)
+    if state_dtype == "bfloat16":
+        ref = O.bf16_round(ref).astype(np.float64)
+    worst = 0.0
+    for t in range(steps):
+        q = rng.standard_normal((B, 1, Hk, 128)).astype(np.float32)
+        k = rng.standard_normal((B, 1, Hk, 128)).astype(np.float32)
+        v = rng.standard_normal((B, 1, Hv, 128)).astype(np.float32)
+        b = sig(0.39 * rng.standard_normal((B, 1, Hk, 128))).astype(np.float32)
+        w = sig(0.39 * rng.standard_normal((B, 1, Hv, 128))).astype(np.float32)
+        g = (-np.exp(0.39 * rng.standard_normal((B, 1, Hk, 128)) - 1)).astype(np.float32)
+        tb = lambda x: to_dev(x, torch.bfloat16)
+        o, st = gdn2_decode_step(tb(q), tb(k), tb(v), to_dev(g), to_dev(b), to_dev(w), st, qk_l2norm=True,
+                                 state_dtype=state_dtype)
+        bfr = lambda x: O.bf16_round(x[rows]).astype(np.float64)
+        ro, ref = O.decode_step(bfr(q), bfr(k), bfr(v), g[rows], b[rows], w[rows], ref, qk_l2norm=True)
+        if state_dtype == "bfloat16":
+            ref = O.bf16_round(ref).astype(np.float64)  # the reference stores the state as bf16 each step
+        prec = "fp32" if state_dtype == "float32" else "bf16"
+        e = check(o[rows][:, 0], ro, st[rows], ref, prec, "bf16", f"config4 step {t} {state_dtype}")
+        worst = max(worst, e)
+    print(f"[measured] config4 {state_dtype}: worst step out maxabs/rms {worst:.3e}")
+
+
+def test_config5_streaming_fused_prologue():
+    rng = np.random.default_rng(5000)
+    B, L, Hk, Hv = 1, 65536, 16, 32
+    hk_sel = [5]
+    hv_sel = [10, 11]
+    q = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    k = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    v = rng.standard_normal((B, L, Hv, 128)).astype(np.float32)
+    g = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    b = rng.standard_normal((B, L, Hk, 128)).astype(np.float32)
+    w = rng.standard_normal((B, L, Hv, 128)).astype(np.float32)
+    seg = geometric_segments(rng, B, L, 8192)
+    tb = lambda x: to_dev(x, torch.bfloat16)
+    out, st = chunk_gdn2(tb(q), tb(k), tb(v), to_dev(g), to_dev(b), to_dev(w), segment_ids=to_dev(seg, torch.int32),
+                         output_final_state=True, qk_l2norm=True, fuse_prologue=True, is_inference=True,
+                         streaming_prefill=True, prefill_block_size=8192, precision="bf16")
+    torch.cuda.synchronize()
+    o = out[:, :, hv_sel]
+    s = st[:, hv_sel]
+    del out
+    bfr = lambda x: O.bf16_round(x).astype(np.float64)
+    ro, rs = oracle_prefill(bfr(q[:, :, hk_sel]), bfr(k[:, :, hk_sel]), bfr(v[:, :, hv_sel]), g[:, :, hk_sel],
+                            b[:, :, hk_sel], w[:, :, hv_sel], segment_ids=seg, qk_l2norm=True, fuse_prologue=True,
+                            qk_dtype="fp32", use_c=True)
+    check(o, ro, s, rs, "bf16", "bf16", "config5 (head 5)")

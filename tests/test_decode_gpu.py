@@ -1,0 +1,169 @@
+"""GPU parity of the decode step (gdn2_decode_step and variants) against the
+oracle, mirroring the reference's test_inference.py:64-185, test_matrix.py
+decode cases (367-428), test_variants.py decode cases and
+test_streaming_and_stability.py:65-91."""
+
+import numpy as np
+import pytest
+import torch
+
+from deltanet_tpu_amd import (chunk_gdn2, delta_rule_decode_step, gdn2_decode_step, gdn_decode_step,
+                              gla_decode_step, kda_decode_step)
+from oracle import gdn_oracle as O
+from tests._util import rel_l2, sig
+from tests.gpu_common import as_np, check, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def dec_inputs(seed, B, Hk, Hv, g_shape="hk_k", b_shape="hk_k", w_shape="hv_v", four_d=True):
+    rng = np.random.default_rng(seed)
+    K = 128
+
+    def gate(spec, last):
+        heads, chan = spec.split("_")
+        H = {"hk": Hk, "hv": Hv, "one": 1}[heads]
+        shape = (B, H) if chan == "none" else (B, H, 1 if chan == "1" else last)
+        return shape
+
+    q = rng.standard_normal((B, Hk, K))
+    k = rng.standard_normal((B, Hk, K))
+    v = rng.standard_normal((B, Hv, K))
+    g = -np.exp(rng.standard_normal(gate(g_shape, K)) - 1.0)
+    b = sig(rng.standard_normal(gate(b_shape, K)))
+    w = sig(rng.standard_normal(gate(w_shape, K)))
+    if four_d:
+        q, k, v = q[:, None], k[:, None], v[:, None]
+        if g.ndim == 3:
+            g = g[:, None]
+        if b.ndim == 3:
+            b = b[:, None]
+        if w.ndim == 3:
+            w = w[:, None]
+    return q, k, v, g, b, w
+
+
+@pytest.mark.parametrize("layout", [("hk_k", "hk_k", "hv_v"), ("hv_none", "hv_none", "hv_none"),
+                                    ("hk_1", "hk_none", "hk_v"), ("one_k", "one_1", "one_none")])
+@pytest.mark.parametrize("Hk,Hv", [(2, 2), (2, 4), (1, 4)])
+@pytest.mark.parametrize("four_d", [True, False])
+def test_decode_matrix(layout, Hk, Hv, four_d):
+    B = 3
+    q, k, v, g, b, w = dec_inputs(Hk * 7 + Hv, B, Hk, Hv, *layout, four_d=four_d)
+    S = 0.1 * np.random.default_rng(1).standard_normal((B, Hv, 128, 128))
+    reset = np.array([False, True, False])
+    T = lambda x: to_dev(x)
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), reset=torch.tensor(reset), qk_l2norm=True)
+    ro, rs = O.decode_step(q, k, v, g, b, w, S, reset=reset, qk_l2norm=True)
+    assert o.shape == ((B, 1, Hv, 128) if four_d else (B, Hv, 128))
+    check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", f"decode {layout} {Hk}/{Hv} 4d={four_d}")
+
+
+@pytest.mark.parametrize("state_dtype", [None, "bfloat16", torch.float32, torch.bfloat16])
+def test_decode_state_dtype_contract(state_dtype):
+    B, Hk, Hv = 2, 2, 4
+    q, k, v, g, b, w = dec_inputs(3, B, Hk, Hv)
+    S = 0.1 * np.random.default_rng(2).standard_normal((B, Hv, 128, 128))
+    T = lambda x: to_dev(x)
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), state_dtype=state_dtype)
+    exp = torch.bfloat16 if state_dtype in ("bfloat16", torch.bfloat16) else torch.float32
+    assert s.dtype == exp and o.dtype == torch.float32
+    ro, rs = O.decode_step(q, k, v, g, b, w, S)
+    tol = 1e-2 if exp == torch.bfloat16 else 1e-5
+    assert rel_l2(as_np(s), rs) < tol
+
+
+def test_decode_bf16_state_tracks_fp32_over_10_steps():
+    # test_inference.py:150-185
+    B, Hk, Hv = 2, 2, 4
+    T = lambda x: to_dev(x)
+    S0 = 0.02 * np.random.default_rng(3).standard_normal((B, Hv, 128, 128))
+    s32 = T(S0)
+    s16 = T(S0).to(torch.bfloat16)
+    for t in range(10):
+        q, k, v, g, b, w = dec_inputs(100 + t, B, Hk, Hv)
+        args = [T(x) for x in (q, k, v, g, b, w)]
+        o32, s32 = gdn2_decode_step(*args, s32, qk_l2norm=True)
+        o16, s16 = gdn2_decode_step(*args, s16, qk_l2norm=True, state_dtype="bfloat16")
+    assert rel_l2(as_np(s16), as_np(s32)) < 1e-2
+    assert rel_l2(as_np(o16), as_np(o32)) < 1e-2
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_decode_steps_equal_chunk_gdn2_with_reset(dtype):
+    # test_inference.py:64-110
+    B, N, Hk, Hv = 1, 128, 2, 4
+    rng = np.random.default_rng(101)
+    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    q = to_dev(0.1 * rng.standard_normal((B, N, Hk, 128)), tdt)
+    k = to_dev(0.1 * rng.standard_normal((B, N, Hk, 128)), tdt)
+    v = to_dev(0.1 * rng.standard_normal((B, N, Hv, 128)), tdt)
+    g = to_dev(-np.exp(rng.standard_normal((B, N, Hk, 128)) - 1.0))
+    b = to_dev(sig(rng.standard_normal((B, N, Hk, 128))))
+    w = to_dev(sig(rng.standard_normal((B, N, Hv, 128))))
+    reset_idx = N // 2
+    seg = to_dev((np.arange(N) >= reset_idx)[None], torch.int32)
+    out_c, st_c = chunk_gdn2(q, k, v, g, b, w, segment_ids=seg, is_inference=True, output_final_state=True,
+                             precision=dtype)
+    state = torch.zeros(B, Hv, 128, 128, device="cuda:0")
+    outs = []
+    for t in range(N):
+        ot, state = gdn2_decode_step(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], g[:, t:t + 1], b[:, t:t + 1],
+                                     w[:, t:t + 1], state, reset=(t == reset_idx))
+        outs.append(ot)
+    tol = 1e-4 if dtype == "fp32" else 1e-2
+    assert rel_l2(as_np(torch.cat(outs, 1)), as_np(out_c)) < tol
+    assert rel_l2(as_np(state), as_np(st_c)) < tol
+
+
+def test_decode_stability_guard():
+    # test_streaming_and_stability.py:65-91: the returned state is capped, the
+    # output of the step uses the uncapped state
+    B, Hk, Hv = 2, 2, 4
+    q, k, v, g, b, w = dec_inputs(5, B, Hk, Hv)
+    S = 10.0 * np.random.default_rng(4).standard_normal((B, Hv, 128, 128))
+    T = lambda x: to_dev(x)
+    tau = 100.0
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), stability_guard=True, stability_tau=tau)
+    assert bool((torch.linalg.vector_norm(s, dim=(-2, -1)) <= tau * 1.001).all())
+    ro, rs = O.decode_step(q, k, v, g, b, w, S, stability_guard=True, stability_tau=tau)
+    check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", "decode guard")
+
+
+def test_decode_in_place_state():
+    B, Hk, Hv = 2, 2, 4
+    q, k, v, g, b, w = dec_inputs(6, B, Hk, Hv)
+    S = 0.1 * np.random.default_rng(5).standard_normal((B, Hv, 128, 128))
+    T = lambda x: to_dev(x)
+    st = T(S)
+    o1, s1 = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), st)
+    o2, s2 = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), st, out_state=st)
+    assert s2.data_ptr() == st.data_ptr()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("variant", ["gdn", "kda", "gla", "delta"])
+def test_decode_variants(variant):
+    B, Hk, Hv = 2, 2, 4
+    rng = np.random.default_rng(7)
+    q, k = rng.standard_normal((2, B, 1, Hk, 128))
+    v = rng.standard_normal((B, 1, Hv, 128))
+    S = 0.1 * rng.standard_normal((B, Hv, 128, 128))
+    T = lambda x: to_dev(x)
+    beta = sig(rng.standard_normal((B, 1, Hv)))
+    if variant == "gdn":
+        g = -np.exp(rng.standard_normal((B, 1, Hv)))
+        o, s = gdn_decode_step(T(q), T(k), T(v), T(g), T(beta), T(S), qk_l2norm=True)
+        ro, rs = O.gdn_decode_step(q, k, v, g, beta, S, qk_l2norm=True)
+    elif variant == "kda":
+        g = -np.exp(rng.standard_normal((B, 1, Hk, 128)))
+        o, s = kda_decode_step(T(q), T(k), T(v), T(g), T(beta), T(S), qk_l2norm=True)
+        ro, rs = O.gdn_decode_step(q, k, v, g, beta, S, qk_l2norm=True)
+    elif variant == "gla":
+        g = -np.exp(rng.standard_normal((B, 1, Hk, 128)))
+        o, s = gla_decode_step(T(q), T(k), T(v), T(g), T(S), qk_l2norm=True)
+        ro, rs = O.decode_step(q, k, v, g, np.zeros((B, 1)), np.ones((B, 1)), S, qk_l2norm=True)
+    else:
+        o, s = delta_rule_decode_step(T(q), T(k), T(v), T(beta), T(S), qk_l2norm=True)
+        ro, rs = O.decode_step(q, k, v, np.zeros((B, 1)), beta[:, 0], beta[:, 0], S, qk_l2norm=True)
+    check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", f"decode {variant}")
