@@ -145,4 +145,54 @@ template <bool BF> __device__ __forceinline__ Frag<BF> frag_from_acc(const f32x4
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// ---------------------------------------------------------------------------
+// Precision policy.  "bf16" mode runs plain products on bf16 MFMA and the
+// products that set the output accuracy as split-bf16 products: an fp32
+// operand x is carried as hi = bf16(x), lo = bf16(x - hi) (16 significant
+// bits) and a*b ~ a_hi*b_hi + a_hi*b_lo + a_lo*b_hi, all accumulated in fp32.
+// "fp32" mode runs every product on v_mfma_f32_16x16x4_f32.
+// ---------------------------------------------------------------------------
+template <bool BF> struct Pol;
+
+template <> struct Pol<true> {
+  using F1 = Frag<true>;
+  struct F3 { Frag<true> hi, lo; };
+  static __device__ __forceinline__ F1 f1(const float* x) { return make_frag<true>(x); }
+  static __device__ __forceinline__ F3 f3(const float* x) {
+    F3 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bf16 h = (bf16)x[e];
+      r.hi.v[e] = h;
+      r.lo.v[e] = (bf16)(x[e] - (float)h);
+    }
+    return r;
+  }
+  static __device__ __forceinline__ F1 hi(const F3& a) { return a.hi; }
+  static __device__ __forceinline__ void m11(f32x4& c, const F1& a, const F1& b) { mma(c, a, b); }
+  static __device__ __forceinline__ void m13(f32x4& c, const F1& a, const F3& b) { mma(c, a, b.hi); mma(c, a, b.lo); }
+  static __device__ __forceinline__ void m33(f32x4& c, const F3& a, const F3& b) {
+    mma(c, a.hi, b.hi);
+    mma(c, a.hi, b.lo);
+    mma(c, a.lo, b.hi);
+  }
+};
+
+template <> struct Pol<false> {
+  using F1 = Frag<false>;
+  using F3 = Frag<false>;
+  static __device__ __forceinline__ F1 f1(const float* x) { return make_frag<false>(x); }
+  static __device__ __forceinline__ F3 f3(const float* x) { return make_frag<false>(x); }
+  static __device__ __forceinline__ F1 hi(const F3& a) { return a; }
+  static __device__ __forceinline__ void m11(f32x4& c, const F1& a, const F1& b) { mma(c, a, b); }
+  static __device__ __forceinline__ void m13(f32x4& c, const F1& a, const F3& b) { mma(c, a, b); }
+  static __device__ __forceinline__ void m33(f32x4& c, const F3& a, const F3& b) { mma(c, a, b); }
+};
+
+// 8 fragment values (pi order) from a row-major row pointer at the slab start
+template <class T> __device__ __forceinline__ void row8(const T* rowp, int q, float* x) {
+  ld4<T>(rowp + 4 * q, x);
+  ld4<T>(rowp + 16 + 4 * q, x + 4);
+}
+
 }  // namespace dn

@@ -14,6 +14,7 @@ struct PF {
   int B, L, Hk, Hv, G;       // tensor dims, G = Hv / Hk
   int Hx, Vp, gates_at_hv;   // execution heads, value width per execution head
   int t0, nt, NCb;           // token block [t0, t0+nt), chunks in the block
+  int ncg;                   // 256-column groups of the value width (k_output)
   const void *q, *k, *v;
   int v_dt;
   const void* g; int g_dt, g_h, g_c;
@@ -27,13 +28,13 @@ struct PF {
   float scale; int l2norm, fuse, guard;
   // workspace arrays (one unit = one (batch, exec head, chunk))
   int32_t* flags;            // [B][NCb][2] : is_new_doc, all_same_doc
-  float* dvec;               // [unit][K]   : e^{Lambda_end}
-  void *Wn, *qe, *be, *ke;   // [unit][C][K]: -W, qe, be, ke
-  void* M;                   // [unit][C][C]
-  void* U;                   // [unit][C][Vp]
-  void* Pn;                  // [unit][K][K]: -ke^T W
+  float* dvec;               // [unit][K]    : e^{Lambda_end}
+  void* Pn;                  // [unit][K][K] : -ke^T W (bf16 in bf16 mode)
   float* Q;                  // [unit][K][Vp]: ke^T U
-  void* St;                  // [unit][Vp][K]: entry state of the chunk, transposed
+  float* X;                  // [unit][C][K] : qe - M W   (effective queries)
+  float* Oi;                 // [unit][C][Vp]: M U        (intra-chunk output)
+  float* St;                 // [unit][Vp][K]: entry state of the chunk, transposed
+  float *beT, *keT, *Mg, *qe;  // prepass scratch: [K][C], [K][C], [C][C], [C][K]
 };
 
 // Records the message for dn_last_error() and returns `code`.

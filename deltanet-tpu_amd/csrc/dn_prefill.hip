@@ -9,19 +9,20 @@
 //                                segment canonicalisation, padding)
 //
 // The MI355X design splits the work into three launches per token block so
-// that only a 128x128-by-128x16 product sits on the sequential critical path:
-//
+// that only a 128x128-by-128x16 product sits on the sequential critical path.
+// With Vnew = U - W S the reference's per-chunk update and output become
+//     S_next = [same doc] diag(e^Lend) S + Pn S + Q,  Pn = -ke^T W,  Q = ke^T U
+//     O      = X S + Oi,                              X = qe - M W,  Oi = M U
+// so:
 //   k_prepass (grid: chunk x exec-head x batch, 4 waves, one chunk each)
 //       everything that is parallel over chunks: fused prologue, Lambda,
-//       A and M on MFMA, T by blocked substitution on fp32 MFMA, W = T be,
-//       U = T (w*v), and the chunk's affine state map
-//           S_next = [same doc] diag(e^Lend) S + Pn S + Q,
-//           Pn = -ke^T W (K x K),   Q = ke^T U (K x V').
-//   k_chain   (grid: 16-column tile x exec-head x batch, 1 wave)
-//       the sequential scan S_{c+1} = D S_c + Pn_c S_c + Q_c with the fp32
-//       state in VGPRs; stores each chunk's entry state S_c.
-//   k_output  (grid: chunk x exec-head x batch, V'/64 waves)
-//       parallel again: Vnew = U - W S_c, O = qe S_c + M Vnew.
+//       A and M on MFMA, T by blocked substitution on fp32 MFMA, W, U and
+//       the four chunk operators Pn, Q, X, Oi.
+//   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
+//       the sequential scan over chunks with the fp32 state in VGPRs;
+//       stores each chunk's entry state S_c.
+//   k_output  (grid: chunk x exec-head x batch, 4 waves)
+//       parallel again: O = X S_c + Oi.
 //
 // All intermediates live in a caller-provided workspace sized for one token
 // block, small enough to stay resident in the 256 MB Infinity Cache.
@@ -79,16 +80,28 @@ __device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
 template <bool BF> using MTy = typename std::conditional<BF, bf16, float>::type;
 
 // ===========================================================================
-// k_prepass
+// k_prepass: everything that is parallel over chunks (one workgroup, 4 waves,
+// per (chunk, execution head, batch)).
+//
+// Lambda is kept block-local: X[i] = sum of g over the 16-token block of i up
+// to and including i (log2 units), so a difference of two Lambdas is never
+// the difference of two large cumulative sums (no fp32 cancellation after a
+// strongly decayed stretch).  Cross-block factors come from the per-block
+// totals: Off[a] / Suf[a] = sum of the totals before / after block a.
 // ===========================================================================
 template <bool BF, class TIn>
 __global__ __launch_bounds__(256) void k_prepass(const PF p) {
+  using P = Pol<BF>;
+  using F1 = typename P::F1;
+  using F3 = typename P::F3;
   using MT = MTy<BF>;
-  constexpr int YP = BF ? 136 : 132;  // Kc pitch (elements)
-  __shared__ float X[CH * XP];        // Lambda (log2 units) -> A -> T
-  __shared__ MT Y[CH * YP];           // Kc = k * e^{Lambda_end(block) - Lambda}
-  __shared__ float Ftab[8 * KD];      // e^{Lambda(16b+15) - Lambda(16b-1)}
-  __shared__ float Mid0[8 * KD];      // e^{Lambda(16a) - Lambda(16a-1)}
+  constexpr int YP = 132;
+  __shared__ float X[CH * XP];      // local Lambda (log2) -> A -> T
+  __shared__ float Y[CH * YP];      // Lambda low words (1-2), Kc (2-3), w*v transposed (6)
+  __shared__ float Ftab[8 * KD];    // e^{total of block b}
+  __shared__ float Mid0[8 * KD];    // e^{g at the first token of block a}
+  __shared__ float Off[9 * KD];     // log2: sum of totals of blocks < a (Off[8] = Lambda_end)
+  __shared__ float Suf[8 * KD];     // log2: sum of totals of blocks > a
   __shared__ int doc[CH];
 
   const int tid = threadIdx.x;
@@ -99,15 +112,15 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
   const int hk = p.gates_at_hv ? h / p.G : h;
 
-  MT* g_Wn = (MT*)p.Wn + u * CH * KD;
-  MT* g_qe = (MT*)p.qe + u * CH * KD;
-  MT* g_be = (MT*)p.be + u * CH * KD;
-  MT* g_ke = (MT*)p.ke + u * CH * KD;
-  MT* g_M = (MT*)p.M + u * CH * CH;
-  MT* g_U = (MT*)p.U + u * CH * p.Vp;
   MT* g_Pn = (MT*)p.Pn + u * KD * KD;
   float* g_Q = p.Q + u * KD * p.Vp;
+  float* g_X = p.X + u * CH * KD;
+  float* g_Oi = p.Oi + u * CH * p.Vp;
   float* g_dv = p.dvec + u * KD;
+  float* g_beT = p.beT + u * KD * CH;
+  float* g_keT = p.keT + u * KD * CH;
+  float* g_M = p.Mg + u * CH * CH;
+  float* g_qe = p.qe + u * CH * KD;
 
   // ---- phase 0: in-chunk document index (segment canonicalisation) -------
   if (tid < CH) {
@@ -147,30 +160,62 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     p.flags[((int64_t)b * p.NCb + c) * 2 + 1] = (doc[CH - 1] == 0);
   }
 
-  // ---- phase 1: Lambda = inclusive cumsum of g over the chunk -------------
+  // ---- phase 1: block-local Lambda (double-float: X = hi, Y = lo), totals --
   {
     const int kap = tid & 127, half = tid >> 7;
     const int hg = kgate_head(p, p.g_h, h);
-    float run = 0.f;
-    for (int i = 64 * half; i < 64 * half + 64; ++i) {
-      const int t = tb + i;
-      float gv = 0.f;
+    float gl[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int t = tb + 64 * half + i;
+      gl[i] = 0.f;
       if (t < t_end) {
         const int64_t gi = (((int64_t)b * p.L + t) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
-        gv = act_g(ld_f(p.g, gi, p.g_dt), p.fuse, p.guard);
+        gl[i] = act_g(ld_f(p.g, gi, p.g_dt), p.fuse, p.guard);
       }
-      run += gv;
-      X[i * XP + kap] = run;
     }
-    __syncthreads();
-    const float add = half ? X[63 * XP + kap] : 0.f;
-    __syncthreads();
-    for (int i = 64 * half; i < 64 * half + 64; ++i) X[i * XP + kap] = (X[i * XP + kap] + add) * kLog2e;
-    __syncthreads();
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      float hi = 0.f, lo = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        // error-free accumulation (TwoSum), then an exact split of hi * log2(e)
+        const float gv = gl[16 * blk + j];
+        const float sum = hi + gv;
+        const float bb = sum - hi;
+        lo += (hi - (sum - bb)) + (gv - bb);
+        hi = sum;
+        const float ph = hi * kLog2e;
+        const float pe = fmaf(hi, kLog2e, -ph);
+        const int row = 64 * half + 16 * blk + j;
+        X[row * XP + kap] = ph;
+        Y[row * XP + kap] = pe + lo * kLog2e;
+      }
+    }
   }
+  __syncthreads();
+  if (tid < KD) {
+    float tot[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) tot[a] = X[(16 * a + 15) * XP + tid] + Y[(16 * a + 15) * XP + tid];
+    float acc = 0.f;
+#pragma unroll
+    for (int a = 0; a < 8; ++a) { Off[a * KD + tid] = acc; acc += tot[a]; }
+    Off[8 * KD + tid] = acc;
+    acc = 0.f;
+#pragma unroll
+    for (int a = 7; a >= 0; --a) { Suf[a * KD + tid] = acc; acc += tot[a]; }
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      Ftab[a * KD + tid] = fast_exp2(tot[a]);
+      Mid0[a * KD + tid] = fast_exp2(X[(16 * a) * XP + tid] + Y[(16 * a) * XP + tid]);
+    }
+    g_dv[tid] = fast_exp2(Off[8 * KD + tid]);
+  }
+  __syncthreads();
 
   // ---- phase 2: per-row quantities, diagonal A/M blocks --------------------
-  Frag<BF> Rf[2][4], Qf[2][4];
+  F3 Rf[2][4], Qf[2][4];
   f32x4 Adiag[2];
   const int hbg = kgate_head(p, p.b_h, h);
 #pragma unroll
@@ -179,16 +224,14 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     const int i = 16 * a + r16;
     const int t = tb + i;
     const bool valid = t < t_end;
-    float qv[32], kv[32];
+    float qv[32], kv[32], bet[32];
     {
       const TIn* qp = (const TIn*)p.q + (((int64_t)b * p.L + (valid ? t : 0)) * p.Hk + hk) * KD;
       const TIn* kp = (const TIn*)p.k + (((int64_t)b * p.L + (valid ? t : 0)) * p.Hk + hk) * KD;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        ld4<TIn>(qp + 32 * s + 4 * q, qv + 8 * s);
-        ld4<TIn>(qp + 32 * s + 16 + 4 * q, qv + 8 * s + 4);
-        ld4<TIn>(kp + 32 * s + 4 * q, kv + 8 * s);
-        ld4<TIn>(kp + 32 * s + 16 + 4 * q, kv + 8 * s + 4);
+        row8<TIn>(qp + 32 * s, q, qv + 8 * s);
+        row8<TIn>(kp + 32 * s, q, kv + 8 * s);
       }
       if (!valid) {
 #pragma unroll
@@ -211,87 +254,68 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
         for (int e = 0; e < 32; ++e) qv[e] = round_as<TIn>(qv[e] * p.scale);
       }
+      const int64_t brow = (((int64_t)b * p.L + (valid ? t : 0)) * p.b_h + hbg) * p.b_c;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) {
+        const int kap = 32 * (e >> 3) + pi_k(q, e & 7);
+        const float bg = valid ? act_b(ld_f(p.b, brow + (p.b_c == 1 ? 0 : kap), p.b_dt), p.fuse, p.guard) : 0.f;
+        bet[e] = bg * kv[e];
+      }
     }
     const bool first = doc[i] == 0;
     const bool last = doc[i] == doc[CH - 1];
-    float dq = 0.f;  // q . k of this row (diagonal of M)
+    float dq = 0.f;
     bool unsafe = false;
-    float bnext[32];  // beta, kept for the robust diagonal path
     f32x4 accA = zero4(), accM = zero4();
-    Frag<BF> Bd[4];
+    F3 Bd[4];
+    float kcs[32];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      float lam[8], lsa[8], lea[8], lend[8], lpv[8];
-      ld4<float>(&X[i * XP + 32 * s + 4 * q], lam);
-      ld4<float>(&X[i * XP + 32 * s + 16 + 4 * q], lam + 4);
-      ld4<float>(&X[(16 * a) * XP + 32 * s + 4 * q], lsa);
-      ld4<float>(&X[(16 * a) * XP + 32 * s + 16 + 4 * q], lsa + 4);
-      ld4<float>(&X[(16 * a + 15) * XP + 32 * s + 4 * q], lea);
-      ld4<float>(&X[(16 * a + 15) * XP + 32 * s + 16 + 4 * q], lea + 4);
-      ld4<float>(&X[(CH - 1) * XP + 32 * s + 4 * q], lend);
-      ld4<float>(&X[(CH - 1) * XP + 32 * s + 16 + 4 * q], lend + 4);
-      if (a > 0) {
-        ld4<float>(&X[(16 * a - 1) * XP + 32 * s + 4 * q], lpv);
-        ld4<float>(&X[(16 * a - 1) * XP + 32 * s + 16 + 4 * q], lpv + 4);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) lpv[e] = 0.f;
-      }
-      float bet[8], rA[8], rM[8], kc[8], bd[8], qe[8], be[8], ke[8];
+      float lam[8], lsa[8], ta[8], laml[8], lsal[8], tal[8], off[8], suf[8];
+      row8<float>(&X[i * XP + 32 * s], q, lam);
+      row8<float>(&X[(16 * a) * XP + 32 * s], q, lsa);
+      row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
+      row8<float>(&Y[i * XP + 32 * s], q, laml);
+      row8<float>(&Y[(16 * a) * XP + 32 * s], q, lsal);
+      row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
+      row8<float>(&Off[a * KD + 32 * s], q, off);
+      row8<float>(&Suf[a * KD + 32 * s], q, suf);
+      float rA[8], rM[8], bd[8], qe[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int kap = 32 * s + pi_k(q, e);
-        float bg = 0.f;
-        if (valid) {
-          const int64_t bix = (((int64_t)b * p.L + t) * p.b_h + hbg) * p.b_c + (p.b_c == 1 ? 0 : kap);
-          bg = act_b(ld_f(p.b, bix, p.b_dt), p.fuse, p.guard);
-        }
-        const float qh = qv[8 * s + e], kh = kv[8 * s + e];
-        bet[e] = bg * kh;
-        bnext[8 * s + e] = bet[e];
-        const float er = fast_exp2(lam[e] - lsa[e]);
-        rA[e] = bet[e] * er;
+        const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
+        const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
+        const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
+        const float d_sa_ea = (lsa[e] - ta[e]) + (lsal[e] - tal[e]);    // >= 0
+        const float er = fast_exp2(d_i_sa);
+        rA[e] = be * er;
         rM[e] = qh * er;
-        kc[e] = kh * fast_exp2(lea[e] - lam[e]);
-        const float eL = fast_exp2(lam[e]);
-        qe[e] = first ? qh * eL : 0.f;
-        be[e] = first ? bet[e] * eL : 0.f;
-        ke[e] = last ? kh * fast_exp2(lend[e] - lam[e]) : 0.f;
-        unsafe |= (lsa[e] - lea[e]) > kDiagSafeLog2;
-        bd[e] = kc[e] * fast_exp2(lsa[e] - lea[e]);
+        kcs[8 * s + e] = kh * fast_exp2(d_ea_i);
+        const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
+        g_beT[(int64_t)kap * CH + i] = first ? be * eL : 0.f;
+        g_keT[(int64_t)kap * CH + i] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
+        unsafe |= d_sa_ea > kDiagSafeLog2;
+        bd[e] = kh * fast_exp2(-d_i_sa);
         dq += qh * kh;
+        qe[e] = first ? qh * eL : 0.f;
       }
-      Rf[bi][s] = make_frag<BF>(rA);
-      Qf[bi][s] = make_frag<BF>(rM);
-      Bd[s] = make_frag<BF>(bd);
-      st4<MT>(&Y[i * YP + 32 * s + 4 * q], kc);
-      st4<MT>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
-      MT* rowq = g_qe + (int64_t)i * KD + 32 * s;
-      st4<MT>(rowq + 4 * q, qe); st4<MT>(rowq + 16 + 4 * q, qe + 4);
-      MT* rowb = g_be + (int64_t)i * KD + 32 * s;
-      st4<MT>(rowb + 4 * q, be); st4<MT>(rowb + 16 + 4 * q, be + 4);
-      MT* rowk = g_ke + (int64_t)i * KD + 32 * s;
-      st4<MT>(rowk + 4 * q, ke); st4<MT>(rowk + 16 + 4 * q, ke + 4);
-      if (r16 == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int kap = 32 * s + pi_k(q, e);
-          Ftab[a * KD + kap] = fast_exp2(lea[e] - lpv[e]);
-          Mid0[a * KD + kap] = a > 0 ? fast_exp2(lsa[e] - lpv[e]) : 0.f;
-          if (a == 7) g_dv[kap] = fast_exp2(lend[e]);
-        }
-      }
+      st4<float>(g_qe + (int64_t)i * KD + 32 * s + 4 * q, qe);
+      st4<float>(g_qe + (int64_t)i * KD + 32 * s + 16 + 4 * q, qe + 4);
+      Rf[bi][s] = P::f3(rA);
+      Qf[bi][s] = P::f3(rM);
+      Bd[s] = P::f3(bd);
     }
     dq += __shfl_xor(dq, 16);
     dq += __shfl_xor(dq, 32);
 
     if (!__any(unsafe)) {
-      // A_aa, M_aa = (R, Qr) (Kc e^{Lambda_sa - Lambda_ea})^T : every factor is
-      // within e^{+-69} of 1, so the factorisation cannot overflow.
+      // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
+      // within 2^{+-100} of 1, so the factorisation cannot overflow.
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        mma(accA, Rf[bi][s], Bd[s]);
-        mma(accM, Qf[bi][s], Bd[s]);
+        P::m33(accA, Rf[bi][s], Bd[s]);
+        P::m33(accM, Qf[bi][s], Bd[s]);
       }
     } else {
       // Overflow-free hierarchical factorisation: the pair (i, j) is split at
@@ -307,21 +331,22 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         f32x4 tA = zero4(), tM = zero4();
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          float lam[8], lsp[8], xa[8], xm[8], xb[8];
-          ld4<float>(&X[i * XP + 32 * s + 4 * q], lam);
-          ld4<float>(&X[i * XP + 32 * s + 16 + 4 * q], lam + 4);
-          ld4<float>(&X[srow * XP + 32 * s + 4 * q], lsp);
-          ld4<float>(&X[srow * XP + 32 * s + 16 + 4 * q], lsp + 4);
+          float lam[8], lsp[8], laml[8], lspl[8], xa[8], xm[8], xb[8];
+          row8<float>(&X[i * XP + 32 * s], q, lam);
+          row8<float>(&X[srow * XP + 32 * s], q, lsp);
+          row8<float>(&Y[i * XP + 32 * s], q, laml);
+          row8<float>(&Y[srow * XP + 32 * s], q, lspl);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float x = upper ? fast_exp2(lam[e] - lsp[e]) : fast_exp2(lsp[e] - lam[e]);
-            xa[e] = upper ? bnext[8 * s + e] * x : 0.f;
+            const float d = (lam[e] - lsp[e]) + (laml[e] - lspl[e]);
+            const float x = fast_exp2(upper ? d : -d);
+            xa[e] = upper ? bet[8 * s + e] * x : 0.f;
             xm[e] = upper ? qv[8 * s + e] * x : 0.f;
             xb[e] = upper ? 0.f : kv[8 * s + e] * x;
           }
-          const Frag<BF> fa = make_frag<BF>(xa), fm = make_frag<BF>(xm), fb = make_frag<BF>(xb);
-          mma(tA, fa, fb);
-          mma(tM, fm, fb);
+          const F3 fb = P::f3(xb);
+          P::m33(tA, P::f3(xa), fb);
+          P::m33(tM, P::f3(xm), fb);
         }
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
@@ -334,53 +359,54 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       for (int ii = 0; ii < 4; ++ii)
         if (4 * q + ii == r16) accM[ii] = dq;
     }
-    // masks and M store (diagonal block a)
+    // Kc replaces this block's rows of the Lambda low words only after every
+    // lane of the wave has finished reading them
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      st4<float>(&Y[i * YP + 32 * s + 4 * q], kcs + 8 * s);
+      st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kcs + 8 * s + 4);
+    }
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
       const int il = 4 * q + ii, ia = 16 * a + il, ja = 16 * a + r16;
       const bool same = doc[ia] == doc[ja];
       Adiag[bi][ii] = (il > r16 && same) ? accA[ii] : 0.f;
-      g_M[(int64_t)ia * CH + ja] = from_f<MT>((il >= r16 && same) ? accM[ii] : 0.f);
-      if ((a & 1) == 0) g_M[(int64_t)ia * CH + ja + 16] = from_f<MT>(0.f);
+      g_M[(int64_t)ia * CH + ja] = (il >= r16 && same) ? accM[ii] : 0.f;
+      if ((a & 1) == 0) g_M[(int64_t)ia * CH + ja + 16] = 0.f;
     }
   }
   __syncthreads();
 
-  // ---- phase 3: off-diagonal A/M blocks on MFMA (X becomes A) -------------
+  // ---- phase 3: off-diagonal A/M blocks (X becomes A) -----------------------
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi) {
     const int a = bi == 0 ? w : 7 - w;
     float mloc[32];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      ld4<float>(&Mid0[a * KD + 32 * s + 4 * q], mloc + 8 * s);
-      ld4<float>(&Mid0[a * KD + 32 * s + 16 + 4 * q], mloc + 8 * s + 4);
-    }
+    for (int s = 0; s < 4; ++s) row8<float>(&Mid0[a * KD + 32 * s], q, mloc + 8 * s);
     for (int bb = a - 1; bb >= 0; --bb) {
       f32x4 accA = zero4(), accM = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         float x[8];
-        ld4<MT>(&Y[(16 * bb + r16) * YP + 32 * s + 4 * q], x);
-        ld4<MT>(&Y[(16 * bb + r16) * YP + 32 * s + 16 + 4 * q], x + 4);
+        row8<float>(&Y[(16 * bb + r16) * YP + 32 * s], q, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= mloc[8 * s + e];
-        const Frag<BF> fb = make_frag<BF>(x);
-        mma(accA, Rf[bi][s], fb);
-        mma(accM, Qf[bi][s], fb);
+        const F3 fb = P::f3(x);
+        P::m33(accA, Rf[bi][s], fb);
+        P::m33(accM, Qf[bi][s], fb);
       }
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
         const bool same = doc[ia] == doc[jb];
         X[ia * XP + jb] = same ? accA[ii] : 0.f;
-        g_M[(int64_t)ia * CH + jb] = from_f<MT>(same ? accM[ii] : 0.f);
+        g_M[(int64_t)ia * CH + jb] = same ? accM[ii] : 0.f;
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         float f[8];
-        ld4<float>(&Ftab[bb * KD + 32 * s + 4 * q], f);
-        ld4<float>(&Ftab[bb * KD + 32 * s + 16 + 4 * q], f + 4);
+        row8<float>(&Ftab[bb * KD + 32 * s], q, f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) mloc[8 * s + e] *= f[e];
       }
@@ -448,15 +474,19 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     __syncthreads();
   }
 
-  // ---- phase 5: W = T be, Pn = -ke^T W  (wave: key-dim tiles w, w+4) ------
+  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tiles w, w+4) ---
   {
     f32x4 Wc[2][8];
-    Frag<BF> Bf[2][4];
+    F1 Bbe[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int n = 16 * (w + 4 * nt) + r16;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Bf[nt][s] = frag_col<BF, MT>(g_be + (int64_t)(32 * s) * KD + n, KD, q);
+      for (int s = 0; s < 4; ++s) {
+        float x[8];
+        row8<float>(g_beT + (int64_t)n * CH + 32 * s, q, x);
+        Bbe[nt][s] = P::f1(x);
+      }
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) Wc[nt][rt] = zero4();
     }
@@ -465,32 +495,32 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s <= rt / 2) {
-          const Frag<BF> fa = frag_row<BF, float>(&X[(16 * rt + r16) * XP + 32 * s], q);
-          mma(Wc[0][rt], fa, Bf[0][s]);
-          mma(Wc[1][rt], fa, Bf[1][s]);
+          float x[8];
+          row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
+          const F1 fa = P::f1(x);
+          P::m11(Wc[0][rt], fa, Bbe[0][s]);
+          P::m11(Wc[1][rt], fa, Bbe[1][s]);
         }
       }
     }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int n = 16 * (w + 4 * nt) + r16;
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) g_Wn[(int64_t)(16 * rt + 4 * q + ii) * KD + n] = from_f<MT>(-Wc[nt][rt][ii]);
-    }
-    Frag<BF> Wf[2][4];
+    F3 W3[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Wf[nt][s] = frag_from_acc<BF>(Wc[nt][2 * s], Wc[nt][2 * s + 1]);
+      for (int s = 0; s < 4; ++s) {
+        const float x[8] = {Wc[nt][2 * s][0], Wc[nt][2 * s][1], Wc[nt][2 * s][2], Wc[nt][2 * s][3],
+                            Wc[nt][2 * s + 1][0], Wc[nt][2 * s + 1][1], Wc[nt][2 * s + 1][2], Wc[nt][2 * s + 1][3]};
+        W3[nt][s] = P::f3(x);
+      }
     for (int m = 0; m < 8; ++m) {
       f32x4 P0 = zero4(), P1 = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const Frag<BF> fa = frag_col<BF, MT>(g_ke + (int64_t)(32 * s) * KD + 16 * m + r16, KD, q);
-        mma(P0, fa, Wf[0][s]);
-        mma(P1, fa, Wf[1][s]);
+        float x[8];
+        row8<float>(g_keT + (int64_t)(16 * m + r16) * CH + 32 * s, q, x);
+        const F1 fa = P::f1(x);
+        P::m11(P0, fa, P::hi(W3[0][s]));
+        P::m11(P1, fa, P::hi(W3[1][s]));
       }
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
@@ -499,233 +529,307 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         g_Pn[row + 16 * (w + 4) + r16] = from_f<MT>(-P1[ii]);
       }
     }
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      f32x4 X0, X1;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * KD;
+        X0[ii] = g_qe[row + 16 * w + r16];
+        X1[ii] = g_qe[row + 16 * (w + 4) + r16];
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s <= rt / 2) {
+          float x[8];
+          row8<float>(g_M + (int64_t)(16 * rt + r16) * CH + 32 * s, q, x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = -x[e];
+          const F3 fa = P::f3(x);
+          P::m33(X0, fa, W3[0][s]);
+          P::m33(X1, fa, W3[1][s]);
+        }
+      }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * KD;
+        g_X[row + 16 * w + r16] = X0[ii];
+        g_X[row + 16 * (w + 4) + r16] = X1[ii];
+      }
+    }
   }
 
-  // ---- phase 6: U = T (w*v), Q = ke^T U  (wave: value tiles w, w+4, ...) --
-  {
-    const int ntiles = p.Vp / 16;
-    for (int n0 = w; n0 < ntiles; n0 += 8) {
-      const int n1 = n0 + 4;
-      const bool has1 = n1 < ntiles;
-      f32x4 Uc[2][8];
-      Frag<BF> Bf[2][4];
+  // ---- phase 6: U = T (w*v) ; Q = ke^T U ; Oi = M U  (128 value columns per pass)
+  for (int n0 = 0; n0 < p.Vp; n0 += 128) {
+    __syncthreads();
+    {
+      // w*v for 128 tokens x 128 columns, transposed into Y[col][token]
+      const int tok = tid >> 1, half = tid & 1;
+      const int t = tb + tok;
+      const int hv = p.gates_at_hv ? h : h * p.G + n0 / KD;
+      const int hw = vgate_head(p, p.w_h, hv);
+      const bool valid = t < t_end;
+      const int64_t bt = (int64_t)b * p.L + (valid ? t : 0);
+      const int64_t vrow = (bt * p.Hv + hv) * KD + 64 * half;
+      const int64_t wrow = (bt * p.w_h + hw) * p.w_c;
+#pragma unroll 4
+      for (int j = 0; j < 64; ++j) {
+        const int col = 64 * half + j;
+        float val = 0.f;
+        if (valid) {
+          const float vv = ld_f(p.v, vrow + j, p.v_dt);
+          const float ww = act_w(ld_f(p.w, wrow + (p.w_c == 1 ? 0 : col), p.w_dt), p.fuse);
+          val = ww * vv;
+        }
+        Y[col * YP + tok] = val;
+      }
+    }
+    __syncthreads();
+    f32x4 Uc[2][8];
+    F3 Bwv[2][4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int n = 16 * (nt == 0 ? n0 : n1) + r16;
-        const bool act = nt == 0 || has1;
-        const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-        const int vcol = n % KD;
-        const int hw = vgate_head(p, p.w_h, hv);
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = 16 * (w + 4 * nt) + r16;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+      for (int s = 0; s < 4; ++s) {
+        float x[8];
+        row8<float>(&Y[col * YP + 32 * s], q, x);
+        Bwv[nt][s] = P::f3(x);
+      }
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
+    }
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s <= rt / 2) {
           float x[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int t = tb + 32 * s + pi_k(q, e);
-            float val = 0.f;
-            if (act && t < t_end) {
-              const int64_t bt = (int64_t)b * p.L + t;
-              const float vv = ld_f(p.v, (bt * p.Hv + hv) * KD + vcol, p.v_dt);
-              const float ww = act_w(ld_f(p.w, (bt * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : vcol), p.w_dt), p.fuse);
-              val = ww * vv;
-            }
-            x[e] = val;
-          }
-          Bf[nt][s] = make_frag<BF>(x);
-        }
-#pragma unroll
-        for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
-      }
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          if (s <= rt / 2) {
-            const Frag<BF> fa = frag_row<BF, float>(&X[(16 * rt + r16) * XP + 32 * s], q);
-            mma(Uc[0][rt], fa, Bf[0][s]);
-            if (has1) mma(Uc[1][rt], fa, Bf[1][s]);
-          }
+          row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
+          const F1 fa = P::f1(x);
+          P::m13(Uc[0][rt], fa, Bwv[0][s]);
+          P::m13(Uc[1][rt], fa, Bwv[1][s]);
         }
       }
+    }
+    F3 U3[2][4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        if (nt == 1 && !has1) break;
-        const int n = 16 * (nt == 0 ? n0 : n1) + r16;
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) g_U[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + n] = from_f<MT>(Uc[nt][rt][ii]);
+      for (int s = 0; s < 4; ++s) {
+        const float x[8] = {Uc[nt][2 * s][0], Uc[nt][2 * s][1], Uc[nt][2 * s][2], Uc[nt][2 * s][3],
+                            Uc[nt][2 * s + 1][0], Uc[nt][2 * s + 1][1], Uc[nt][2 * s + 1][2], Uc[nt][2 * s + 1][3]};
+        U3[nt][s] = P::f3(x);
       }
-      Frag<BF> Uf[2][4];
+    const int c0 = n0 + 16 * w + r16, c1 = n0 + 16 * (w + 4) + r16;
+    for (int m = 0; m < 8; ++m) {
+      f32x4 Q0 = zero4(), Q1 = zero4();
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int s = 0; s < 4; ++s) {
+        float x[8];
+        row8<float>(g_keT + (int64_t)(16 * m + r16) * CH + 32 * s, q, x);
+        const F3 fa = P::f3(x);
+        P::m33(Q0, fa, U3[0][s]);
+        P::m33(Q1, fa, U3[1][s]);
+      }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) Uf[nt][s] = frag_from_acc<BF>(Uc[nt][2 * s], Uc[nt][2 * s + 1]);
-      for (int m = 0; m < 8; ++m) {
-        f32x4 Q0 = zero4(), Q1 = zero4();
+      for (int ii = 0; ii < 4; ++ii) {
+        const int64_t row = (int64_t)(16 * m + 4 * q + ii) * p.Vp;
+        g_Q[row + c0] = Q0[ii];
+        g_Q[row + c1] = Q1[ii];
+      }
+    }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const Frag<BF> fa = frag_col<BF, MT>(g_ke + (int64_t)(32 * s) * KD + 16 * m + r16, KD, q);
-          mma(Q0, fa, Uf[0][s]);
-          if (has1) mma(Q1, fa, Uf[1][s]);
+    for (int rt = 0; rt < 8; ++rt) {
+      f32x4 O0 = zero4(), O1 = zero4();
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s <= rt / 2) {
+          float x[8];
+          row8<float>(g_M + (int64_t)(16 * rt + r16) * CH + 32 * s, q, x);
+          const F3 fa = P::f3(x);
+          P::m33(O0, fa, U3[0][s]);
+          P::m33(O1, fa, U3[1][s]);
         }
+      }
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int64_t row = (int64_t)(16 * m + 4 * q + ii) * p.Vp;
-          g_Q[row + 16 * n0 + r16] = Q0[ii];
-          if (has1) g_Q[row + 16 * n1 + r16] = Q1[ii];
-        }
+      for (int ii = 0; ii < 4; ++ii) {
+        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * p.Vp;
+        g_Oi[row + c0] = O0[ii];
+        g_Oi[row + c1] = O1[ii];
       }
     }
   }
 }
 
 // ===========================================================================
-// k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c  (one wave / 16 cols)
+// k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c.
+// One workgroup per (16-column tile, exec head, batch); wave w owns state rows
+// 32w..32w+31 (fp32, in VGPRs); the full S_c is exchanged through LDS each
+// chunk so that only 8 MFMAs per wave sit on the sequential path.
 // ===========================================================================
 template <bool BF>
-__global__ __launch_bounds__(64) void k_chain(const PF p) {
+__global__ __launch_bounds__(256) void k_chain(const PF p) {
+  using P = Pol<BF>;
+  using F1 = typename P::F1;
   using MT = MTy<BF>;
-  const int l = threadIdx.x & 63, r16 = l & 15, q = l >> 4;
+  __shared__ float Sx[2][16 * XP];   // S^T of the current chunk, double-buffered
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
   const int ct = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int n = 16 * ct + r16;
   const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
   const int vcol = n % KD;
   const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + vcol;
 
-  f32x4 S[8];
+  f32x4 S[2];
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt)
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii)
-      S[rt][ii] = p.has_init ? p.init[sbase + (int64_t)(16 * rt + 4 * q + ii) * KD] : 0.f;
+      S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
 
-  for (int c = 0; c < p.NCb; ++c) {
+  // operands of chunk c, prefetched one chunk ahead
+  auto load_ops = [&](int c, F1 (&pf)[2][4], f32x4 (&qc)[2], float (&dv)[8], int& is_new, int& same) {
     const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-    const int is_new = p.flags[((int64_t)b * p.NCb + c) * 2 + 0];
-    const int same = p.flags[((int64_t)b * p.NCb + c) * 2 + 1];
-    if (is_new) {
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) S[rt] = zero4();
-    }
-    // entry state of this chunk, transposed (V' x K), for k_output
-    MT* st = (MT*)p.St + u * (int64_t)p.Vp * KD + (int64_t)n * KD;
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-      float x[4] = {S[rt][0], S[rt][1], S[rt][2], S[rt][3]};
-      st4<MT>(st + 16 * rt + 4 * q, x);
-    }
-    const float* Qc = p.Q + u * KD * p.Vp;
-    const float* dv = p.dvec + u * KD;
     const MT* Pn = (const MT*)p.Pn + u * KD * KD;
-    f32x4 acc[8];
+    const float* Qc = p.Q + u * KD * p.Vp;
+    const float* dvp = p.dvec + u * KD;
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) acc[rt][ii] = Qc[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + n];
-    Frag<BF> Sf[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Sf[s] = frag_from_acc<BF>(S[2 * s], S[2 * s + 1]);
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
+    for (int r = 0; r < 2; ++r) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const Frag<BF> fa = frag_row<BF, MT>(Pn + (int64_t)(16 * rt + r16) * KD + 32 * s, q);
-        mma(acc[rt], fa, Sf[s]);
+        float x[8];
+        row8<MT>(Pn + (int64_t)(32 * w + 16 * r + r16) * KD + 32 * s, q, x);
+        pf[r][s] = P::f1(x);
       }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) qc[r][ii] = Qc[(int64_t)(32 * w + 16 * r + 4 * q + ii) * p.Vp + n];
+      ld4<float>(dvp + 32 * w + 16 * r + 4 * q, dv + 4 * r);
+    }
+    is_new = p.flags[((int64_t)b * p.NCb + c) * 2 + 0];
+    same = p.flags[((int64_t)b * p.NCb + c) * 2 + 1];
+  };
+
+  F1 pf[2][4];
+  f32x4 qc[2];
+  float dv[8];
+  int is_new = 0, same = 0;
+  load_ops(0, pf, qc, dv, is_new, same);
+  for (int c = 0; c < p.NCb; ++c) {
+    const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
+    if (is_new) { S[0] = zero4(); S[1] = zero4(); }
+    float* sx = Sx[c & 1];
+    float* st = p.St + u * (int64_t)p.Vp * KD + (int64_t)n * KD;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float x[4] = {S[r][0], S[r][1], S[r][2], S[r][3]};
+      st4<float>(&sx[r16 * XP + 32 * w + 16 * r + 4 * q], x);
+      st4<float>(st + 32 * w + 16 * r + 4 * q, x);
+    }
+    // next chunk's operands while this chunk's exchange completes
+    F1 pf_n[2][4];
+    f32x4 qc_n[2];
+    float dv_n[8];
+    int is_new_n = 0, same_n = 0;
+    if (c + 1 < p.NCb) load_ops(c + 1, pf_n, qc_n, dv_n, is_new_n, same_n);
+    __syncthreads();
+    F1 Sf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float x[8];
+      row8<float>(&sx[r16 * XP + 32 * s], q, x);
+      Sf[s] = P::f1(x);
     }
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-      float d[4];
-      ld4<float>(dv + 16 * rt + 4 * q, d);
+    for (int r = 0; r < 2; ++r) {
+      f32x4 acc = qc[r];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) S[rt][ii] = acc[rt][ii] + (same ? d[ii] * S[rt][ii] : 0.f);
+      for (int s = 0; s < 4; ++s) P::m11(acc, pf[r][s], Sf[s]);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? dv[4 * r + ii] * S[r][ii] : 0.f);
+    }
+    if (c + 1 < p.NCb) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) pf[r][s] = pf_n[r][s];
+        qc[r] = qc_n[r];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dv[e] = dv_n[e];
+      is_new = is_new_n;
+      same = same_n;
     }
   }
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt)
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(16 * rt + 4 * q + ii) * KD] = S[rt][ii];
+    for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
 }
 
 // ===========================================================================
-// k_output: Vnew = U - W S_c ; O = qe S_c + M Vnew   (wave: 64 value columns)
+// k_output: O_c = X_c S_c + Oi_c  (one workgroup per chunk and 256 value
+// columns; each wave owns 64 columns).  X S is a split-bf16 product in
+// bf16 mode.
 // ===========================================================================
 template <bool BF>
 __global__ __launch_bounds__(256) void k_output(const PF p) {
-  using MT = MTy<BF>;
+  using P = Pol<BF>;
+  using F3 = typename P::F3;
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int b = blockIdx.z / p.ncg, cg = blockIdx.z % p.ncg;
+  const int col0 = 256 * cg + 64 * w;
+  if (col0 >= p.Vp) return;
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-  const MT* Wn = (const MT*)p.Wn + u * CH * KD;
-  const MT* qe = (const MT*)p.qe + u * CH * KD;
-  const MT* Mm = (const MT*)p.M + u * CH * CH;
-  const MT* U = (const MT*)p.U + u * CH * p.Vp;
-  const MT* St = (const MT*)p.St + u * (int64_t)p.Vp * KD;
+  const float* Xc = p.X + u * CH * KD;
+  const float* Oi = p.Oi + u * CH * p.Vp;
+  const float* St = p.St + u * (int64_t)p.Vp * KD;
 
-  Frag<BF> Sf[4][4];
+  F3 Sf[4][4];
   int ncol[4];
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
-    ncol[ct] = 16 * (4 * w + ct) + r16;
+    ncol[ct] = col0 + 16 * ct + r16;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) Sf[ct][s] = frag_row<BF, MT>(St + (int64_t)ncol[ct] * KD + 32 * s, q);
+    for (int s = 0; s < 4; ++s) {
+      float x[8];
+      row8<float>(St + (int64_t)ncol[ct] * KD + 32 * s, q, x);
+      Sf[ct][s] = P::f3(x);
+    }
   }
-  f32x4 Vn[8][4];
+  const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
+  const int vcol0 = col0 % KD;
+#pragma unroll 2
+  for (int rt = 0; rt < 8; ++rt) {
+    f32x4 O[4];
 #pragma unroll
-  for (int sp = 0; sp < 4; ++sp) {
+    for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int rt = 2 * sp + rr;
+      for (int ii = 0; ii < 4; ++ii) O[ct][ii] = Oi[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + ncol[ct]];
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
+    for (int s = 0; s < 4; ++s) {
+      float x[8];
+      row8<float>(Xc + (int64_t)(16 * rt + r16) * KD + 32 * s, q, x);
+      const F3 fa = P::f3(x);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) Vn[rt][ct][ii] = to_f(U[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + ncol[ct]]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const Frag<BF> fa = frag_row<BF, MT>(Wn + (int64_t)(16 * rt + r16) * KD + 32 * s, q);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) mma(Vn[rt][ct], fa, Sf[ct][s]);
-      }
+      for (int ct = 0; ct < 4; ++ct) P::m33(O[ct], fa, Sf[ct][s]);
     }
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int rt = 2 * sp + rr;
-      f32x4 O[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) O[ct] = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const Frag<BF> fa = frag_row<BF, MT>(qe + (int64_t)(16 * rt + r16) * KD + 32 * s, q);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) mma(O[ct], fa, Sf[ct][s]);
-      }
-#pragma unroll
-      for (int s2 = 0; s2 <= sp; ++s2) {
-        const Frag<BF> fa = frag_row<BF, MT>(Mm + (int64_t)(16 * rt + r16) * CH + 32 * s2, q);
+    for (int ii = 0; ii < 4; ++ii) {
+      const int t = tb + 16 * rt + 4 * q + ii;
+      if (t < t_end) {
+        const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol0 + r16;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
-          const Frag<BF> fb = frag_from_acc<BF>(Vn[2 * s2][ct], Vn[2 * s2 + 1][ct]);
-          mma(O[ct], fa, fb);
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int n = ncol[ct];
-        const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-        const int vcol = n % KD;
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int t = tb + 16 * rt + 4 * q + ii;
-          if (t < t_end) {
-            const int64_t oi = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol;
-            if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)O[ct][ii];
-            else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)O[ct][ii];
-            else ((float*)p.out)[oi] = O[ct][ii];
-          }
+          const int64_t oi = ob + 16 * ct;
+          if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)O[ct][ii];
+          else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)O[ct][ii];
+          else ((float*)p.out)[oi] = O[ct][ii];
         }
       }
     }
@@ -738,7 +842,7 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, Wn, qe, be, ke, M, U, Pn, Q, St, carry, total;
+  size_t flags, dvec, Pn, Q, X, Oi, St, beT, keT, Mg, qe, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -751,15 +855,15 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
   L.flags = take((size_t)a->B * NCb * 2 * 4);
   L.dvec = take(units * KD * 4);
-  L.Wn = take(units * CH * KD * es);
-  L.qe = take(units * CH * KD * es);
-  L.be = take(units * CH * KD * es);
-  L.ke = take(units * CH * KD * es);
-  L.M = take(units * CH * CH * es);
-  L.U = take(units * CH * Vp * es);
   L.Pn = take(units * KD * KD * es);
   L.Q = take(units * KD * Vp * 4);
-  L.St = take(units * (size_t)Vp * KD * es);
+  L.X = take(units * CH * KD * 4);
+  L.Oi = take(units * CH * Vp * 4);
+  L.St = take(units * (size_t)Vp * KD * 4);
+  L.beT = take(units * KD * CH * 4);
+  L.keT = take(units * KD * CH * 4);
+  L.Mg = take(units * CH * CH * 4);
+  L.qe = take(units * CH * KD * 4);
   L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
   L.total = off;
   return L;
@@ -809,10 +913,10 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   hipLaunchKernelGGL((k_prepass<BF, TIn>), g1, dim3(256), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(64), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_output<BF>), g1, dim3(64 * (p.Vp / 64)), 0, st, p);
+  hipLaunchKernelGGL((k_output<BF>), dim3(p.NCb, p.Hx, p.B * p.ncg), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -854,10 +958,18 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.init_seg = a->init_seg;
   p.out = a->out;
   p.scale = a->scale; p.l2norm = a->qk_l2norm; p.fuse = a->fuse_prologue; p.guard = a->stability_guard;
+  p.ncg = (Vp + 255) / 256;
   p.flags = (int32_t*)(ws + Lw.flags);
   p.dvec = (float*)(ws + Lw.dvec);
-  p.Wn = ws + Lw.Wn; p.qe = ws + Lw.qe; p.be = ws + Lw.be; p.ke = ws + Lw.ke; p.M = ws + Lw.M;
-  p.U = ws + Lw.U; p.Pn = ws + Lw.Pn; p.Q = (float*)(ws + Lw.Q); p.St = ws + Lw.St;
+  p.Pn = ws + Lw.Pn;
+  p.Q = (float*)(ws + Lw.Q);
+  p.X = (float*)(ws + Lw.X);
+  p.Oi = (float*)(ws + Lw.Oi);
+  p.St = (float*)(ws + Lw.St);
+  p.beT = (float*)(ws + Lw.beT);
+  p.keT = (float*)(ws + Lw.keT);
+  p.Mg = (float*)(ws + Lw.Mg);
+  p.qe = (float*)(ws + Lw.qe);
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
 
   hipStream_t st = (hipStream_t)stream;
