@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Benchmark of the delta-rule recurrence core on one MI355X.
+
+Workload (the configuration the headline metric is
+quoted on): chunk_gdn2 prefill, is_inference=True, B=1, L=2048, Hk=12, Hv=24,
+K=V=128, bf16 q/k/v, fp32 gates (channel-wise g, b at Hk; w at Hv), segment
+ids 0 for t<1024 and 1 after, chunk 128, precision="bf16", qk_l2norm=True,
+fp32 final state.  A "step" is one such call on inputs already resident in
+HBM.  The same run also times the GDN-2 decode step of BASELINE.json
+configs[3] (B=256, Hk=16, Hv=32, fp32 and bf16 state), which the metric's
+second half ("decode step us + state HBM GB/s") refers to.
+
+Prints ONE JSON line (see the "roofline" and "cpu_baseline" objects).
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deltanet-tpu_amd"))
+
+# MI355X published peaks
+PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2516.6
+
+METRIC = "prefill tokens/s + %bf16 MFMA peak; decode step µs + state HBM GB/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def prefill_inputs(torch, dev, B=1, L=2048, Hk=12, Hv=24, K=128, seed=2):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = rn(B, L, Hk, K).to(torch.bfloat16)
+    k = rn(B, L, Hk, K).to(torch.bfloat16)
+    v = rn(B, L, Hv, K).to(torch.bfloat16)
+    b = torch.sigmoid(0.39 * rn(B, L, Hk, K))
+    w = torch.sigmoid(0.39 * rn(B, L, Hv, K))
+    gg = -torch.exp(0.39 * rn(B, L, Hk, K) - 1.0)
+    seg = (torch.arange(L, device=dev) >= 1024).to(torch.int32)[None].repeat(B, 1)
+    return q, k, v, gg, b, w, seg
+
+
+def decode_inputs(torch, dev, B=256, Hk=16, Hv=32, K=128, seed=4):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = rn(B, 1, Hk, K).to(torch.bfloat16)
+    k = rn(B, 1, Hk, K).to(torch.bfloat16)
+    v = rn(B, 1, Hv, K).to(torch.bfloat16)
+    b = torch.sigmoid(0.39 * rn(B, 1, Hk, K))
+    w = torch.sigmoid(0.39 * rn(B, 1, Hv, K))
+    gg = -torch.exp(0.39 * rn(B, 1, Hk, K) - 1.0)
+    state = 0.02 * rn(B, Hv, K, K)
+    return q, k, v, gg, b, w, state
+
+
+def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128):
+    """Algorithmic flops / bytes of config 2, split by kernel (per-(head, chunk)
+    figures of the chunked WY algorithm x the units one launch processes)."""
+    Vp = (Hv // Hk) * K
+    units = B * Hk * math.ceil(L / C)
+    f_pre = 6 * C * C * K + C ** 3 / 3 + 2 * C * C * Vp      # A, M, W=T be ; T ; U=T wv
+    f_chain = 2 * C * K * Vp + 2 * C * K * Vp                 # W S ; ke^T Vnew
+    f_out = 2 * C * K * Vp + 2 * C * C * Vp                   # qe S ; M Vnew
+    in_bytes = B * L * (2 * Hk * K * 2 + Hv * K * 2 + 2 * Hk * K * 4 + Hv * K * 4) + 4 * B * L
+    out_bytes = B * L * Hv * K * 2
+    state_bytes = B * Hv * K * K * 4
+    return dict(units=units, flops_total=units * (f_pre + f_chain + f_out),
+                prepass=dict(flops=units * f_pre, bytes=in_bytes),
+                chain=dict(flops=units * f_chain, bytes=state_bytes),
+                output=dict(flops=units * f_out, bytes=out_bytes),
+                bytes_total=in_bytes + out_bytes + state_bytes)
+
+
+def cpu_baseline(max_seconds=20.0):
+    """The C token-serial restatement (oracle/gdn_serial.c, fp32, OpenMP over
+    (batch, value head)) on this host's cores, on config 2 repeated."""
+    import numpy as np
+
+    from oracle import c_oracle as C
+    from oracle import gdn_oracle as O
+
+    rng = np.random.default_rng(0)
+    B, L, Hk, Hv, K = 1, 2048, 12, 24, 128
+    q = O.bf16_round(rng.standard_normal((B, L, Hk, K)))
+    k = O.bf16_round(rng.standard_normal((B, L, Hk, K)))
+    v = O.bf16_round(rng.standard_normal((B, L, Hv, K)))
+    b = 1 / (1 + np.exp(-0.39 * rng.standard_normal((B, L, Hk, K))))
+    w = 1 / (1 + np.exp(-0.39 * rng.standard_normal((B, L, Hv, K))))
+    g = -np.exp(0.39 * rng.standard_normal((B, L, Hk, K)) - 1)
+    seg = (np.arange(L) >= 1024).astype(np.int64)[None]
+    threads = min(os.cpu_count() or 1, 16)
+    t0 = time.perf_counter()
+    # the wrapper work (L2-norm, gate activation) is part of the measured CPU path
+    reps, tok = 0, 0
+    while True:
+        qh, kh, vv, ga, ba, wa = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, qk_dtype="bf16",
+                                                   broadcast=False)
+        C.serial(qh, kh, vv, ga, ba, wa, O.canonical_segments(seg, B, L), nthreads=threads, dtype=np.float32)
+        reps += 1
+        tok += B * L
+        if time.perf_counter() - t0 >= max_seconds or reps >= 200:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": tok / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 (B=1, L=2048, Hk=12, Hv=24) x {reps} full prefills, fp32 token-serial C "
+                      f"(oracle/gdn_serial.c, OpenMP over 24 (batch, value-head) chains), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (for PMC byte-counter scaling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one MI355X only; the hot path shards over (batch, head) "
+              "with no communication (see DESIGN.md), so no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from deltanet_tpu_amd import _lib, chunk_gdn2, gdn2_decode_step
+
+    dev = torch.device("cuda:0")
+    q, k, v, g, b, w, seg = prefill_inputs(torch, dev)
+    work = prefill_work()
+
+    def step():
+        return chunk_gdn2(q, k, v, g, b, w, segment_ids=seg, is_inference=True, output_final_state=True,
+                          qk_l2norm=True, precision="bf16", chunk_size=128)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_begin()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    prof = _lib.profile_end()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    tok_s = 2048 / (ms_step * 1e-3)
+    kern = {name: (ms / max(n, 1)) for name, (ms, n) in prof.items() if n}
+    log(f"prefill: {ms_step * 1e3:.1f} us/step; kernels (us): " +
+        ", ".join(f"{k_}={v_ * 1e3:.1f}" for k_, v_ in kern.items()))
+
+    # dominant kernel and its roofline
+    dom = max(("prepass", "chain", "output"), key=lambda n: kern.get(n, 0.0))
+    t_dom = kern[dom] * 1e-3
+    wk = work[dom]
+    t_hbm = wk["bytes"] / (PEAK_HBM_GBPS * 1e9)
+    t_mfma = wk["flops"] / (PEAK_BF16_TFLOPS * 1e12)
+    if t_hbm >= t_mfma:
+        roof = {"bound": "hbm", "achieved": wk["bytes"] / t_dom / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
+    else:
+        roof = {"bound": "mfma", "achieved": wk["flops"] / t_dom / 1e12, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["kernel"] = f"k_prepass" if dom == "prepass" else f"k_{dom}"
+    roof["avg_launch_us"] = kern[dom] * 1e3
+    roof["traffic"] = None
+
+    # whole-step roofline (HBM-bound at this arithmetic intensity)
+    t_roof = max(work["bytes_total"] / (PEAK_HBM_GBPS * 1e9), work["flops_total"] / (PEAK_BF16_TFLOPS * 1e12))
+    mfma_pct = work["flops_total"] / (ms_step * 1e-3) / (PEAK_BF16_TFLOPS * 1e12) * 100
+
+    # ---- decode (config 4) ------------------------------------------------
+    dq, dk, dv, dg, db, dw, st = decode_inputs(torch, dev)
+    dec = {}
+    for sd, elt in (("float32", 4), ("bfloat16", 2)):
+        s_in = st if sd == "float32" else st.to(torch.bfloat16)
+        s_out = torch.empty_like(s_in)
+        n = args.decode_steps
+
+        def dstep(a, bb):
+            return gdn2_decode_step(dq, dk, dv, dg, db, dw, a, qk_l2norm=True, state_dtype=sd, out_state=bb)
+
+        for _ in range(5):
+            dstep(s_in, s_out)
+        torch.cuda.synchronize()
+        _lib.profile_begin()
+        t0 = time.perf_counter()
+        a_, b_ = s_in, s_out
+        for _ in range(n):
+            dstep(a_, b_)
+            a_, b_ = b_, a_
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dprof = _lib.profile_end()
+        us = (t1 - t0) * 1e6 / n
+        kus = dprof["decode"][0] * 1e3 / max(dprof["decode"][1], 1)
+        sbytes = 2 * st.numel() * elt
+        dec[sd] = {"us_per_step": round(us, 2), "kernel_us": round(kus, 2),
+                   "state_GBps": round(sbytes / (kus * 1e-6) / 1e9, 1),
+                   "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"decode {sd}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[sd]['state_GBps']} GB/s)")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(args.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
+        except Exception as e:  # the GPU figure stands on its own
+            log(f"cpu baseline unavailable: {e}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, sigmoid/exp gates as BASELINE.json configs[1])",
+        "config": {"workload": "chunk_gdn2 prefill, BASELINE config 2: B=1 L=2048 Hk=12 Hv=24 K=V=128, "
+                               "bf16 qkv, fp32 gates, 2 segments, chunk 128, precision bf16, qk_l2norm, "
+                               "is_inference, fp32 final state",
+                   "B": 1, "L": 2048, "Hk": 12, "Hv": 24, "K": 128, "V": 128},
+        "mfma_pct_peak": round(mfma_pct, 3),
+        "step_roofline": {"t_roof_us": round(t_roof * 1e6, 2), "frac": round(t_roof / (ms_step * 1e-3), 4),
+                          "bytes": work["bytes_total"], "flops": work["flops_total"]},
+        "kernels_us": {k_: round(v_ * 1e3, 2) for k_, v_ in kern.items()},
+        "roofline": roof,
+        "decode": {"workload": "gdn2_decode_step, BASELINE config 4: B=256 Hk=16 Hv=32 K=V=128, bf16 qkv, "
+                               "channel-wise fp32 gates, qk_l2norm", **dec},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

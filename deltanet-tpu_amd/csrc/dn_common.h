@@ -145,6 +145,14 @@ template <bool BF> __device__ __forceinline__ Frag<BF> frag_from_acc(const f32x4
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, not for its outstanding global loads, so prefetches issued
+// before the barrier stay in flight across it.  (__syncthreads() also drains
+// the vector-memory counter.)  Not for exchanging data through global memory.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Precision policy.  "bf16" mode runs plain products on bf16 MFMA and the
 // products that set the output accuracy as split-bf16 products: an fp32
@@ -187,6 +195,50 @@ template <> struct Pol<false> {
   static __device__ __forceinline__ void m11(f32x4& c, const F1& a, const F1& b) { mma(c, a, b); }
   static __device__ __forceinline__ void m13(f32x4& c, const F1& a, const F3& b) { mma(c, a, b); }
   static __device__ __forceinline__ void m33(f32x4& c, const F3& a, const F3& b) { mma(c, a, b); }
+};
+
+// ---------------------------------------------------------------------------
+// Operand storage.  Operands that feed split products are stored already
+// split (bf16 mode: two bf16 arrays hi / lo; fp32 mode: one fp32 array), and
+// plain operands as ST (bf16 / fp32), so a consumer loads MFMA fragments with
+// no conversion work.  Producers call put() once per element.
+// ---------------------------------------------------------------------------
+template <bool BF> struct Store;
+
+template <> struct Store<true> {
+  using ST = bf16;
+  using F1 = Pol<true>::F1;
+  using F3 = Pol<true>::F3;
+  static __device__ __forceinline__ void put(bf16* hi, bf16* lo, int64_t i, float v) {
+    const bf16 h = (bf16)v;
+    hi[i] = h;
+    lo[i] = (bf16)(v - (float)h);
+  }
+  static __device__ __forceinline__ void put1(bf16* p, int64_t i, float v) { p[i] = (bf16)v; }
+  // fragment (pi order) from a row pointer at the slab start
+  static __device__ __forceinline__ F1 f1(const bf16* rowp, int q) {
+    const bf16x4 a = *reinterpret_cast<const bf16x4*>(rowp + 4 * q);
+    const bf16x4 b = *reinterpret_cast<const bf16x4*>(rowp + 16 + 4 * q);
+    F1 f;
+    f.v = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return f;
+  }
+  static __device__ __forceinline__ F3 f3(const bf16* hi, const bf16* lo, int q) {
+    F3 r;
+    r.hi = f1(hi, q);
+    r.lo = f1(lo, q);
+    return r;
+  }
+};
+
+template <> struct Store<false> {
+  using ST = float;
+  using F1 = Pol<false>::F1;
+  using F3 = Pol<false>::F3;
+  static __device__ __forceinline__ void put(float* hi, float*, int64_t i, float v) { hi[i] = v; }
+  static __device__ __forceinline__ void put1(float* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ F1 f1(const float* rowp, int q) { return frag_row<false, float>(rowp, q); }
+  static __device__ __forceinline__ F3 f3(const float* hi, const float*, int q) { return f1(hi, q); }
 };
 
 // 8 fragment values (pi order) from a row-major row pointer at the slab start

@@ -15,6 +15,7 @@
 // The read-out uses o_j = sum_i q_i d_i S_ij + (q.k) vn_j, which equals
 // S'^T q exactly in real arithmetic and needs only the single pass over S.
 #include <string>
+#include <vector>
 
 #include "dn_common.h"
 #include "dn_host.h"
@@ -28,6 +29,36 @@ thread_local std::string g_last_error;
 int set_error(int code, const char* msg) {
   g_last_error = msg ? msg : "";
   return code;
+}
+
+namespace {
+struct ProfRec { int kind; hipEvent_t a, b; };
+thread_local bool g_prof = false;
+thread_local std::vector<ProfRec> g_recs;
+thread_local std::vector<hipEvent_t> g_pool;
+thread_local hipEvent_t g_open = nullptr;
+
+hipEvent_t take_event() {
+  if (!g_pool.empty()) { hipEvent_t e = g_pool.back(); g_pool.pop_back(); return e; }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+bool profiling() { return g_prof; }
+
+void prof_mark(int kind, hipStream_t st, bool after) {
+  if (!g_prof) return;
+  hipEvent_t e = take_event();
+  if (e == nullptr) return;
+  (void)hipEventRecord(e, st);
+  if (!after) {
+    g_open = e;
+  } else if (g_open != nullptr) {
+    g_recs.push_back(ProfRec{kind, g_open, e});
+    g_open = nullptr;
+  }
 }
 
 struct DP {
@@ -210,6 +241,34 @@ using namespace dn;
 
 extern "C" const char* dn_last_error(void) { return g_last_error.c_str(); }
 
+extern "C" int dn_profile_begin(void) {
+  g_prof = true;
+  g_recs.clear();
+  return DN_OK;
+}
+
+extern "C" int dn_profile_end(double* ms_sum, int64_t* launches) {
+  g_prof = false;
+  for (int k = 0; k < DN_PROFILE_KINDS; ++k) {
+    if (ms_sum) ms_sum[k] = 0.0;
+    if (launches) launches[k] = 0;
+  }
+  int rc = DN_OK;
+  for (const ProfRec& r : g_recs) {
+    float ms = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) {
+      rc = set_error(DN_E_LAUNCH, "profiling event failed");
+    } else if (r.kind >= 0 && r.kind < DN_PROFILE_KINDS) {
+      if (ms_sum) ms_sum[r.kind] += ms;
+      if (launches) launches[r.kind] += 1;
+    }
+    g_pool.push_back(r.a);
+    g_pool.push_back(r.b);
+  }
+  g_recs.clear();
+  return rc;
+}
+
 extern "C" int dn_abi_version(void) { return DN_ABI_VERSION; }
 
 extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
@@ -241,10 +300,12 @@ extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
   const dim3 grid((unsigned)(a->B * a->Hv));
   hipStream_t st = (hipStream_t)stream;
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
+  prof_mark(3, st, false);
   if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(512), 0, st, p);
   else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(512), 0, st, p);
   else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(512), 0, st, p);
   else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(512), 0, st, p);
+  prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;

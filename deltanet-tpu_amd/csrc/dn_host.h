@@ -40,4 +40,10 @@ struct PF {
 // Records the message for dn_last_error() and returns `code`.
 int set_error(int code, const char* msg);
 
+// Kernel timing (dn_profile_begin / dn_profile_end): returns true when the
+// calling thread is profiling; mark() records an event for `kind` on `st`
+// (call it once before and once after each launch).
+bool profiling();
+void prof_mark(int kind, hipStream_t st, bool after);
+
 }  // namespace dn

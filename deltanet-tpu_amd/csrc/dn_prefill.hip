@@ -89,7 +89,7 @@ template <bool BF> using MTy = typename std::conditional<BF, bf16, float>::type;
 // strongly decayed stretch).  Cross-block factors come from the per-block
 // totals: Off[a] / Suf[a] = sum of the totals before / after block a.
 // ===========================================================================
-template <bool BF, class TIn>
+template <bool BF, class TIn, class TV>
 __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
@@ -103,6 +103,7 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   __shared__ float Off[9 * KD];     // log2: sum of totals of blocks < a (Off[8] = Lambda_end)
   __shared__ float Suf[8 * KD];     // log2: sum of totals of blocks > a
   __shared__ int doc[CH];
+  __shared__ int unsafe_part[2][8];  // per 64-channel half: block needs the hierarchical path
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
@@ -164,16 +165,18 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   {
     const int kap = tid & 127, half = tid >> 7;
     const int hg = kgate_head(p, p.g_h, h);
+    // all 64 loads issued back to back: out-of-range tokens read a valid
+    // address and are zeroed afterwards (no branch between the loads)
+    const float* gp = (const float*)p.g;
+    const int tbase = tb + 64 * half;
     float gl[64];
 #pragma unroll
     for (int i = 0; i < 64; ++i) {
-      const int t = tb + 64 * half + i;
-      gl[i] = 0.f;
-      if (t < t_end) {
-        const int64_t gi = (((int64_t)b * p.L + t) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
-        gl[i] = act_g(ld_f(p.g, gi, p.g_dt), p.fuse, p.guard);
-      }
+      const int t = min(tbase + i, t_end - 1);
+      gl[i] = gp[(((int64_t)b * p.L + t) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap)];
     }
+#pragma unroll
+    for (int i = 0; i < 64; ++i) gl[i] = (tbase + i < t_end) ? act_g(gl[i], p.fuse, p.guard) : 0.f;
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       float hi = 0.f, lo = 0.f;
@@ -209,6 +212,11 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     for (int a = 0; a < 8; ++a) {
       Ftab[a * KD + tid] = fast_exp2(tot[a]);
       Mid0[a * KD + tid] = fast_exp2(X[(16 * a) * XP + tid] + Y[(16 * a) * XP + tid]);
+      // span of the block after its first token: Lambda(sa) - Lambda(ea) >= 0
+      const int sa = 16 * a, ea = sa + 15;
+      const float span = (X[sa * XP + tid] - X[ea * XP + tid]) + (Y[sa * XP + tid] - Y[ea * XP + tid]);
+      const bool un = __any(span > kDiagSafeLog2);
+      if (l == 0) unsafe_part[w][a] = un;
     }
     g_dv[tid] = fast_exp2(Off[8 * KD + tid]);
   }
@@ -254,21 +262,24 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
         for (int e = 0; e < 32; ++e) qv[e] = round_as<TIn>(qv[e] * p.scale);
       }
-      const int64_t brow = (((int64_t)b * p.L + (valid ? t : 0)) * p.b_h + hbg) * p.b_c;
+      const float* bp = (const float*)p.b + (((int64_t)b * p.L + (valid ? t : 0)) * p.b_h + hbg) * p.b_c;
+      float bgv[32];
+      if (p.b_c == 1) {
+        const float bs = bp[0];
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        const int kap = 32 * (e >> 3) + pi_k(q, e & 7);
-        const float bg = valid ? act_b(ld_f(p.b, brow + (p.b_c == 1 ? 0 : kap), p.b_dt), p.fuse, p.guard) : 0.f;
-        bet[e] = bg * kv[e];
+        for (int e = 0; e < 32; ++e) bgv[e] = bs;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) row8<float>(bp + 32 * s, q, bgv + 8 * s);
       }
+#pragma unroll
+      for (int e = 0; e < 32; ++e) bet[e] = valid ? act_b(bgv[e], p.fuse, p.guard) * kv[e] : 0.f;
     }
     const bool first = doc[i] == 0;
     const bool last = doc[i] == doc[CH - 1];
+    const bool blk_unsafe = unsafe_part[0][a] | unsafe_part[1][a];
     float dq = 0.f;
-    bool unsafe = false;
     f32x4 accA = zero4(), accM = zero4();
-    F3 Bd[4];
-    float kcs[32];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       float lam[8], lsa[8], ta[8], laml[8], lsal[8], tal[8], off[8], suf[8];
@@ -280,22 +291,20 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
       row8<float>(&Off[a * KD + 32 * s], q, off);
       row8<float>(&Suf[a * KD + 32 * s], q, suf);
-      float rA[8], rM[8], bd[8], qe[8];
+      float rA[8], rM[8], bd[8], kc[8], qe[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int kap = 32 * s + pi_k(q, e);
         const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
         const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
         const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
-        const float d_sa_ea = (lsa[e] - ta[e]) + (lsal[e] - tal[e]);    // >= 0
         const float er = fast_exp2(d_i_sa);
         rA[e] = be * er;
         rM[e] = qh * er;
-        kcs[8 * s + e] = kh * fast_exp2(d_ea_i);
+        kc[e] = kh * fast_exp2(d_ea_i);
         const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
         g_beT[(int64_t)kap * CH + i] = first ? be * eL : 0.f;
         g_keT[(int64_t)kap * CH + i] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
-        unsafe |= d_sa_ea > kDiagSafeLog2;
         bd[e] = kh * fast_exp2(-d_i_sa);
         dq += qh * kh;
         qe[e] = first ? qh * eL : 0.f;
@@ -304,20 +313,22 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       st4<float>(g_qe + (int64_t)i * KD + 32 * s + 16 + 4 * q, qe + 4);
       Rf[bi][s] = P::f3(rA);
       Qf[bi][s] = P::f3(rM);
-      Bd[s] = P::f3(bd);
+      if (!blk_unsafe) {
+        // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
+        // within 2^{+-100} of 1, so the factorisation cannot overflow.  Kc
+        // replaces this slab of the row's Lambda low words once all lanes of
+        // the wave have read it (the other slabs' columns are untouched).
+        const F3 fb = P::f3(bd);
+        P::m33(accA, Rf[bi][s], fb);
+        P::m33(accM, Qf[bi][s], fb);
+        st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
+        st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
+      }
     }
     dq += __shfl_xor(dq, 16);
     dq += __shfl_xor(dq, 32);
 
-    if (!__any(unsafe)) {
-      // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
-      // within 2^{+-100} of 1, so the factorisation cannot overflow.
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        P::m33(accA, Rf[bi][s], Bd[s]);
-        P::m33(accM, Qf[bi][s], Bd[s]);
-      }
-    } else {
+    if (blk_unsafe) {
       // Overflow-free hierarchical factorisation: the pair (i, j) is split at
       // the highest bit where the in-block indices differ; rows above and
       // columns below the split point are scaled toward it, so every
@@ -358,13 +369,20 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
         if (4 * q + ii == r16) accM[ii] = dq;
-    }
-    // Kc replaces this block's rows of the Lambda low words only after every
-    // lane of the wave has finished reading them
+      // Kc of this block's rows, written after every lane has read the rows'
+      // Lambda low words
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      st4<float>(&Y[i * YP + 32 * s + 4 * q], kcs + 8 * s);
-      st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kcs + 8 * s + 4);
+      for (int s = 0; s < 4; ++s) {
+        float lam[8], ta[8], laml[8], tal[8], kc[8];
+        row8<float>(&X[i * XP + 32 * s], q, lam);
+        row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
+        row8<float>(&Y[i * XP + 32 * s], q, laml);
+        row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kc[e] = kv[8 * s + e] * fast_exp2((ta[e] - lam[e]) + (tal[e] - laml[e]));
+        st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
+        st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
+      }
     }
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
@@ -512,13 +530,21 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
                             Wc[nt][2 * s + 1][0], Wc[nt][2 * s + 1][1], Wc[nt][2 * s + 1][2], Wc[nt][2 * s + 1][3]};
         W3[nt][s] = P::f3(x);
       }
+    // rows of ke^T / M are read from the (L2-resident) scratch one step ahead
+    float kx[2][32];
+    auto ld_rows = [&](const float* base, int row, int nslab, float* x) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < nslab) row8<float>(base + (int64_t)row * CH + 32 * s, q, x + 8 * s);
+    };
+    ld_rows(g_keT, r16, 4, kx[0]);
+#pragma unroll
     for (int m = 0; m < 8; ++m) {
+      if (m < 7) ld_rows(g_keT, 16 * (m + 1) + r16, 4, kx[(m + 1) & 1]);
       f32x4 P0 = zero4(), P1 = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(g_keT + (int64_t)(16 * m + r16) * CH + 32 * s, q, x);
-        const F1 fa = P::f1(x);
+        const F1 fa = P::f1(kx[m & 1] + 8 * s);
         P::m11(P0, fa, P::hi(W3[0][s]));
         P::m11(P1, fa, P::hi(W3[1][s]));
       }
@@ -529,22 +555,32 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         g_Pn[row + 16 * (w + 4) + r16] = from_f<MT>(-P1[ii]);
       }
     }
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-      f32x4 X0, X1;
+    float qx[2][8];
+    auto ld_qe = [&](int rt, float* x) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * KD;
-        X0[ii] = g_qe[row + 16 * w + r16];
-        X1[ii] = g_qe[row + 16 * (w + 4) + r16];
+        x[ii] = g_qe[row + 16 * w + r16];
+        x[4 + ii] = g_qe[row + 16 * (w + 4) + r16];
       }
+    };
+    ld_rows(g_M, r16, 1, kx[0]);
+    ld_qe(0, qx[0]);
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      if (rt < 7) {
+        ld_rows(g_M, 16 * (rt + 1) + r16, (rt + 1) / 2 + 1, kx[(rt + 1) & 1]);
+        ld_qe(rt + 1, qx[(rt + 1) & 1]);
+      }
+      f32x4 X0, X1;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) { X0[ii] = qx[rt & 1][ii]; X1[ii] = qx[rt & 1][4 + ii]; }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s <= rt / 2) {
           float x[8];
-          row8<float>(g_M + (int64_t)(16 * rt + r16) * CH + 32 * s, q, x);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = -x[e];
+          for (int e = 0; e < 8; ++e) x[e] = -kx[rt & 1][8 * s + e];
           const F3 fa = P::f3(x);
           P::m33(X0, fa, W3[0][s]);
           P::m33(X1, fa, W3[1][s]);
@@ -569,20 +605,22 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       const int hv = p.gates_at_hv ? h : h * p.G + n0 / KD;
       const int hw = vgate_head(p, p.w_h, hv);
       const bool valid = t < t_end;
-      const int64_t bt = (int64_t)b * p.L + (valid ? t : 0);
-      const int64_t vrow = (bt * p.Hv + hv) * KD + 64 * half;
-      const int64_t wrow = (bt * p.w_h + hw) * p.w_c;
-#pragma unroll 4
-      for (int j = 0; j < 64; ++j) {
-        const int col = 64 * half + j;
-        float val = 0.f;
-        if (valid) {
-          const float vv = ld_f(p.v, vrow + j, p.v_dt);
-          const float ww = act_w(ld_f(p.w, wrow + (p.w_c == 1 ? 0 : col), p.w_dt), p.fuse);
-          val = ww * vv;
-        }
-        Y[col * YP + tok] = val;
+      const int64_t bt = (int64_t)b * p.L + (valid ? t : tb);
+      const TV* vp = (const TV*)p.v + (bt * p.Hv + hv) * KD + 64 * half;
+      const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
+      float vv[64], ww[64];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ld4<TV>(vp + 4 * j, vv + 4 * j);
+      if (p.w_c == 1) {
+        const float ws = wp[0];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) ww[j] = ws;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) ld4<float>(wp + 64 * half + 4 * j, ww + 4 * j);
       }
+#pragma unroll
+      for (int j = 0; j < 64; ++j) Y[(64 * half + j) * YP + tok] = valid ? act_w(ww[j], p.fuse) * vv[j] : 0.f;
     }
     __syncthreads();
     f32x4 Uc[2][8];
@@ -622,13 +660,21 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         U3[nt][s] = P::f3(x);
       }
     const int c0 = n0 + 16 * w + r16, c1 = n0 + 16 * (w + 4) + r16;
+    float kx[2][32];
+    auto ld_rows = [&](const float* base, int row, int nslab, float* x) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < nslab) row8<float>(base + (int64_t)row * CH + 32 * s, q, x + 8 * s);
+    };
+    ld_rows(g_keT, r16, 4, kx[0]);
+#pragma unroll
     for (int m = 0; m < 8; ++m) {
+      if (m < 7) ld_rows(g_keT, 16 * (m + 1) + r16, 4, kx[(m + 1) & 1]);
+      else ld_rows(g_M, r16, 1, kx[0]);
       f32x4 Q0 = zero4(), Q1 = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(g_keT + (int64_t)(16 * m + r16) * CH + 32 * s, q, x);
-        const F3 fa = P::f3(x);
+        const F3 fa = P::f3(kx[m & 1] + 8 * s);
         P::m33(Q0, fa, U3[0][s]);
         P::m33(Q1, fa, U3[1][s]);
       }
@@ -639,15 +685,14 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         g_Q[row + c1] = Q1[ii];
       }
     }
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
+    // two row tiles per iteration (static prefetch buffers) without unrolling
+    // the whole loop, so the scheduler cannot hoist every row's loads at once
+    auto oi_tile = [&](int rt, const float* xcur) {
       f32x4 O0 = zero4(), O1 = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s <= rt / 2) {
-          float x[8];
-          row8<float>(g_M + (int64_t)(16 * rt + r16) * CH + 32 * s, q, x);
-          const F3 fa = P::f3(x);
+          const F3 fa = P::f3(xcur + 8 * s);
           P::m33(O0, fa, U3[0][s]);
           P::m33(O1, fa, U3[1][s]);
         }
@@ -658,6 +703,13 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         g_Oi[row + c0] = O0[ii];
         g_Oi[row + c1] = O1[ii];
       }
+    };
+#pragma unroll 1
+    for (int rt = 0; rt < 8; rt += 2) {
+      ld_rows(g_M, 16 * (rt + 1) + r16, (rt + 1) / 2 + 1, kx[1]);
+      oi_tile(rt, kx[0]);
+      if (rt + 2 < 8) ld_rows(g_M, 16 * (rt + 2) + r16, (rt + 2) / 2 + 1, kx[0]);
+      oi_tile(rt + 1, kx[1]);
     }
   }
 }
@@ -733,7 +785,7 @@ __global__ __launch_bounds__(256) void k_chain(const PF p) {
     float dv_n[8];
     int is_new_n = 0, same_n = 0;
     if (c + 1 < p.NCb) load_ops(c + 1, pf_n, qc_n, dv_n, is_new_n, same_n);
-    __syncthreads();
+    lds_barrier();
     F1 Sf[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -804,18 +856,28 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
   }
   const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
   const int vcol0 = col0 % KD;
-#pragma unroll 2
+  // X rows and Oi tiles of row tile rt+1 are loaded while rt computes
+  float xr[2][32], oi[2][16];
+  auto ld = [&](int rt, float* x, float* o) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) row8<float>(Xc + (int64_t)(16 * rt + r16) * KD + 32 * s, q, x + 8 * s);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) o[4 * ct + ii] = Oi[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + ncol[ct]];
+  };
+  ld(0, xr[0], oi[0]);
+#pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
+    if (rt < 7) ld(rt + 1, xr[(rt + 1) & 1], oi[(rt + 1) & 1]);
     f32x4 O[4];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) O[ct][ii] = Oi[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + ncol[ct]];
+      for (int ii = 0; ii < 4; ++ii) O[ct][ii] = oi[rt & 1][4 * ct + ii];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      float x[8];
-      row8<float>(Xc + (int64_t)(16 * rt + r16) * KD + 32 * s, q, x);
-      const F3 fa = P::f3(x);
+      const F3 fa = P::f3(xr[rt & 1] + 8 * s);
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) P::m33(O[ct], fa, Sf[ct][s]);
     }
@@ -826,10 +888,9 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
         const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol0 + r16;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
-          const int64_t oi = ob + 16 * ct;
-          if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)O[ct][ii];
-          else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)O[ct][ii];
-          else ((float*)p.out)[oi] = O[ct][ii];
+          const int64_t oi_ = ob + 16 * ct;
+          if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi_] = (bf16)O[ct][ii];
+          else ((float*)p.out)[oi_] = O[ct][ii];
         }
       }
     }
@@ -890,15 +951,17 @@ int check_args(const dn_prefill_args* a) {
     return set_error(DN_E_INVALID, "token range must satisfy 0 <= t0 < t0+nt <= L with t0 % 128 == 0");
   if (!a->q || !a->k || !a->v || !a->g || !a->b || !a->w || !a->out)
     return set_error(DN_E_INVALID, "missing tensor pointer");
-  if (a->qk_dtype < DN_F32 || a->qk_dtype > DN_F16 || a->v_dtype < DN_F32 || a->v_dtype > DN_F16)
-    return set_error(DN_E_INVALID, "q/k/v dtype must be f32, bf16 or f16");
+  if (a->qk_dtype < DN_F32 || a->qk_dtype > DN_F16)
+    return set_error(DN_E_INVALID, "q/k dtype must be f32, bf16 or f16");
+  if (a->v_dtype != DN_F32 && a->v_dtype != DN_BF16)
+    return set_error(DN_E_INVALID, "v dtype must be f32 or bf16");
   const int G = a->Hv / a->Hk;
   auto gate_ok = [&](int H, int Cc, int dt, int full) {
-    return (H == 1 || H == a->Hk || H == a->Hv) && (Cc == 1 || Cc == full) && dt >= DN_F32 && dt <= DN_F16;
+    return (H == 1 || H == a->Hk || H == a->Hv) && (Cc == 1 || Cc == full) && dt == DN_F32;
   };
   if (!gate_ok(a->g_heads, a->g_chans, a->g_dtype, a->K) || !gate_ok(a->b_heads, a->b_chans, a->b_dtype, a->K) ||
       !gate_ok(a->w_heads, a->w_chans, a->w_dtype, a->V))
-    return set_error(DN_E_INVALID, "gate shape/dtype not supported");
+    return set_error(DN_E_INVALID, "gates must be float32 with 1, Hk or Hv heads and 1 or 128 channels");
   if (!a->gates_at_hv && G > 1 && (a->g_heads == a->Hv || a->b_heads == a->Hv))
     return set_error(DN_E_INVALID, "g or b has Hv heads: gates_at_hv must be set");
   if (a->seg && a->seg_dtype != DN_I32 && a->seg_dtype != DN_I64) return set_error(DN_E_INVALID, "segment ids must be int32 or int64");
@@ -907,17 +970,38 @@ int check_args(const dn_prefill_args* a) {
   return DN_OK;
 }
 
-template <bool BF, class TIn>
+template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
-  const dim3 g1(p.NCb, p.Hx, p.B);
-  hipLaunchKernelGGL((k_prepass<BF, TIn>), g1, dim3(256), 0, st, p);
+  prof_mark(0, st, false);
+  hipLaunchKernelGGL((k_prepass<BF, TIn, TV>), dim3(p.NCb, p.Hx, p.B), dim3(256), 0, st, p);
+  prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  prof_mark(1, st, false);
   hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(256), 0, st, p);
+  prof_mark(1, st, true);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  prof_mark(2, st, false);
   hipLaunchKernelGGL((k_output<BF>), dim3(p.NCb, p.Hx, p.B * p.ncg), dim3(256), 0, st, p);
+  prof_mark(2, st, true);
   return hipGetLastError();
+}
+
+template <bool BF, class TIn>
+hipError_t dispatch_v(const PF& p, hipStream_t st, bool v_bf16) {
+  return v_bf16 ? launch_all<BF, TIn, bf16>(p, st) : launch_all<BF, TIn, float>(p, st);
+}
+
+template <bool BF>
+hipError_t dispatch_qk(const PF& p, hipStream_t st, int qk_dt, bool v_bf16) {
+  if (qk_dt == DN_BF16) return dispatch_v<BF, bf16>(p, st, v_bf16);
+  if (qk_dt == DN_F16) return dispatch_v<BF, f16>(p, st, v_bf16);
+  return dispatch_v<BF, float>(p, st, v_bf16);
+}
+
+hipError_t dispatch(const PF& p, hipStream_t st, bool bf, int qk_dt, bool v_bf16) {
+  return bf ? dispatch_qk<true>(p, st, qk_dt, v_bf16) : dispatch_qk<false>(p, st, qk_dt, v_bf16);
 }
 
 }  // namespace
@@ -982,16 +1066,7 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
     p.has_init = first ? (a->init_state != nullptr) : 1;
     p.init = first ? a->init_state : carry;
     p.fin = carry;
-    hipError_t e;
-    if (bf) {
-      if (a->qk_dtype == DN_BF16) e = launch_all<true, bf16>(p, st);
-      else if (a->qk_dtype == DN_F16) e = launch_all<true, f16>(p, st);
-      else e = launch_all<true, float>(p, st);
-    } else {
-      if (a->qk_dtype == DN_BF16) e = launch_all<false, bf16>(p, st);
-      else if (a->qk_dtype == DN_F16) e = launch_all<false, f16>(p, st);
-      else e = launch_all<false, float>(p, st);
-    }
+    const hipError_t e = dispatch(p, st, bf, a->qk_dtype, a->v_dtype == DN_BF16);
     if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   }
   return DN_OK;

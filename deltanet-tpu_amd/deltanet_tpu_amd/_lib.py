@@ -73,7 +73,10 @@ EXPORTED_SYMBOLS = (
     "dn_state_frob_cap",
     "dn_last_error",
     "dn_abi_version",
+    "dn_profile_begin",
+    "dn_profile_end",
 )
+PROFILE_KINDS = ("prepass", "chain", "output", "decode")
 
 _lock = threading.Lock()
 _lib = None
@@ -103,11 +106,28 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         lib.dn_last_error.restype = ctypes.c_char_p
         lib.dn_abi_version.argtypes = []
         lib.dn_abi_version.restype = ctypes.c_int
+        lib.dn_profile_begin.argtypes = []
+        lib.dn_profile_begin.restype = ctypes.c_int
+        lib.dn_profile_end.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]
+        lib.dn_profile_end.restype = ctypes.c_int
         if lib.dn_abi_version() != DN_ABI_VERSION:
             raise RuntimeError("deltanet_tpu_amd: library ABI version mismatch; rebuild it")
         if path is None:
             _lib = lib
         return lib
+
+
+def profile_begin() -> None:
+    check(load_library().dn_profile_begin(), "dn_profile_begin")
+
+
+def profile_end() -> dict:
+    """Per kernel kind: (summed milliseconds, launches) since profile_begin()."""
+    n = len(PROFILE_KINDS)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int64 * n)()
+    check(load_library().dn_profile_end(ms, cnt), "dn_profile_end")
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(PROFILE_KINDS)}
 
 
 def check(rc: int, what: str) -> None:

@@ -225,7 +225,7 @@ def chunk_gdn2(
     gates_at_hv = ((g.shape[2] == Hv) or (b.shape[2] == Hv)) and (Hk < Hv)
 
     def gate(t):
-        t = _float_arg(t)
+        t = t.to(torch.float32).contiguous()
         if t.ndim == 3:
             t = t.unsqueeze(-1)
         return t, int(t.shape[2]), int(t.shape[3])
@@ -239,7 +239,7 @@ def chunk_gdn2(
     q = q.contiguous()
     k = k.contiguous()
     out_dtype = v.dtype
-    v_in = _float_arg(v)
+    v_in = v.contiguous() if v.dtype in (torch.float32, torch.bfloat16) else v.to(torch.float32).contiguous()
 
     init = None
     if initial_state is not None:

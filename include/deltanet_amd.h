@@ -15,7 +15,7 @@
  *
  * Tensor layouts (all row-major / C-contiguous, element strides implied):
  *   q, k   (B, L, Hk, K)         v, out (B, L, Hv, V)
- *   g, b   (B, L, Hx, Cx)        w      (B, L, Hx, Cx)
+ *   g, b   (B, L, Hx, Cx)        w      (B, L, Hx, Cx)    (prefill: float32)
  *          Hx in {1, Hk, Hv}; Cx in {1, K} for g/b and {1, V} for w.
  *          A gate with Hx == Hk is shared by the G = Hv/Hk value heads of a
  *          key head (value head hv reads head hv / G); Hx == 1 is shared by
@@ -63,8 +63,8 @@ typedef struct dn_prefill_args {
   const void* q;                /* (B,L,Hk,K)                                   */
   const void* k;                /* (B,L,Hk,K)                                   */
   const void* v;                /* (B,L,Hv,V)                                   */
-  int32_t qk_dtype, v_dtype;    /* DN_F32 / DN_BF16 / DN_F16                    */
-  const void* g; int32_t g_dtype, g_heads, g_chans;
+  int32_t qk_dtype, v_dtype;    /* q/k: DN_F32 / DN_BF16 / DN_F16; v: F32 / BF16 */
+  const void* g; int32_t g_dtype, g_heads, g_chans;   /* gates: DN_F32          */
   const void* b; int32_t b_dtype, b_heads, b_chans;
   const void* w; int32_t w_dtype, w_heads, w_chans;
   const void* seg;              /* NULL or segment ids                          */
@@ -122,6 +122,17 @@ int dn_decode_step(const dn_decode_args* a, void* stream);
  * `nmat` consecutive (rows x cols) float32 matrices (the stability_guard cap of
  * gdn2.py:2180-2188 / 2224-2226 / 2236-2238). */
 int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, float tau, void* stream);
+
+/* Kernel timing instrumentation (no counterpart in the reference; for
+ * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
+ * every dn_prefill_fwd call on the calling thread records HIP events on its
+ * stream around each of its kernels (prepass, chain, output) and every
+ * dn_decode_step call around its kernel.  dn_profile_end() waits for those
+ * events and writes, per kernel kind, the summed duration in milliseconds
+ * and the number of launches (arrays of DN_PROFILE_KINDS entries). */
+#define DN_PROFILE_KINDS 4   /* 0 prepass, 1 chain, 2 output, 3 decode */
+int dn_profile_begin(void);
+int dn_profile_end(double* ms_sum, int64_t* launches);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* dn_last_error(void);
