@@ -198,24 +198,68 @@ template <> struct Pol<false> {
 };
 
 // ---------------------------------------------------------------------------
-// Operand storage.  Operands that feed split products are stored already
-// split (bf16 mode: two bf16 arrays hi / lo; fp32 mode: one fp32 array), and
-// plain operands as ST (bf16 / fp32), so a consumer loads MFMA fragments with
-// no conversion work.  Producers call put() once per element.
+// Operand storage.  Intermediates are written in the lane order of the MFMA
+// operand that consumes them ("fragment-native"): a 16 x 32 operand slab is 64
+// lanes x 8 elements, lane (r, q) holding row r and reduction indices
+// pi(q, 0..7), so a consumer loads 16 (bf16) or 32 (fp32) contiguous bytes per
+// lane.  An accumulator tile of the transposed product (lane (c, q) holding
+// rows 4q..4q+3 of column c) is one half (e = 0..3 or 4..7) of such a slab.
+// Operands of split products are stored split (bf16 mode: hi and lo bf16
+// arrays; fp32 mode: one fp32 array, lo aliases hi).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int fofs(int tile, int slab, int lane) { return ((tile * 4 + slab) * 64 + lane) * 8; }
+__device__ __forceinline__ int cofs(int rtile, int ctile, int nct, int lane) { return ((rtile * nct + ctile) * 64 + lane) * 4; }
+
 template <bool BF> struct Store;
 
 template <> struct Store<true> {
   using ST = bf16;
   using F1 = Pol<true>::F1;
   using F3 = Pol<true>::F3;
-  static __device__ __forceinline__ void put(bf16* hi, bf16* lo, int64_t i, float v) {
-    const bf16 h = (bf16)v;
-    hi[i] = h;
-    lo[i] = (bf16)(v - (float)h);
+  static __device__ __forceinline__ F1 fa(const bf16* p) {
+    F1 f;
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+    return f;
   }
-  static __device__ __forceinline__ void put1(bf16* p, int64_t i, float v) { p[i] = (bf16)v; }
-  // fragment (pi order) from a row pointer at the slab start
+  static __device__ __forceinline__ F3 fa3(const bf16* hi, const bf16* lo) {
+    F3 r;
+    r.hi = fa(hi);
+    r.lo = fa(lo);
+    return r;
+  }
+  static __device__ __forceinline__ void st8(bf16* p, const float* x) {
+    bf16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (bf16)x[e];
+    *reinterpret_cast<bf16x8*>(p) = h;
+  }
+  static __device__ __forceinline__ void st8s(bf16* hi, bf16* lo, const float* x) {
+    bf16x8 h, l;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      h[e] = (bf16)x[e];
+      l[e] = (bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x8*>(hi) = h;
+    *reinterpret_cast<bf16x8*>(lo) = l;
+  }
+  static __device__ __forceinline__ void st4(bf16* p, const float* x) {
+    bf16x4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = (bf16)x[e];
+    *reinterpret_cast<bf16x4*>(p) = h;
+  }
+  static __device__ __forceinline__ void st4s(bf16* hi, bf16* lo, const float* x) {
+    bf16x4 h, l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = (bf16)x[e];
+      l[e] = (bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x4*>(hi) = h;
+    *reinterpret_cast<bf16x4*>(lo) = l;
+  }
+  // fragment (pi order) from a row-major row pointer at the slab start
   static __device__ __forceinline__ F1 f1(const bf16* rowp, int q) {
     const bf16x4 a = *reinterpret_cast<const bf16x4*>(rowp + 4 * q);
     const bf16x4 b = *reinterpret_cast<const bf16x4*>(rowp + 16 + 4 * q);
@@ -229,17 +273,66 @@ template <> struct Store<true> {
     r.lo = f1(lo, q);
     return r;
   }
+  static __device__ __forceinline__ void put(bf16* hi, bf16* lo, int i, float v) {
+    const bf16 h = (bf16)v;
+    hi[i] = h;
+    lo[i] = (bf16)(v - (float)h);
+  }
 };
 
 template <> struct Store<false> {
   using ST = float;
   using F1 = Pol<false>::F1;
   using F3 = Pol<false>::F3;
-  static __device__ __forceinline__ void put(float* hi, float*, int64_t i, float v) { hi[i] = v; }
-  static __device__ __forceinline__ void put1(float* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ F1 fa(const float* p) {
+    F1 f;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { f.v[e] = a[e]; f.v[4 + e] = b[e]; }
+    return f;
+  }
+  static __device__ __forceinline__ F3 fa3(const float* hi, const float*) { return fa(hi); }
+  static __device__ __forceinline__ void st8(float* p, const float* x) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+  static __device__ __forceinline__ void st8s(float* hi, float*, const float* x) { st8(hi, x); }
+  static __device__ __forceinline__ void st4(float* p, const float* x) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  }
+  static __device__ __forceinline__ void st4s(float* hi, float*, const float* x) { st4(hi, x); }
   static __device__ __forceinline__ F1 f1(const float* rowp, int q) { return frag_row<false, float>(rowp, q); }
   static __device__ __forceinline__ F3 f3(const float* hi, const float*, int q) { return f1(hi, q); }
+  static __device__ __forceinline__ void put(float* hi, float*, int i, float v) { hi[i] = v; }
 };
+
+// B fragments of the two halves of a 32 x 32 identity: A (16 x 32) times
+// ident(0) / ident(1) is the left / right 16 x 16 half of A, delivered in
+// accumulator layout, i.e. transposed relative to the A fragment (exact: one
+// product by 1 per output element).
+template <bool BF> __device__ __forceinline__ Frag<BF> ident_frag(int half, int r16, int q) {
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (pi_k(q, e) == 16 * half + r16) ? 1.f : 0.f;
+  return make_frag<BF>(x);
+}
+
+// XCD-aware block index.  Consecutive workgroups of a launch are dealt to the
+// 8 XCDs round-robin; this remaps the linear block id so that each XCD works
+// on one contiguous range of the logical grid (x fastest), keeping the
+// operands those blocks share in one XCD's L2.  Identity when the grid does
+// not divide evenly.
+__device__ __forceinline__ void xcd_block(int& x, int& y, int& z) {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int tot = gx * gy * gridDim.z;
+  int id = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  if ((tot & 7) == 0) id = (id & 7) * (tot >> 3) + (id >> 3);
+  x = id % gx;
+  id /= gx;
+  y = id % gy;
+  z = id / gy;
+}
 
 // 8 fragment values (pi order) from a row-major row pointer at the slab start
 template <class T> __device__ __forceinline__ void row8(const T* rowp, int q, float* x) {

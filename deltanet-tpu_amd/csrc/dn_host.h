@@ -29,12 +29,23 @@ struct PF {
   // workspace arrays (one unit = one (batch, exec head, chunk))
   int32_t* flags;            // [B][NCb][2] : is_new_doc, all_same_doc
   float* dvec;               // [unit][K]    : e^{Lambda_end}
-  void* Pn;                  // [unit][K][K] : -ke^T W (bf16 in bf16 mode)
-  float* Q;                  // [unit][K][Vp]: ke^T U
-  float* X;                  // [unit][C][K] : qe - M W   (effective queries)
-  float* Oi;                 // [unit][C][Vp]: M U        (intra-chunk output)
-  float* St;                 // [unit][Vp][K]: entry state of the chunk, transposed
-  float *beT, *keT, *Mg, *qe;  // prepass scratch: [K][C], [K][C], [C][C], [C][K]
+  int nct;                   // 16-column tiles of the value width (Vp / 16)
+  // Workspace, per unit = (batch, exec head, chunk).  Every operand array is
+  // fragment-native for its consumer (F = [tile][slab][lane][8] elements of a
+  // 16 x 32 MFMA operand slab, C = [row tile][col tile][lane][4] accumulator
+  // tiles).  Split operands have a high and a low array (bf16 mode; in fp32
+  // mode the low pointer aliases the high one).  "ST" = bf16 in bf16 mode,
+  // fp32 in fp32 mode.
+  void* PnA;                 // F  [8][4]      ST : Pn = -ke^T W, rows = state row (chain A)
+  float* QC;                 // C  [8][nct]    f32: Q = ke^T U (chain accumulator init)
+  void *XAh, *XAl;           // F  [8][4]      ST : X = qe - M W, rows = token (output B)
+  float* OiT;                // C  [8][nct]    f32: (M U)^T tiles (output accumulator init)
+  void *StBh, *StBl;         // F  [nct][4]    ST : S_c^T, rows = value column (output A)
+  void* BeB;                 // F  [8][4]      ST : (b k e^Lambda)^T, first document
+  void *KeBh, *KeBl;         // F  [8][4]      ST : (k e^{Lend - Lambda})^T, last document
+  void *MAh, *MAl;           // F  [8][4]      ST : M, rows = token
+  float* QeA;                // F  [8][4]      f32: q e^Lambda, first document
+  void* TA;                  // F  [8][4]      ST : T = (I + A)^-1
 };
 
 // Records the message for dn_last_error() and returns `code`.

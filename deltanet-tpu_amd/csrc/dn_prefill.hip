@@ -26,8 +26,6 @@
 //
 // All intermediates live in a caller-provided workspace sized for one token
 // block, small enough to stay resident in the 256 MB Infinity Cache.
-#include <type_traits>
-
 #include "dn_common.h"
 #include "dn_host.h"
 
@@ -42,23 +40,11 @@ constexpr int XP = 132;   // fp32 LDS pitch (floats): conflict-free 16-lane colu
 constexpr float kDiagSafeLog2 = 100.f;
 
 // ---------------------------------------------------------------------------
-// gate activations (gdn2.py:38-47, 133-142, 1970-1974)
+// gate activations (gdn2.py:38-47, 133-142, 1970-1974): g = -exp(min(g, 5)),
+// b, w = sigmoid.  The sigmoid uses the hardware reciprocal (v_rcp_f32, 1 ulp):
+// 1 + e^{-x} >= 1, and an infinite denominator gives exactly 0.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float act_g(float x, int fuse, int guard) {
-  if (fuse) {
-    x = -__expf(fminf(x, 5.f));
-  } else {
-    x = fminf(x, 0.f);  // _nonpositive: x <= 0 ? x : 0 (NaN -> 0)
-  }
-  if (guard) x = fminf(x, -1e-6f);
-  return x;
-}
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
-__device__ __forceinline__ float act_b(float x, int fuse, int guard) {
-  if (fuse) return sigmoidf_(x);
-  return guard ? fmaxf(x, 0.f) : x;
-}
-__device__ __forceinline__ float act_w(float x, int fuse) { return fuse ? sigmoidf_(x) : x; }
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // head of a K-side gate (g, b) used by execution head h
 __device__ __forceinline__ int kgate_head(const PF& p, int H, int h) {
@@ -77,51 +63,61 @@ __device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
   return ld_i(p.seg, i, p.seg_dt);
 }
 
-template <bool BF> using MTy = typename std::conditional<BF, bf16, float>::type;
-
 // ===========================================================================
-// k_prepass: everything that is parallel over chunks (one workgroup, 4 waves,
-// per (chunk, execution head, batch)).
+// k_prepass: everything per chunk that does not depend on the values (one
+// workgroup, 4 waves, per (chunk, execution head, batch)): chunk flags,
+// Lambda, A and M, T = (I + A)^-1, W = T (b k e^Lambda), Pn = -ke^T W and
+// X = qe - M W; it also leaves T, ke^T and M for k_value.
 //
 // Lambda is kept block-local: X[i] = sum of g over the 16-token block of i up
-// to and including i (log2 units), so a difference of two Lambdas is never
-// the difference of two large cumulative sums (no fp32 cancellation after a
-// strongly decayed stretch).  Cross-block factors come from the per-block
-// totals: Off[a] / Suf[a] = sum of the totals before / after block a.
+// to and including i (log2 units, double-float hi in X / lo in Y), so a
+// difference of two Lambdas is never the difference of two large cumulative
+// sums (no fp32 cancellation after a strongly decayed stretch).  Cross-block
+// factors come from the per-block totals: Off[a] / Suf[a] = sum of the totals
+// before / after block a.
+//
+// Products whose result feeds another kernel are computed transposed where
+// that puts the result directly in its consumer's fragment layout (M^T, Pn^T,
+// X^T); (b k e^Lambda)^T and ke^T are transposed by an identity product.
 // ===========================================================================
-template <bool BF, class TIn, class TV>
+template <bool BF, class TIn>
 __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
-  using MT = MTy<BF>;
+  using SS = Store<BF>;
+  using ST = typename SS::ST;
   constexpr int YP = 132;
-  __shared__ float X[CH * XP];      // local Lambda (log2) -> A -> T
-  __shared__ float Y[CH * YP];      // Lambda low words (1-2), Kc (2-3), w*v transposed (6)
-  __shared__ float Ftab[8 * KD];    // e^{total of block b}
-  __shared__ float Mid0[8 * KD];    // e^{g at the first token of block a}
-  __shared__ float Off[9 * KD];     // log2: sum of totals of blocks < a (Off[8] = Lambda_end)
-  __shared__ float Suf[8 * KD];     // log2: sum of totals of blocks > a
+  __shared__ float X[CH * XP];        // Lambda hi -> A -> T (fp32)
+  __shared__ float Y[CH * YP];        // Lambda lo -> Kc -> T fragment-native (ST)
+  __shared__ float Ftab[8 * KD];      // e^{total of block b}
+  __shared__ float Mid0[8 * KD];      // e^{g at the first token of block a}
+  __shared__ float Off[9 * KD];       // log2: sum of totals of blocks < a (Off[8] = Lambda_end)
+  __shared__ float Suf[8 * KD];       // log2: sum of totals of blocks > a
   __shared__ int doc[CH];
-  __shared__ int unsafe_part[2][8];  // per 64-channel half: block needs the hierarchical path
+  __shared__ int unsafe_part[2][8];   // per 64-channel half: block needs the hierarchical path
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  int c, h, b;
+  xcd_block(c, h, b);
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
+  const int64_t uf = u * (CH * KD);   // one 128 x 128 fragment-native array per unit
   const int hk = p.gates_at_hv ? h / p.G : h;
 
-  MT* g_Pn = (MT*)p.Pn + u * KD * KD;
-  float* g_Q = p.Q + u * KD * p.Vp;
-  float* g_X = p.X + u * CH * KD;
-  float* g_Oi = p.Oi + u * CH * p.Vp;
+  ST* g_Pn = (ST*)p.PnA + uf;
+  ST* g_Xh = (ST*)p.XAh + uf;
+  ST* g_Xl = (ST*)p.XAl + uf;
+  ST* g_be = (ST*)p.BeB + uf;
+  ST* g_keh = (ST*)p.KeBh + uf;
+  ST* g_kel = (ST*)p.KeBl + uf;
+  ST* g_Mh = (ST*)p.MAh + uf;
+  ST* g_Ml = (ST*)p.MAl + uf;
+  ST* g_T = (ST*)p.TA + uf;
+  float* g_qe = p.QeA + uf;
   float* g_dv = p.dvec + u * KD;
-  float* g_beT = p.beT + u * KD * CH;
-  float* g_keT = p.keT + u * KD * CH;
-  float* g_M = p.Mg + u * CH * CH;
-  float* g_qe = p.qe + u * CH * KD;
 
   // ---- phase 0: in-chunk document index (segment canonicalisation) -------
   if (tid < CH) {
@@ -165,18 +161,27 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   {
     const int kap = tid & 127, half = tid >> 7;
     const int hg = kgate_head(p, p.g_h, h);
-    // all 64 loads issued back to back: out-of-range tokens read a valid
-    // address and are zeroed afterwards (no branch between the loads)
-    const float* gp = (const float*)p.g;
     const int tbase = tb + 64 * half;
+    const int nvalid = t_end - tbase;  // tokens of this half inside the range (may be <= 0)
+    const int tload = min(tbase, t_end - 1);
+    const int nload = t_end - tload;   // >= 1
+    const int gstride = p.g_h * p.g_c;
+    const float* gp = (const float*)p.g + (((int64_t)b * p.L + tload) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
+    // all 64 loads issued back to back; out-of-range tokens read the last
+    // valid token and are zeroed below
     float gl[64];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const int t = min(tbase + i, t_end - 1);
-      gl[i] = gp[(((int64_t)b * p.L + t) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap)];
-    }
+    for (int i = 0; i < 64; ++i) gl[i] = gp[min(i, nload - 1) * gstride];
+    if (p.fuse) {
 #pragma unroll
-    for (int i = 0; i < 64; ++i) gl[i] = (tbase + i < t_end) ? act_g(gl[i], p.fuse, p.guard) : 0.f;
+      for (int i = 0; i < 64; ++i) gl[i] = -__expf(fminf(gl[i], 5.f));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) gl[i] = fminf(gl[i], 0.f);  // _nonpositive (NaN -> 0)
+    }
+    const float gmax = p.guard ? -1e-6f : 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) gl[i] = (i < nvalid) ? fminf(gl[i], gmax) : 0.f;
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       float hi = 0.f, lo = 0.f;
@@ -232,18 +237,24 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     const int i = 16 * a + r16;
     const int t = tb + i;
     const bool valid = t < t_end;
+    const int tt = valid ? t : tb;
     float qv[32], kv[32], bet[32];
     {
-      const TIn* qp = (const TIn*)p.q + (((int64_t)b * p.L + (valid ? t : 0)) * p.Hk + hk) * KD;
-      const TIn* kp = (const TIn*)p.k + (((int64_t)b * p.L + (valid ? t : 0)) * p.Hk + hk) * KD;
+      const TIn* qp = (const TIn*)p.q + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
+      const TIn* kp = (const TIn*)p.k + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
+      const float* bp = (const float*)p.b + (((int64_t)b * p.L + tt) * p.b_h + hbg) * p.b_c;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         row8<TIn>(qp + 32 * s, q, qv + 8 * s);
         row8<TIn>(kp + 32 * s, q, kv + 8 * s);
       }
-      if (!valid) {
+      if (p.b_c == 1) {
+        const float bs = bp[0];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) { qv[e] = 0.f; kv[e] = 0.f; }
+        for (int e = 0; e < 32; ++e) bet[e] = bs;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) row8<float>(bp + 32 * s, q, bet + 8 * s);
       }
       float ssq = 0.f, ssk = 0.f;
 #pragma unroll
@@ -251,9 +262,13 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       ssq += __shfl_xor(ssq, 16); ssq += __shfl_xor(ssq, 32);
       ssk += __shfl_xor(ssk, 16); ssk += __shfl_xor(ssk, 32);
       if (p.fuse) {
-        const float rq = rsqrtf(ssq + 1e-6f), rk = rsqrtf(ssk + 1e-6f);
+        const float rq = rsqrtf(ssq + 1e-6f) , rk = rsqrtf(ssk + 1e-6f);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) { qv[e] = (qv[e] * rq) * p.scale; kv[e] = kv[e] * rk; }
+        for (int e = 0; e < 32; ++e) {
+          qv[e] = (qv[e] * rq) * p.scale;
+          kv[e] = kv[e] * rk;
+          bet[e] = sigmoid_fast(bet[e]);
+        }
       } else if (p.l2norm) {
         const float rq = rsqrtf(ssq + 1e-6f), rk = rsqrtf(ssk + 1e-6f);
 #pragma unroll
@@ -262,23 +277,22 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
         for (int e = 0; e < 32; ++e) qv[e] = round_as<TIn>(qv[e] * p.scale);
       }
-      const float* bp = (const float*)p.b + (((int64_t)b * p.L + (valid ? t : 0)) * p.b_h + hbg) * p.b_c;
-      float bgv[32];
-      if (p.b_c == 1) {
-        const float bs = bp[0];
+      if (p.guard && !p.fuse) {
 #pragma unroll
-        for (int e = 0; e < 32; ++e) bgv[e] = bs;
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) row8<float>(bp + 32 * s, q, bgv + 8 * s);
+        for (int e = 0; e < 32; ++e) bet[e] = fmaxf(bet[e], 0.f);
       }
 #pragma unroll
-      for (int e = 0; e < 32; ++e) bet[e] = valid ? act_b(bgv[e], p.fuse, p.guard) * kv[e] : 0.f;
+      for (int e = 0; e < 32; ++e) {
+        qv[e] = valid ? qv[e] : 0.f;
+        kv[e] = valid ? kv[e] : 0.f;
+        bet[e] = valid ? bet[e] * kv[e] : 0.f;
+      }
     }
     const bool first = doc[i] == 0;
     const bool last = doc[i] == doc[CH - 1];
     const bool blk_unsafe = unsafe_part[0][a] | unsafe_part[1][a];
     float dq = 0.f;
+    // accA: A tile (lane = column token); accM: M^T tile (lane = row token)
     f32x4 accA = zero4(), accM = zero4();
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -291,10 +305,9 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
       row8<float>(&Off[a * KD + 32 * s], q, off);
       row8<float>(&Suf[a * KD + 32 * s], q, suf);
-      float rA[8], rM[8], bd[8], kc[8], qe[8];
+      float rA[8], rM[8], bd[8], kc[8], qe[8], bt[8], kt[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int kap = 32 * s + pi_k(q, e);
         const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
         const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
         const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
@@ -303,14 +316,36 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         rM[e] = qh * er;
         kc[e] = kh * fast_exp2(d_ea_i);
         const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
-        g_beT[(int64_t)kap * CH + i] = first ? be * eL : 0.f;
-        g_keT[(int64_t)kap * CH + i] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
+        bt[e] = first ? be * eL : 0.f;
+        kt[e] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
         bd[e] = kh * fast_exp2(-d_i_sa);
         dq += qh * kh;
         qe[e] = first ? qh * eL : 0.f;
       }
-      st4<float>(g_qe + (int64_t)i * KD + 32 * s + 4 * q, qe);
-      st4<float>(g_qe + (int64_t)i * KD + 32 * s + 16 + 4 * q, qe + 4);
+      Store<false>::st8(g_qe + fofs(a, s, l), qe);
+      {
+        // (b k e^Lambda)^T and ke^T in fragment layout (row = key, k = token)
+        const F1 fbt = P::f1(bt);
+        const F3 fkt = P::f3(kt);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const F1 id = ident_frag<BF>(hf, r16, q);
+          f32x4 cb = zero4(), chi = zero4();
+          mma(cb, fbt, id);
+          mma(chi, P::hi(fkt), id);
+          const int o = fofs(2 * s + hf, a >> 1, l) + 4 * (a & 1);
+          const float xb[4] = {cb[0], cb[1], cb[2], cb[3]};
+          const float xh[4] = {chi[0], chi[1], chi[2], chi[3]};
+          SS::st4(g_be + o, xb);
+          SS::st4(g_keh + o, xh);
+          if constexpr (BF) {
+            f32x4 clo = zero4();
+            mma(clo, fkt.lo, id);
+            const float xl[4] = {clo[0], clo[1], clo[2], clo[3]};
+            SS::st4(g_kel + o, xl);
+          }
+        }
+      }
       Rf[bi][s] = P::f3(rA);
       Qf[bi][s] = P::f3(rM);
       if (!blk_unsafe) {
@@ -320,7 +355,7 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         // the wave have read it (the other slabs' columns are untouched).
         const F3 fb = P::f3(bd);
         P::m33(accA, Rf[bi][s], fb);
-        P::m33(accM, Qf[bi][s], fb);
+        P::m33(accM, fb, Qf[bi][s]);
         st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
         st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
       }
@@ -332,7 +367,7 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       // Overflow-free hierarchical factorisation: the pair (i, j) is split at
       // the highest bit where the in-block indices differ; rows above and
       // columns below the split point are scaled toward it, so every
-      // exponent is <= 0.
+      // exponent is <= 0.  (accM holds the transposed tile, as above.)
 #pragma unroll
       for (int hl = 3; hl >= 0; --hl) {
         const int hh = 1 << hl;
@@ -357,13 +392,14 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
           }
           const F3 fb = P::f3(xb);
           P::m33(tA, P::f3(xa), fb);
-          P::m33(tM, P::f3(xm), fb);
+          P::m33(tM, fb, P::f3(xm));
         }
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) {
           const int il = 4 * q + ii;
-          const int d = il ^ r16;
-          if (il > r16 && (31 - __builtin_clz(d)) == hl) { accA[ii] = tA[ii]; accM[ii] = tM[ii]; }
+          const int hb = 31 - __builtin_clz((il ^ r16) | 1);  // il == r16 selects nothing
+          if (il > r16 && hb == hl) accA[ii] = tA[ii];
+          if (r16 > il && hb == hl) accM[ii] = tM[ii];
         }
       }
 #pragma unroll
@@ -384,13 +420,20 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
       }
     }
+    // diagonal blocks: A (row-major, LDS) and M (fragment-native, rows = token)
+    float mv[4];
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
       const int il = 4 * q + ii, ia = 16 * a + il, ja = 16 * a + r16;
       const bool same = doc[ia] == doc[ja];
-      Adiag[bi][ii] = (il > r16 && same) ? accA[ii] : 0.f;
-      g_M[(int64_t)ia * CH + ja] = (il >= r16 && same) ? accM[ii] : 0.f;
-      if ((a & 1) == 0) g_M[(int64_t)ia * CH + ja + 16] = 0.f;
+      Adiag[bi][ii] = (il > r16 && same) ? accA[ii] : 0.f;   // A[ia][ja]
+      mv[ii] = (r16 >= il && same) ? accM[ii] : 0.f;          // M[ja][ia]
+    }
+    const int mo = fofs(a, a >> 1, l) + 4 * (a & 1);
+    SS::st4s(g_Mh + mo, g_Ml + mo, mv);
+    if ((a & 1) == 0) {
+      const float z[4] = {0.f, 0.f, 0.f, 0.f};
+      SS::st4s(g_Mh + mo + 4, g_Ml + mo + 4, z);
     }
   }
   __syncthreads();
@@ -411,16 +454,18 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= mloc[8 * s + e];
         const F3 fb = P::f3(x);
-        P::m33(accA, Rf[bi][s], fb);
-        P::m33(accM, Qf[bi][s], fb);
+        P::m33(accA, Rf[bi][s], fb);   // A[16a + 4q + ii][16bb + r16]
+        P::m33(accM, fb, Qf[bi][s]);   // M[16a + r16][16bb + 4q + ii]
       }
+      float mv[4];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
-        const bool same = doc[ia] == doc[jb];
-        X[ia * XP + jb] = same ? accA[ii] : 0.f;
-        g_M[(int64_t)ia * CH + jb] = same ? accM[ii] : 0.f;
+        X[ia * XP + jb] = (doc[ia] == doc[jb]) ? accA[ii] : 0.f;
+        mv[ii] = (doc[16 * a + r16] == doc[16 * bb + 4 * q + ii]) ? accM[ii] : 0.f;
       }
+      const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
+      SS::st4s(g_Mh + mo, g_Ml + mo, mv);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         float f[8];
@@ -491,20 +536,26 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     }
     __syncthreads();
   }
+  // T in fragment-native layout: Y (LDS) for W here, global for k_value
+  ST* Ts = reinterpret_cast<ST*>(Y);
+  for (int idx = w; idx < 32; idx += 4) {
+    const int rt = idx >> 2, s = idx & 3;
+    if (s > (rt >> 1)) continue;
+    float x[8];
+    row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
+    SS::st8(Ts + fofs(rt, s, l), x);
+    SS::st8(g_T + fofs(rt, s, l), x);
+  }
+  __syncthreads();
 
-  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tiles w, w+4) ---
+  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tiles 2w, 2w+1) --
+  f32x4 Wc[2][8];
   {
-    f32x4 Wc[2][8];
     F1 Bbe[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const int n = 16 * (w + 4 * nt) + r16;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(g_beT + (int64_t)n * CH + 32 * s, q, x);
-        Bbe[nt][s] = P::f1(x);
-      }
+      for (int s = 0; s < 4; ++s) Bbe[nt][s] = SS::fa(g_be + fofs(2 * w + nt, s, l));
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) Wc[nt][rt] = zero4();
     }
@@ -513,127 +564,148 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s <= rt / 2) {
-          float x[8];
-          row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
-          const F1 fa = P::f1(x);
+          const F1 fa = SS::fa(Ts + fofs(rt, s, l));
           P::m11(Wc[0][rt], fa, Bbe[0][s]);
           P::m11(Wc[1][rt], fa, Bbe[1][s]);
         }
       }
     }
-    F3 W3[2][4];
+  }
+  // W^T fragments (rows = key j, k = token), and their negation
+  F3 W3[2][4], W3n[2][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float x[8] = {Wc[nt][2 * s][0], Wc[nt][2 * s][1], Wc[nt][2 * s][2], Wc[nt][2 * s][3],
-                            Wc[nt][2 * s + 1][0], Wc[nt][2 * s + 1][1], Wc[nt][2 * s + 1][2], Wc[nt][2 * s + 1][3]};
-        W3[nt][s] = P::f3(x);
-      }
-    // rows of ke^T / M are read from the (L2-resident) scratch one step ahead
-    float kx[2][32];
-    auto ld_rows = [&](const float* base, int row, int nslab, float* x) {
+    for (int s = 0; s < 4; ++s) {
+      float x[8] = {Wc[nt][2 * s][0], Wc[nt][2 * s][1], Wc[nt][2 * s][2], Wc[nt][2 * s][3],
+                    Wc[nt][2 * s + 1][0], Wc[nt][2 * s + 1][1], Wc[nt][2 * s + 1][2], Wc[nt][2 * s + 1][3]};
+      W3[nt][s] = P::f3(x);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (s < nslab) row8<float>(base + (int64_t)row * CH + 32 * s, q, x + 8 * s);
-    };
-    ld_rows(g_keT, r16, 4, kx[0]);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m < 7) ld_rows(g_keT, 16 * (m + 1) + r16, 4, kx[(m + 1) & 1]);
-      f32x4 P0 = zero4(), P1 = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const F1 fa = P::f1(kx[m & 1] + 8 * s);
-        P::m11(P0, fa, P::hi(W3[0][s]));
-        P::m11(P1, fa, P::hi(W3[1][s]));
-      }
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int64_t row = (int64_t)(16 * m + 4 * q + ii) * KD;
-        g_Pn[row + 16 * w + r16] = from_f<MT>(-P0[ii]);
-        g_Pn[row + 16 * (w + 4) + r16] = from_f<MT>(-P1[ii]);
-      }
+      for (int e = 0; e < 8; ++e) x[e] = -x[e];
+      W3n[nt][s] = P::f3(x);
     }
-    float qx[2][8];
-    auto ld_qe = [&](int rt, float* x) {
+  // Pn^T tile (keys 32w.., state rows 16m..): lane (c, q) holds
+  // Pn[16m + c][32w + 16nt + 4q + ii] = element 4nt + ii of Pn's fragment
+  auto pn_tile = [&](int m, const F1 (&kb)[4]) {
+    f32x4 P0 = zero4(), P1 = zero4();
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * KD;
-        x[ii] = g_qe[row + 16 * w + r16];
-        x[4 + ii] = g_qe[row + 16 * (w + 4) + r16];
+    for (int s = 0; s < 4; ++s) {
+      P::m11(P0, P::hi(W3[0][s]), kb[s]);
+      P::m11(P1, P::hi(W3[1][s]), kb[s]);
+    }
+    const float x[8] = {-P0[0], -P0[1], -P0[2], -P0[3], -P1[0], -P1[1], -P1[2], -P1[3]};
+    SS::st8(g_Pn + fofs(m, w, l), x);
+  };
+  {
+    F1 kb0[4], kb1[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(g_keh + fofs(0, s, l));
+#pragma unroll 1
+    for (int m = 0; m < 8; m += 2) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kb1[s] = SS::fa(g_keh + fofs(m + 1, s, l));
+      pn_tile(m, kb0);
+      if (m + 2 < 8) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(g_keh + fofs(m + 2, s, l));
       }
-    };
-    ld_rows(g_M, r16, 1, kx[0]);
-    ld_qe(0, qx[0]);
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-      if (rt < 7) {
-        ld_rows(g_M, 16 * (rt + 1) + r16, (rt + 1) / 2 + 1, kx[(rt + 1) & 1]);
-        ld_qe(rt + 1, qx[(rt + 1) & 1]);
-      }
-      f32x4 X0, X1;
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) { X0[ii] = qx[rt & 1][ii]; X1[ii] = qx[rt & 1][4 + ii]; }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s <= rt / 2) {
-          float x[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = -kx[rt & 1][8 * s + e];
-          const F3 fa = P::f3(x);
-          P::m33(X0, fa, W3[0][s]);
-          P::m33(X1, fa, W3[1][s]);
-        }
-      }
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * KD;
-        g_X[row + 16 * w + r16] = X0[ii];
-        g_X[row + 16 * (w + 4) + r16] = X1[ii];
-      }
+      pn_tile(m + 1, kb1);
     }
   }
-
-  // ---- phase 6: U = T (w*v) ; Q = ke^T U ; Oi = M U  (128 value columns per pass)
-  for (int n0 = 0; n0 < p.Vp; n0 += 128) {
-    __syncthreads();
-    {
-      // w*v for 128 tokens x 128 columns, transposed into Y[col][token]
-      const int tok = tid >> 1, half = tid & 1;
-      const int t = tb + tok;
-      const int hv = p.gates_at_hv ? h : h * p.G + n0 / KD;
-      const int hw = vgate_head(p, p.w_h, hv);
-      const bool valid = t < t_end;
-      const int64_t bt = (int64_t)b * p.L + (valid ? t : tb);
-      const TV* vp = (const TV*)p.v + (bt * p.Hv + hv) * KD + 64 * half;
-      const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
-      float vv[64], ww[64];
+  // X^T tile (keys 32w.., tokens 16rt..): lane (c, q) holds
+  // X[16rt + c][32w + 16nt + 4q + ii] = element 4nt + ii of X's fragment
+  auto x_tile = [&](int rt) {
+    const float* qp = g_qe + fofs(rt, w, l);
+    f32x4 X0 = *reinterpret_cast<const f32x4*>(qp);
+    f32x4 X1 = *reinterpret_cast<const f32x4*>(qp + 4);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) ld4<TV>(vp + 4 * j, vv + 4 * j);
-      if (p.w_c == 1) {
-        const float ws = wp[0];
-#pragma unroll
-        for (int j = 0; j < 64; ++j) ww[j] = ws;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) ld4<float>(wp + 64 * half + 4 * j, ww + 4 * j);
+    for (int s = 0; s < 4; ++s) {
+      if (s <= rt / 2) {
+        const F3 mb = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
+        P::m33(X0, W3n[0][s], mb);
+        P::m33(X1, W3n[1][s], mb);
       }
-#pragma unroll
-      for (int j = 0; j < 64; ++j) Y[(64 * half + j) * YP + tok] = valid ? act_w(ww[j], p.fuse) * vv[j] : 0.f;
     }
-    __syncthreads();
-    f32x4 Uc[2][8];
+    const float x[8] = {X0[0], X0[1], X0[2], X0[3], X1[0], X1[1], X1[2], X1[3]};
+    SS::st8s(g_Xh + fofs(rt, w, l), g_Xl + fofs(rt, w, l), x);
+  };
+#pragma unroll 1
+  for (int rt = 0; rt < 8; rt += 2) {
+    x_tile(rt);
+    x_tile(rt + 1);
+  }
+}
+
+// ===========================================================================
+// k_value: U = T (w*v), Q = ke^T U and (M U)^T for one chunk and 128 value
+// columns (one workgroup, 4 waves; wave w owns value tiles 2w, 2w+1).
+// ===========================================================================
+template <bool BF, class TV>
+__global__ __launch_bounds__(256) void k_value(const PF p) {
+  using P = Pol<BF>;
+  using F1 = typename P::F1;
+  using F3 = typename P::F3;
+  using SS = Store<BF>;
+  using ST = typename SS::ST;
+  constexpr int WP = BF ? 136 : 132;   // pitch (elements) of the transposed w*v rows
+  __shared__ ST wvh_s[128 * WP];
+  __shared__ ST wvl_s[BF ? 128 * WP : 1];
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+  int c, pass, zh;
+  xcd_block(c, pass, zh);
+  const int h = zh % p.Hx, b = zh / p.Hx;
+  const int tb = p.t0 + c * CH;
+  const int t_end = min(p.t0 + p.nt, p.L);
+  const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
+  const int64_t uf = u * (CH * KD);
+  const ST* g_T = (const ST*)p.TA + uf;
+  const ST* g_keh = (const ST*)p.KeBh + uf;
+  const ST* g_kel = (const ST*)p.KeBl + uf;
+  const ST* g_Mh = (const ST*)p.MAh + uf;
+  const ST* g_Ml = (const ST*)p.MAl + uf;
+  float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
+  float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
+  ST* wvl = BF ? wvl_s : wvh_s;
+
+  // w*v for 128 tokens x 128 columns, transposed ([column][token]) into LDS
+  {
+    const int tok = tid >> 1, half = tid & 1;
+    const int t = tb + tok;
+    const int hv = p.gates_at_hv ? h : h * p.G + pass;
+    const int hw = vgate_head(p, p.w_h, hv);
+    const bool valid = t < t_end;
+    const int64_t bt = (int64_t)b * p.L + (valid ? t : tb);
+    const TV* vp = (const TV*)p.v + (bt * p.Hv + hv) * KD + 64 * half;
+    const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
+    float vv[64], ww[64];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ld4<TV>(vp + 4 * j, vv + 4 * j);
+    if (p.w_c == 1) {
+      const float ws = wp[0];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) ww[j] = ws;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ld4<float>(wp + 64 * half + 4 * j, ww + 4 * j);
+    }
+    if (p.fuse) {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) ww[j] = sigmoid_fast(ww[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 64; ++j) SS::put(wvh_s, wvl, (64 * half + j) * WP + tok, valid ? ww[j] * vv[j] : 0.f);
+  }
+  __syncthreads();
+
+  f32x4 Uc[2][8];
+  {
     F3 Bwv[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const int col = 16 * (w + 4 * nt) + r16;
+      const int col = 16 * (2 * w + nt) + r16;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(&Y[col * YP + 32 * s], q, x);
-        Bwv[nt][s] = P::f3(x);
-      }
+      for (int s = 0; s < 4; ++s) Bwv[nt][s] = SS::f3(wvh_s + col * WP + 32 * s, wvl + col * WP + 32 * s, q);
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
     }
@@ -642,75 +714,68 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s <= rt / 2) {
-          float x[8];
-          row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
-          const F1 fa = P::f1(x);
+          const F1 fa = SS::fa(g_T + fofs(rt, s, l));
           P::m13(Uc[0][rt], fa, Bwv[0][s]);
           P::m13(Uc[1][rt], fa, Bwv[1][s]);
         }
       }
     }
-    F3 U3[2][4];
+  }
+  // U^T fragments (rows = value column, k = token)
+  F3 U3[2][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float x[8] = {Uc[nt][2 * s][0], Uc[nt][2 * s][1], Uc[nt][2 * s][2], Uc[nt][2 * s][3],
-                            Uc[nt][2 * s + 1][0], Uc[nt][2 * s + 1][1], Uc[nt][2 * s + 1][2], Uc[nt][2 * s + 1][3]};
-        U3[nt][s] = P::f3(x);
-      }
-    const int c0 = n0 + 16 * w + r16, c1 = n0 + 16 * (w + 4) + r16;
-    float kx[2][32];
-    auto ld_rows = [&](const float* base, int row, int nslab, float* x) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (s < nslab) row8<float>(base + (int64_t)row * CH + 32 * s, q, x + 8 * s);
-    };
-    ld_rows(g_keT, r16, 4, kx[0]);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m < 7) ld_rows(g_keT, 16 * (m + 1) + r16, 4, kx[(m + 1) & 1]);
-      else ld_rows(g_M, r16, 1, kx[0]);
-      f32x4 Q0 = zero4(), Q1 = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const F3 fa = P::f3(kx[m & 1] + 8 * s);
-        P::m33(Q0, fa, U3[0][s]);
-        P::m33(Q1, fa, U3[1][s]);
-      }
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int64_t row = (int64_t)(16 * m + 4 * q + ii) * p.Vp;
-        g_Q[row + c0] = Q0[ii];
-        g_Q[row + c1] = Q1[ii];
-      }
+    for (int s = 0; s < 4; ++s) {
+      const float x[8] = {Uc[nt][2 * s][0], Uc[nt][2 * s][1], Uc[nt][2 * s][2], Uc[nt][2 * s][3],
+                          Uc[nt][2 * s + 1][0], Uc[nt][2 * s + 1][1], Uc[nt][2 * s + 1][2], Uc[nt][2 * s + 1][3]};
+      U3[nt][s] = P::f3(x);
     }
-    // two row tiles per iteration (static prefetch buffers) without unrolling
-    // the whole loop, so the scheduler cannot hoist every row's loads at once
-    auto oi_tile = [&](int rt, const float* xcur) {
-      f32x4 O0 = zero4(), O1 = zero4();
+  const int ct0 = 8 * pass + 2 * w;   // value tile of nt = 0 within the execution head
+  // Q tiles (rows = key, columns = value), the chain's accumulator layout
+  auto q_tile = [&](int m, const F3 (&ka)[4]) {
+    f32x4 Q0 = zero4(), Q1 = zero4();
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s <= rt / 2) {
-          const F3 fa = P::f3(xcur + 8 * s);
-          P::m33(O0, fa, U3[0][s]);
-          P::m33(O1, fa, U3[1][s]);
-        }
-      }
+    for (int s = 0; s < 4; ++s) {
+      P::m33(Q0, ka[s], U3[0][s]);
+      P::m33(Q1, ka[s], U3[1][s]);
+    }
+    *reinterpret_cast<f32x4*>(g_Q + cofs(m, ct0, p.nct, l)) = Q0;
+    *reinterpret_cast<f32x4*>(g_Q + cofs(m, ct0 + 1, p.nct, l)) = Q1;
+  };
+  auto ld_ke = [&](int m, F3 (&ka)[4]) {
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int64_t row = (int64_t)(16 * rt + 4 * q + ii) * p.Vp;
-        g_Oi[row + c0] = O0[ii];
-        g_Oi[row + c1] = O1[ii];
-      }
-    };
+    for (int s = 0; s < 4; ++s) ka[s] = SS::fa3(g_keh + fofs(m, s, l), g_kel + fofs(m, s, l));
+  };
+  {
+    F3 kb0[4], kb1[4];
+    ld_ke(0, kb0);
 #pragma unroll 1
-    for (int rt = 0; rt < 8; rt += 2) {
-      ld_rows(g_M, 16 * (rt + 1) + r16, (rt + 1) / 2 + 1, kx[1]);
-      oi_tile(rt, kx[0]);
-      if (rt + 2 < 8) ld_rows(g_M, 16 * (rt + 2) + r16, (rt + 2) / 2 + 1, kx[0]);
-      oi_tile(rt + 1, kx[1]);
+    for (int m = 0; m < 8; m += 2) {
+      ld_ke(m + 1, kb1);
+      q_tile(m, kb0);
+      if (m + 2 < 8) ld_ke(m + 2, kb0);
+      q_tile(m + 1, kb1);
     }
+  }
+  // (M U)^T tiles (rows = value, columns = token), the output kernel's layout
+  auto oi_tile = [&](int rt) {
+    f32x4 O0 = zero4(), O1 = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s <= rt / 2) {
+        const F3 mb = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
+        P::m33(O0, U3[0][s], mb);
+        P::m33(O1, U3[1][s], mb);
+      }
+    }
+    *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0, p.nct, l)) = O0;
+    *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0 + 1, p.nct, l)) = O1;
+  };
+#pragma unroll 1
+  for (int rt = 0; rt < 8; rt += 2) {
+    oi_tile(rt);
+    oi_tile(rt + 1);
   }
 }
 
@@ -718,17 +783,20 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 // k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c.
 // One workgroup per (16-column tile, exec head, batch); wave w owns state rows
 // 32w..32w+31 (fp32, in VGPRs); the full S_c is exchanged through LDS each
-// chunk so that only 8 MFMAs per wave sit on the sequential path.
+// chunk so that only 8 MFMAs per wave sit on the sequential path.  The next
+// chunk's operands load while the current one computes.
 // ===========================================================================
 template <bool BF>
 __global__ __launch_bounds__(256) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
-  using MT = MTy<BF>;
+  using SS = Store<BF>;
+  using ST = typename SS::ST;
   __shared__ float Sx[2][16 * XP];   // S^T of the current chunk, double-buffered
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int ct = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  int ct, h, b;
+  xcd_block(ct, h, b);
   const int n = 16 * ct + r16;
   const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
   const int vcol = n % KD;
@@ -741,50 +809,42 @@ __global__ __launch_bounds__(256) void k_chain(const PF p) {
     for (int ii = 0; ii < 4; ++ii)
       S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
 
-  // operands of chunk c, prefetched one chunk ahead
-  auto load_ops = [&](int c, F1 (&pf)[2][4], f32x4 (&qc)[2], float (&dv)[8], int& is_new, int& same) {
-    const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-    const MT* Pn = (const MT*)p.Pn + u * KD * KD;
-    const float* Qc = p.Q + u * KD * p.Vp;
+  struct Ops {
+    F1 pf[2][4];
+    f32x4 qc[2], dv[2];
+    int is_new, same;
+  };
+  auto load_ops = [&](int c, Ops& o) {
+    const int cc = min(c, p.NCb - 1);
+    const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
+    const ST* Pn = (const ST*)p.PnA + u * (KD * KD);
+    const float* Qc = p.QC + u * (int64_t)(KD * p.Vp);
     const float* dvp = p.dvec + u * KD;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<MT>(Pn + (int64_t)(32 * w + 16 * r + r16) * KD + 32 * s, q, x);
-        pf[r][s] = P::f1(x);
-      }
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) qc[r][ii] = Qc[(int64_t)(32 * w + 16 * r + 4 * q + ii) * p.Vp + n];
-      ld4<float>(dvp + 32 * w + 16 * r + 4 * q, dv + 4 * r);
+      for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
+      o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
+      o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
     }
-    is_new = p.flags[((int64_t)b * p.NCb + c) * 2 + 0];
-    same = p.flags[((int64_t)b * p.NCb + c) * 2 + 1];
+    o.is_new = p.flags[((int64_t)b * p.NCb + cc) * 2 + 0];
+    o.same = p.flags[((int64_t)b * p.NCb + cc) * 2 + 1];
   };
-
-  F1 pf[2][4];
-  f32x4 qc[2];
-  float dv[8];
-  int is_new = 0, same = 0;
-  load_ops(0, pf, qc, dv, is_new, same);
-  for (int c = 0; c < p.NCb; ++c) {
+  auto step = [&](int c, const Ops& o) {
     const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-    if (is_new) { S[0] = zero4(); S[1] = zero4(); }
+    if (o.is_new) { S[0] = zero4(); S[1] = zero4(); }
     float* sx = Sx[c & 1];
-    float* st = p.St + u * (int64_t)p.Vp * KD + (int64_t)n * KD;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float x[4] = {S[r][0], S[r][1], S[r][2], S[r][3]};
       st4<float>(&sx[r16 * XP + 32 * w + 16 * r + 4 * q], x);
-      st4<float>(st + 32 * w + 16 * r + 4 * q, x);
     }
-    // next chunk's operands while this chunk's exchange completes
-    F1 pf_n[2][4];
-    f32x4 qc_n[2];
-    float dv_n[8];
-    int is_new_n = 0, same_n = 0;
-    if (c + 1 < p.NCb) load_ops(c + 1, pf_n, qc_n, dv_n, is_new_n, same_n);
+    {
+      // entry state, as the output kernel's S^T fragment (rows = value column)
+      const int64_t so = u * (int64_t)(p.Vp * KD) + fofs(ct, w, l);
+      const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
+      SS::st8s((ST*)p.StBh + so, (ST*)p.StBl + so, x);
+    }
     lds_barrier();
     F1 Sf[4];
 #pragma unroll
@@ -795,24 +855,22 @@ __global__ __launch_bounds__(256) void k_chain(const PF p) {
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      f32x4 acc = qc[r];
+      f32x4 acc = o.qc[r];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) P::m11(acc, pf[r][s], Sf[s]);
+      for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? dv[4 * r + ii] * S[r][ii] : 0.f);
+      for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (o.same ? o.dv[r][ii] * S[r][ii] : 0.f);
     }
-    if (c + 1 < p.NCb) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) pf[r][s] = pf_n[r][s];
-        qc[r] = qc_n[r];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dv[e] = dv_n[e];
-      is_new = is_new_n;
-      same = same_n;
-    }
+  };
+  Ops o0, o1;
+  load_ops(0, o0);
+#pragma unroll 1
+  for (int c = 0; c < p.NCb; c += 2) {
+    load_ops(c + 1, o1);
+    step(c, o0);
+    if (c + 1 >= p.NCb) break;
+    load_ops(c + 2, o0);
+    step(c + 1, o1);
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r)
@@ -821,79 +879,68 @@ __global__ __launch_bounds__(256) void k_chain(const PF p) {
 }
 
 // ===========================================================================
-// k_output: O_c = X_c S_c + Oi_c  (one workgroup per chunk and 256 value
-// columns; each wave owns 64 columns).  X S is a split-bf16 product in
-// bf16 mode.
+// k_output: O_c^T = S_c^T X_c^T + (M U)^T  (one workgroup per chunk and 256
+// value columns; each wave owns 64 columns).  The transposed product leaves
+// each lane 4 consecutive columns of one token row to store.
 // ===========================================================================
 template <bool BF>
 __global__ __launch_bounds__(256) void k_output(const PF p) {
   using P = Pol<BF>;
   using F3 = typename P::F3;
+  using SS = Store<BF>;
+  using ST = typename SS::ST;
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int c = blockIdx.x, h = blockIdx.y;
-  const int b = blockIdx.z / p.ncg, cg = blockIdx.z % p.ncg;
+  int c, cg, zh;
+  xcd_block(c, cg, zh);
+  const int h = zh % p.Hx, b = zh / p.Hx;
   const int col0 = 256 * cg + 64 * w;
   if (col0 >= p.Vp) return;
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-  const float* Xc = p.X + u * CH * KD;
-  const float* Oi = p.Oi + u * CH * p.Vp;
-  const float* St = p.St + u * (int64_t)p.Vp * KD;
+  const int64_t uf = u * (CH * KD);
+  const ST* Xh = (const ST*)p.XAh + uf;
+  const ST* Xl = (const ST*)p.XAl + uf;
+  const float* Oi = p.OiT + u * (int64_t)(CH * p.Vp);
+  const int64_t so = u * (int64_t)(p.Vp * KD);
+  const ST* Sh = (const ST*)p.StBh + so;
+  const ST* Sl = (const ST*)p.StBl + so;
+  const int ctb = col0 / 16;
 
   F3 Sf[4][4];
-  int ncol[4];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    ncol[ct] = col0 + 16 * ct + r16;
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float x[8];
-      row8<float>(St + (int64_t)ncol[ct] * KD + 32 * s, q, x);
-      Sf[ct][s] = P::f3(x);
-    }
-  }
+    for (int s = 0; s < 4; ++s) Sf[j][s] = SS::fa3(Sh + fofs(ctb + j, s, l), Sl + fofs(ctb + j, s, l));
   const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
   const int vcol0 = col0 % KD;
-  // X rows and Oi tiles of row tile rt+1 are loaded while rt computes
-  float xr[2][32], oi[2][16];
-  auto ld = [&](int rt, float* x, float* o) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) row8<float>(Xc + (int64_t)(16 * rt + r16) * KD + 32 * s, q, x + 8 * s);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) o[4 * ct + ii] = Oi[(int64_t)(16 * rt + 4 * q + ii) * p.Vp + ncol[ct]];
-  };
-  ld(0, xr[0], oi[0]);
-#pragma unroll
-  for (int rt = 0; rt < 8; ++rt) {
-    if (rt < 7) ld(rt + 1, xr[(rt + 1) & 1], oi[(rt + 1) & 1]);
+  auto tile = [&](int rt) {
     f32x4 O[4];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) O[ct][ii] = oi[rt & 1][4 * ct + ii];
+    for (int j = 0; j < 4; ++j) O[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ctb + j, p.nct, l));
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const F3 fa = P::f3(xr[rt & 1] + 8 * s);
+      const F3 xb = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) P::m33(O[ct], fa, Sf[ct][s]);
+      for (int j = 0; j < 4; ++j) P::m33(O[j], Sf[j][s], xb);
     }
+    // lane (c, q) holds O[token 16rt + c][columns 16j + 4q .. 16j + 4q + 3]
+    const int t = tb + 16 * rt + r16;
+    if (t < t_end) {
+      const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol0 + 4 * q;
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int t = tb + 16 * rt + 4 * q + ii;
-      if (t < t_end) {
-        const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol0 + r16;
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const int64_t oi_ = ob + 16 * ct;
-          if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi_] = (bf16)O[ct][ii];
-          else ((float*)p.out)[oi_] = O[ct][ii];
-        }
+      for (int j = 0; j < 4; ++j) {
+        const float x[4] = {O[j][0], O[j][1], O[j][2], O[j][3]};
+        if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob + 16 * j, x);
+        else st4<float>((float*)p.out + ob + 16 * j, x);
       }
     }
+  };
+#pragma unroll 1
+  for (int rt = 0; rt < 8; rt += 2) {
+    tile(rt);
+    tile(rt + 1);
   }
 }
 
@@ -903,28 +950,36 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, Pn, Q, X, Oi, St, beT, keT, Mg, qe, carry, total;
+  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, StBh, StBl, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Split operands (X, St, ke^T, M) have a low-word array in bf16 mode only.
 WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   WsLayout L{};
   const size_t es = bf ? 2 : 4;
+  const size_t ls = bf ? 2 : 0;
   const size_t units = (size_t)a->B * Hx * NCb;
+  const size_t sq = (size_t)CH * KD;   // elements of one 128 x 128 operand
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
   L.flags = take((size_t)a->B * NCb * 2 * 4);
   L.dvec = take(units * KD * 4);
-  L.Pn = take(units * KD * KD * es);
-  L.Q = take(units * KD * Vp * 4);
-  L.X = take(units * CH * KD * 4);
-  L.Oi = take(units * CH * Vp * 4);
-  L.St = take(units * (size_t)Vp * KD * 4);
-  L.beT = take(units * KD * CH * 4);
-  L.keT = take(units * KD * CH * 4);
-  L.Mg = take(units * CH * CH * 4);
-  L.qe = take(units * CH * KD * 4);
+  L.PnA = take(units * sq * es);
+  L.QC = take(units * KD * Vp * 4);
+  L.XAh = take(units * sq * es);
+  L.XAl = take(units * sq * ls);
+  L.OiT = take(units * CH * Vp * 4);
+  L.StBh = take(units * (size_t)Vp * KD * es);
+  L.StBl = take(units * (size_t)Vp * KD * ls);
+  L.BeB = take(units * sq * es);
+  L.KeBh = take(units * sq * es);
+  L.KeBl = take(units * sq * ls);
+  L.MAh = take(units * sq * es);
+  L.MAl = take(units * sq * ls);
+  L.QeA = take(units * sq * 4);
+  L.TA = take(units * sq * es);
   L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
   L.total = off;
   return L;
@@ -973,18 +1028,23 @@ int check_args(const dn_prefill_args* a) {
 template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_prepass<BF, TIn, TV>), dim3(p.NCb, p.Hx, p.B), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.NCb, p.Hx, p.B), dim3(256), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(1, st, false);
-  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.NCb, p.Vp / KD, p.Hx * p.B), dim3(256), 0, st, p);
   prof_mark(1, st, true);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_output<BF>), dim3(p.NCb, p.Hx, p.B * p.ncg), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(256), 0, st, p);
   prof_mark(2, st, true);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  prof_mark(3, st, false);
+  hipLaunchKernelGGL((k_output<BF>), dim3(p.NCb, p.ncg, p.Hx * p.B), dim3(256), 0, st, p);
+  prof_mark(3, st, true);
   return hipGetLastError();
 }
 
@@ -1045,15 +1105,21 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.ncg = (Vp + 255) / 256;
   p.flags = (int32_t*)(ws + Lw.flags);
   p.dvec = (float*)(ws + Lw.dvec);
-  p.Pn = ws + Lw.Pn;
-  p.Q = (float*)(ws + Lw.Q);
-  p.X = (float*)(ws + Lw.X);
-  p.Oi = (float*)(ws + Lw.Oi);
-  p.St = (float*)(ws + Lw.St);
-  p.beT = (float*)(ws + Lw.beT);
-  p.keT = (float*)(ws + Lw.keT);
-  p.Mg = (float*)(ws + Lw.Mg);
-  p.qe = (float*)(ws + Lw.qe);
+  p.nct = Vp / 16;
+  p.PnA = ws + Lw.PnA;
+  p.QC = (float*)(ws + Lw.QC);
+  p.XAh = ws + Lw.XAh;
+  p.XAl = bf ? ws + Lw.XAl : p.XAh;
+  p.OiT = (float*)(ws + Lw.OiT);
+  p.StBh = ws + Lw.StBh;
+  p.StBl = bf ? ws + Lw.StBl : p.StBh;
+  p.BeB = ws + Lw.BeB;
+  p.KeBh = ws + Lw.KeBh;
+  p.KeBl = bf ? ws + Lw.KeBl : p.KeBh;
+  p.MAh = ws + Lw.MAh;
+  p.MAl = bf ? ws + Lw.MAl : p.MAh;
+  p.QeA = (float*)(ws + Lw.QeA);
+  p.TA = ws + Lw.TA;
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
 
   hipStream_t st = (hipStream_t)stream;
