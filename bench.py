@@ -152,15 +152,18 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    _lib.profile_begin()
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    prof = _lib.profile_end()
     ms_step = (t1 - t0) * 1e3 / args.steps
+    # per-kernel durations from HIP events on the launch stream, in a separate
+    # pass (the events themselves add inter-kernel gaps)
+    _lib.profile_begin()
+    for _ in range(args.steps):
+        step()
+    prof = _lib.profile_end()
     tok_s = 2048 / (ms_step * 1e-3)
     kern = {name: (ms / max(n, 1)) for name, (ms, n) in prof.items() if n}
     log(f"prefill: {ms_step * 1e3:.1f} us/step; kernels (us): " +

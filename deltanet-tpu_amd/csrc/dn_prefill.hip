@@ -613,26 +613,42 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     }
   }
   // X^T tile (keys 32w.., tokens 16rt..): lane (c, q) holds
-  // X[16rt + c][32w + 16nt + 4q + ii] = element 4nt + ii of X's fragment
-  auto x_tile = [&](int rt) {
+  // X[16rt + c][32w + 16nt + 4q + ii] = element 4nt + ii of X's fragment.
+  // Operands of tile rt + 1 load while tile rt computes.
+  struct XOps {
+    f32x4 q0, q1;
+    F3 m[4];
+  };
+  auto ld_x = [&](int rt, XOps& o) {
     const float* qp = g_qe + fofs(rt, w, l);
-    f32x4 X0 = *reinterpret_cast<const f32x4*>(qp);
-    f32x4 X1 = *reinterpret_cast<const f32x4*>(qp + 4);
+    o.q0 = *reinterpret_cast<const f32x4*>(qp);
+    o.q1 = *reinterpret_cast<const f32x4*>(qp + 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      if (s <= rt / 2) o.m[s] = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
+  };
+  auto x_tile = [&](int rt, const XOps& o) {
+    f32x4 X0 = o.q0, X1 = o.q1;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s <= rt / 2) {
-        const F3 mb = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
-        P::m33(X0, W3n[0][s], mb);
-        P::m33(X1, W3n[1][s], mb);
+        P::m33(X0, W3n[0][s], o.m[s]);
+        P::m33(X1, W3n[1][s], o.m[s]);
       }
     }
     const float x[8] = {X0[0], X0[1], X0[2], X0[3], X1[0], X1[1], X1[2], X1[3]};
     SS::st8s(g_Xh + fofs(rt, w, l), g_Xl + fofs(rt, w, l), x);
   };
+  {
+    XOps xa, xb;
+    ld_x(0, xa);
 #pragma unroll 1
-  for (int rt = 0; rt < 8; rt += 2) {
-    x_tile(rt);
-    x_tile(rt + 1);
+    for (int rt = 0; rt < 8; rt += 2) {
+      ld_x(rt + 1, xb);
+      x_tile(rt, xa);
+      if (rt + 2 < 8) ld_x(rt + 2, xa);
+      x_tile(rt + 1, xb);
+    }
   }
 }
 
@@ -647,9 +663,6 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
   using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
-  constexpr int WP = BF ? 136 : 132;   // pitch (elements) of the transposed w*v rows
-  __shared__ ST wvh_s[128 * WP];
-  __shared__ ST wvl_s[BF ? 128 * WP : 1];
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
   int c, pass, zh;
@@ -666,58 +679,75 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
   const ST* g_Ml = (const ST*)p.MAl + uf;
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
-  ST* wvl = BF ? wvl_s : wvh_s;
 
-  // w*v for 128 tokens x 128 columns, transposed ([column][token]) into LDS
+  // (w*v)^T fragments of this wave's 32 value columns (rows = column, k =
+  // token): each 16-token block is loaded row-wise and transposed by an
+  // identity product into half of a slab.
+  F3 Bwv[2][4];
   {
-    const int tok = tid >> 1, half = tid & 1;
-    const int t = tb + tok;
     const int hv = p.gates_at_hv ? h : h * p.G + pass;
     const int hw = vgate_head(p, p.w_h, hv);
-    const bool valid = t < t_end;
-    const int64_t bt = (int64_t)b * p.L + (valid ? t : tb);
-    const TV* vp = (const TV*)p.v + (bt * p.Hv + hv) * KD + 64 * half;
-    const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
-    float vv[64], ww[64];
+    float vv[8][8], ww[8][8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ld4<TV>(vp + 4 * j, vv + 4 * j);
-    if (p.w_c == 1) {
-      const float ws = wp[0];
+    for (int a = 0; a < 8; ++a) {
+      const int t = tb + 16 * a + r16;
+      const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
+      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + 32 * w, q, vv[a]);
+      const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
+      if (p.w_c == 1) {
+        const float ws = wp[0];
 #pragma unroll
-      for (int j = 0; j < 64; ++j) ww[j] = ws;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) ld4<float>(wp + 64 * half + 4 * j, ww + 4 * j);
+        for (int e = 0; e < 8; ++e) ww[a][e] = ws;
+      } else {
+        row8<float>(wp + 32 * w, q, ww[a]);
+      }
     }
-    if (p.fuse) {
+    const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
 #pragma unroll
-      for (int j = 0; j < 64; ++j) ww[j] = sigmoid_fast(ww[j]);
-    }
+    for (int a = 0; a < 8; ++a) {
+      const bool valid = tb + 16 * a + r16 < t_end;
+      float x[8];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) SS::put(wvh_s, wvl, (64 * half + j) * WP + tok, valid ? ww[j] * vv[j] : 0.f);
-  }
-  __syncthreads();
-
-  f32x4 Uc[2][8];
-  {
-    F3 Bwv[2][4];
+      for (int e = 0; e < 8; ++e) {
+        const float wg = p.fuse ? sigmoid_fast(ww[a][e]) : ww[a][e];
+        x[e] = valid ? wg * vv[a][e] : 0.f;
+      }
+      const F3 fx = P::f3(x);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = 16 * (2 * w + nt) + r16;
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x4 chi = zero4();
+        mma(chi, P::hi(fx), nt ? id1 : id0);
+        // lane (c, q): column 16nt + c, tokens 16a + 4q + ii -> slab a/2, half a&1
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Bwv[nt][s] = SS::f3(wvh_s + col * WP + 32 * s, wvl + col * WP + 32 * s, q);
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
-    }
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s <= rt / 2) {
-          const F1 fa = SS::fa(g_T + fofs(rt, s, l));
-          P::m13(Uc[0][rt], fa, Bwv[0][s]);
-          P::m13(Uc[1][rt], fa, Bwv[1][s]);
+        for (int ii = 0; ii < 4; ++ii) {
+          if constexpr (BF) {
+            Bwv[nt][a >> 1].hi.v[4 * (a & 1) + ii] = (bf16)chi[ii];
+          } else {
+            Bwv[nt][a >> 1].v[4 * (a & 1) + ii] = chi[ii];
+          }
         }
+        if constexpr (BF) {
+          f32x4 clo = zero4();
+          mma(clo, fx.lo, nt ? id1 : id0);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) Bwv[nt][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)clo[ii];
+        }
+      }
+    }
+  }
+  f32x4 Uc[2][8];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s <= rt / 2) {
+        const F1 fa = SS::fa(g_T + fofs(rt, s, l));
+        P::m13(Uc[0][rt], fa, Bwv[0][s]);
+        P::m13(Uc[1][rt], fa, Bwv[1][s]);
       }
     }
   }
@@ -759,23 +789,36 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
     }
   }
   // (M U)^T tiles (rows = value, columns = token), the output kernel's layout
-  auto oi_tile = [&](int rt) {
+  struct MOps {
+    F3 m[4];
+  };
+  auto ld_m = [&](int rt, MOps& o) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      if (s <= rt / 2) o.m[s] = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
+  };
+  auto oi_tile = [&](int rt, const MOps& o) {
     f32x4 O0 = zero4(), O1 = zero4();
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s <= rt / 2) {
-        const F3 mb = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
-        P::m33(O0, U3[0][s], mb);
-        P::m33(O1, U3[1][s], mb);
+        P::m33(O0, U3[0][s], o.m[s]);
+        P::m33(O1, U3[1][s], o.m[s]);
       }
     }
     *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0, p.nct, l)) = O0;
     *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0 + 1, p.nct, l)) = O1;
   };
+  {
+    MOps ma, mb;
+    ld_m(0, ma);
 #pragma unroll 1
-  for (int rt = 0; rt < 8; rt += 2) {
-    oi_tile(rt);
-    oi_tile(rt + 1);
+    for (int rt = 0; rt < 8; rt += 2) {
+      ld_m(rt + 1, mb);
+      oi_tile(rt, ma);
+      if (rt + 2 < 8) ld_m(rt + 2, ma);
+      oi_tile(rt + 1, mb);
+    }
   }
 }
 
@@ -915,16 +958,25 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
     for (int s = 0; s < 4; ++s) Sf[j][s] = SS::fa3(Sh + fofs(ctb + j, s, l), Sl + fofs(ctb + j, s, l));
   const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
   const int vcol0 = col0 % KD;
-  auto tile = [&](int rt) {
+  // operands of row tile rt + 1 load while rt computes
+  struct OOps {
+    f32x4 o[4];
+    F3 x[4];
+  };
+  auto ld = [&](int rt, OOps& o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.o[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ctb + j, p.nct, l));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) o.x[s] = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
+  };
+  auto tile = [&](int rt, const OOps& o) {
     f32x4 O[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) O[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ctb + j, p.nct, l));
+    for (int j = 0; j < 4; ++j) O[j] = o.o[j];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const F3 xb = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) P::m33(O[j], Sf[j][s], xb);
-    }
+      for (int j = 0; j < 4; ++j) P::m33(O[j], Sf[j][s], o.x[s]);
     // lane (c, q) holds O[token 16rt + c][columns 16j + 4q .. 16j + 4q + 3]
     const int t = tb + 16 * rt + r16;
     if (t < t_end) {
@@ -937,10 +989,14 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
       }
     }
   };
+  OOps oa, ob;
+  ld(0, oa);
 #pragma unroll 1
   for (int rt = 0; rt < 8; rt += 2) {
-    tile(rt);
-    tile(rt + 1);
+    ld(rt + 1, ob);
+    tile(rt, oa);
+    if (rt + 2 < 8) ld(rt + 2, oa);
+    tile(rt + 1, ob);
   }
 }
 
