@@ -220,12 +220,22 @@ def main():
                    "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"decode {sd}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[sd]['state_GBps']} GB/s)")
 
+    copy_gbps = None
     if args.copy_calibration:
-        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        # a plain device copy of the decode state's size: the practical
+        # read + write HBM rate the decode step is compared against
+        src = torch.empty(256 * 32 * 128 * 128, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
-        for _ in range(3):
+        for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(50):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 50
+        copy_gbps = round(2 * src.numel() * 4 / dt / 1e9, 1)
+        log(f"device copy of {src.numel() * 4 >> 20} MiB: {dt * 1e6:.1f} us, {copy_gbps} GB/s (read + write)")
 
     cpu = None
     if not args.no_cpu_baseline:

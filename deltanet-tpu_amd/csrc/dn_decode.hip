@@ -80,115 +80,169 @@ __device__ __forceinline__ int dgate_head(int H, int Hk, int Hv, int hv, int G) 
   return (H == Hv) ? hv : hv / G;
 }
 
-// sum over the 512 lanes of the workgroup; `buf` holds 8 floats
-__device__ __forceinline__ float block_sum512(float x, float* buf) {
+// sum over the 256 lanes of the workgroup; `buf` holds 4 floats
+__device__ __forceinline__ float block_sum256(float x, float* buf) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
   const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) buf[w] = x;
   __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) t += buf[i];
-  return t;
+  return buf[0] + buf[1] + buf[2] + buf[3];
 }
 
-template <class TS> __device__ __forceinline__ void ld_row4(const TS* p, float* o) { ld4<TS>(p, o); }
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
 
+// 8 consecutive state elements (16 bytes for bf16, 32 for fp32)
+template <class T> __device__ __forceinline__ void ld8(const T* p, float* o);
+template <> __device__ __forceinline__ void ld8<float>(const float* p, float* o) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { o[e] = a[e]; o[4 + e] = b[e]; }
+}
+template <> __device__ __forceinline__ void ld8<bf16>(const bf16* p, float* o) {
+  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (float)a[e];
+}
+template <class T> __device__ __forceinline__ void st8(T* p, const float* x);
+template <> __device__ __forceinline__ void st8<float>(float* p, const float* x) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+}
+template <> __device__ __forceinline__ void st8<bf16>(bf16* p, const float* x) {
+  bf16x8 h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = (bf16)x[e];
+  *reinterpret_cast<bf16x8*>(p) = h;
+}
+
+// One workgroup (4 waves) per (batch row, value head).  Lane (rg, cg) holds
+// state rows 8rg..8rg+7 and 8 columns: 8cg..8cg+7 for a bf16 state (one
+// 16-byte load per row), 4cg..4cg+3 and 64+4cg..64+4cg+3 for an fp32 state
+// (two 16-byte loads that each cover 256 contiguous bytes of the row).  Every global load (state, q, k,
+// gates, v) is issued at entry so their latencies overlap; the column sums
+// reduce inside each wave by shuffles, then across the 4 waves through LDS.
+// Small workgroups let several state matrices stream through a CU at once.
 template <class TSin, class TSout>
-__global__ __launch_bounds__(512) void k_decode(const DP p) {
-  constexpr int K = 128, V = 128;
+__global__ __launch_bounds__(256) void k_decode(const DP p) {
+  constexpr int K = 128, V = 128, R = 8;   // rows per lane
   __shared__ float qn[K], kn[K], dd[K], bt[K], vn[V];
-  __shared__ float red[2][16][V];
-  __shared__ float rbuf[8];
+  __shared__ float red[2][4][V];
+  __shared__ float rbuf[3][2];
+  __shared__ float gbuf[4];
 
   const int tid = threadIdx.x;
-  const int cg = tid & 31, rg = tid >> 5;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int cg = tid & 15, rg = tid >> 4;
   const int bh = blockIdx.x;
   const int bb = bh / p.Hv, hv = bh % p.Hv;
   const int hk = hv / p.G;
   const bool rst = p.reset != nullptr && p.reset[bb] != 0;
   const int64_t sbase = (int64_t)bh * K * V;
 
-  // issue the state loads first: 8 rows x 4 columns per lane
-  float S[8][4];
+  constexpr bool kSplit = sizeof(TSin) == 4;
+  auto col = [&](int e) { return kSplit ? ((e < 4) ? 4 * cg + e : 60 + 4 * cg + e) : 8 * cg + e; };
+  float S[R][8];
   const TSin* sp = (const TSin*)p.sin + sbase;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int r = 0; r < R; ++r) {
     if (!rst) {
-      ld_row4<TSin>(sp + (int64_t)(8 * rg + r) * V + 4 * cg, S[r]);
+      if constexpr (kSplit) {
+        ld4<TSin>(sp + (R * rg + r) * V + 4 * cg, S[r]);
+        ld4<TSin>(sp + (R * rg + r) * V + 64 + 4 * cg, S[r] + 4);
+      } else {
+        ld8<TSin>(sp + (R * rg + r) * V + 8 * cg, S[r]);
+      }
     } else {
-      S[r][0] = S[r][1] = S[r][2] = S[r][3] = 0.f;
-    }
-  }
-
-  // q / k normalisation (lanes 0-127: q, 128-255: k), gates
-  float x = 0.f;
-  if (tid < 256) {
-    const int i = tid & 127;
-    const void* src = tid < 128 ? p.q : p.k;
-    x = ld_f(src, ((int64_t)bb * p.Hk + hk) * K + i, p.qk_dt);
-  }
-  float sq = x * x;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
-  if ((tid & 63) == 0 && tid < 256) rbuf[tid >> 6] = sq;
-  __syncthreads();
-  if (tid < 256) {
-    const int i = tid & 127;
-    const float ss = tid < 128 ? rbuf[0] + rbuf[1] : rbuf[2] + rbuf[3];
-    float y;
-    if (p.l2norm) {
-      y = x / sqrtf(ss + 1e-6f);
-      if (tid < 128) y *= p.scale;
-    } else {
-      y = tid < 128 ? x * p.scale : x;
+      for (int e = 0; e < 8; ++e) S[r][e] = 0.f;
     }
-    if (tid < 128) qn[i] = y; else kn[i] = y;
   }
-  __syncthreads();
-  if (tid < K) {
+  // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v
+  float xq = 0.f, xk = 0.f, gv = 0.f, bv = 0.f, wv = 0.f, vv = 0.f;
+  if (tid < 128) {
     const int i = tid;
+    const int64_t qo = ((int64_t)bb * p.Hk + hk) * K + i;
+    xq = ld_f(p.q, qo, p.qk_dt);
+    xk = ld_f(p.k, qo, p.qk_dt);
     const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
     const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
-    float gv = ld_f(p.g, ((int64_t)bb * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
-    float bv = ld_f(p.b, ((int64_t)bb * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
-    gv = fminf(gv, 0.f);
-    if (p.guard) { bv = fmaxf(bv, 0.f); gv = fminf(gv, -1e-6f); }
-    dd[i] = __expf(gv);
-    bt[i] = bv * kn[i];
+    const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+    gv = ld_f(p.g, ((int64_t)bb * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
+    bv = ld_f(p.b, ((int64_t)bb * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
+    wv = ld_f(p.w, ((int64_t)bb * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
+    vv = ld_f(p.v, ((int64_t)bb * p.Hv + hv) * V + i, p.v_dt);
   }
-  float qk_part = (tid < K) ? qn[tid] * kn[tid] : 0.f;
-  const float qk = block_sum512(qk_part, rbuf);
+  {
+    const float sq = wave_sum(xq * xq), sk = wave_sum(xk * xk);
+    if (lane == 0 && wid < 2) { rbuf[0][wid] = sq; rbuf[1][wid] = sk; }
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const int i = tid;
+    float yq, yk;
+    if (p.l2norm) {
+      yq = xq / sqrtf(rbuf[0][0] + rbuf[0][1] + 1e-6f) * p.scale;
+      yk = xk / sqrtf(rbuf[1][0] + rbuf[1][1] + 1e-6f);
+    } else {
+      yq = xq * p.scale;
+      yk = xk;
+    }
+    float g_ = fminf(gv, 0.f);
+    float b_ = bv;
+    if (p.guard) { b_ = fmaxf(b_, 0.f); g_ = fminf(g_, -1e-6f); }
+    qn[i] = yq;
+    kn[i] = yk;
+    dd[i] = __expf(g_);
+    bt[i] = b_ * yk;
+    const float qk = wave_sum(yq * yk);
+    if (lane == 0) rbuf[2][wid] = qk;
+  }
+  __syncthreads();
+  const float qk = rbuf[2][0] + rbuf[2][1];
 
-  // partial column sums over this lane's 8 rows
-  float pa[4] = {0.f, 0.f, 0.f, 0.f}, pc[4] = {0.f, 0.f, 0.f, 0.f};
+  // decay, then this lane's partial column sums of b k^T S and q^T S
+  float pa[8], pc[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int i = 8 * rg + r;
-    const float di = dd[i];
+  for (int e = 0; e < 8; ++e) { pa[e] = 0.f; pc[e] = 0.f; }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      S[r][j] *= di;
-      pa[j] += bt[i] * S[r][j];
-      pc[j] += qn[i] * S[r][j];
+  for (int r = 0; r < R; ++r) {
+    const int i = R * rg + r;
+    const float di = dd[i], bi = bt[i], qi = qn[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      S[r][e] *= di;
+      pa[e] += bi * S[r][e];
+      pc[e] += qi * S[r][e];
     }
   }
+  // the 4 row groups of a wave differ in lane bits 4 and 5
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    red[0][rg][4 * cg + j] = pa[j];
-    red[1][rg][4 * cg + j] = pc[j];
+  for (int e = 0; e < 8; ++e) {
+    pa[e] += __shfl_xor(pa[e], 16);
+    pa[e] += __shfl_xor(pa[e], 32);
+    pc[e] += __shfl_xor(pc[e], 16);
+    pc[e] += __shfl_xor(pc[e], 32);
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      red[0][wid][col(e)] = pa[e];
+      red[1][wid][col(e)] = pc[e];
+    }
   }
   __syncthreads();
   if (tid < V) {
     const int j = tid;
     float A = 0.f, Cc = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { A += red[0][r][j]; Cc += red[1][r][j]; }
-    const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
-    const float wv = ld_f(p.w, ((int64_t)bb * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : j), p.w_dt);
-    const float vv = ld_f(p.v, ((int64_t)bb * p.Hv + hv) * V + j, p.v_dt);
+    for (int r = 0; r < 4; ++r) { A += red[0][r][j]; Cc += red[1][r][j]; }
     const float nv = wv * vv - A;
     vn[j] = nv;
     const float o = Cc + qk * nv;
@@ -198,26 +252,36 @@ __global__ __launch_bounds__(512) void k_decode(const DP p) {
     else ((float*)p.out)[oi] = o;
   }
   __syncthreads();
+  float vc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vc[e] = vn[col(e)];
   float ss = 0.f;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float ki = kn[8 * rg + r];
+  for (int r = 0; r < R; ++r) {
+    const float ki = kn[R * rg + r];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      S[r][j] += ki * vn[4 * cg + j];
-      ss += S[r][j] * S[r][j];
+    for (int e = 0; e < 8; ++e) {
+      S[r][e] += ki * vc[e];
+      ss += S[r][e] * S[r][e];
     }
   }
   float fac = 1.f;
   if (p.guard) {
-    const float tot = block_sum512(ss, rbuf);
+    const float tot = block_sum256(ss, gbuf);
     fac = fminf(1.f, p.tau / sqrtf(tot + 1e-6f));
   }
   TSout* op = (TSout*)p.sout + sbase;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    float y[4] = {S[r][0] * fac, S[r][1] * fac, S[r][2] * fac, S[r][3] * fac};
-    st4<TSout>(op + (int64_t)(8 * rg + r) * V + 4 * cg, y);
+  for (int r = 0; r < R; ++r) {
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = S[r][e] * fac;
+    if constexpr (kSplit) {
+      st4<TSout>(op + (R * rg + r) * V + 4 * cg, y);
+      st4<TSout>(op + (R * rg + r) * V + 64 + 4 * cg, y + 4);
+    } else {
+      st8<TSout>(op + (R * rg + r) * V + 8 * cg, y);
+    }
   }
 }
 
@@ -301,10 +365,10 @@ extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
   prof_mark(4, st, false);
-  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(512), 0, st, p);
-  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(512), 0, st, p);
-  else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(512), 0, st, p);
-  else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(512), 0, st, p);
+  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(256), 0, st, p);
+  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(256), 0, st, p);
+  else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(256), 0, st, p);
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
