@@ -121,7 +121,96 @@ def cpu_baseline(max_seconds=20.0):
                       f"(oracle/gdn_serial.c, OpenMP over 24 (batch, value-head) chains), {dt:.1f} s"}
 
 
+PROFILE_DIR = os.path.join(ROOT, "profiles")
+TRAFFIC_JSON = os.path.join(PROFILE_DIR, "pmc_traffic_cfg2_cfg4.json")
+KT_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --stats "
+          "--output-format csv -d gpurun_out/kt -o run -- python3 bench.py --no-cpu-baseline --steps 50 "
+          "--warmup 5 --decode-steps 16 --copy-calibration")
+PMC_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --pmc {ctr} --output-format csv "
+           "-d gpurun_out/{d} -o run -- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1 "
+           "--decode-steps 2 --copy-calibration")
+COPY_BYTES = 256 * 32 * 128 * 128 * 4   # the --copy-calibration copy (read and write this many bytes)
+
+
+def _kname(n):
+    if "copyBuffer" in n:
+        return "copy (calibration)"
+    for k in ("k_prepass", "k_value", "k_chain", "k_output", "k_decode", "k_frob_cap"):
+        if k in n:
+            if k == "k_decode":
+                return "k_decode<bf16>" if ("DF16b" in n or "bf16" in n) else "k_decode<f32>"
+            return k
+    return None
+
+
+def rocprof_summary(kt_dir, f_dir, w_dir):
+    """Summarise rocprofv3 CSV output of the KT_CMD / PMC_CMD runs into
+    profiles/ (text for readers, JSON for bench.py's roofline.traffic)."""
+    import csv
+    import collections
+
+    os.makedirs(PROFILE_DIR, exist_ok=True)
+    dur = collections.defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))):
+        k = _kname(r["Kernel_Name"])
+        if k:
+            dur[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    dur["copy (calibration)"] = [x for x in dur["copy (calibration)"] if x > 0.5 * max(dur["copy (calibration)"])]
+    ctr = {}
+    for d, name in ((f_dir, "FETCH_SIZE"), (w_dir, "WRITE_SIZE")):
+        acc = collections.defaultdict(list)
+        for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
+            k = _kname(r["Kernel_Name"])
+            if k and r["Counter_Name"] == name:
+                acc[k].append(float(r["Counter_Value"]) * 1024.0)   # KiB -> bytes
+        # the calibration copy is the large one (torch issues small copies too)
+        acc["copy (calibration)"] = [x for x in acc["copy (calibration)"] if x > 0.5 * max(acc["copy (calibration)"])]
+        ctr[name] = {k: sum(v) / len(v) for k, v in acc.items()}
+    f_scale = COPY_BYTES / ctr["FETCH_SIZE"]["copy (calibration)"]
+    w_scale = COPY_BYTES / ctr["WRITE_SIZE"]["copy (calibration)"]
+    work = prefill_work()
+    out = {"fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
+    lines = ["# rocprofv3 kernel trace + PMC traffic, bench.py workload (prefill BASELINE config 2, "
+             "decode config 4)", "",
+             "Kernel durations from:", "    " + KT_CMD, "",
+             "HBM traffic per dispatch from two counter runs:",
+             "    " + PMC_CMD.format(ctr="FETCH_SIZE", d="pmc_f"),
+             "    " + PMC_CMD.format(ctr="WRITE_SIZE", d="pmc_w"),
+             "summarised by:", "    python bench.py --rocprof-summary gpurun_out/kt gpurun_out/pmc_f gpurun_out/pmc_w", "",
+             f"Calibration: a plain {COPY_BYTES >> 20} MiB device copy reads FETCH_SIZE x {f_scale:.3f} and "
+             f"writes WRITE_SIZE x {w_scale:.3f} bytes; both factors are applied below.", "",
+             "| kernel | dispatches | avg us | min us | max us | fetch MB | write MB | algorithmic MB | "
+             "traffic / algorithmic |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    alg = {"k_prepass": work["prepass"]["bytes"], "k_value": work["value"]["bytes"],
+           "k_chain": work["chain"]["bytes"], "k_output": work["output"]["bytes"],
+           "k_decode<f32>": 2 * 256 * 32 * 128 * 128 * 4, "k_decode<bf16>": 2 * 256 * 32 * 128 * 128 * 2,
+           "copy (calibration)": 2 * COPY_BYTES}
+    for k in ("k_prepass", "k_value", "k_chain", "k_output", "k_decode<f32>", "k_decode<bf16>",
+              "copy (calibration)"):
+        if k not in dur:
+            continue
+        v = dur[k]
+        fb = ctr["FETCH_SIZE"].get(k, float("nan")) * f_scale
+        wb = ctr["WRITE_SIZE"].get(k, float("nan")) * w_scale
+        out["kernels"][k] = {"avg_us": sum(v) / len(v), "fetch_bytes": fb, "write_bytes": wb,
+                             "traffic_bytes": fb + wb, "algorithmic_bytes": alg.get(k)}
+        lines.append(f"| {k} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                     f"{fb / 1e6:.1f} | {wb / 1e6:.1f} | {alg.get(k, 0) / 1e6:.1f} | "
+                     f"{(fb + wb) / alg[k]:.2f} |")
+    lines += ["", "Prefill intermediates (workspace) travel between the four launches; their round trips "
+              "are the traffic above the algorithmic bytes."]
+    with open(os.path.join(PROFILE_DIR, "prefill_cfg2_decode_cfg4_rocprof.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(out, f, indent=1)
+    print("\n".join(lines))
+
+
 def main():
+    if len(sys.argv) == 5 and sys.argv[1] == "--rocprof-summary":
+        rocprof_summary(*sys.argv[2:5])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -184,6 +273,12 @@ def main():
     roof["kernel"] = f"k_{dom}"
     roof["avg_launch_us"] = kern[dom] * 1e3
     roof["traffic"] = None
+    if os.path.exists(TRAFFIC_JSON):
+        # HBM bytes per launch from the committed rocprofv3 --pmc summary
+        t = json.load(open(TRAFFIC_JSON)).get("kernels", {}).get(roof["kernel"])
+        if t:
+            roof["traffic"] = round(t["traffic_bytes"])
+            roof["traffic_source"] = os.path.relpath(TRAFFIC_JSON, ROOT)
 
     # whole-step roofline (HBM-bound at this arithmetic intensity)
     t_roof = max(work["bytes_total"] / (PEAK_HBM_GBPS * 1e9), work["flops_total"] / (PEAK_BF16_TFLOPS * 1e12))
