@@ -81,7 +81,7 @@ __device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
 // X^T); (b k e^Lambda)^T and ke^T are transposed by an identity product.
 // ===========================================================================
 template <bool BF, class TIn>
-__global__ __launch_bounds__(256) void k_prepass(const PF p) {
+__global__ __launch_bounds__(512) void k_prepass(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
@@ -159,31 +159,31 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 
   // ---- phase 1: block-local Lambda (double-float: X = hi, Y = lo), totals --
   {
-    const int kap = tid & 127, half = tid >> 7;
+    const int kap = tid & 127, part = tid >> 7;   // 4 parts of 32 tokens
     const int hg = kgate_head(p, p.g_h, h);
-    const int tbase = tb + 64 * half;
-    const int nvalid = t_end - tbase;  // tokens of this half inside the range (may be <= 0)
+    const int tbase = tb + 32 * part;
+    const int nvalid = t_end - tbase;  // tokens of this part inside the range (may be <= 0)
     const int tload = min(tbase, t_end - 1);
     const int nload = t_end - tload;   // >= 1
     const int gstride = p.g_h * p.g_c;
     const float* gp = (const float*)p.g + (((int64_t)b * p.L + tload) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
-    // all 64 loads issued back to back; out-of-range tokens read the last
+    // all 32 loads issued back to back; out-of-range tokens read the last
     // valid token and are zeroed below
-    float gl[64];
+    float gl[32];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) gl[i] = gp[min(i, nload - 1) * gstride];
+    for (int i = 0; i < 32; ++i) gl[i] = gp[min(i, nload - 1) * gstride];
     if (p.fuse) {
 #pragma unroll
-      for (int i = 0; i < 64; ++i) gl[i] = -__expf(fminf(gl[i], 5.f));
+      for (int i = 0; i < 32; ++i) gl[i] = -__expf(fminf(gl[i], 5.f));
     } else {
 #pragma unroll
-      for (int i = 0; i < 64; ++i) gl[i] = fminf(gl[i], 0.f);  // _nonpositive (NaN -> 0)
+      for (int i = 0; i < 32; ++i) gl[i] = fminf(gl[i], 0.f);  // _nonpositive (NaN -> 0)
     }
     const float gmax = p.guard ? -1e-6f : 0.f;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) gl[i] = (i < nvalid) ? fminf(gl[i], gmax) : 0.f;
+    for (int i = 0; i < 32; ++i) gl[i] = (i < nvalid) ? fminf(gl[i], gmax) : 0.f;
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
+    for (int blk = 0; blk < 2; ++blk) {
       float hi = 0.f, lo = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
         hi = sum;
         const float ph = hi * kLog2e;
         const float pe = fmaf(hi, kLog2e, -ph);
-        const int row = 64 * half + 16 * blk + j;
+        const int row = 32 * part + 16 * blk + j;
         X[row * XP + kap] = ph;
         Y[row * XP + kap] = pe + lo * kLog2e;
       }
@@ -228,12 +228,12 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   __syncthreads();
 
   // ---- phase 2: per-row quantities, diagonal A/M blocks --------------------
-  F3 Rf[2][4], Qf[2][4];
-  f32x4 Adiag[2];
+  F3 Rf[1][4], Qf[1][4];
+  f32x4 Adiag[1];
   const int hbg = kgate_head(p, p.b_h, h);
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi) {
-    const int a = bi == 0 ? w : 7 - w;
+  for (int bi = 0; bi < 1; ++bi) {
+    const int a = w;
     const int i = 16 * a + r16;
     const int t = tb + i;
     const bool valid = t < t_end;
@@ -291,78 +291,15 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     const bool first = doc[i] == 0;
     const bool last = doc[i] == doc[CH - 1];
     const bool blk_unsafe = unsafe_part[0][a] | unsafe_part[1][a];
-    float dq = 0.f;
     // accA: A tile (lane = column token); accM: M^T tile (lane = row token)
     f32x4 accA = zero4(), accM = zero4();
+    float dq = 0.f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float lam[8], lsa[8], ta[8], laml[8], lsal[8], tal[8], off[8], suf[8];
-      row8<float>(&X[i * XP + 32 * s], q, lam);
-      row8<float>(&X[(16 * a) * XP + 32 * s], q, lsa);
-      row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
-      row8<float>(&Y[i * XP + 32 * s], q, laml);
-      row8<float>(&Y[(16 * a) * XP + 32 * s], q, lsal);
-      row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
-      row8<float>(&Off[a * KD + 32 * s], q, off);
-      row8<float>(&Suf[a * KD + 32 * s], q, suf);
-      float rA[8], rM[8], bd[8], kc[8], qe[8], bt[8], kt[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
-        const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
-        const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
-        const float er = fast_exp2(d_i_sa);
-        rA[e] = be * er;
-        rM[e] = qh * er;
-        kc[e] = kh * fast_exp2(d_ea_i);
-        const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
-        bt[e] = first ? be * eL : 0.f;
-        kt[e] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
-        bd[e] = kh * fast_exp2(-d_i_sa);
-        dq += qh * kh;
-        qe[e] = first ? qh * eL : 0.f;
-      }
-      Store<false>::st8(g_qe + fofs(a, s, l), qe);
-      {
-        // (b k e^Lambda)^T and ke^T in fragment layout (row = key, k = token)
-        const F1 fbt = P::f1(bt);
-        const F3 fkt = P::f3(kt);
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const F1 id = ident_frag<BF>(hf, r16, q);
-          f32x4 cb = zero4(), chi = zero4();
-          mma(cb, fbt, id);
-          mma(chi, P::hi(fkt), id);
-          const int o = fofs(2 * s + hf, a >> 1, l) + 4 * (a & 1);
-          const float xb[4] = {cb[0], cb[1], cb[2], cb[3]};
-          const float xh[4] = {chi[0], chi[1], chi[2], chi[3]};
-          SS::st4(g_be + o, xb);
-          SS::st4(g_keh + o, xh);
-          if constexpr (BF) {
-            f32x4 clo = zero4();
-            mma(clo, fkt.lo, id);
-            const float xl[4] = {clo[0], clo[1], clo[2], clo[3]};
-            SS::st4(g_kel + o, xl);
-          }
-        }
-      }
-      Rf[bi][s] = P::f3(rA);
-      Qf[bi][s] = P::f3(rM);
-      if (!blk_unsafe) {
-        // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
-        // within 2^{+-100} of 1, so the factorisation cannot overflow.  Kc
-        // replaces this slab of the row's Lambda low words once all lanes of
-        // the wave have read it (the other slabs' columns are untouched).
-        const F3 fb = P::f3(bd);
-        P::m33(accA, Rf[bi][s], fb);
-        P::m33(accM, fb, Qf[bi][s]);
-        st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
-        st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
-      }
-    }
+    for (int e = 0; e < 32; ++e) dq += qv[e] * kv[e];
     dq += __shfl_xor(dq, 16);
     dq += __shfl_xor(dq, 32);
-
+    // Blocks with a large in-block decay span take the hierarchical path
+    // first, while the slab loop's fragments are not yet live.
     if (blk_unsafe) {
       // Overflow-free hierarchical factorisation: the pair (i, j) is split at
       // the highest bit where the in-block indices differ; rows above and
@@ -405,20 +342,71 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
         if (4 * q + ii == r16) accM[ii] = dq;
-      // Kc of this block's rows, written after every lane has read the rows'
-      // Lambda low words
+    }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float lam[8], ta[8], laml[8], tal[8], kc[8];
-        row8<float>(&X[i * XP + 32 * s], q, lam);
-        row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
-        row8<float>(&Y[i * XP + 32 * s], q, laml);
-        row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
+    for (int s = 0; s < 4; ++s) {
+      float lam[8], lsa[8], ta[8], laml[8], lsal[8], tal[8], off[8], suf[8];
+      row8<float>(&X[i * XP + 32 * s], q, lam);
+      row8<float>(&X[(16 * a) * XP + 32 * s], q, lsa);
+      row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
+      row8<float>(&Y[i * XP + 32 * s], q, laml);
+      row8<float>(&Y[(16 * a) * XP + 32 * s], q, lsal);
+      row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
+      row8<float>(&Off[a * KD + 32 * s], q, off);
+      row8<float>(&Suf[a * KD + 32 * s], q, suf);
+      float rA[8], rM[8], bd[8], kc[8], qe[8], bt[8], kt[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kc[e] = kv[8 * s + e] * fast_exp2((ta[e] - lam[e]) + (tal[e] - laml[e]));
-        st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
-        st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
+      for (int e = 0; e < 8; ++e) {
+        const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
+        const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
+        const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
+        const float er = fast_exp2(d_i_sa);
+        rA[e] = be * er;
+        rM[e] = qh * er;
+        kc[e] = kh * fast_exp2(d_ea_i);
+        const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
+        bt[e] = first ? be * eL : 0.f;
+        kt[e] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
+        bd[e] = kh * fast_exp2(-d_i_sa);
+        qe[e] = first ? qh * eL : 0.f;
       }
+      Store<false>::st8(g_qe + fofs(a, s, l), qe);
+      {
+        // (b k e^Lambda)^T and ke^T in fragment layout (row = key, k = token)
+        const F1 fbt = P::f1(bt);
+        const F3 fkt = P::f3(kt);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const F1 id = ident_frag<BF>(hf, r16, q);
+          f32x4 cb = zero4(), chi = zero4();
+          mma(cb, fbt, id);
+          mma(chi, P::hi(fkt), id);
+          const int o = fofs(2 * s + hf, a >> 1, l) + 4 * (a & 1);
+          const float xb[4] = {cb[0], cb[1], cb[2], cb[3]};
+          const float xh[4] = {chi[0], chi[1], chi[2], chi[3]};
+          SS::st4(g_be + o, xb);
+          SS::st4(g_keh + o, xh);
+          if constexpr (BF) {
+            f32x4 clo = zero4();
+            mma(clo, fkt.lo, id);
+            const float xl[4] = {clo[0], clo[1], clo[2], clo[3]};
+            SS::st4(g_kel + o, xl);
+          }
+        }
+      }
+      Rf[bi][s] = P::f3(rA);
+      Qf[bi][s] = P::f3(rM);
+      if (!blk_unsafe) {
+        // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
+        // within 2^{+-100} of 1, so the factorisation cannot overflow.
+        const F3 fb = P::f3(bd);
+        P::m33(accA, Rf[bi][s], fb);
+        P::m33(accM, fb, Qf[bi][s]);
+      }
+      // Kc replaces this slab of the row's Lambda low words once all lanes of
+      // the wave have read it (the other slabs' columns are untouched)
+      st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
+      st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
     }
     // diagonal blocks: A (row-major, LDS) and M (fragment-native, rows = token)
     float mv[4];
@@ -440,8 +428,8 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
 
   // ---- phase 3: off-diagonal A/M blocks (X becomes A) -----------------------
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi) {
-    const int a = bi == 0 ? w : 7 - w;
+  for (int bi = 0; bi < 1; ++bi) {
+    const int a = w;
     float mloc[32];
 #pragma unroll
     for (int s = 0; s < 4; ++s) row8<float>(&Mid0[a * KD + 32 * s], q, mloc + 8 * s);
@@ -501,10 +489,10 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   }
   __syncthreads();
   for (int a = 1; a < 8; ++a) {
-    f32x4 res[2];
+    f32x4 res[1];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const int bt = w + 4 * k2;
+    for (int k2 = 0; k2 < 1; ++k2) {
+      const int bt = w;
       res[k2] = zero4();
       if (bt < a) {
         f32x4 acc = zero4();
@@ -527,8 +515,8 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
     }
     __syncthreads();
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const int bt = w + 4 * k2;
+    for (int k2 = 0; k2 < 1; ++k2) {
+      const int bt = w;
       if (bt < a) {
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) X[(16 * a + 4 * q + ii) * XP + 16 * bt + r16] = res[k2][ii];
@@ -538,7 +526,7 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   }
   // T in fragment-native layout: Y (LDS) for W here, global for k_value
   ST* Ts = reinterpret_cast<ST*>(Y);
-  for (int idx = w; idx < 32; idx += 4) {
+  for (int idx = w; idx < 32; idx += 8) {
     const int rt = idx >> 2, s = idx & 3;
     if (s > (rt >> 1)) continue;
     float x[8];
@@ -548,53 +536,42 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
   }
   __syncthreads();
 
-  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tiles 2w, 2w+1) --
-  f32x4 Wc[2][8];
+  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tile w) -----------
+  f32x4 Wc[8];
   {
-    F1 Bbe[2][4];
+    F1 Bbe[4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int s = 0; s < 4; ++s) Bbe[s] = SS::fa(g_be + fofs(w, s, l));
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Bbe[nt][s] = SS::fa(g_be + fofs(2 * w + nt, s, l));
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) Wc[nt][rt] = zero4();
-    }
+    for (int rt = 0; rt < 8; ++rt) Wc[rt] = zero4();
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        if (s <= rt / 2) {
-          const F1 fa = SS::fa(Ts + fofs(rt, s, l));
-          P::m11(Wc[0][rt], fa, Bbe[0][s]);
-          P::m11(Wc[1][rt], fa, Bbe[1][s]);
-        }
+        if (s <= rt / 2) P::m11(Wc[rt], SS::fa(Ts + fofs(rt, s, l)), Bbe[s]);
       }
     }
   }
   // W^T fragments (rows = key j, k = token), and their negation
-  F3 W3[2][4], W3n[2][4];
+  F3 W3[4], W3n[4];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int s = 0; s < 4; ++s) {
+    float x[8] = {Wc[2 * s][0], Wc[2 * s][1], Wc[2 * s][2], Wc[2 * s][3],
+                  Wc[2 * s + 1][0], Wc[2 * s + 1][1], Wc[2 * s + 1][2], Wc[2 * s + 1][3]};
+    W3[s] = P::f3(x);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float x[8] = {Wc[nt][2 * s][0], Wc[nt][2 * s][1], Wc[nt][2 * s][2], Wc[nt][2 * s][3],
-                    Wc[nt][2 * s + 1][0], Wc[nt][2 * s + 1][1], Wc[nt][2 * s + 1][2], Wc[nt][2 * s + 1][3]};
-      W3[nt][s] = P::f3(x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = -x[e];
-      W3n[nt][s] = P::f3(x);
-    }
-  // Pn^T tile (keys 32w.., state rows 16m..): lane (c, q) holds
-  // Pn[16m + c][32w + 16nt + 4q + ii] = element 4nt + ii of Pn's fragment
+    for (int e = 0; e < 8; ++e) x[e] = -x[e];
+    W3n[s] = P::f3(x);
+  }
+  // Pn^T tile (keys 16w.., state rows 16m..): lane (c, q) holds
+  // Pn[16m + c][16w + 4q + ii] = element 4(w & 1) + ii of slab w / 2 of Pn's fragment
+  const int hofs = 4 * (w & 1);
   auto pn_tile = [&](int m, const F1 (&kb)[4]) {
-    f32x4 P0 = zero4(), P1 = zero4();
+    f32x4 P0 = zero4();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      P::m11(P0, P::hi(W3[0][s]), kb[s]);
-      P::m11(P1, P::hi(W3[1][s]), kb[s]);
-    }
-    const float x[8] = {-P0[0], -P0[1], -P0[2], -P0[3], -P1[0], -P1[1], -P1[2], -P1[3]};
-    SS::st8(g_Pn + fofs(m, w, l), x);
+    for (int s = 0; s < 4; ++s) P::m11(P0, P::hi(W3[s]), kb[s]);
+    const float x[4] = {-P0[0], -P0[1], -P0[2], -P0[3]};
+    SS::st4(g_Pn + fofs(m, w >> 1, l) + hofs, x);
   };
   {
     F1 kb0[4], kb1[4];
@@ -612,32 +589,27 @@ __global__ __launch_bounds__(256) void k_prepass(const PF p) {
       pn_tile(m + 1, kb1);
     }
   }
-  // X^T tile (keys 32w.., tokens 16rt..): lane (c, q) holds
-  // X[16rt + c][32w + 16nt + 4q + ii] = element 4nt + ii of X's fragment.
+  // X^T tile (keys 16w.., tokens 16rt..): lane (c, q) holds
+  // X[16rt + c][16w + 4q + ii] = element 4(w & 1) + ii of slab w / 2 of X's fragment.
   // Operands of tile rt + 1 load while tile rt computes.
   struct XOps {
-    f32x4 q0, q1;
+    f32x4 q0;
     F3 m[4];
   };
   auto ld_x = [&](int rt, XOps& o) {
-    const float* qp = g_qe + fofs(rt, w, l);
-    o.q0 = *reinterpret_cast<const f32x4*>(qp);
-    o.q1 = *reinterpret_cast<const f32x4*>(qp + 4);
+    o.q0 = *reinterpret_cast<const f32x4*>(g_qe + fofs(rt, w >> 1, l) + hofs);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       if (s <= rt / 2) o.m[s] = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
   };
   auto x_tile = [&](int rt, const XOps& o) {
-    f32x4 X0 = o.q0, X1 = o.q1;
+    f32x4 X0 = o.q0;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s <= rt / 2) {
-        P::m33(X0, W3n[0][s], o.m[s]);
-        P::m33(X1, W3n[1][s], o.m[s]);
-      }
-    }
-    const float x[8] = {X0[0], X0[1], X0[2], X0[3], X1[0], X1[1], X1[2], X1[3]};
-    SS::st8s(g_Xh + fofs(rt, w, l), g_Xl + fofs(rt, w, l), x);
+    for (int s = 0; s < 4; ++s)
+      if (s <= rt / 2) P::m33(X0, W3n[s], o.m[s]);
+    const float x[4] = {X0[0], X0[1], X0[2], X0[3]};
+    const int xo = fofs(rt, w >> 1, l) + hofs;
+    SS::st4s(g_Xh + xo, g_Xl + xo, x);
   };
   {
     XOps xa, xb;
@@ -1084,7 +1056,7 @@ int check_args(const dn_prefill_args* a) {
 template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.NCb, p.Hx, p.B), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.NCb, p.Hx, p.B), dim3(512), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
