@@ -72,17 +72,15 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128):
     units = B * Hk * math.ceil(L / C)
     f_pre = 6 * C * C * K + C ** 3 / 3                        # A, M, W = T be ; T
     f_val = 2 * C * C * Vp                                    # U = T (w*v)
-    f_chain = 2 * C * K * Vp + 2 * C * K * Vp                 # W S ; ke^T Vnew
-    f_out = 2 * C * K * Vp + 2 * C * C * Vp                   # qe S ; M Vnew
+    f_chain = 4 * C * K * Vp + 2 * C * K * Vp + 2 * C * C * Vp   # W S ; ke^T Vnew ; qe S ; M Vnew
     qkgb_bytes = B * L * (2 * Hk * K * 2 + 2 * Hk * K * 4) + 4 * B * L
     vw_bytes = B * L * (Hv * K * 2 + Hv * K * 4)
     out_bytes = B * L * Hv * K * 2
     state_bytes = B * Hv * K * K * 4
-    return dict(units=units, flops_total=units * (f_pre + f_val + f_chain + f_out),
+    return dict(units=units, flops_total=units * (f_pre + f_val + f_chain),
                 prepass=dict(flops=units * f_pre, bytes=qkgb_bytes),
                 value=dict(flops=units * f_val, bytes=vw_bytes),
-                chain=dict(flops=units * f_chain, bytes=state_bytes),
-                output=dict(flops=units * f_out, bytes=out_bytes),
+                chain=dict(flops=units * f_chain, bytes=state_bytes + out_bytes),
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
 
 
@@ -183,7 +181,7 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
              "traffic / algorithmic |",
              "|---|---|---|---|---|---|---|---|---|"]
     alg = {"k_prepass": work["prepass"]["bytes"], "k_value": work["value"]["bytes"],
-           "k_chain": work["chain"]["bytes"], "k_output": work["output"]["bytes"],
+           "k_chain": work["chain"]["bytes"],
            "k_decode<f32>": 2 * 256 * 32 * 128 * 128 * 4, "k_decode<bf16>": 2 * 256 * 32 * 128 * 128 * 2,
            "copy (calibration)": 2 * COPY_BYTES}
     for k in ("k_prepass", "k_value", "k_chain", "k_output", "k_decode<f32>", "k_decode<bf16>",
@@ -259,7 +257,7 @@ def main():
         ", ".join(f"{k_}={v_ * 1e3:.1f}" for k_, v_ in kern.items()))
 
     # dominant kernel and its roofline
-    dom = max(("prepass", "value", "chain", "output"), key=lambda n: kern.get(n, 0.0))
+    dom = max(("prepass", "value", "chain"), key=lambda n: kern.get(n, 0.0))
     t_dom = kern[dom] * 1e-3
     wk = work[dom]
     t_hbm = wk["bytes"] / (PEAK_HBM_GBPS * 1e9)

@@ -77,6 +77,25 @@ template <> __device__ __forceinline__ void ld4<bf16>(const bf16* p, float* o) {
   o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
 }
 
+// The 8 fragment-order elements of a row slab (rowp[4q..4q+3], rowp[16+4q..])
+// held exactly as loaded, so the loads can be issued long before the values
+// are needed (the wait lands at the first use, not at the load).
+template <class T> struct Raw8 {
+  typedef T V __attribute__((ext_vector_type(4)));
+  V a, b;
+  __device__ __forceinline__ void load(const T* rowp, int q) {
+    a = *reinterpret_cast<const V*>(rowp + 4 * q);
+    b = *reinterpret_cast<const V*>(rowp + 16 + 4 * q);
+  }
+  __device__ __forceinline__ void to(float* x) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = (float)a[e];
+      x[4 + e] = (float)b[e];
+    }
+  }
+};
+
 template <class T> __device__ __forceinline__ void st4(T* p, const float* v) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = from_f<T>(v[i]);

@@ -364,12 +364,12 @@ extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
   const dim3 grid((unsigned)(a->B * a->Hv));
   hipStream_t st = (hipStream_t)stream;
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
-  prof_mark(4, st, false);
+  prof_mark(3, st, false);
   if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(256), 0, st, p);
   else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(256), 0, st, p);
   else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(256), 0, st, p);
   else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(256), 0, st, p);
-  prof_mark(4, st, true);
+  prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;

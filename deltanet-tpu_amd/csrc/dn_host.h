@@ -14,7 +14,6 @@ struct PF {
   int B, L, Hk, Hv, G;       // tensor dims, G = Hv / Hk
   int Hx, Vp, gates_at_hv;   // execution heads, value width per execution head
   int t0, nt, NCb;           // token block [t0, t0+nt), chunks in the block
-  int ncg;                   // 256-column groups of the value width (k_output)
   const void *q, *k, *v;
   int v_dt;
   const void* g; int g_dt, g_h, g_c;
@@ -38,9 +37,8 @@ struct PF {
   // fp32 in fp32 mode.
   void* PnA;                 // F  [8][4]      ST : Pn = -ke^T W, rows = state row (chain A)
   float* QC;                 // C  [8][nct]    f32: Q = ke^T U (chain accumulator init)
-  void *XAh, *XAl;           // F  [8][4]      ST : X = qe - M W, rows = token (output B)
-  float* OiT;                // C  [8][nct]    f32: (M U)^T tiles (output accumulator init)
-  void *StBh, *StBl;         // F  [nct][4]    ST : S_c^T, rows = value column (output A)
+  void *XAh, *XAl;           // F  [8][4]      ST : X = qe - M W, rows = token (chain output B)
+  float* OiT;                // C  [8][nct]    f32: (M U)^T tiles (chain output accumulator init)
   void* BeB;                 // F  [8][4]      ST : (b k e^Lambda)^T, first document
   void *KeBh, *KeBl;         // F  [8][4]      ST : (k e^{Lend - Lambda})^T, last document
   void *MAh, *MAl;           // F  [8][4]      ST : M, rows = token

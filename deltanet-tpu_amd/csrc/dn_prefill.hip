@@ -14,18 +14,18 @@
 //     S_next = [same doc] diag(e^Lend) S + Pn S + Q,  Pn = -ke^T W,  Q = ke^T U
 //     O      = X S + Oi,                              X = qe - M W,  Oi = M U
 // so:
-//   k_prepass (grid: chunk x exec-head x batch, 4 waves, one chunk each)
-//       everything that is parallel over chunks: fused prologue, Lambda,
-//       A and M on MFMA, T by blocked substitution on fp32 MFMA, W, U and
-//       the four chunk operators Pn, Q, X, Oi.
+//   k_prepass (grid: chunk x exec-head x batch, 8 waves, one chunk each)
+//       fused prologue, Lambda, A and M on MFMA, T by blocked substitution
+//       on fp32 MFMA, W, and the chunk operators Pn and X.
+//   k_value   (grid: chunk x 128-column pass x exec-head, 4 waves)
+//       U = T (w*v), Q = ke^T U and Oi = M U.
 //   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
-//       the sequential scan over chunks with the fp32 state in VGPRs;
-//       stores each chunk's entry state S_c.
-//   k_output  (grid: chunk x exec-head x batch, 4 waves)
-//       parallel again: O = X S_c + Oi.
+//       the sequential scan over chunks with the fp32 state in VGPRs, and
+//       each chunk's output O = X S_c + Oi from the same S_c fragments.
 //
-// All intermediates live in a caller-provided workspace sized for one token
-// block, small enough to stay resident in the 256 MB Infinity Cache.
+// Intermediates live in a caller-provided workspace sized for one token
+// block, small enough to stay resident in the 256 MB Infinity Cache; every
+// array is stored in the MFMA lane order of its consumer.
 #include "dn_common.h"
 #include "dn_host.h"
 
@@ -33,7 +33,8 @@ namespace dn {
 
 constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
-constexpr int XP = 132;   // fp32 LDS pitch (floats): conflict-free 16-lane column groups
+constexpr int XP = 132;
+   // fp32 LDS pitch (floats): conflict-free 16-lane column groups
 
 // diag blocks whose in-block log2-decay span exceeds this use the
 // overflow-free hierarchical path (e^{69} stays far inside the fp32 range)
@@ -118,6 +119,31 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   ST* g_T = (ST*)p.TA + uf;
   float* g_qe = p.QeA + uf;
   float* g_dv = p.dvec + u * KD;
+
+  // q, k, b rows of this wave's token block (phase 2), loaded now so their
+  // latency overlaps phases 0 and 1
+  const int hbg = kgate_head(p, p.b_h, h);
+  Raw8<TIn> rq[4], rk[4];
+  Raw8<float> rb[4];
+  float b_scalar = 0.f;
+  {
+    const int t = tb + 16 * w + r16;
+    const int tt = t < t_end ? t : tb;
+    const TIn* qp = (const TIn*)p.q + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
+    const TIn* kp = (const TIn*)p.k + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
+    const float* bp = (const float*)p.b + (((int64_t)b * p.L + tt) * p.b_h + hbg) * p.b_c;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      rq[s].load(qp + 32 * s, q);
+      rk[s].load(kp + 32 * s, q);
+    }
+    if (p.b_c == 1) {
+      b_scalar = bp[0];
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) rb[s].load(bp + 32 * s, q);
+    }
+  }
 
   // ---- phase 0: in-chunk document index (segment canonicalisation) -------
   if (tid < CH) {
@@ -230,31 +256,25 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   // ---- phase 2: per-row quantities, diagonal A/M blocks --------------------
   F3 Rf[1][4], Qf[1][4];
   f32x4 Adiag[1];
-  const int hbg = kgate_head(p, p.b_h, h);
 #pragma unroll
   for (int bi = 0; bi < 1; ++bi) {
     const int a = w;
     const int i = 16 * a + r16;
     const int t = tb + i;
     const bool valid = t < t_end;
-    const int tt = valid ? t : tb;
     float qv[32], kv[32], bet[32];
     {
-      const TIn* qp = (const TIn*)p.q + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
-      const TIn* kp = (const TIn*)p.k + (((int64_t)b * p.L + tt) * p.Hk + hk) * KD;
-      const float* bp = (const float*)p.b + (((int64_t)b * p.L + tt) * p.b_h + hbg) * p.b_c;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        row8<TIn>(qp + 32 * s, q, qv + 8 * s);
-        row8<TIn>(kp + 32 * s, q, kv + 8 * s);
+        rq[s].to(qv + 8 * s);
+        rk[s].to(kv + 8 * s);
       }
       if (p.b_c == 1) {
-        const float bs = bp[0];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) bet[e] = bs;
+        for (int e = 0; e < 32; ++e) bet[e] = b_scalar;
       } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) row8<float>(bp + 32 * s, q, bet + 8 * s);
+        for (int s = 0; s < 4; ++s) rb[s].to(bet + 8 * s);
       }
       float ssq = 0.f, ssk = 0.f;
 #pragma unroll
@@ -471,6 +491,20 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   }
   __syncthreads();
 
+  // M (and, in bf16 mode, the high words of ke^T) are staged into LDS for
+  // phase 5 once T no longer needs it; their loads are issued here so they
+  // overlap the substitution.  16 bytes per load, 4 per array and thread.
+  constexpr bool kStageKe = BF;
+  using V16 = f32x4;
+  V16 st_mh[4], st_ml[4], st_ke[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int o = (tid + 512 * j) * (16 / (int)sizeof(ST));   // element offset of chunk
+    st_mh[j] = *reinterpret_cast<const V16*>(g_Mh + o);
+    if constexpr (BF) st_ml[j] = *reinterpret_cast<const V16*>(g_Ml + o);
+    if constexpr (kStageKe) st_ke[j] = *reinterpret_cast<const V16*>(g_keh + o);
+  }
+
   // ---- phase 4: T = (I + A)^-1 (blocked forward substitution, fp32) -------
   if (w < 2) {
     const int a = 4 * w + q;
@@ -535,6 +569,28 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     SS::st8(g_T + fofs(rt, s, l), x);
   }
   __syncthreads();
+  // X (T in fp32) is free now: M high / low words there, ke^T high words
+  // after T in Y (bf16 mode)
+  ST* Mh_s = reinterpret_cast<ST*>(X);
+  ST* Ml_s = BF ? Mh_s + CH * CH : Mh_s;
+  ST* ke_s = Ts + CH * KD;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int o = (tid + 512 * j) * (16 / (int)sizeof(ST));
+    *reinterpret_cast<V16*>(Mh_s + o) = st_mh[j];
+    if constexpr (BF) *reinterpret_cast<V16*>(Ml_s + o) = st_ml[j];
+    if constexpr (kStageKe) *reinterpret_cast<V16*>(ke_s + o) = st_ke[j];
+  }
+  const ST* keA = kStageKe ? ke_s : g_keh;
+  if constexpr (!BF) {
+    // fp32 mode: M is 64 KB (the 4 loads above covered 32 KB); finish it
+#pragma unroll
+    for (int j = 4; j < 8; ++j) {
+      const int o = (tid + 512 * j) * 4;
+      *reinterpret_cast<V16*>(Mh_s + o) = *reinterpret_cast<const V16*>(g_Mh + o);
+    }
+  }
+  __syncthreads();
 
   // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tile w) -----------
   f32x4 Wc[8];
@@ -576,15 +632,15 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   {
     F1 kb0[4], kb1[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(g_keh + fofs(0, s, l));
+    for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(keA + fofs(0, s, l));
 #pragma unroll 1
     for (int m = 0; m < 8; m += 2) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kb1[s] = SS::fa(g_keh + fofs(m + 1, s, l));
+      for (int s = 0; s < 4; ++s) kb1[s] = SS::fa(keA + fofs(m + 1, s, l));
       pn_tile(m, kb0);
       if (m + 2 < 8) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(g_keh + fofs(m + 2, s, l));
+        for (int s = 0; s < 4; ++s) kb0[s] = SS::fa(keA + fofs(m + 2, s, l));
       }
       pn_tile(m + 1, kb1);
     }
@@ -600,7 +656,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     o.q0 = *reinterpret_cast<const f32x4*>(g_qe + fofs(rt, w >> 1, l) + hofs);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      if (s <= rt / 2) o.m[s] = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
+      if (s <= rt / 2) o.m[s] = SS::fa3(Mh_s + fofs(rt, s, l), Ml_s + fofs(rt, s, l));
   };
   auto x_tile = [&](int rt, const XOps& o) {
     f32x4 X0 = o.q0;
@@ -795,180 +851,164 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
 }
 
 // ===========================================================================
-// k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c.
-// One workgroup per (16-column tile, exec head, batch); wave w owns state rows
-// 32w..32w+31 (fp32, in VGPRs); the full S_c is exchanged through LDS each
-// chunk so that only 8 MFMAs per wave sit on the sequential path.  The next
-// chunk's operands load while the current one computes.
+// k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c, and the output
+// O_c = X_c S_c + Oi_c of every chunk.
+// One workgroup of 8 waves per (16-column tile, exec head, batch), in two
+// roles that meet at one LDS barrier per chunk:
+//   waves 0-3 (recurrence): wave w owns state rows 32w..32w+31 (fp32, in
+//     VGPRs), publishes them to LDS, and after the barrier reads the full
+//     S_c^T to form S_{c+1}; only 8 MFMAs per wave sit on the sequential path.
+//   waves 4-7 (output): after the same barrier, wave 4+w' reads S_c^T and
+//     computes token tiles 2w', 2w'+1 as O^T = S^T X^T + (M U)^T, running
+//     beside the recurrence on the other wave slot of each SIMD.
+// Each role prefetches its next chunk's operands while the current one
+// computes.  The role is a scalar (wave-uniform) branch, and both roles
+// execute exactly one barrier per chunk.
 // ===========================================================================
 template <bool BF>
-__global__ __launch_bounds__(256) void k_chain(const PF p) {
+__global__ __launch_bounds__(512) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
+  using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
   __shared__ float Sx[2][16 * XP];   // S^T of the current chunk, double-buffered
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wid & 3, l = tid & 63, r16 = l & 15, q = l >> 4;
   int ct, h, b;
   xcd_block(ct, h, b);
-  const int n = 16 * ct + r16;
-  const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-  const int vcol = n % KD;
-  const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + vcol;
 
-  f32x4 S[2];
+  if (wid < 4) {
+    // ---------------- recurrence ----------------
+    const int n = 16 * ct + r16;
+    const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
+    const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
+    f32x4 S[2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii)
-      S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
-
-  struct Ops {
-    F1 pf[2][4];
-    f32x4 qc[2], dv[2];
-    int is_new, same;
-  };
-  auto load_ops = [&](int c, Ops& o) {
-    const int cc = min(c, p.NCb - 1);
-    const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
-    const ST* Pn = (const ST*)p.PnA + u * (KD * KD);
-    const float* Qc = p.QC + u * (int64_t)(KD * p.Vp);
-    const float* dvp = p.dvec + u * KD;
+      for (int ii = 0; ii < 4; ++ii)
+        S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
+    struct Ops {
+      F1 pf[2][4];
+      f32x4 qc[2], dv[2];
+      int is_new, same;
+    };
+    auto load_ops = [&](int c, Ops& o) {
+      const int cc = min(c, p.NCb - 1);
+      const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
+      const ST* Pn = (const ST*)p.PnA + u * (KD * KD);
+      const float* Qc = p.QC + u * (int64_t)(KD * p.Vp);
+      const float* dvp = p.dvec + u * KD;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < 2; ++r) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
-      o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
-      o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
-    }
-    o.is_new = p.flags[((int64_t)b * p.NCb + cc) * 2 + 0];
-    o.same = p.flags[((int64_t)b * p.NCb + cc) * 2 + 1];
-  };
-  auto step = [&](int c, const Ops& o) {
-    const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-    if (o.is_new) { S[0] = zero4(); S[1] = zero4(); }
-    float* sx = Sx[c & 1];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const float x[4] = {S[r][0], S[r][1], S[r][2], S[r][3]};
-      st4<float>(&sx[r16 * XP + 32 * w + 16 * r + 4 * q], x);
-    }
-    {
-      // entry state, as the output kernel's S^T fragment (rows = value column)
-      const int64_t so = u * (int64_t)(p.Vp * KD) + fofs(ct, w, l);
-      const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
-      SS::st8s((ST*)p.StBh + so, (ST*)p.StBl + so, x);
-    }
-    lds_barrier();
-    F1 Sf[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float x[8];
-      row8<float>(&sx[r16 * XP + 32 * s], q, x);
-      Sf[s] = P::f1(x);
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      f32x4 acc = o.qc[r];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (o.same ? o.dv[r][ii] * S[r][ii] : 0.f);
-    }
-  };
-  Ops o0, o1;
-  load_ops(0, o0);
-#pragma unroll 1
-  for (int c = 0; c < p.NCb; c += 2) {
-    load_ops(c + 1, o1);
-    step(c, o0);
-    if (c + 1 >= p.NCb) break;
-    load_ops(c + 2, o0);
-    step(c + 1, o1);
-  }
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
-}
-
-// ===========================================================================
-// k_output: O_c^T = S_c^T X_c^T + (M U)^T  (one workgroup per chunk and 256
-// value columns; each wave owns 64 columns).  The transposed product leaves
-// each lane 4 consecutive columns of one token row to store.
-// ===========================================================================
-template <bool BF>
-__global__ __launch_bounds__(256) void k_output(const PF p) {
-  using P = Pol<BF>;
-  using F3 = typename P::F3;
-  using SS = Store<BF>;
-  using ST = typename SS::ST;
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  int c, cg, zh;
-  xcd_block(c, cg, zh);
-  const int h = zh % p.Hx, b = zh / p.Hx;
-  const int col0 = 256 * cg + 64 * w;
-  if (col0 >= p.Vp) return;
-  const int tb = p.t0 + c * CH;
-  const int t_end = min(p.t0 + p.nt, p.L);
-  const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-  const int64_t uf = u * (CH * KD);
-  const ST* Xh = (const ST*)p.XAh + uf;
-  const ST* Xl = (const ST*)p.XAl + uf;
-  const float* Oi = p.OiT + u * (int64_t)(CH * p.Vp);
-  const int64_t so = u * (int64_t)(p.Vp * KD);
-  const ST* Sh = (const ST*)p.StBh + so;
-  const ST* Sl = (const ST*)p.StBl + so;
-  const int ctb = col0 / 16;
-
-  F3 Sf[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Sf[j][s] = SS::fa3(Sh + fofs(ctb + j, s, l), Sl + fofs(ctb + j, s, l));
-  const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
-  const int vcol0 = col0 % KD;
-  // operands of row tile rt + 1 load while rt computes
-  struct OOps {
-    f32x4 o[4];
-    F3 x[4];
-  };
-  auto ld = [&](int rt, OOps& o) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o.o[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ctb + j, p.nct, l));
-#pragma unroll
-    for (int s = 0; s < 4; ++s) o.x[s] = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
-  };
-  auto tile = [&](int rt, const OOps& o) {
-    f32x4 O[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) O[j] = o.o[j];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) P::m33(O[j], Sf[j][s], o.x[s]);
-    // lane (c, q) holds O[token 16rt + c][columns 16j + 4q .. 16j + 4q + 3]
-    const int t = tb + 16 * rt + r16;
-    if (t < t_end) {
-      const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hv) * KD + vcol0 + 4 * q;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x[4] = {O[j][0], O[j][1], O[j][2], O[j][3]};
-        if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob + 16 * j, x);
-        else st4<float>((float*)p.out + ob + 16 * j, x);
+        for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
+        o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
+        o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
       }
-    }
-  };
-  OOps oa, ob;
-  ld(0, oa);
+      o.is_new = p.flags[((int64_t)b * p.NCb + cc) * 2 + 0];
+      o.same = p.flags[((int64_t)b * p.NCb + cc) * 2 + 1];
+    };
+    auto step = [&](int c, const Ops& o) {
+      if (o.is_new) { S[0] = zero4(); S[1] = zero4(); }
+      float* sx = Sx[c & 1];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float x[4] = {S[r][0], S[r][1], S[r][2], S[r][3]};
+        st4<float>(&sx[r16 * XP + 32 * w + 16 * r + 4 * q], x);
+      }
+      lds_barrier();
+      F1 Sf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float x[8];
+        row8<float>(&sx[r16 * XP + 32 * s], q, x);
+        Sf[s] = P::f1(x);
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        f32x4 acc = o.qc[r];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (o.same ? o.dv[r][ii] * S[r][ii] : 0.f);
+      }
+    };
+    Ops o0, o1;
+    load_ops(0, o0);
 #pragma unroll 1
-  for (int rt = 0; rt < 8; rt += 2) {
-    ld(rt + 1, ob);
-    tile(rt, oa);
-    if (rt + 2 < 8) ld(rt + 2, oa);
-    tile(rt + 1, ob);
+    for (int c = 0; c < p.NCb; c += 2) {
+      load_ops(c + 1, o1);
+      step(c, o0);
+      if (c + 1 >= p.NCb) break;
+      load_ops(c + 2, o0);
+      step(c + 1, o1);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
+  } else {
+    // ---------------- output ----------------
+    const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
+    const int vco = (16 * ct) % KD;
+    struct Ops {
+      F3 xb[2][4];   // X fragments of token tiles 2w, 2w+1
+      f32x4 oi[2];   // (M U)^T tiles of token tiles 2w, 2w+1, this column tile
+    };
+    auto load_ops = [&](int c, Ops& o) {
+      const int cc = min(c, p.NCb - 1);
+      const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
+      const ST* Xh = (const ST*)p.XAh + u * (CH * KD);
+      const ST* Xl = (const ST*)p.XAl + u * (CH * KD);
+      const float* Oi = p.OiT + u * (int64_t)(CH * p.Vp);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) o.xb[r][s] = SS::fa3(Xh + fofs(2 * w + r, s, l), Xl + fofs(2 * w + r, s, l));
+        o.oi[r] = *reinterpret_cast<const f32x4*>(Oi + cofs(2 * w + r, ct, p.nct, l));
+      }
+    };
+    auto step = [&](int c, const Ops& o) {
+      lds_barrier();
+      const float* sx = Sx[c & 1];
+      // S_c^T fragments (rows = value column, k = state row), split
+      F3 Sf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float x[8];
+        row8<float>(&sx[r16 * XP + 32 * s], q, x);
+        Sf[s] = P::f3(x);
+      }
+      const int tb = p.t0 + c * CH;
+      const int t_end = min(p.t0 + p.nt, p.L);
+      // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        f32x4 acc = o.oi[r];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) P::m33(acc, Sf[s], o.xb[r][s]);
+        const int t = tb + 16 * (2 * w + r) + r16;
+        if (t < t_end) {
+          const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + vco + 4 * q;
+          const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+          if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob, x);
+          else st4<float>((float*)p.out + ob, x);
+        }
+      }
+    };
+    Ops o0, o1;
+    load_ops(0, o0);
+#pragma unroll 1
+    for (int c = 0; c < p.NCb; c += 2) {
+      load_ops(c + 1, o1);
+      step(c, o0);
+      if (c + 1 >= p.NCb) break;
+      load_ops(c + 2, o0);
+      step(c + 1, o1);
+    }
   }
 }
 
@@ -978,7 +1018,7 @@ __global__ __launch_bounds__(256) void k_output(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, StBh, StBl, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, carry, total;
+  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -999,8 +1039,6 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   L.XAh = take(units * sq * es);
   L.XAl = take(units * sq * ls);
   L.OiT = take(units * CH * Vp * 4);
-  L.StBh = take(units * (size_t)Vp * KD * es);
-  L.StBl = take(units * (size_t)Vp * KD * ls);
   L.BeB = take(units * sq * es);
   L.KeBh = take(units * sq * es);
   L.KeBl = take(units * sq * ls);
@@ -1066,13 +1104,8 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
   prof_mark(2, st, true);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  prof_mark(3, st, false);
-  hipLaunchKernelGGL((k_output<BF>), dim3(p.NCb, p.ncg, p.Hx * p.B), dim3(256), 0, st, p);
-  prof_mark(3, st, true);
   return hipGetLastError();
 }
 
@@ -1130,7 +1163,6 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.init_seg = a->init_seg;
   p.out = a->out;
   p.scale = a->scale; p.l2norm = a->qk_l2norm; p.fuse = a->fuse_prologue; p.guard = a->stability_guard;
-  p.ncg = (Vp + 255) / 256;
   p.flags = (int32_t*)(ws + Lw.flags);
   p.dvec = (float*)(ws + Lw.dvec);
   p.nct = Vp / 16;
@@ -1139,8 +1171,6 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.XAh = ws + Lw.XAh;
   p.XAl = bf ? ws + Lw.XAl : p.XAh;
   p.OiT = (float*)(ws + Lw.OiT);
-  p.StBh = ws + Lw.StBh;
-  p.StBl = bf ? ws + Lw.StBl : p.StBh;
   p.BeB = ws + Lw.BeB;
   p.KeBh = ws + Lw.KeBh;
   p.KeBl = bf ? ws + Lw.KeBl : p.KeBh;

@@ -76,7 +76,7 @@ EXPORTED_SYMBOLS = (
     "dn_profile_begin",
     "dn_profile_end",
 )
-PROFILE_KINDS = ("prepass", "value", "chain", "output", "decode")
+PROFILE_KINDS = ("prepass", "value", "chain", "decode")
 
 _lock = threading.Lock()
 _lib = None

@@ -126,11 +126,11 @@ int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, fl
 /* Kernel timing instrumentation (no counterpart in the reference; for
  * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
  * every dn_prefill_fwd call on the calling thread records HIP events on its
- * stream around each of its kernels (prepass, value, chain, output) and every
+ * stream around each of its kernels (prepass, value, chain) and every
  * dn_decode_step call around its kernel.  dn_profile_end() waits for those
  * events and writes, per kernel kind, the summed duration in milliseconds
  * and the number of launches (arrays of DN_PROFILE_KINDS entries). */
-#define DN_PROFILE_KINDS 5   /* 0 prepass, 1 value, 2 chain, 3 output, 4 decode */
+#define DN_PROFILE_KINDS 4   /* 0 prepass, 1 value, 2 chain, 3 decode */
 int dn_profile_begin(void);
 int dn_profile_end(double* ms_sum, int64_t* launches);
 
