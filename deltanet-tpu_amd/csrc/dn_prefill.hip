@@ -34,6 +34,14 @@ namespace dn {
 constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
 constexpr int XP = 132;
+constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
+// 16-column tiles per chain workgroup (1 or 2: the workgroup has 4 * tiles + 8
+// waves).  One tile measured fastest: with two, each SIMD's MFMA pipe
+// carries two recurrence waves and the sequential path slows down.
+#ifndef DN_CHAIN_TILES
+#define DN_CHAIN_TILES 1
+#endif
+constexpr int kChainTiles = DN_CHAIN_TILES;
    // fp32 LDS pitch (floats): conflict-free 16-lane column groups
 
 // diag blocks whose in-block log2-decay span exceeds this use the
@@ -853,34 +861,51 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
 // ===========================================================================
 // k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c, and the output
 // O_c = X_c S_c + Oi_c of every chunk.
-// One workgroup of 8 waves per (16-column tile, exec head, batch), in two
+// One workgroup per (NCT 16-column tiles, exec head, batch), with waves in two
 // roles that meet at one LDS barrier per chunk:
-//   waves 0-3 (recurrence): wave w owns state rows 32w..32w+31 (fp32, in
-//     VGPRs), publishes them to LDS, and after the barrier reads the full
-//     S_c^T to form S_{c+1}; only 8 MFMAs per wave sit on the sequential path.
-//   waves 4-7 (output): after the same barrier, wave 4+w' reads S_c^T and
-//     computes token tiles 2w', 2w'+1 as O^T = S^T X^T + (M U)^T, running
-//     beside the recurrence on the other wave slot of each SIMD.
+//   4 NCT recurrence waves: wave (j, w) owns state rows 32w..32w+31 of column
+//     tile j (fp32, in VGPRs) and publishes them to LDS as slab w of that
+//     tile's S_c^T fragment (split high / low bf16 in bf16 mode); after the
+//     barrier it reads the tile's four slabs to form S_{c+1}.  Only 8 MFMAs
+//     per wave sit on the sequential path.
+//   8 output waves: after the same barrier, output wave t reads the S_c^T
+//     fragments and computes token tile t of all NCT column tiles as
+//     O^T = S^T X^T + (M U)^T, beside the recurrence on the other wave slots
+//     of each SIMD.  X is loaded once per workgroup and chunk for all NCT
+//     tiles, which is what NCT > 1 saves (X and Pn are shared by every
+//     column tile of a head).
 // Each role prefetches its next chunk's operands while the current one
 // computes.  The role is a scalar (wave-uniform) branch, and both roles
 // execute exactly one barrier per chunk.
 // ===========================================================================
-template <bool BF>
-__global__ __launch_bounds__(512) void k_chain(const PF p) {
+template <bool BF, int NCT>
+__global__ __launch_bounds__(64 * (4 * NCT + 8)) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
-  __shared__ float Sx[2][16 * XP];   // S^T of the current chunk, double-buffered
+  constexpr int NT = 64 * (4 * NCT + 8);
+  constexpr int FR = 4 * 64 * 8;   // elements of one tile's S^T fragment
+  // S_c^T fragments per column tile, high and low words, double-buffered
+  __shared__ __align__(16) ST Sh_s[2][NCT * FR];
+  __shared__ __align__(16) ST Sl_s[2][BF ? NCT * FR : 1];
+  __shared__ int flg[2 * kMaxBlockChunks];   // is_new_doc, all_same_doc per chunk
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wid & 3, l = tid & 63, r16 = l & 15, q = l >> 4;
-  int ct, h, b;
-  xcd_block(ct, h, b);
+  const int l = tid & 63, r16 = l & 15, q = l >> 4;
+  int cg, h, b;
+  xcd_block(cg, h, b);
+  const int ct0 = NCT * cg;
+  auto frag_lo = [&](int buf) -> ST* { return BF ? &Sl_s[buf][0] : &Sh_s[buf][0]; };
+  // chunk flags into LDS once, so testing them never waits on vector loads
+  for (int i = tid; i < 2 * p.NCb; i += NT) flg[i] = p.flags[(int64_t)b * p.NCb * 2 + i];
+  __syncthreads();
 
-  if (wid < 4) {
-    // ---------------- recurrence ----------------
+  if (wid < 4 * NCT) {
+    // ---------------- recurrence: column tile j, rows 32w.. ----------------
+    const int j = wid >> 2, w = wid & 3;
+    const int ct = ct0 + j;
     const int n = 16 * ct + r16;
     const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
     const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
@@ -893,7 +918,6 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
     struct Ops {
       F1 pf[2][4];
       f32x4 qc[2], dv[2];
-      int is_new, same;
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
@@ -908,32 +932,27 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
         o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
         o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
       }
-      o.is_new = p.flags[((int64_t)b * p.NCb + cc) * 2 + 0];
-      o.same = p.flags[((int64_t)b * p.NCb + cc) * 2 + 1];
     };
     auto step = [&](int c, const Ops& o) {
-      if (o.is_new) { S[0] = zero4(); S[1] = zero4(); }
-      float* sx = Sx[c & 1];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float x[4] = {S[r][0], S[r][1], S[r][2], S[r][3]};
-        st4<float>(&sx[r16 * XP + 32 * w + 16 * r + 4 * q], x);
+      const int is_new = flg[2 * c], same = flg[2 * c + 1];
+      if (is_new) { S[0] = zero4(); S[1] = zero4(); }
+      // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
+      {
+        const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
+        const int fo = j * FR + (w * 64 + l) * 8;
+        SS::st8s(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo, x);
       }
       lds_barrier();
       F1 Sf[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(&sx[r16 * XP + 32 * s], q, x);
-        Sf[s] = P::f1(x);
-      }
+      for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][j * FR + (s * 64 + l) * 8]);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         f32x4 acc = o.qc[r];
 #pragma unroll
         for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (o.same ? o.dv[r][ii] * S[r][ii] : 0.f);
+        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][ii] : 0.f);
       }
     };
     Ops o0, o1;
@@ -951,12 +970,11 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
   } else {
-    // ---------------- output ----------------
-    const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
-    const int vco = (16 * ct) % KD;
+    // ---------------- output: token tile rt of all NCT column tiles ----------------
+    const int rt = wid - 4 * NCT;
     struct Ops {
-      F3 xb[2][4];   // X fragments of token tiles 2w, 2w+1
-      f32x4 oi[2];   // (M U)^T tiles of token tiles 2w, 2w+1, this column tile
+      F3 xb[4];      // X fragments of token tile rt
+      f32x4 oi[NCT]; // (M U)^T tiles of token tile rt
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
@@ -965,49 +983,44 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
       const ST* Xl = (const ST*)p.XAl + u * (CH * KD);
       const float* Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int s = 0; s < 4; ++s) o.xb[s] = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
 #pragma unroll
-        for (int s = 0; s < 4; ++s) o.xb[r][s] = SS::fa3(Xh + fofs(2 * w + r, s, l), Xl + fofs(2 * w + r, s, l));
-        o.oi[r] = *reinterpret_cast<const f32x4*>(Oi + cofs(2 * w + r, ct, p.nct, l));
-      }
+      for (int j = 0; j < NCT; ++j) o.oi[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ct0 + j, p.nct, l));
     };
     auto step = [&](int c, const Ops& o) {
       lds_barrier();
-      const float* sx = Sx[c & 1];
-      // S_c^T fragments (rows = value column, k = state row), split
-      F3 Sf[4];
+      const int t = p.t0 + c * CH + 16 * rt + r16;
+      const bool tv = t < min(p.t0 + p.nt, p.L);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(&sx[r16 * XP + 32 * s], q, x);
-        Sf[s] = P::f3(x);
-      }
-      const int tb = p.t0 + c * CH;
-      const int t_end = min(p.t0 + p.nt, p.L);
-      // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
+      for (int j = 0; j < NCT; ++j) {
+        f32x4 acc = o.oi[j];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        f32x4 acc = o.oi[r];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) P::m33(acc, Sf[s], o.xb[r][s]);
-        const int t = tb + 16 * (2 * w + r) + r16;
-        if (t < t_end) {
-          const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + vco + 4 * q;
+        for (int s = 0; s < 4; ++s) {
+          const int fo = j * FR + (s * 64 + l) * 8;
+          P::m33(acc, SS::fa3(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo), o.xb[s]);
+        }
+        // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
+        const int ct = ct0 + j;
+        const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
+        if (tv) {
+          const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
           const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
           if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob, x);
           else st4<float>((float*)p.out + ob, x);
         }
       }
     };
+    // chunk c computes (and stores) before chunk c + 1's loads are issued
     Ops o0, o1;
     load_ops(0, o0);
 #pragma unroll 1
     for (int c = 0; c < p.NCb; c += 2) {
-      load_ops(c + 1, o1);
       step(c, o0);
-      if (c + 1 >= p.NCb) break;
       load_ops(c + 2, o0);
+      if (c + 1 >= p.NCb) break;
+      if (c == 0) load_ops(1, o1);
       step(c + 1, o1);
+      load_ops(c + 3, o1);
     }
   }
 }
@@ -1055,9 +1068,9 @@ constexpr size_t kAutoBudget = size_t(160) << 20;
 
 int block_chunks(const dn_prefill_args* a, int Hx, int Vp) {
   const int nct = (a->nt + CH - 1) / CH;
-  if (a->block_tokens > 0) return std::max(1, std::min(nct, a->block_tokens / CH));
+  if (a->block_tokens > 0) return std::max(1, std::min(std::min(nct, kMaxBlockChunks), a->block_tokens / CH));
   const bool bf = a->precision == 0;
-  int ncb = nct;
+  int ncb = std::min(nct, kMaxBlockChunks);
   while (ncb > 1 && ws_layout(a, Hx, Vp, ncb, bf).total > kAutoBudget) ncb = (ncb + 1) / 2;
   return std::max(1, ncb);
 }
@@ -1104,7 +1117,8 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF, kChainTiles>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B),
+                     dim3(64 * (4 * kChainTiles + 8)), 0, st, p);
   prof_mark(2, st, true);
   return hipGetLastError();
 }
