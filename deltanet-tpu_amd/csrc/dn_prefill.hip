@@ -693,7 +693,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
 // columns (one workgroup, 4 waves; wave w owns value tiles 2w, 2w+1).
 // ===========================================================================
 template <bool BF, class TV>
-__global__ __launch_bounds__(256) void k_value(const PF p) {
+__global__ __launch_bounds__(256, 2) void k_value(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
@@ -715,6 +715,17 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
   const ST* g_Ml = (const ST*)p.MAl + uf;
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
+
+  // the 20 nonzero T fragments (lower slabs), loaded first so their latency
+  // overlaps the w*v loads from HBM
+  F1 Tf[20];
+  {
+    int k = 0;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int s = 0; s <= rt / 2; ++s) Tf[k++] = SS::fa(g_T + fofs(rt, s, l));
+  }
 
   // (w*v)^T fragments of this wave's 32 value columns (rows = column, k =
   // token): each 16-token block is loaded row-wise and transposed by an
@@ -776,14 +787,15 @@ __global__ __launch_bounds__(256) void k_value(const PF p) {
   for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
+  {
+    int k = 0;
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt) {
+    for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s <= rt / 2) {
-        const F1 fa = SS::fa(g_T + fofs(rt, s, l));
-        P::m13(Uc[0][rt], fa, Bwv[0][s]);
-        P::m13(Uc[1][rt], fa, Bwv[1][s]);
+      for (int s = 0; s <= rt / 2; ++s) {
+        P::m13(Uc[0][rt], Tf[k], Bwv[0][s]);
+        P::m13(Uc[1][rt], Tf[k], Bwv[1][s]);
+        ++k;
       }
     }
   }
