@@ -35,9 +35,9 @@ constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
 constexpr int XP = 132;
 constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
-// 16-column tiles per chain workgroup (1 or 2: the workgroup has 4 * tiles + 8
-// waves).  One tile measured fastest: with two, each SIMD's MFMA pipe
-// carries two recurrence waves and the sequential path slows down.
+// 16-column tiles per chain workgroup.  One tile measured fastest: more tiles
+// share each chunk's Pn and X loads but lengthen the per-chunk MFMA work of
+// the recurrence and output waves.
 #ifndef DN_CHAIN_TILES
 #define DN_CHAIN_TILES 1
 #endif
@@ -74,7 +74,8 @@ __device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
 
 // ===========================================================================
 // k_prepass: everything per chunk that does not depend on the values (one
-// workgroup, 4 waves, per (chunk, execution head, batch)): chunk flags,
+// workgroup of 8 waves per (chunk, execution head, batch); wave w owns token
+// block w in the per-row phases and key tile w in phase 5): chunk flags,
 // Lambda, A and M, T = (I + A)^-1, W = T (b k e^Lambda), Pn = -ke^T W and
 // X = qe - M W; it also leaves T, ke^T and M for k_value.
 //
@@ -873,31 +874,29 @@ __global__ __launch_bounds__(256, 2) void k_value(const PF p) {
 // ===========================================================================
 // k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c, and the output
 // O_c = X_c S_c + Oi_c of every chunk.
-// One workgroup per (NCT 16-column tiles, exec head, batch), with waves in two
-// roles that meet at one LDS barrier per chunk:
-//   4 NCT recurrence waves: wave (j, w) owns state rows 32w..32w+31 of column
-//     tile j (fp32, in VGPRs) and publishes them to LDS as slab w of that
-//     tile's S_c^T fragment (split high / low bf16 in bf16 mode); after the
-//     barrier it reads the tile's four slabs to form S_{c+1}.  Only 8 MFMAs
-//     per wave sit on the sequential path.
-//   8 output waves: after the same barrier, output wave t reads the S_c^T
-//     fragments and computes token tile t of all NCT column tiles as
-//     O^T = S^T X^T + (M U)^T, beside the recurrence on the other wave slots
-//     of each SIMD.  X is loaded once per workgroup and chunk for all NCT
-//     tiles, which is what NCT > 1 saves (X and Pn are shared by every
-//     column tile of a head).
+// One workgroup of 12 waves per (NCT 16-column tiles, exec head, batch), in
+// two roles that meet at one LDS barrier per chunk:
+//   waves 0-3 (recurrence): wave w owns state rows 32w..32w+31 of the NCT
+//     column tiles (fp32, in VGPRs) and publishes them to LDS as slab w of
+//     each tile's S_c^T fragment (split high / low bf16 in bf16 mode); after
+//     the barrier it reads the fragments to form S_{c+1}.  Only 8 MFMAs per
+//     wave and tile sit on the sequential path.
+//   waves 4-11 (output): after the same barrier, wave 4+t reads the S_c^T
+//     fragments and computes token tile t of the NCT column tiles as
+//     O^T = S^T X^T + (M U)^T, beside the recurrence on the other wave
+//     slots of each SIMD.
 // Each role prefetches its next chunk's operands while the current one
 // computes.  The role is a scalar (wave-uniform) branch, and both roles
 // execute exactly one barrier per chunk.
 // ===========================================================================
 template <bool BF, int NCT>
-__global__ __launch_bounds__(64 * (4 * NCT + 8)) void k_chain(const PF p) {
+__global__ __launch_bounds__(768) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
-  constexpr int NT = 64 * (4 * NCT + 8);
+  constexpr int NT = 768;
   constexpr int FR = 4 * 64 * 8;   // elements of one tile's S^T fragment
   // S_c^T fragments per column tile, high and low words, double-buffered
   __shared__ __align__(16) ST Sh_s[2][NCT * FR];
@@ -914,22 +913,24 @@ __global__ __launch_bounds__(64 * (4 * NCT + 8)) void k_chain(const PF p) {
   for (int i = tid; i < 2 * p.NCb; i += NT) flg[i] = p.flags[(int64_t)b * p.NCb * 2 + i];
   __syncthreads();
 
-  if (wid < 4 * NCT) {
-    // ---------------- recurrence: column tile j, rows 32w.. ----------------
-    const int j = wid >> 2, w = wid & 3;
-    const int ct = ct0 + j;
-    const int n = 16 * ct + r16;
-    const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-    const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
-    f32x4 S[2];
+  if (wid < 4) {
+    // ---------------- recurrence: rows 32w.. of all NCT column tiles ----------------
+    const int w = wid;
+    f32x4 S[2][NCT];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int j = 0; j < NCT; ++j) {
+      const int n = 16 * (ct0 + j) + r16;
+      const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
+      const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          S[r][j][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
+    }
     struct Ops {
       F1 pf[2][4];
-      f32x4 qc[2], dv[2];
+      f32x4 qc[2][NCT], dv[2];
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
@@ -941,30 +942,36 @@ __global__ __launch_bounds__(64 * (4 * NCT + 8)) void k_chain(const PF p) {
       for (int r = 0; r < 2; ++r) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
-        o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) o.qc[r][j] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct0 + j, p.nct, l));
         o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
       }
     };
     auto step = [&](int c, const Ops& o) {
       const int is_new = flg[2 * c], same = flg[2 * c + 1];
-      if (is_new) { S[0] = zero4(); S[1] = zero4(); }
-      // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
-      {
-        const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
+#pragma unroll
+      for (int j = 0; j < NCT; ++j) {
+        if (is_new) { S[0][j] = zero4(); S[1][j] = zero4(); }
+        // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
+        const float x[8] = {S[0][j][0], S[0][j][1], S[0][j][2], S[0][j][3],
+                            S[1][j][0], S[1][j][1], S[1][j][2], S[1][j][3]};
         const int fo = j * FR + (w * 64 + l) * 8;
         SS::st8s(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo, x);
       }
       lds_barrier();
-      F1 Sf[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][j * FR + (s * 64 + l) * 8]);
+      for (int j = 0; j < NCT; ++j) {
+        F1 Sf[4];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        f32x4 acc = o.qc[r];
+        for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][j * FR + (s * 64 + l) * 8]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
+        for (int r = 0; r < 2; ++r) {
+          f32x4 acc = o.qc[r][j];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][ii] : 0.f);
+          for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) S[r][j][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][j][ii] : 0.f);
+        }
       }
     };
     Ops o0, o1;
@@ -978,12 +985,18 @@ __global__ __launch_bounds__(64 * (4 * NCT + 8)) void k_chain(const PF p) {
       step(c + 1, o1);
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int j = 0; j < NCT; ++j) {
+      const int n = 16 * (ct0 + j) + r16;
+      const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
+      const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][j][ii];
+    }
   } else {
     // ---------------- output: token tile rt of all NCT column tiles ----------------
-    const int rt = wid - 4 * NCT;
+    const int rt = wid - 4;
     struct Ops {
       F3 xb[4];      // X fragments of token tile rt
       f32x4 oi[NCT]; // (M U)^T tiles of token tile rt
@@ -1129,8 +1142,7 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF, kChainTiles>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B),
-                     dim3(64 * (4 * kChainTiles + 8)), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF, kChainTiles>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B), dim3(768), 0, st, p);
   prof_mark(2, st, true);
   return hipGetLastError();
 }
