@@ -83,8 +83,8 @@ __device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
 // to and including i (log2 units, double-float hi in X / lo in Y), so a
 // difference of two Lambdas is never the difference of two large cumulative
 // sums (no fp32 cancellation after a strongly decayed stretch).  Cross-block
-// factors come from the per-block totals: Off[a] / Suf[a] = sum of the totals
-// before / after block a.
+// factors come from the per-block totals (sums of the totals before / after
+// block a, kept as the exponentials Ea / Sa).
 //
 // Products whose result feeds another kernel are computed transposed where
 // that puts the result directly in its consumer's fragment layout (M^T, Pn^T,
@@ -102,8 +102,9 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   __shared__ float Y[CH * YP];        // Lambda lo -> Kc -> T fragment-native (ST)
   __shared__ float Ftab[8 * KD];      // e^{total of block b}
   __shared__ float Mid0[8 * KD];      // e^{g at the first token of block a}
-  __shared__ float Off[9 * KD];       // log2: sum of totals of blocks < a (Off[8] = Lambda_end)
-  __shared__ float Suf[8 * KD];       // log2: sum of totals of blocks > a
+  __shared__ float Ea[8 * KD];        // e^{Lambda at the first token of block a} (chunk-global)
+  __shared__ float Sa[8 * KD];        // e^{sum of the totals of blocks > a}
+  __shared__ float Fa[8 * KD];        // e^{Lambda(last) - Lambda(first token) of block a}
   __shared__ int doc[CH];
   __shared__ int unsafe_part[2][8];   // per 64-channel half: block needs the hierarchical path
 
@@ -243,11 +244,15 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     for (int a = 0; a < 8; ++a) tot[a] = X[(16 * a + 15) * XP + tid] + Y[(16 * a + 15) * XP + tid];
     float acc = 0.f;
 #pragma unroll
-    for (int a = 0; a < 8; ++a) { Off[a * KD + tid] = acc; acc += tot[a]; }
-    Off[8 * KD + tid] = acc;
+    for (int a = 0; a < 8; ++a) {
+      const float lsa = X[(16 * a) * XP + tid] + Y[(16 * a) * XP + tid];
+      Ea[a * KD + tid] = fast_exp2(acc + lsa);
+      acc += tot[a];
+    }
+    g_dv[tid] = fast_exp2(acc);   // e^{Lambda_end}
     acc = 0.f;
 #pragma unroll
-    for (int a = 7; a >= 0; --a) { Suf[a * KD + tid] = acc; acc += tot[a]; }
+    for (int a = 7; a >= 0; --a) { Sa[a * KD + tid] = fast_exp2(acc); acc += tot[a]; }
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
       Ftab[a * KD + tid] = fast_exp2(tot[a]);
@@ -255,10 +260,10 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
       // span of the block after its first token: Lambda(sa) - Lambda(ea) >= 0
       const int sa = 16 * a, ea = sa + 15;
       const float span = (X[sa * XP + tid] - X[ea * XP + tid]) + (Y[sa * XP + tid] - Y[ea * XP + tid]);
+      Fa[a * KD + tid] = fast_exp2(-span);
       const bool un = __any(span > kDiagSafeLog2);
       if (l == 0) unsafe_part[w][a] = un;
     }
-    g_dv[tid] = fast_exp2(Off[8 * KD + tid]);
   }
   __syncthreads();
 
@@ -374,30 +379,55 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      float lam[8], lsa[8], ta[8], laml[8], lsal[8], tal[8], off[8], suf[8];
+      float lam[8], lsa[8], laml[8], lsal[8], ea[8], sa[8];
       row8<float>(&X[i * XP + 32 * s], q, lam);
       row8<float>(&X[(16 * a) * XP + 32 * s], q, lsa);
-      row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
       row8<float>(&Y[i * XP + 32 * s], q, laml);
       row8<float>(&Y[(16 * a) * XP + 32 * s], q, lsal);
-      row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
-      row8<float>(&Off[a * KD + 32 * s], q, off);
-      row8<float>(&Suf[a * KD + 32 * s], q, suf);
+      row8<float>(&Ea[a * KD + 32 * s], q, ea);
+      row8<float>(&Sa[a * KD + 32 * s], q, sa);
       float rA[8], rM[8], bd[8], kc[8], qe[8], bt[8], kt[8];
+      if (!blk_unsafe) {
+        // every factor within 2^{+-100}: the exponentials of the row's
+        // decay relative to the block's first token and their products
+        float fa[8];
+        row8<float>(&Fa[a * KD + 32 * s], q, fa);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
-        const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
-        const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
-        const float er = fast_exp2(d_i_sa);
-        rA[e] = be * er;
-        rM[e] = qh * er;
-        kc[e] = kh * fast_exp2(d_ea_i);
-        const float eL = fast_exp2(off[e] + (lam[e] + laml[e]));
-        bt[e] = first ? be * eL : 0.f;
-        kt[e] = last ? kh * fast_exp2(suf[e] + d_ea_i) : 0.f;
-        bd[e] = kh * fast_exp2(-d_i_sa);
-        qe[e] = first ? qh * eL : 0.f;
+        for (int e = 0; e < 8; ++e) {
+          const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
+          const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
+          const float er = fast_exp2(d_i_sa);
+          const float rr = fast_exp2(-d_i_sa);
+          rA[e] = be * er;
+          rM[e] = qh * er;
+          const float ekc = fa[e] * rr;                 // e^{Lambda(ea) - Lambda(i)}
+          kc[e] = kh * ekc;
+          const float eL = ea[e] * er;                  // e^{Lambda(i)} (chunk-global)
+          bt[e] = first ? be * eL : 0.f;
+          kt[e] = last ? kc[e] * sa[e] : 0.f;
+          bd[e] = kh * rr;
+          qe[e] = first ? qh * eL : 0.f;
+        }
+      } else {
+        float ta[8], tal[8];
+        row8<float>(&X[(16 * a + 15) * XP + 32 * s], q, ta);
+        row8<float>(&Y[(16 * a + 15) * XP + 32 * s], q, tal);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float qh = qv[8 * s + e], kh = kv[8 * s + e], be = bet[8 * s + e];
+          const float d_i_sa = (lam[e] - lsa[e]) + (laml[e] - lsal[e]);   // <= 0
+          const float d_ea_i = (ta[e] - lam[e]) + (tal[e] - laml[e]);     // <= 0
+          const float er = fast_exp2(d_i_sa);
+          rA[e] = be * er;
+          rM[e] = qh * er;
+          const float ekc = fast_exp2(d_ea_i);
+          kc[e] = kh * ekc;
+          const float eL = ea[e] * er;
+          bt[e] = first ? be * eL : 0.f;
+          kt[e] = last ? kh * ekc * sa[e] : 0.f;
+          bd[e] = 0.f;   // unused: the hierarchical path formed this block's A and M
+          qe[e] = first ? qh * eL : 0.f;
+        }
       }
       Store<false>::st8(g_qe + fofs(a, s, l), qe);
       {
