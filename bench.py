@@ -196,7 +196,7 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
         lines.append(f"| {k} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
                      f"{fb / 1e6:.1f} | {wb / 1e6:.1f} | {alg.get(k, 0) / 1e6:.1f} | "
                      f"{(fb + wb) / alg[k]:.2f} |")
-    lines += ["", "Prefill intermediates (workspace) travel between the four launches; their round trips "
+    lines += ["", "Prefill intermediates (workspace) travel between the three launches; their round trips "
               "are the traffic above the algorithmic bytes."]
     with open(os.path.join(PROFILE_DIR, "prefill_cfg2_decode_cfg4_rocprof.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
