@@ -17,7 +17,7 @@
 //   k_prepass (grid: chunk x exec-head x batch, 8 waves, one chunk each)
 //       fused prologue, Lambda, A and M on MFMA, T by blocked substitution
 //       on fp32 MFMA, W, and the chunk operators Pn and X.
-//   k_value   (grid: chunk x 128-column pass x exec-head, 4 waves)
+//   k_value   (grid: chunk x 64-column group x exec-head, 2 waves)
 //       U = T (w*v), Q = ke^T U and Oi = M U.
 //   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
 //       the sequential scan over chunks with the fp32 state in VGPRs, and
@@ -34,6 +34,11 @@ namespace dn {
 constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
 constexpr int XP = 132;
+// waves per k_value workgroup (each owns 32 value columns); 2 measured fastest
+#ifndef DN_VALUE_WAVES
+#define DN_VALUE_WAVES 2
+#endif
+constexpr int kValueWaves = DN_VALUE_WAVES;
 constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
 // 16-column tiles per chain workgroup.  One tile measured fastest: more tiles
 // share each chunk's Pn and X loads but lengthen the per-chunk MFMA work of
@@ -720,11 +725,12 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
 }
 
 // ===========================================================================
-// k_value: U = T (w*v), Q = ke^T U and (M U)^T for one chunk and 128 value
-// columns (one workgroup, 4 waves; wave w owns value tiles 2w, 2w+1).
+// k_value: U = T (w*v), Q = ke^T U and (M U)^T for one chunk and 32 x
+// kValueWaves value columns (wave w owns value tiles 2w, 2w+1 of its group).
+// Small workgroups spread the work evenly over the CUs (3 per CU at config 2).
 // ===========================================================================
 template <bool BF, class TV>
-__global__ __launch_bounds__(256, 2) void k_value(const PF p) {
+__global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_value(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
@@ -763,21 +769,22 @@ __global__ __launch_bounds__(256, 2) void k_value(const PF p) {
   // identity product into half of a slab.
   F3 Bwv[2][4];
   {
-    const int hv = p.gates_at_hv ? h : h * p.G + pass;
+    const int col0 = 32 * (kValueWaves * pass + w);   // first of this wave's 32 columns
+    const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
     const int hw = vgate_head(p, p.w_h, hv);
     float vv[8][8], ww[8][8];
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
       const int t = tb + 16 * a + r16;
       const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
-      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + 32 * w, q, vv[a]);
+      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
       const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
       if (p.w_c == 1) {
         const float ws = wp[0];
 #pragma unroll
         for (int e = 0; e < 8; ++e) ww[a][e] = ws;
       } else {
-        row8<float>(wp + 32 * w, q, ww[a]);
+        row8<float>(wp + col0 % KD, q, ww[a]);
       }
     }
     const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
@@ -840,7 +847,7 @@ __global__ __launch_bounds__(256, 2) void k_value(const PF p) {
                           Uc[nt][2 * s + 1][0], Uc[nt][2 * s + 1][1], Uc[nt][2 * s + 1][2], Uc[nt][2 * s + 1][3]};
       U3[nt][s] = P::f3(x);
     }
-  const int ct0 = 8 * pass + 2 * w;   // value tile of nt = 0 within the execution head
+  const int ct0 = 2 * (kValueWaves * pass + w);   // value tile of nt = 0 within the execution head
   // Q tiles (rows = key, columns = value), the chain's accumulator layout
   auto q_tile = [&](int m, const F3 (&ka)[4]) {
     f32x4 Q0 = zero4(), Q1 = zero4();
@@ -1167,7 +1174,8 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(1, st, false);
-  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.NCb, p.Vp / KD, p.Hx * p.B), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.NCb, p.Vp / (32 * kValueWaves), p.Hx * p.B), dim3(64 * kValueWaves), 0,
+                     st, p);
   prof_mark(1, st, true);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
