@@ -262,6 +262,7 @@ template <> struct Store<true> {
     *reinterpret_cast<bf16x8*>(hi) = h;
     *reinterpret_cast<bf16x8*>(lo) = l;
   }
+  static __device__ __forceinline__ void stf(bf16* p, const F1& f) { *reinterpret_cast<bf16x8*>(p) = f.v; }
   static __device__ __forceinline__ void st4(bf16* p, const float* x) {
     bf16x4 h;
 #pragma unroll
@@ -317,6 +318,7 @@ template <> struct Store<false> {
     *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
   }
   static __device__ __forceinline__ void st8s(float* hi, float*, const float* x) { st8(hi, x); }
+  static __device__ __forceinline__ void stf(float* p, const F1& f) { st8(p, f.v); }
   static __device__ __forceinline__ void st4(float* p, const float* x) {
     *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
   }

@@ -491,46 +491,114 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   __syncthreads();
 
   // ---- phase 3: off-diagonal A/M blocks (X becomes A) -----------------------
-#pragma unroll
-  for (int bi = 0; bi < 1; ++bi) {
-    const int a = w;
-    float mloc[32];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) row8<float>(&Mid0[a * KD + 32 * s], q, mloc + 8 * s);
-    for (int bb = a - 1; bb >= 0; --bb) {
-      f32x4 accA = zero4(), accM = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float x[8];
-        row8<float>(&Y[(16 * bb + r16) * YP + 32 * s], q, x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= mloc[8 * s + e];
-        const F3 fb = P::f3(x);
-        P::m33(accA, Rf[bi][s], fb);   // A[16a + 4q + ii][16bb + r16]
-        P::m33(accM, fb, Qf[bi][s]);   // M[16a + r16][16bb + 4q + ii]
-      }
-      float mv[4];
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
-        X[ia * XP + jb] = (doc[ia] == doc[jb]) ? accA[ii] : 0.f;
-        mv[ii] = (doc[16 * a + r16] == doc[16 * bb + 4 * q + ii]) ? accM[ii] : 0.f;
-      }
-      const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
-      SS::st4s(g_Mh + mo, g_Ml + mo, mv);
+  // Block a has a pairs (a, bb < a).  Blocks 4..7 keep the pairs with
+  // bb >= lo(a) = 1, 2, 3, 3 and hand the others to wave 7 - a, whose own
+  // block has 7 - a pairs, so no wave computes more than 4.  The R / Q
+  // fragments of blocks 4..7 reach those waves through X, which holds nothing
+  // live between phases 2 and 4: every wave keeps its A tiles in registers
+  // until all pairs are done and writes them to X afterwards.
+  {
+    constexpr int RQA = 2048;                       // elements per fragment array
+    constexpr int RQB = (BF ? 4 : 2) * RQA;         // per block: R hi, (R lo,) Q hi, (Q lo)
+    ST* rq_s = reinterpret_cast<ST*>(X);
+    auto rq_ptr = [&](int a, int which, bool lo) -> ST* {   // which: 0 = R, 1 = Q
+      return rq_s + (a - 4) * RQB + (BF ? (2 * which + (lo ? 1 : 0)) : which) * RQA;
+    };
+    if (w >= 4) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        float f[8];
-        row8<float>(&Ftab[bb * KD + 32 * s], q, f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) mloc[8 * s + e] *= f[e];
+        const int o = (s * 64 + l) * 8;
+        SS::stf(rq_ptr(w, 0, false) + o, P::hi(Rf[0][s]));
+        SS::stf(rq_ptr(w, 1, false) + o, P::hi(Qf[0][s]));
+        if constexpr (BF) {
+          SS::stf(rq_ptr(w, 0, true) + o, Rf[0][s].lo);
+          SS::stf(rq_ptr(w, 1, true) + o, Qf[0][s].lo);
+        }
       }
     }
+    __syncthreads();
+    auto lo_of = [](int a) { return a < 4 ? 0 : (a == 4 ? 1 : (a == 5 ? 2 : 3)); };
+    f32x4 Ap[4];
+    int pa[4], pb[4];
+    int np = 0;
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int ia = 16 * a + 4 * q + ii;
-      X[ia * XP + 16 * a + r16] = Adiag[bi][ii];
-      if ((a & 1) == 0) X[ia * XP + 16 * a + 16 + r16] = 0.f;
+    for (int k = 0; k < 4; ++k) { Ap[k] = zero4(); pa[k] = 0; pb[k] = 0; }
+    auto pairs = [&](int a, const F3 (&RF)[4], const F3 (&QF)[4], int bb_hi, int bb_lo) {
+      float mloc[32];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) row8<float>(&Mid0[a * KD + 32 * s], q, mloc + 8 * s);
+      for (int b2 = a - 1; b2 > bb_hi; --b2) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float f[8];
+          row8<float>(&Ftab[b2 * KD + 32 * s], q, f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mloc[8 * s + e] *= f[e];
+        }
+      }
+      for (int bb = bb_hi; bb >= bb_lo; --bb) {
+        f32x4 accA = zero4(), accM = zero4();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float x[8];
+          row8<float>(&Y[(16 * bb + r16) * YP + 32 * s], q, x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] *= mloc[8 * s + e];
+          const F3 fb = P::f3(x);
+          P::m33(accA, RF[s], fb);   // A[16a + 4q + ii][16bb + r16]
+          P::m33(accM, fb, QF[s]);   // M[16a + r16][16bb + 4q + ii]
+        }
+        float mv[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
+          accA[ii] = (doc[ia] == doc[jb]) ? accA[ii] : 0.f;
+          mv[ii] = (doc[16 * a + r16] == doc[16 * bb + 4 * q + ii]) ? accM[ii] : 0.f;
+        }
+        const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
+        SS::st4s(g_Mh + mo, g_Ml + mo, mv);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (np == k) { Ap[k] = accA; pa[k] = a; pb[k] = bb; }
+        ++np;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float f[8];
+          row8<float>(&Ftab[bb * KD + 32 * s], q, f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mloc[8 * s + e] *= f[e];
+        }
+      }
+    };
+    pairs(w, Rf[0], Qf[0], w - 1, lo_of(w));
+    if (w < 4) {
+      const int a1 = 7 - w;
+      F3 RF[4], QF[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int o = (s * 64 + l) * 8;
+        RF[s] = SS::fa3(rq_ptr(a1, 0, false) + o, rq_ptr(a1, 0, true) + o);
+        QF[s] = SS::fa3(rq_ptr(a1, 1, false) + o, rq_ptr(a1, 1, true) + o);
+      }
+      pairs(a1, RF, QF, lo_of(a1) - 1, 0);
+    }
+    __syncthreads();
+    // A tiles of this wave's pairs and of its own diagonal block
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k < np) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) X[(16 * pa[k] + 4 * q + ii) * XP + 16 * pb[k] + r16] = Ap[k][ii];
+      }
+    }
+    {
+      const int a = w;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int ia = 16 * a + 4 * q + ii;
+        X[ia * XP + 16 * a + r16] = Adiag[0][ii];
+        if ((a & 1) == 0) X[ia * XP + 16 * a + 16 + r16] = 0.f;
+      }
     }
   }
   __syncthreads();
