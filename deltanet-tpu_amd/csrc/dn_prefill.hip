@@ -72,9 +72,19 @@ __device__ __forceinline__ int vgate_head(const PF& p, int H, int hv) {
   return (H == p.Hv) ? hv : hv / p.G;
 }
 
-__device__ __forceinline__ int64_t seg_at(const PF& p, int b, int t) {
+// A segment id as two 32-bit words loaded without a branch, so the loads can
+// be issued early (the value is only compared for equality).  int32 ids read
+// their word twice.
+struct SegId {
+  int32_t lo, hi;
+  __device__ __forceinline__ bool operator!=(const SegId& o) const { return lo != o.lo || hi != o.hi; }
+};
+__device__ __forceinline__ SegId seg_raw(const PF& p, int b, int t) {
   const int64_t i = p.seg_batched ? (int64_t)b * p.L + t : (int64_t)t;
-  return ld_i(p.seg, i, p.seg_dt);
+  const bool w64 = p.seg_dt == DT_I64;
+  const int32_t* s32 = (const int32_t*)p.seg + (w64 ? 2 * i : i);
+  const int32_t hi = s32[w64 ? 1 : 0];
+  return SegId{s32[0], w64 ? hi : 0};
 }
 
 // ===========================================================================
@@ -135,8 +145,37 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   float* g_qe = p.QeA + uf;
   float* g_dv = p.dvec + u * KD;
 
-  // q, k, b rows of this wave's token block (phase 2), loaded now so their
-  // latency overlaps phases 0 and 1
+  // Global loads are issued up front, in the order their values are needed
+  // (the vector-memory counter drains in order, so a load is only ever waited
+  // for together with the loads issued before it): segment ids (phase 0),
+  // gates g (phase 1), then the q, k, b rows of this wave's token block
+  // (phase 2), whose latency then overlaps phases 0 and 1.
+  // (every lane loads, under wave-uniform conditions only, so no value is
+  // consumed inside a divergent branch before it is needed)
+  SegId sg_t{0, 0}, sg_tp{0, 0}, sg_0{0, 0}, sg_a{0, 0}, sg_b{0, 0};
+  int32_t iseg = 0;
+  if (p.seg != nullptr) {
+    const int ti = tid & (CH - 1);
+    sg_t = seg_raw(p, b, min(tb + ti, t_end - 1));
+    sg_tp = seg_raw(p, b, max(min(tb + ti - 1, t_end - 1), 0));
+    sg_0 = seg_raw(p, b, 0);
+    sg_a = seg_raw(p, b, tb);
+    sg_b = seg_raw(p, b, max(tb - 1, 0));
+  }
+  if (p.init_seg != nullptr) iseg = p.init_seg[b];
+  const int g_part = tid >> 7;   // phase 1: 4 parts of 32 tokens, channel tid & 127
+  float gl[32];
+  {
+    const int kap = tid & 127;
+    const int hg = kgate_head(p, p.g_h, h);
+    const int tload = min(tb + 32 * g_part, t_end - 1);
+    const int nload = t_end - tload;   // >= 1
+    const int gstride = p.g_h * p.g_c;
+    const float* gp = (const float*)p.g + (((int64_t)b * p.L + tload) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
+    // out-of-range tokens read the last valid token and are zeroed in phase 1
+#pragma unroll
+    for (int i = 0; i < 32; ++i) gl[i] = gp[min(i, nload - 1) * gstride];
+  }
   const int hbg = kgate_head(p, p.b_h, h);
   Raw8<TIn> rq[4], rk[4];
   Raw8<float> rb[4];
@@ -159,16 +198,14 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
       for (int s = 0; s < 4; ++s) rb[s].load(bp + 32 * s, q);
     }
   }
+  // first use of the segment ids: only now, after every entry load is issued
+  // (an empty asm that "updates" them keeps the compiler from comparing them
+  // earlier, which would wait before the later loads are even issued)
+  asm volatile("" : "+v"(sg_t.lo), "+v"(sg_t.hi), "+v"(sg_tp.lo), "+v"(sg_tp.hi));
+  asm volatile("" : "+v"(sg_0.lo), "+v"(sg_0.hi), "+v"(sg_a.lo), "+v"(sg_a.hi), "+v"(sg_b.lo), "+v"(sg_b.hi));
 
   // ---- phase 0: in-chunk document index (segment canonicalisation) -------
-  if (tid < CH) {
-    int ch = 0;
-    if (p.seg != nullptr && tid > 0) {
-      const int t = min(tb + tid, t_end - 1), tp = min(tb + tid - 1, t_end - 1);
-      ch = seg_at(p, b, t) != seg_at(p, b, tp);
-    }
-    doc[tid] = ch;
-  }
+  if (tid < CH) doc[tid] = (p.seg != nullptr && tid > 0) ? (sg_t != sg_tp) : 0;
   __syncthreads();
   for (int off = 1; off < CH; off <<= 1) {
     int v = 0;
@@ -182,17 +219,17 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     if (tb == 0) {
       if (p.has_init) {
         is_new = 0;
-        if (p.init_seg != nullptr) {
-          const int64_t s0 = p.seg ? seg_at(p, b, 0) : 0;
-          is_new = s0 != (int64_t)p.init_seg[b];
-        }
+        // initial_state_segment_id is int32; a wider first id differs from it
+        // when its high word is not the sign extension of its low word
+        if (p.init_seg != nullptr)
+          is_new = (sg_0.lo != iseg) || (p.seg_dt == DT_I64 && sg_0.hi != (iseg < 0 ? -1 : 0));
       } else {
         is_new = 1;
       }
     } else if (c == 0 && !p.has_init) {
       is_new = 1;
     } else {
-      is_new = p.seg ? (seg_at(p, b, tb) != seg_at(p, b, tb - 1)) : 0;
+      is_new = p.seg ? (sg_a != sg_b) : 0;
     }
     p.flags[((int64_t)b * p.NCb + c) * 2 + 0] = is_new;
     p.flags[((int64_t)b * p.NCb + c) * 2 + 1] = (doc[CH - 1] == 0);
@@ -200,19 +237,8 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
 
   // ---- phase 1: block-local Lambda (double-float: X = hi, Y = lo), totals --
   {
-    const int kap = tid & 127, part = tid >> 7;   // 4 parts of 32 tokens
-    const int hg = kgate_head(p, p.g_h, h);
-    const int tbase = tb + 32 * part;
-    const int nvalid = t_end - tbase;  // tokens of this part inside the range (may be <= 0)
-    const int tload = min(tbase, t_end - 1);
-    const int nload = t_end - tload;   // >= 1
-    const int gstride = p.g_h * p.g_c;
-    const float* gp = (const float*)p.g + (((int64_t)b * p.L + tload) * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : kap);
-    // all 32 loads issued back to back; out-of-range tokens read the last
-    // valid token and are zeroed below
-    float gl[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) gl[i] = gp[min(i, nload - 1) * gstride];
+    const int kap = tid & 127, part = g_part;
+    const int nvalid = t_end - (tb + 32 * part);   // tokens of this part in range (may be <= 0)
     if (p.fuse) {
 #pragma unroll
       for (int i = 0; i < 32; ++i) gl[i] = -__expf(fminf(gl[i], 5.f));
