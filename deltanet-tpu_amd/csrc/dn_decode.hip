@@ -1,7 +1,7 @@
 // Single-token GDN-2 decode step on gfx950: a pure HBM stream of the
-// (B, Hv, K, V) state.  One workgroup of 512 lanes owns one (batch, value
-// head) 128x128 state: it reads the state once with 16-byte loads, keeps it in
-// VGPRs, and writes the updated state once.
+// (B, Hv, K, V) state.  One workgroup of 256 lanes owns one (batch, value
+// head) 128x128 state: it reads the state once with 16-byte non-temporal
+// loads, keeps it in VGPRs, and writes the updated state once.
 //
 // Reference: gdn2_decode_step (maelie-labs/deltanet-tpu v0.3.0,
 // src/deltanet_tpu/gdn2.py:2289-2490):
@@ -80,62 +80,95 @@ __device__ __forceinline__ int dgate_head(int H, int Hk, int Hv, int hv, int G) 
   return (H == Hv) ? hv : hv / G;
 }
 
-// sum over the 256 lanes of the workgroup; `buf` holds 4 floats
-__device__ __forceinline__ float block_sum256(float x, float* buf) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) buf[w] = x;
-  __syncthreads();
-  return buf[0] + buf[1] + buf[2] + buf[3];
-}
-
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
   return x;
 }
 
-// 8 consecutive state elements (16 bytes for bf16, 32 for fp32)
-template <class T> __device__ __forceinline__ void ld8(const T* p, float* o);
-template <> __device__ __forceinline__ void ld8<float>(const float* p, float* o) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) { o[e] = a[e]; o[4 + e] = b[e]; }
+#ifndef DN_DECODE_NT
+#define DN_DECODE_NT 1
+#endif
+
+template <class T> __device__ __forceinline__ T ldg(const T* p) {
+  if constexpr (DN_DECODE_NT) return __builtin_nontemporal_load(p);
+  else return *p;
 }
-template <> __device__ __forceinline__ void ld8<bf16>(const bf16* p, float* o) {
-  const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = (float)a[e];
-}
-template <class T> __device__ __forceinline__ void st8(T* p, const float* x);
-template <> __device__ __forceinline__ void st8<float>(float* p, const float* x) {
-  *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
-  *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
-}
-template <> __device__ __forceinline__ void st8<bf16>(bf16* p, const float* x) {
-  bf16x8 h;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = (bf16)x[e];
-  *reinterpret_cast<bf16x8*>(p) = h;
+template <class T> __device__ __forceinline__ void stg(T* p, const T& x) {
+  if constexpr (DN_DECODE_NT) __builtin_nontemporal_store(x, p);
+  else *p = x;
 }
 
-// One workgroup (4 waves) per (batch row, value head).  Lane (rg, cg) holds
-// state rows 8rg..8rg+7 and 8 columns: 8cg..8cg+7 for a bf16 state (one
-// 16-byte load per row), 4cg..4cg+3 and 64+4cg..64+4cg+3 for an fp32 state
-// (two 16-byte loads that each cover 256 contiguous bytes of the row).  Every global load (state, q, k,
-// gates, v) is issued at entry so their latencies overlap; the column sums
-// reduce inside each wave by shuffles, then across the 4 waves through LDS.
-// Small workgroups let several state matrices stream through a CU at once.
+// 8 state elements of one row held by one lane, kept in the stored format
+// until use: 8 consecutive bf16 (one 16-byte load), or for fp32 columns
+// 4c..4c+3 and 64+4c..64+4c+3 (two 16-byte loads that each cover 256
+// contiguous bytes of the row across the 16 column lanes).
+template <class T> struct Row8;
+template <> struct Row8<bf16> {
+  bf16x8 a;
+  __device__ __forceinline__ void load(const bf16* row, int cg) { a = ldg(reinterpret_cast<const bf16x8*>(row + 8 * cg)); }
+  __device__ __forceinline__ void zero() { a = bf16x8{}; }
+  __device__ __forceinline__ float at(int e) const { return (float)a[e]; }
+  static __device__ __forceinline__ int col(int cg, int e) { return 8 * cg + e; }
+  static __device__ __forceinline__ void store(bf16* row, int cg, const float* y) {
+    bf16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (bf16)y[e];
+    stg(reinterpret_cast<bf16x8*>(row + 8 * cg), h);
+  }
+};
+template <> struct Row8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* row, int cg) {
+    a = ldg(reinterpret_cast<const f32x4*>(row + 4 * cg));
+    b = ldg(reinterpret_cast<const f32x4*>(row + 64 + 4 * cg));
+  }
+  __device__ __forceinline__ void zero() { a = zero4(); b = zero4(); }
+  __device__ __forceinline__ float at(int e) const { return e < 4 ? a[e] : b[e - 4]; }
+  static __device__ __forceinline__ int col(int cg, int e) { return e < 4 ? 4 * cg + e : 60 + 4 * cg + e; }
+  static __device__ __forceinline__ void store(float* row, int cg, const float* y) {
+    stg(reinterpret_cast<f32x4*>(row + 4 * cg), f32x4{y[0], y[1], y[2], y[3]});
+    stg(reinterpret_cast<f32x4*>(row + 64 + 4 * cg), f32x4{y[4], y[5], y[6], y[7]});
+  }
+};
+// writes the 8 values of one lane's row segment in the output state format,
+// at the columns the input format gave that lane
 template <class TSin, class TSout>
-__global__ __launch_bounds__(256) void k_decode(const DP p) {
-  constexpr int K = 128, V = 128, R = 8;   // rows per lane
+__device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
+  if constexpr (sizeof(TSin) == sizeof(TSout)) {
+    Row8<TSin>::store(row, cg, y);
+  } else if constexpr (sizeof(TSin) == 4) {           // fp32 in, bf16 out
+    bf16x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { lo[e] = (bf16)y[e]; hi[e] = (bf16)y[4 + e]; }
+    stg(reinterpret_cast<bf16x4*>(row + 4 * cg), lo);
+    stg(reinterpret_cast<bf16x4*>(row + 64 + 4 * cg), hi);
+  } else {                                            // bf16 in, fp32 out
+    stg(reinterpret_cast<f32x4*>(row + 8 * cg), f32x4{y[0], y[1], y[2], y[3]});
+    stg(reinterpret_cast<f32x4*>(row + 8 * cg + 4), f32x4{y[4], y[5], y[6], y[7]});
+  }
+}
+
+#ifndef DN_DECODE_WAVES
+#define DN_DECODE_WAVES 4
+#endif
+constexpr int kDecodeWaves = DN_DECODE_WAVES;
+
+// One workgroup of NW waves per (batch row, value head).  Lane (rg, cg)
+// holds state rows R*rg..R*rg+R-1 (R = 32/NW), 8 columns per row (Row8
+// above).  Every global load (state, q, k, gates, v) is issued at entry so
+// their latencies overlap; the state loads and stores are non-temporal (each
+// byte is touched once per step).  The column sums reduce inside each wave by
+// shuffles, then across the NW waves through LDS.
+template <class TSin, class TSout, int NW>
+__global__ __launch_bounds__(64 * NW) void k_decode(const DP p) {
+  constexpr int K = 128, V = 128, R = K / (4 * NW);   // rows per lane
+  static_assert(NW >= 2 && K % (4 * NW) == 0, "waves per workgroup");
+  using RowIn = Row8<TSin>;
   __shared__ float qn[K], kn[K], dd[K], bt[K], vn[V];
-  __shared__ float red[2][4][V];
+  __shared__ float red[2][NW][V];
   __shared__ float rbuf[3][2];
-  __shared__ float gbuf[4];
+  __shared__ float gbuf[NW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -146,28 +179,17 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
   const bool rst = p.reset != nullptr && p.reset[bb] != 0;
   const int64_t sbase = (int64_t)bh * K * V;
 
-  constexpr bool kSplit = sizeof(TSin) == 4;
-  auto col = [&](int e) { return kSplit ? ((e < 4) ? 4 * cg + e : 60 + 4 * cg + e) : 8 * cg + e; };
-  float S[R][8];
+  RowIn S[R];
   const TSin* sp = (const TSin*)p.sin + sbase;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if (!rst) {
-      if constexpr (kSplit) {
-        ld4<TSin>(sp + (R * rg + r) * V + 4 * cg, S[r]);
-        ld4<TSin>(sp + (R * rg + r) * V + 64 + 4 * cg, S[r] + 4);
-      } else {
-        ld8<TSin>(sp + (R * rg + r) * V + 8 * cg, S[r]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) S[r][e] = 0.f;
-    }
+    if (!rst) S[r].load(sp + (R * rg + r) * V, cg);
+    else S[r].zero();
   }
   // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v
+  const int i = tid;
   float xq = 0.f, xk = 0.f, gv = 0.f, bv = 0.f, wv = 0.f, vv = 0.f;
   if (tid < 128) {
-    const int i = tid;
     const int64_t qo = ((int64_t)bb * p.Hk + hk) * K + i;
     xq = ld_f(p.q, qo, p.qk_dt);
     xk = ld_f(p.k, qo, p.qk_dt);
@@ -185,7 +207,6 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
   }
   __syncthreads();
   if (tid < 128) {
-    const int i = tid;
     float yq, yk;
     if (p.l2norm) {
       yq = xq / sqrtf(rbuf[0][0] + rbuf[0][1] + 1e-6f) * p.scale;
@@ -207,19 +228,19 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
   __syncthreads();
   const float qk = rbuf[2][0] + rbuf[2][1];
 
-  // decay, then this lane's partial column sums of b k^T S and q^T S
+  // this lane's partial column sums of b k^T (D S) and q^T (D S), D = diag(e^g)
   float pa[8], pc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) { pa[e] = 0.f; pc[e] = 0.f; }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int i = R * rg + r;
-    const float di = dd[i], bi = bt[i], qi = qn[i];
+    const int ii = R * rg + r;
+    const float di = dd[ii], bi = bt[ii] * di, qi = qn[ii] * di;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      S[r][e] *= di;
-      pa[e] += bi * S[r][e];
-      pc[e] += qi * S[r][e];
+      const float s = S[r].at(e);
+      pa[e] += bi * s;
+      pc[e] += qi * s;
     }
   }
   // the 4 row groups of a wave differ in lane bits 4 and 5
@@ -233,8 +254,8 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
   if (lane < 16) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      red[0][wid][col(e)] = pa[e];
-      red[1][wid][col(e)] = pc[e];
+      red[0][wid][RowIn::col(cg, e)] = pa[e];
+      red[1][wid][RowIn::col(cg, e)] = pc[e];
     }
   }
   __syncthreads();
@@ -242,7 +263,7 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
     const int j = tid;
     float A = 0.f, Cc = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { A += red[0][r][j]; Cc += red[1][r][j]; }
+    for (int r = 0; r < NW; ++r) { A += red[0][r][j]; Cc += red[1][r][j]; }
     const float nv = wv * vv - A;
     vn[j] = nv;
     const float o = Cc + qk * nv;
@@ -254,34 +275,38 @@ __global__ __launch_bounds__(256) void k_decode(const DP p) {
   __syncthreads();
   float vc[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) vc[e] = vn[col(e)];
-  float ss = 0.f;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float ki = kn[R * rg + r];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      S[r][e] += ki * vc[e];
-      ss += S[r][e] * S[r][e];
-    }
-  }
+  for (int e = 0; e < 8; ++e) vc[e] = vn[RowIn::col(cg, e)];
+  // S' = D S + k vn^T, then the optional Frobenius cap
   float fac = 1.f;
   if (p.guard) {
-    const float tot = block_sum256(ss, gbuf);
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ii = R * rg + r;
+      const float di = dd[ii], ki = kn[ii];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = fmaf(di, S[r].at(e), ki * vc[e]);
+        ss += y * y;
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) gbuf[wid] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += gbuf[w];
     fac = fminf(1.f, p.tau / sqrtf(tot + 1e-6f));
   }
   TSout* op = (TSout*)p.sout + sbase;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    const int ii = R * rg + r;
+    const float di = dd[ii], ki = kn[ii];
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = S[r][e] * fac;
-    if constexpr (kSplit) {
-      st4<TSout>(op + (R * rg + r) * V + 4 * cg, y);
-      st4<TSout>(op + (R * rg + r) * V + 64 + 4 * cg, y + 4);
-    } else {
-      st8<TSout>(op + (R * rg + r) * V + 8 * cg, y);
-    }
+    for (int e = 0; e < 8; ++e) y[e] = fmaf(di, S[r].at(e), ki * vc[e]) * fac;
+    store_row<TSin, TSout>(op + (R * rg + r) * V, cg, y);
   }
 }
 
@@ -361,14 +386,14 @@ extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
   p.w = a->w; p.w_dt = a->w_dtype; p.w_h = a->w_heads; p.w_c = a->w_chans;
   p.sin = a->state_in; p.sout = a->state_out; p.reset = a->reset; p.out = a->out;
   p.scale = a->scale; p.l2norm = a->qk_l2norm; p.guard = a->stability_guard; p.tau = a->stability_tau;
-  const dim3 grid((unsigned)(a->B * a->Hv));
   hipStream_t st = (hipStream_t)stream;
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
+  const dim3 grid((unsigned)(a->B * a->Hv)), blk(64 * kDecodeWaves);
   prof_mark(3, st, false);
-  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float>), grid, dim3(256), 0, st, p);
-  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16>), grid, dim3(256), 0, st, p);
-  else if (!fi && fo) hipLaunchKernelGGL((k_decode<bf16, float>), grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((k_decode<bf16, bf16>), grid, dim3(256), 0, st, p);
+  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float, kDecodeWaves>), grid, blk, 0, st, p);
+  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+  else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
+  else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
   prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));

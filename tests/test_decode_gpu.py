@@ -73,6 +73,23 @@ def test_decode_state_dtype_contract(state_dtype):
     assert rel_l2(as_np(s), rs) < tol
 
 
+@pytest.mark.parametrize("guard", [False, True])
+def test_decode_bf16_state_in_fp32_state_out(guard):
+    # a bf16 state read and an fp32 state written: the kernel's column layout
+    # follows the input format, the store widens it
+    B, Hk, Hv = 3, 2, 4
+    q, k, v, g, b, w = dec_inputs(8, B, Hk, Hv)
+    S = 0.1 * np.random.default_rng(6).standard_normal((B, Hv, 128, 128))
+    T = lambda x: to_dev(x)
+    s16 = T(S).to(torch.bfloat16)
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), s16, reset=torch.tensor([False, True, False]),
+                            state_dtype=torch.float32, stability_guard=guard, stability_tau=5.0)
+    assert s.dtype == torch.float32
+    ro, rs = O.decode_step(q, k, v, g, b, w, as_np(s16), reset=[False, True, False],
+                           stability_guard=guard, stability_tau=5.0)
+    check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", f"decode bf16->fp32 guard={guard}")
+
+
 def test_decode_bf16_state_tracks_fp32_over_10_steps():
     # test_inference.py:150-185
     B, Hk, Hv = 2, 2, 4
