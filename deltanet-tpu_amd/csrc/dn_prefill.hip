@@ -120,8 +120,10 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   __shared__ float Ea[8 * KD];        // e^{Lambda at the first token of block a} (chunk-global)
   __shared__ float Sa[8 * KD];        // e^{sum of the totals of blocks > a}
   __shared__ float Fa[8 * KD];        // e^{Lambda(last) - Lambda(first token) of block a}
+  __shared__ float Gt[8 * KD];        // e^{Lambda(first token of block a) - Lambda(row 64)}
   __shared__ int doc[CH];
   __shared__ int unsafe_part[2][8];   // per 64-channel half: block needs the hierarchical path
+  __shared__ int wide_part[2];        // per 64-channel half: the chunk-reference path is unsafe
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
@@ -273,14 +275,21 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     float tot[8];
 #pragma unroll
     for (int a = 0; a < 8; ++a) tot[a] = X[(16 * a + 15) * XP + tid] + Y[(16 * a + 15) * XP + tid];
-    float acc = 0.f;
+    float acc = 0.f, lg[8];
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
       const float lsa = X[(16 * a) * XP + tid] + Y[(16 * a) * XP + tid];
-      Ea[a * KD + tid] = fast_exp2(acc + lsa);
+      lg[a] = acc + lsa;   // chunk-global Lambda at the first token of block a
+      Ea[a * KD + tid] = fast_exp2(lg[a]);
       acc += tot[a];
     }
     g_dv[tid] = fast_exp2(acc);   // e^{Lambda_end}
+    // chunk reference row 64: every off-diagonal A / M entry factors as
+    // (row i: e^{Lambda_i - Lambda_64}) (column j: e^{Lambda_64 - Lambda_j}),
+    // both within 2^{+-100} when the spans on either side of row 64 are
+    bool wide = (lg[0] - lg[4] > kDiagSafeLog2) || (lg[4] - acc > kDiagSafeLog2);
+#pragma unroll
+    for (int a = 0; a < 8; ++a) Gt[a * KD + tid] = fast_exp2(lg[a] - lg[4]);
     acc = 0.f;
 #pragma unroll
     for (int a = 7; a >= 0; --a) { Sa[a * KD + tid] = fast_exp2(acc); acc += tot[a]; }
@@ -294,9 +303,16 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
       Fa[a * KD + tid] = fast_exp2(-span);
       const bool un = __any(span > kDiagSafeLog2);
       if (l == 0) unsafe_part[w][a] = un;
+      wide = wide || un;
     }
+    wide = __any(wide);
+    if (l == 0) wide_part[w] = wide;
   }
   __syncthreads();
+  // no block needs the hierarchical path and the chunk reference is safe:
+  // phase 2 leaves the column factors of every block as split fragments in
+  // Y, and phase 3 is MFMA products of stored fragments only
+  const bool chunk_ref = __builtin_amdgcn_readfirstlane(!(wide_part[0] | wide_part[1]));
 
   // ---- phase 2: per-row quantities, diagonal A/M blocks --------------------
   F3 Rf[1][4], Qf[1][4];
@@ -484,19 +500,41 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
           }
         }
       }
+      if (chunk_ref) {
+        // rows relative to row 64 instead of the block's first token
+        float gt[8];
+        row8<float>(&Gt[a * KD + 32 * s], q, gt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rA[e] *= gt[e];
+          rM[e] *= gt[e];
+          bd[e] *= __builtin_amdgcn_rcpf(gt[e]);
+        }
+      }
       Rf[bi][s] = P::f3(rA);
       Qf[bi][s] = P::f3(rM);
       if (!blk_unsafe) {
-        // A_aa, M_aa = (R, Qr) (k e^{Lambda_sa - Lambda})^T: every factor stays
+        // A_aa, M_aa = (R, Qr) (k e^{Lambda_ref - Lambda})^T: every factor stays
         // within 2^{+-100} of 1, so the factorisation cannot overflow.
         const F3 fb = P::f3(bd);
         P::m33(accA, Rf[bi][s], fb);
         P::m33(accM, fb, Qf[bi][s]);
+        if (chunk_ref) {
+          // the column factors replace this slab's 16 rows x 32 columns of
+          // Lambda low words (2 KB, once all lanes of the wave have read
+          // them) as the split fragment of lane l: row l / 4, 32 bytes at
+          // (l % 4) * 32 of the slab's 128 bytes in that row
+          ST* fp = reinterpret_cast<ST*>(&Y[(16 * a + (l >> 2)) * YP + 32 * s]) + (l & 3) * (32 / sizeof(ST));
+          SS::stf(fp, P::hi(fb));
+          if constexpr (BF) SS::stf(fp + 8, fb.lo);
+        }
       }
-      // Kc replaces this slab of the row's Lambda low words once all lanes of
-      // the wave have read it (the other slabs' columns are untouched)
-      st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
-      st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
+      if (!chunk_ref) {
+        // Kc replaces this slab of the row's Lambda low words once all lanes
+        // of the wave have read it (the other slabs' columns are untouched)
+        st4<float>(&Y[i * YP + 32 * s + 4 * q], kc);
+        st4<float>(&Y[i * YP + 32 * s + 16 + 4 * q], kc + 4);
+      }
     }
     // diagonal blocks: A (row-major, LDS) and M (fragment-native, rows = token)
     float mv[4];
@@ -549,7 +587,46 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     int np = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) { Ap[k] = zero4(); pa[k] = 0; pb[k] = 0; }
+    // one pair's A tile (rows of block a) and M^T tile, masked by document
+    auto pair_out = [&](int a, int bb, f32x4 accA, const f32x4& accM) {
+      float mv[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
+        accA[ii] = (doc[ia] == doc[jb]) ? accA[ii] : 0.f;
+        mv[ii] = (doc[16 * a + r16] == doc[16 * bb + 4 * q + ii]) ? accM[ii] : 0.f;
+      }
+      const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
+      SS::st4s(g_Mh + mo, g_Ml + mo, mv);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (np == k) { Ap[k] = accA; pa[k] = a; pb[k] = bb; }
+      ++np;
+    };
+    auto pairs_ref = [&](int a, const F3 (&RF)[4], const F3 (&QF)[4], int bb_hi, int bb_lo) {
+      for (int bb = bb_hi; bb >= bb_lo; --bb) {
+        f32x4 accA = zero4(), accM = zero4();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const ST* fp = reinterpret_cast<const ST*>(&Y[(16 * bb + (l >> 2)) * YP + 32 * s]) + (l & 3) * (32 / sizeof(ST));
+          F3 fb;
+          if constexpr (BF) {
+            fb.hi = SS::fa(fp);
+            fb.lo = SS::fa(fp + 8);
+          } else {
+            fb = SS::fa(fp);
+          }
+          P::m33(accA, RF[s], fb);   // A[16a + 4q + ii][16bb + r16]
+          P::m33(accM, fb, QF[s]);   // M[16a + r16][16bb + 4q + ii]
+        }
+        pair_out(a, bb, accA, accM);
+      }
+    };
     auto pairs = [&](int a, const F3 (&RF)[4], const F3 (&QF)[4], int bb_hi, int bb_lo) {
+      if (chunk_ref) {
+        pairs_ref(a, RF, QF, bb_hi, bb_lo);
+        return;
+      }
       float mloc[32];
 #pragma unroll
       for (int s = 0; s < 4; ++s) row8<float>(&Mid0[a * KD + 32 * s], q, mloc + 8 * s);
@@ -574,19 +651,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
           P::m33(accA, RF[s], fb);   // A[16a + 4q + ii][16bb + r16]
           P::m33(accM, fb, QF[s]);   // M[16a + r16][16bb + 4q + ii]
         }
-        float mv[4];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int ia = 16 * a + 4 * q + ii, jb = 16 * bb + r16;
-          accA[ii] = (doc[ia] == doc[jb]) ? accA[ii] : 0.f;
-          mv[ii] = (doc[16 * a + r16] == doc[16 * bb + 4 * q + ii]) ? accM[ii] : 0.f;
-        }
-        const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
-        SS::st4s(g_Mh + mo, g_Ml + mo, mv);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (np == k) { Ap[k] = accA; pa[k] = a; pb[k] = bb; }
-        ++np;
+        pair_out(a, bb, accA, accM);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           float f[8];

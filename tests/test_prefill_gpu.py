@@ -194,6 +194,29 @@ def test_strong_decay_finite(precision):
     check(out, ro, st, rs, precision, "fp32", f"strong decay {precision}")
 
 
+@pytest.mark.parametrize("decay", ["mild", "near_bound", "wide", "mixed"])
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_decay_span_paths(decay, precision):
+    # Off-diagonal A / M tiles factor around the chunk's row 64 when the decay
+    # on either side of it stays within 2^100 ("mild": ~2^9, "near_bound":
+    # ~2^92 per side), and fall back to per-pair rescaling otherwise ("wide":
+    # ~2^147 per side, each 16-token block still within bounds).  "mixed"
+    # varies the span per channel across the threshold, with a reset.
+    q, k, v, g, b, w = make_inputs(11, 1, 384, 2, 4)
+    rng = np.random.default_rng(12)
+    nat = {"mild": 0.1, "near_bound": 1.0, "wide": 1.6}
+    if decay == "mixed":
+        rate = np.where(np.arange(128) % 3 == 0, 1.6, np.where(np.arange(128) % 3 == 1, 0.9, 0.02))
+        g = -rate * np.exp(0.05 * rng.standard_normal(g.shape))
+    else:
+        g = -nat[decay] * np.exp(0.05 * rng.standard_normal(g.shape))
+    seg = (np.arange(384) >= 200).astype(np.int32)[None] if decay == "mixed" else None
+    init = 0.1 * rng.standard_normal((1, 4, 128, 128))
+    out, st, ro, rs = run_pair(q, k, v, g, b, w, precision=precision, qk_l2norm=True, seg=seg, init=init)
+    assert torch.isfinite(out).all() and torch.isfinite(st).all()
+    check(out, ro, st, rs, precision, "fp32", f"decay {decay} {precision}")
+
+
 def test_positive_decay_clamped():
     # test_strong_decay.py:72-89: g > 0 behaves as g = 0
     q, k, v, g, b, w = make_inputs(2, 1, 200, 2, 4)
