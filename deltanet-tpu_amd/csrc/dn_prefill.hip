@@ -604,21 +604,41 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
       ++np;
     };
     auto pairs_ref = [&](int a, const F3 (&RF)[4], const F3 (&QF)[4], int bb_hi, int bb_lo) {
-      for (int bb = bb_hi; bb >= bb_lo; --bb) {
-        f32x4 accA = zero4(), accM = zero4();
+      auto ld_fb = [&](int bb, F3 (&fb)[4]) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const ST* fp = reinterpret_cast<const ST*>(&Y[(16 * bb + (l >> 2)) * YP + 32 * s]) + (l & 3) * (32 / sizeof(ST));
-          F3 fb;
           if constexpr (BF) {
-            fb.hi = SS::fa(fp);
-            fb.lo = SS::fa(fp + 8);
+            fb[s].hi = SS::fa(fp);
+            fb[s].lo = SS::fa(fp + 8);
           } else {
-            fb = SS::fa(fp);
+            fb[s] = SS::fa(fp);
           }
-          P::m33(accA, RF[s], fb);   // A[16a + 4q + ii][16bb + r16]
-          P::m33(accM, fb, QF[s]);   // M[16a + r16][16bb + 4q + ii]
         }
+      };
+      F3 fb[4];
+      ld_fb(bb_hi, fb);
+      for (int bb = bb_hi; bb >= bb_lo; --bb) {
+        // two accumulators per tile (leading and correction products) halve
+        // the dependent MFMA chains
+        f32x4 accA = zero4(), accM = zero4(), accA2 = zero4(), accM2 = zero4();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          if constexpr (BF) {
+            mma(accA, RF[s].hi, fb[s].hi);   // A[16a + 4q + ii][16bb + r16]
+            mma(accM, fb[s].hi, QF[s].hi);   // M[16a + r16][16bb + 4q + ii]
+            mma(accA2, RF[s].hi, fb[s].lo);
+            mma(accM2, fb[s].hi, QF[s].lo);
+            mma(accA2, RF[s].lo, fb[s].hi);
+            mma(accM2, fb[s].lo, QF[s].hi);
+          } else {
+            P::m33(s & 1 ? accA2 : accA, RF[s], fb[s]);
+            P::m33(s & 1 ? accM2 : accM, fb[s], QF[s]);
+          }
+        }
+        if (bb > bb_lo) ld_fb(bb - 1, fb);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) { accA[ii] += accA2[ii]; accM[ii] += accM2[ii]; }
         pair_out(a, bb, accA, accM);
       }
     };
