@@ -17,7 +17,7 @@
 //   k_prepass (grid: chunk x exec-head x batch, 8 waves, one chunk each)
 //       fused prologue, Lambda, A and M on MFMA, T by blocked substitution
 //       on fp32 MFMA, W, and the chunk operators Pn and X.
-//   k_value   (grid: chunk x 64-column group x exec-head, 2 waves)
+//   k_value   (grid: 64-column group x chunk x exec-head, 2 waves)
 //       U = T (w*v), Q = ke^T U and Oi = M U.
 //   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
 //       the sequential scan over chunks with the fp32 state in VGPRs, and
@@ -918,7 +918,7 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
   int c, pass, zh;
-  xcd_block(c, pass, zh);
+  xcd_block(pass, c, zh);   // column passes of one chunk adjacent: one XCD's L2 serves T, ke, M
   const int h = zh % p.Hx, b = zh / p.Hx;
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
@@ -1353,7 +1353,7 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(1, st, false);
-  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.NCb, p.Vp / (32 * kValueWaves), p.Hx * p.B), dim3(64 * kValueWaves), 0,
+  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.Vp / (32 * kValueWaves), p.NCb, p.Hx * p.B), dim3(64 * kValueWaves), 0,
                      st, p);
   prof_mark(1, st, true);
   e = hipGetLastError();
