@@ -1228,10 +1228,9 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
 #pragma unroll
       for (int j = 0; j < NCT; ++j) o.oi[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ct0 + j, p.nct, l));
     };
+    f32x4 res[NCT];
     auto step = [&](int c, const Ops& o) {
       lds_barrier();
-      const int t = p.t0 + c * CH + 16 * rt + r16;
-      const bool tv = t < min(p.t0 + p.nt, p.L);
 #pragma unroll
       for (int j = 0; j < NCT; ++j) {
         f32x4 acc = o.oi[j];
@@ -1240,28 +1239,38 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
           const int fo = j * FR + (s * 64 + l) * 8;
           P::m33(acc, SS::fa3(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo), o.xb[s]);
         }
-        // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
-        const int ct = ct0 + j;
-        const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
-        if (tv) {
-          const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
-          const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-          if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob, x);
-          else st4<float>((float*)p.out + ob, x);
-        }
+        res[j] = acc;
       }
     };
-    // chunk c computes (and stores) before chunk c + 1's loads are issued
+    // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
+    auto store = [&](int c) {
+      const int t = p.t0 + c * CH + 16 * rt + r16;
+      if (t >= min(p.t0 + p.nt, p.L)) return;
+#pragma unroll
+      for (int j = 0; j < NCT; ++j) {
+        const int ct = ct0 + j;
+        const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
+        const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
+        const float x[4] = {res[j][0], res[j][1], res[j][2], res[j][3]};
+        if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob, x);
+        else st4<float>((float*)p.out + ob, x);
+      }
+    };
+    // Each chunk's prefetch is issued before its output store: the wait for
+    // a prefetched operand then never covers a store (the vector-memory
+    // counter counts stores too and drains in order).
     Ops o0, o1;
     load_ops(0, o0);
+    load_ops(1, o1);
 #pragma unroll 1
     for (int c = 0; c < p.NCb; c += 2) {
       step(c, o0);
       load_ops(c + 2, o0);
+      store(c);
       if (c + 1 >= p.NCb) break;
-      if (c == 0) load_ops(1, o1);
       step(c + 1, o1);
       load_ops(c + 3, o1);
+      store(c + 1);
     }
   }
 }
