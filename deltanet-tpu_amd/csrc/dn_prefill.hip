@@ -14,9 +14,11 @@
 //     S_next = [same doc] diag(e^Lend) S + Pn S + Q,  Pn = -ke^T W,  Q = ke^T U
 //     O      = X S + Oi,                              X = qe - M W,  Oi = M U
 // so:
-//   k_prepass (grid: chunk x exec-head x batch, 8 waves, one chunk each)
+//   k_prepass (grid: one workgroup of 8 waves per (batch, exec head, chunk)
+//       unit, plus one spare workgroup per CU the units leave idle)
 //       fused prologue, Lambda, A and M on MFMA, T by blocked substitution
-//       on fp32 MFMA, W, and the chunk operators Pn and X.
+//       on fp32 MFMA, W, and the chunk operators Pn and X; the spare
+//       workgroups form k_value's (w*v)^T fragments meanwhile.
 //   k_value   (grid: 64-column group x chunk x exec-head, 2 waves)
 //       U = T (w*v), Q = ke^T U and Oi = M U.
 //   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
@@ -87,6 +89,70 @@ __device__ __forceinline__ SegId seg_raw(const PF& p, int b, int t) {
   return SegId{s32[0], w64 ? hi : 0};
 }
 
+// (w*v)^T fragments of 32 value columns of execution head h, chunk c, from
+// column col0 (rows = value column, k = token): Bwv[nt][s] covers columns
+// col0 + 16nt .. + 15 and token slab s.  Each 16-token block is loaded
+// row-wise and transposed by an identity product into half of a slab (exact).
+template <bool BF, class TV>
+__device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int col0, int l,
+                                         typename Pol<BF>::F3 (&Bwv)[2][4]) {
+  using P = Pol<BF>;
+  using F1 = typename P::F1;
+  using F3 = typename P::F3;
+  const int r16 = l & 15, q = l >> 4;
+  const int tb = p.t0 + c * CH;
+  const int t_end = min(p.t0 + p.nt, p.L);
+  const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
+  const int hw = vgate_head(p, p.w_h, hv);
+  float vv[8][8], ww[8][8];
+#pragma unroll
+  for (int a = 0; a < 8; ++a) {
+    const int t = tb + 16 * a + r16;
+    const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
+    row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
+    const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
+    if (p.w_c == 1) {
+      const float ws = wp[0];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ww[a][e] = ws;
+    } else {
+      row8<float>(wp + col0 % KD, q, ww[a]);
+    }
+  }
+  const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
+#pragma unroll
+  for (int a = 0; a < 8; ++a) {
+    const bool valid = tb + 16 * a + r16 < t_end;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float wg = p.fuse ? sigmoid_fast(ww[a][e]) : ww[a][e];
+      x[e] = valid ? wg * vv[a][e] : 0.f;
+    }
+    const F3 fx = P::f3(x);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x4 chi = zero4();
+      mma(chi, P::hi(fx), nt ? id1 : id0);
+      // lane (c, q): column 16nt + c, tokens 16a + 4q + ii -> slab a/2, half a&1
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        if constexpr (BF) {
+          Bwv[nt][a >> 1].hi.v[4 * (a & 1) + ii] = (bf16)chi[ii];
+        } else {
+          Bwv[nt][a >> 1].v[4 * (a & 1) + ii] = chi[ii];
+        }
+      }
+      if constexpr (BF) {
+        f32x4 clo = zero4();
+        mma(clo, fx.lo, nt ? id1 : id0);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) Bwv[nt][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)clo[ii];
+      }
+    }
+  }
+}
+
 // ===========================================================================
 // k_prepass: everything per chunk that does not depend on the values (one
 // workgroup of 8 waves per (chunk, execution head, batch); wave w owns token
@@ -127,8 +193,49 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+  const int units = p.B * p.Hx * p.NCb;
+  if ((int)blockIdx.x >= units) {
+    // Spare workgroup (one per CU the chunk units leave idle): the value
+    // kernel's (w*v)^T fragments.  It first sleeps ~3 us, through most of
+    // the chunk units' HBM-bound entry loads (a fixed delay, not a wait on
+    // other workgroups: nothing here depends on another workgroup).  Measured
+    // at config 2: value 25.3 -> 21.2 us, prepass +1 us, step 88.4 -> 85.2 us.
+#ifndef DN_WV_SLEEP
+#define DN_WV_SLEEP 1
+#endif
+#pragma unroll
+    for (int i = 0; i < DN_WV_SLEEP; ++i) __builtin_amdgcn_s_sleep(127);
+    const int groups = p.Vp / 32;
+    const int nwave = (gridDim.x - units) * 8;
+    for (int it = (blockIdx.x - units) * 8 + w; it < units * groups; it += nwave) {
+      const int u = it / groups, col0 = 32 * (it % groups);
+      const int uc = u % p.NCb, uh = (u / p.NCb) % p.Hx, ub = u / (p.NCb * p.Hx);
+      F3 Bwv[2][4];
+      if (p.v_dt == DT_BF16) wv_frags<BF, bf16>(p, ub, uh, uc, col0, l, Bwv);
+      else wv_frags<BF, float>(p, ub, uh, uc, col0, l, Bwv);
+      const int64_t uw = (int64_t)u * (CH * p.Vp);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int o = fofs(col0 / 16 + nt, s, l);
+          SS::stf((ST*)p.WVh + uw + o, P::hi(Bwv[nt][s]));
+          if constexpr (BF) SS::stf((ST*)p.WVl + uw + o, Bwv[nt][s].lo);
+        }
+    }
+    return;
+  }
+  // chunk unit: the XCD-aware remap over the units only (the hardware deals
+  // linear block ids to the 8 XCDs round-robin; the spare workgroups come last)
   int c, h, b;
-  xcd_block(c, h, b);
+  {
+    int id = blockIdx.x;
+    if ((units & 7) == 0) id = (id & 7) * (units >> 3) + (id >> 3);
+    c = id % p.NCb;
+    id /= p.NCb;
+    h = id % p.Hx;
+    b = id / p.Hx;
+  }
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
@@ -944,59 +1051,20 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
   }
 
   // (w*v)^T fragments of this wave's 32 value columns (rows = column, k =
-  // token): each 16-token block is loaded row-wise and transposed by an
-  // identity product into half of a slab.
+  // token): produced by the prepass launch's spare workgroups, or here
   F3 Bwv[2][4];
   {
     const int col0 = 32 * (kValueWaves * pass + w);   // first of this wave's 32 columns
-    const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
-    const int hw = vgate_head(p, p.w_h, hv);
-    float vv[8][8], ww[8][8];
+    if (p.wv_pre) {
+      const int64_t uw = u * (int64_t)(CH * p.Vp);
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const int t = tb + 16 * a + r16;
-      const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
-      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
-      const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
-      if (p.w_c == 1) {
-        const float ws = wp[0];
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ww[a][e] = ws;
-      } else {
-        row8<float>(wp + col0 % KD, q, ww[a]);
-      }
-    }
-    const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const bool valid = tb + 16 * a + r16 < t_end;
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float wg = p.fuse ? sigmoid_fast(ww[a][e]) : ww[a][e];
-        x[e] = valid ? wg * vv[a][e] : 0.f;
-      }
-      const F3 fx = P::f3(x);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x4 chi = zero4();
-        mma(chi, P::hi(fx), nt ? id1 : id0);
-        // lane (c, q): column 16nt + c, tokens 16a + 4q + ii -> slab a/2, half a&1
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          if constexpr (BF) {
-            Bwv[nt][a >> 1].hi.v[4 * (a & 1) + ii] = (bf16)chi[ii];
-          } else {
-            Bwv[nt][a >> 1].v[4 * (a & 1) + ii] = chi[ii];
-          }
-        }
-        if constexpr (BF) {
-          f32x4 clo = zero4();
-          mma(clo, fx.lo, nt ? id1 : id0);
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) Bwv[nt][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)clo[ii];
-        }
-      }
+        for (int s = 0; s < 4; ++s)
+          Bwv[nt][s] = SS::fa3((const ST*)p.WVh + uw + fofs(col0 / 16 + nt, s, l),
+                               (const ST*)p.WVl + uw + fofs(col0 / 16 + nt, s, l));
+    } else {
+      wv_frags<BF, TV>(p, b, h, c, col0, l, Bwv);
     }
   }
   f32x4 Uc[2][8];
@@ -1281,10 +1349,23 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, carry, total;
+  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, WVh, WVl, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// compute units of the current device (queried once per device)
+int num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = -1;
+    cache[dev] = n > 0 ? n : -1;
+  }
+  return cache[dev] > 0 ? cache[dev] : 0;
+}
 
 // Split operands (X, St, ke^T, M) have a low-word array in bf16 mode only.
 WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
@@ -1309,6 +1390,8 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   L.MAl = take(units * sq * ls);
   L.QeA = take(units * sq * 4);
   L.TA = take(units * sq * es);
+  L.WVh = take(units * CH * Vp * es);
+  L.WVl = take(units * CH * Vp * ls);
   L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
   L.total = off;
   return L;
@@ -1357,7 +1440,7 @@ int check_args(const dn_prefill_args* a) {
 template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.NCb, p.Hx, p.B), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.B * p.Hx * p.NCb + p.wv_wgs), dim3(512), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1442,6 +1525,8 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.MAl = bf ? ws + Lw.MAl : p.MAh;
   p.QeA = (float*)(ws + Lw.QeA);
   p.TA = ws + Lw.TA;
+  p.WVh = ws + Lw.WVh;
+  p.WVl = bf ? ws + Lw.WVl : p.WVh;
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
 
   hipStream_t st = (hipStream_t)stream;
@@ -1450,6 +1535,11 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
     p.t0 = tb;
     p.nt = std::min(ncb * CH, t_stop - tb);
     p.NCb = (p.nt + CH - 1) / CH;
+    // CUs the chunk units leave idle during the prepass (one unit per CU)
+    // take the (w*v)^T fragments off the value kernel
+    const int units = p.B * p.Hx * p.NCb;
+    p.wv_wgs = units < num_cus() ? num_cus() - units : 0;
+    p.wv_pre = p.wv_wgs > 0;
     const bool first = tb == a->t0;
     p.has_init = first ? (a->init_state != nullptr) : 1;
     p.init = first ? a->init_state : carry;

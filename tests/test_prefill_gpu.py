@@ -217,6 +217,20 @@ def test_decay_span_paths(decay, precision):
     check(out, ro, st, rs, precision, "fp32", f"decay {decay} {precision}")
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_units_fill_every_cu(precision):
+    # When the (batch, head, chunk) units leave no CU idle during the prepass,
+    # the value kernel forms (w*v)^T itself instead of reading the fragments
+    # the prepass launch's spare workgroups write.  Size B so that the units
+    # cover every CU of this device.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    L, Hk, Hv = 512, 4, 8
+    B = -(-cus // (Hk * (L // 128)))
+    q, k, v, g, b, w = make_inputs(21, B, L, Hk, Hv)
+    out, st, ro, rs = run_pair(q, k, v, g, b, w, precision=precision, qk_l2norm=True)
+    check(out, ro, st, rs, precision, "fp32", f"units fill CUs B={B} {precision}")
+
+
 def test_positive_decay_clamped():
     # test_strong_decay.py:72-89: g > 0 behaves as g = 0
     q, k, v, g, b, w = make_inputs(2, 1, 200, 2, 4)
