@@ -45,6 +45,7 @@ struct PF {
   float* QeA;                // F  [8][4]      f32: q e^Lambda, first document
   void* TA;                  // F  [8][4]      ST : T = (I + A)^-1
   void *WVh, *WVl;           // F  [Vp/16][4]  ST : (w*v)^T, rows = value column (k_value B operand)
+  void* sink;                // 1 KB the chain's output lanes past the last token store into
   int wv_pre;                // WVh / WVl are produced by the prepass launch's spare workgroups
   int wv_wgs;                // number of those spare workgroups
 };

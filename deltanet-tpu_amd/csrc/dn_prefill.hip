@@ -1173,7 +1173,7 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
 // computes.  The role is a scalar (wave-uniform) branch, and both roles
 // execute exactly one barrier per chunk.
 // ===========================================================================
-template <bool BF, int NCT>
+template <bool BF, int NCT, class TO>
 __global__ __launch_bounds__(768) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
@@ -1310,18 +1310,22 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
         res[j] = acc;
       }
     };
-    // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii]
+    // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii].  Every
+    // lane stores (tokens past the end into the workspace's sink): a store
+    // skipped under a branch would leave the compiler unsure how many
+    // vector-memory operations are pending at the loop head, and it would
+    // then wait for all of them (the prefetches included).
     auto store = [&](int c) {
       const int t = p.t0 + c * CH + 16 * rt + r16;
-      if (t >= min(p.t0 + p.nt, p.L)) return;
+      const bool tv = t < min(p.t0 + p.nt, p.L);
 #pragma unroll
       for (int j = 0; j < NCT; ++j) {
         const int ct = ct0 + j;
         const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
-        const int64_t ob = (((int64_t)b * p.L + t) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
+        const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
+        TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
         const float x[4] = {res[j][0], res[j][1], res[j][2], res[j][3]};
-        if (p.v_dt == DT_BF16) st4<bf16>((bf16*)p.out + ob, x);
-        else st4<float>((float*)p.out + ob, x);
+        st4<TO>(dst, x);
       }
     };
     // Each chunk's prefetch is issued before its output store: the wait for
@@ -1330,15 +1334,23 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
     Ops o0, o1;
     load_ops(0, o0);
     load_ops(1, o1);
+    // whole pairs of chunks in the loop, an odd last chunk after it (an exit
+    // in the middle of the loop body costs a full vector-memory drain at the
+    // loop head)
+    const int npair = p.NCb / 2;
 #pragma unroll 1
-    for (int c = 0; c < p.NCb; c += 2) {
+    for (int k = 0; k < npair; ++k) {
+      const int c = 2 * k;
       step(c, o0);
       load_ops(c + 2, o0);
       store(c);
-      if (c + 1 >= p.NCb) break;
       step(c + 1, o1);
       load_ops(c + 3, o1);
       store(c + 1);
+    }
+    if (p.NCb & 1) {
+      step(p.NCb - 1, o0);
+      store(p.NCb - 1);
     }
   }
 }
@@ -1349,7 +1361,7 @@ __global__ __launch_bounds__(768) void k_chain(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, WVh, WVl, carry, total;
+  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, WVh, WVl, sink, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1392,6 +1404,7 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   L.TA = take(units * sq * es);
   L.WVh = take(units * CH * Vp * es);
   L.WVl = take(units * CH * Vp * ls);
+  L.sink = take(64 * 16);
   L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
   L.total = off;
   return L;
@@ -1451,7 +1464,7 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF, kChainTiles>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B), dim3(768), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF, kChainTiles, TV>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B), dim3(768), 0, st, p);
   prof_mark(2, st, true);
   return hipGetLastError();
 }
@@ -1525,6 +1538,7 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.MAl = bf ? ws + Lw.MAl : p.MAh;
   p.QeA = (float*)(ws + Lw.QeA);
   p.TA = ws + Lw.TA;
+  p.sink = ws + Lw.sink;
   p.WVh = ws + Lw.WVh;
   p.WVl = bf ? ws + Lw.WVl : p.WVh;
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
