@@ -104,19 +104,26 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
   const int t_end = min(p.t0 + p.nt, p.L);
   const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
   const int hw = vgate_head(p, p.w_h, hv);
+  // all 16 row loads are issued before any is used (the w layout test sits
+  // outside the row loops: a branch between them would make each row wait
+  // for the one before)
   float vv[8][8], ww[8][8];
+  auto row_bt = [&](int a) { return (int64_t)b * p.L + min(tb + 16 * a + r16, t_end - 1); };
+  if (p.w_c == 1) {
 #pragma unroll
-  for (int a = 0; a < 8; ++a) {
-    const int t = tb + 16 * a + r16;
-    const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
-    row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
-    const float* wp = (const float*)p.w + (bt * p.w_h + hw) * p.w_c;
-    if (p.w_c == 1) {
-      const float ws = wp[0];
+    for (int a = 0; a < 8; ++a) {
+      const int64_t bt = row_bt(a);
+      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
+      const float ws = ((const float*)p.w)[bt * p.w_h + hw];
 #pragma unroll
       for (int e = 0; e < 8; ++e) ww[a][e] = ws;
-    } else {
-      row8<float>(wp + col0 % KD, q, ww[a]);
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      const int64_t bt = row_bt(a);
+      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
+      row8<float>((const float*)p.w + (bt * p.w_h + hw) * p.w_c + col0 % KD, q, ww[a]);
     }
   }
   const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
