@@ -857,41 +857,60 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     }
 #pragma unroll
     for (int ii = 0; ii < 16; ++ii) X[(16 * a + ii) * XP + 16 * a + r16] = tc[ii];
+    // and transposed (Tt = Y, free during this phase: row 16a + r16 holds
+    // column r16 of the block), the B operand layout of the steps below
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      *reinterpret_cast<f32x4*>(&Y[(16 * a + r16) * YP + 16 * a + 4 * i4]) =
+          f32x4{tc[4 * i4], tc[4 * i4 + 1], tc[4 * i4 + 2], tc[4 * i4 + 3]};
   }
   __syncthreads();
+  // Block row a: T[a][bt] = -D_a sum_{cc = bt}^{a-1} A[a][cc] T[cc][bt], by
+  // wave bt.  Each 16x16x16 product runs as 4 steps of the 16x16x4 fp32
+  // MFMA with lane (r, q) holding reduction index 4q + kk at step kk, so a
+  // lane's A operand (row of A) and B operand (row of T^T, kept in Y) are
+  // one 16-byte LDS read each; all of a step's reads are issued before its
+  // MFMAs, and the sum runs in two accumulation chains.
+  float* Tt = Y;
   for (int a = 1; a < 8; ++a) {
-    f32x4 res[1];
+    const int bt = w;
+    f32x4 res = zero4();
+    if (bt < a) {
+      f32x4 Ar[7], Br[7];
 #pragma unroll
-    for (int k2 = 0; k2 < 1; ++k2) {
-      const int bt = w;
-      res[k2] = zero4();
-      if (bt < a) {
-        f32x4 acc = zero4();
-        for (int cc = bt; cc < a; ++cc) {
+      for (int cc = 0; cc < 7; ++cc) {
+        if (cc >= bt && cc < a) {
+          Ar[cc] = *reinterpret_cast<const f32x4*>(&X[(16 * a + r16) * XP + 16 * cc + 4 * q]);
+          Br[cc] = *reinterpret_cast<const f32x4*>(&Tt[(16 * bt + r16) * YP + 16 * cc + 4 * q]);
+        }
+      }
+      const f32x4 Dr = *reinterpret_cast<const f32x4*>(&X[(16 * a + r16) * XP + 16 * a + 4 * q]);
+      f32x4 acc0 = zero4(), acc1 = zero4();
+#pragma unroll
+      for (int cc = 0; cc < 7; ++cc) {
+        if (cc >= bt && cc < a) {
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
-            const float av = X[(16 * a + r16) * XP + 16 * cc + 4 * kk + q];
-            const float bv = X[(16 * cc + 4 * kk + q) * XP + 16 * bt + r16];
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+            if (cc & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(Ar[cc][kk], Br[cc][kk], acc1, 0, 0, 0);
+            else acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(Ar[cc][kk], Br[cc][kk], acc0, 0, 0, 0);
           }
         }
-        f32x4 r = zero4();
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const float av = X[(16 * a + r16) * XP + 16 * a + 4 * q + kk];
-          r = __builtin_amdgcn_mfma_f32_16x16x4f32(av, acc[kk], r, 0, 0, 0);
-        }
-        res[k2] = -r;
       }
+      f32x4 acc;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) acc[ii] = acc0[ii] + acc1[ii];
+      // lane (j, q) holds P[4q + ii][j]: the B operand of step kk is acc[kk]
+      f32x4 r = zero4();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) r = __builtin_amdgcn_mfma_f32_16x16x4f32(Dr[kk], acc[kk], r, 0, 0, 0);
+      res = -r;
     }
     __syncthreads();
+    if (bt < a) {
+      // lane (j, q) holds T[16a + 4q + ii][16bt + j]
 #pragma unroll
-    for (int k2 = 0; k2 < 1; ++k2) {
-      const int bt = w;
-      if (bt < a) {
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) X[(16 * a + 4 * q + ii) * XP + 16 * bt + r16] = res[k2][ii];
-      }
+      for (int ii = 0; ii < 4; ++ii) X[(16 * a + 4 * q + ii) * XP + 16 * bt + r16] = res[ii];
+      *reinterpret_cast<f32x4*>(&Tt[(16 * bt + r16) * YP + 16 * a + 4 * q]) = res;
     }
     __syncthreads();
   }
