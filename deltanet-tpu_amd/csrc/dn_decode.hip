@@ -109,6 +109,17 @@ template <> struct Row8<bf16> {
   __device__ __forceinline__ void load(const bf16* row, int cg) { a = ldg(reinterpret_cast<const bf16x8*>(row + 8 * cg)); }
   __device__ __forceinline__ void zero() { a = bf16x8{}; }
   __device__ __forceinline__ float at(int e) const { return (float)a[e]; }
+  // the same value through an opaque instruction: the compiler cannot reuse
+  // an earlier conversion, so it keeps the 4 packed words live instead of 8
+  // expanded floats between the two passes over the state
+  __device__ __forceinline__ float at2(int e) const {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const uint32_t wd = __builtin_bit_cast(u4, a)[e >> 1];
+    uint32_t r;
+    if (e & 1) asm("v_and_b32 %0, 0xffff0000, %1" : "=v"(r) : "v"(wd));
+    else asm("v_lshlrev_b32 %0, 16, %1" : "=v"(r) : "v"(wd));
+    return __builtin_bit_cast(float, r);
+  }
   static __device__ __forceinline__ int col(int cg, int e) { return 8 * cg + e; }
   static __device__ __forceinline__ void store(bf16* row, int cg, const float* y) {
     bf16x8 h;
@@ -125,6 +136,7 @@ template <> struct Row8<float> {
   }
   __device__ __forceinline__ void zero() { a = zero4(); b = zero4(); }
   __device__ __forceinline__ float at(int e) const { return e < 4 ? a[e] : b[e - 4]; }
+  __device__ __forceinline__ float at2(int e) const { return at(e); }
   static __device__ __forceinline__ int col(int cg, int e) { return e < 4 ? 4 * cg + e : 60 + 4 * cg + e; }
   static __device__ __forceinline__ void store(float* row, int cg, const float* y) {
     stg(reinterpret_cast<f32x4*>(row + 4 * cg), f32x4{y[0], y[1], y[2], y[3]});
@@ -286,7 +298,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DP p) {
       const float di = dd[ii], ki = kn[ii];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float y = fmaf(di, S[r].at(e), ki * vc[e]);
+        const float y = fmaf(di, S[r].at2(e), ki * vc[e]);
         ss += y * y;
       }
     }
@@ -305,7 +317,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DP p) {
     const float di = dd[ii], ki = kn[ii];
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = fmaf(di, S[r].at(e), ki * vc[e]) * fac;
+    for (int e = 0; e < 8; ++e) y[e] = fmaf(di, S[r].at2(e), ki * vc[e]) * fac;
     store_row<TSin, TSout>(op + (R * rg + r) * V, cg, y);
   }
 }
