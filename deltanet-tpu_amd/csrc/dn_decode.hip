@@ -73,6 +73,7 @@ struct DP {
   const uint8_t* reset;
   void* out;
   float scale; int l2norm, guard; float tau;
+  int T;   // tokens per call (dn_decode_steps); per-token tensors carry a T axis after B
 };
 
 __device__ __forceinline__ int dgate_head(int H, int Hk, int Hv, int hv, int G) {
@@ -322,6 +323,182 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DP p) {
   }
 }
 
+// T consecutive decode steps in one launch: the state stays in registers
+// (fp32) across the tokens and is read and written once.  Every step is the
+// single-step computation above, in the same order; with a bf16 output state
+// the state is rounded to bf16 after every token, as T chained single steps
+// would store it.  The per-token LDS vectors are double-buffered by token
+// parity, so a token's writes never race the previous token's reads (every
+// wave has passed the previous token's barriers before it writes).
+template <class TSin, class TSout, int NW>
+__global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
+  constexpr int K = 128, V = 128, R = K / (4 * NW);   // rows per lane
+  static_assert(NW >= 2 && K % (4 * NW) == 0, "waves per workgroup");
+  using RowIn = Row8<TSin>;
+  __shared__ float qn[2][K], kn[2][K], dd[2][K], bt[2][K], vn[2][V];
+  __shared__ float red[2][2][NW][V];
+  __shared__ float rbuf[2][3][2];
+  __shared__ float gbuf[2][NW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int cg = tid & 15, rg = tid >> 4;
+  const int bh = blockIdx.x;
+  const int bb = bh / p.Hv, hv = bh % p.Hv;
+  const int hk = hv / p.G;
+  const int T = p.T;
+  const int64_t sbase = (int64_t)bh * K * V;
+
+  float S[R][8];
+  {
+    const TSin* sp = (const TSin*)p.sin + sbase;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      RowIn raw;
+      raw.load(sp + (R * rg + r) * V, cg);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) S[r][e] = raw.at(e);
+    }
+  }
+  // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v
+  const int i = tid;
+  const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
+  const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
+  const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+  float xq = 0.f, xk = 0.f, gv = 0.f, bv = 0.f, wv = 0.f, vv = 0.f;
+  auto ld_tok = [&](int t) {
+    if (tid < 128) {
+      const int64_t bt_ = (int64_t)bb * T + t;
+      const int64_t qo = (bt_ * p.Hk + hk) * K + i;
+      xq = ld_f(p.q, qo, p.qk_dt);
+      xk = ld_f(p.k, qo, p.qk_dt);
+      gv = ld_f(p.g, (bt_ * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
+      bv = ld_f(p.b, (bt_ * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
+      wv = ld_f(p.w, (bt_ * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
+      vv = ld_f(p.v, (bt_ * p.Hv + hv) * V + i, p.v_dt);
+    }
+  };
+  ld_tok(0);
+#pragma unroll 1
+  for (int t = 0; t < T; ++t) {
+    const int u = t & 1;
+    if (p.reset != nullptr && p.reset[(int64_t)bb * T + t] != 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) S[r][e] = 0.f;
+    }
+    {
+      const float sq = wave_sum(xq * xq), sk = wave_sum(xk * xk);
+      if (lane == 0 && wid < 2) { rbuf[u][0][wid] = sq; rbuf[u][1][wid] = sk; }
+    }
+    __syncthreads();
+    if (tid < 128) {
+      float yq, yk;
+      if (p.l2norm) {
+        yq = xq / sqrtf(rbuf[u][0][0] + rbuf[u][0][1] + 1e-6f) * p.scale;
+        yk = xk / sqrtf(rbuf[u][1][0] + rbuf[u][1][1] + 1e-6f);
+      } else {
+        yq = xq * p.scale;
+        yk = xk;
+      }
+      float g_ = fminf(gv, 0.f);
+      float b_ = bv;
+      if (p.guard) { b_ = fmaxf(b_, 0.f); g_ = fminf(g_, -1e-6f); }
+      qn[u][i] = yq;
+      kn[u][i] = yk;
+      dd[u][i] = __expf(g_);
+      bt[u][i] = b_ * yk;
+      const float qk = wave_sum(yq * yk);
+      if (lane == 0) rbuf[u][2][wid] = qk;
+    }
+    const float wv_t = wv, vv_t = vv;
+    if (t + 1 < T) ld_tok(t + 1);   // the next token's inputs load meanwhile
+    __syncthreads();
+    const float qk = rbuf[u][2][0] + rbuf[u][2][1];
+
+    float pa[8], pc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { pa[e] = 0.f; pc[e] = 0.f; }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ii = R * rg + r;
+      const float di = dd[u][ii], bi = bt[u][ii] * di, qi = qn[u][ii] * di;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pa[e] += bi * S[r][e];
+        pc[e] += qi * S[r][e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pa[e] += __shfl_xor(pa[e], 16);
+      pa[e] += __shfl_xor(pa[e], 32);
+      pc[e] += __shfl_xor(pc[e], 16);
+      pc[e] += __shfl_xor(pc[e], 32);
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        red[u][0][wid][RowIn::col(cg, e)] = pa[e];
+        red[u][1][wid][RowIn::col(cg, e)] = pc[e];
+      }
+    }
+    __syncthreads();
+    if (tid < V) {
+      const int j = tid;
+      float A = 0.f, Cc = 0.f;
+#pragma unroll
+      for (int r = 0; r < NW; ++r) { A += red[u][0][r][j]; Cc += red[u][1][r][j]; }
+      const float nv = wv_t * vv_t - A;
+      vn[u][j] = nv;
+      const float o = Cc + qk * nv;
+      const int64_t oi = (((int64_t)bb * T + t) * p.Hv + hv) * V + j;
+      if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)o;
+      else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)o;
+      else ((float*)p.out)[oi] = o;
+    }
+    __syncthreads();
+    float vc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vc[e] = vn[u][RowIn::col(cg, e)];
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ii = R * rg + r;
+      const float di = dd[u][ii], ki = kn[u][ii];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        S[r][e] = fmaf(di, S[r][e], ki * vc[e]);
+        ss += S[r][e] * S[r][e];
+      }
+    }
+    if (p.guard) {
+      ss = wave_sum(ss);
+      if (lane == 0) gbuf[u][wid] = ss;
+      __syncthreads();
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) tot += gbuf[u][w];
+      const float fac = fminf(1.f, p.tau / sqrtf(tot + 1e-6f));
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) S[r][e] *= fac;
+    }
+    if constexpr (sizeof(TSout) == 2) {
+      // the state a bf16 single step would store and the next one load
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) S[r][e] = (float)(bf16)S[r][e];
+    }
+  }
+  TSout* op = (TSout*)p.sout + sbase;
+#pragma unroll
+  for (int r = 0; r < R; ++r) store_row<TSin, TSout>(op + (R * rg + r) * V, cg, S[r]);
+}
+
 __global__ __launch_bounds__(256) void k_frob_cap(float* S, int64_t per, float tau) {
   __shared__ float buf[4];
   float* m = S + (int64_t)blockIdx.x * per;
@@ -372,11 +549,13 @@ extern "C" int dn_profile_end(double* ms_sum, int64_t* launches) {
 
 extern "C" int dn_abi_version(void) { return DN_ABI_VERSION; }
 
-extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
+namespace {
+int decode_launch(const dn_decode_args* a, int T, void* stream) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
   if (a->abi_version != DN_ABI_VERSION) return set_error(DN_E_ABI, "dn_decode_args built for another ABI version");
   if (a->K != 128 || a->V != 128) return set_error(DN_E_INVALID, "K and V must both be 128");
   if (a->B <= 0 || a->Hk <= 0 || a->Hv <= 0 || a->Hv % a->Hk) return set_error(DN_E_INVALID, "bad head counts");
+  if (T <= 0) return set_error(DN_E_INVALID, "T must be positive");
   if (!a->q || !a->k || !a->v || !a->g || !a->b || !a->w || !a->state_in || !a->state_out || !a->out)
     return set_error(DN_E_INVALID, "missing tensor pointer");
   auto gate_ok = [&](int H, int Cc, int dt) {
@@ -398,18 +577,33 @@ extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) {
   p.w = a->w; p.w_dt = a->w_dtype; p.w_h = a->w_heads; p.w_c = a->w_chans;
   p.sin = a->state_in; p.sout = a->state_out; p.reset = a->reset; p.out = a->out;
   p.scale = a->scale; p.l2norm = a->qk_l2norm; p.guard = a->stability_guard; p.tau = a->stability_tau;
+  p.T = T;
   hipStream_t st = (hipStream_t)stream;
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
   const dim3 grid((unsigned)(a->B * a->Hv)), blk(64 * kDecodeWaves);
   prof_mark(3, st, false);
-  if (fi && fo) hipLaunchKernelGGL((k_decode<float, float, kDecodeWaves>), grid, blk, 0, st, p);
-  else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16, kDecodeWaves>), grid, blk, 0, st, p);
-  else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
-  else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+  if (T == 1) {
+    if (fi && fo) hipLaunchKernelGGL((k_decode<float, float, kDecodeWaves>), grid, blk, 0, st, p);
+    else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+    else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
+    else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+  } else {
+    if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kDecodeWaves>), grid, blk, 0, st, p);
+    else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+    else if (fo) hipLaunchKernelGGL((k_decode_multi<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
+    else hipLaunchKernelGGL((k_decode_multi<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+  }
   prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;
+}
+}  // namespace
+
+extern "C" int dn_decode_step(const dn_decode_args* a, void* stream) { return decode_launch(a, 1, stream); }
+
+extern "C" int dn_decode_steps(const dn_decode_args* a, int32_t T, void* stream) {
+  return decode_launch(a, T, stream);
 }
 
 extern "C" int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, float tau, void* stream) {

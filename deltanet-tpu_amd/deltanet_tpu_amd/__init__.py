@@ -2,7 +2,7 @@
 delta-rule recurrence core of maelie-labs/deltanet-tpu (chunk_gdn2,
 gdn2_decode_step and their variants).  See ``gdn2.py`` for the API."""
 
-from .gdn2 import chunk_gdn2, gdn2_decode_step
+from .gdn2 import chunk_gdn2, gdn2_decode_step, gdn2_decode_steps
 from .variants import (
     chunk_delta_rule,
     chunk_gdn,
@@ -19,6 +19,7 @@ __version__ = "0.3.0+mi355x.1"
 __all__ = [
     "chunk_gdn2",
     "gdn2_decode_step",
+    "gdn2_decode_steps",
     "chunk_gdn",
     "gdn_decode_step",
     "chunk_kda",

@@ -70,6 +70,7 @@ EXPORTED_SYMBOLS = (
     "dn_prefill_workspace_size",
     "dn_prefill_fwd",
     "dn_decode_step",
+    "dn_decode_steps",
     "dn_state_frob_cap",
     "dn_last_error",
     "dn_abi_version",
@@ -100,6 +101,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         lib.dn_prefill_fwd.restype = ctypes.c_int
         lib.dn_decode_step.argtypes = [ctypes.POINTER(DecodeArgs), _c_ptr]
         lib.dn_decode_step.restype = ctypes.c_int
+        lib.dn_decode_steps.argtypes = [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr]
+        lib.dn_decode_steps.restype = ctypes.c_int
         lib.dn_state_frob_cap.argtypes = [_c_ptr, ctypes.c_int64, _c_i32, _c_i32, ctypes.c_float, _c_ptr]
         lib.dn_state_frob_cap.restype = ctypes.c_int
         lib.dn_last_error.argtypes = []

@@ -458,3 +458,123 @@ def gdn2_decode_step(
         o = o[:, None]
     return o, s_out
 
+
+def gdn2_decode_steps(
+    q, k, v, g, b, w, state, *,
+    reset=None,
+    scale=None,
+    qk_l2norm: bool = False,
+    state_dtype=None,
+    stability_guard: bool = False,
+    stability_tau: float = 1000.0,
+    out_state=None,
+):
+    """T consecutive GDN-2 decode steps in one launch (an extension: the
+    reference has the single step only, gdn2.py:2289-2490).
+
+    q, k: (B, T, Hk, K); v: (B, T, Hv, V); g, b: (B, T, Hx) or (B, T, Hx, K)
+    and w: (B, T, Hx) or (B, T, Hx, V) with Hx in {1, Hk, Hv}; state
+    (B, Hv, K, V).  ``reset`` is None, (B,) (clear the state before the first
+    token) or (B, T) (clear it before each marked token).  Returns
+    ``(output (B, T, Hv, V), new_state)``, equal to T chained
+    ``gdn2_decode_step`` calls: the state is read and written once, and with
+    ``state_dtype`` bfloat16 it is rounded to bf16 after every token as the
+    chained calls would store it.
+    """
+    if stability_guard and isinstance(stability_tau, (int, float)) and not stability_tau > 0:
+        raise ValueError(f"stability_tau must be positive, got {stability_tau}.")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError(f"q, k, v must have rank 4 (B, T, H, D), got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}.")
+    B, T, Hk, K = q.shape
+    if tuple(k.shape) != (B, T, Hk, K):
+        raise ValueError(f"Key tensor k shape {tuple(k.shape)} must match query q shape ({B}, {T}, {Hk}, {K}).")
+    if v.shape[0] != B or v.shape[1] != T:
+        raise ValueError(f"Value tensor v shape {tuple(v.shape)} must start with (B, T) = ({B}, {T}).")
+    Hv, V = v.shape[2], v.shape[3]
+    if K != 128 or V != 128:
+        raise ValueError(f"Unsupported head dimensions (K={K}, V={V}); requires K=128 and V=128.")
+    if Hv % Hk != 0:
+        raise ValueError(f"Value heads ({Hv}) must be divisible by key heads ({Hk}).")
+    if T < 1:
+        raise ValueError(f"T must be at least 1, got {T}.")
+    if tuple(state.shape) != (B, Hv, K, V):
+        raise ValueError(f"state shape {tuple(state.shape)} must match ({B}, {Hv}, {K}, {V}).")
+    if state_dtype is not None:
+        sd = state_dtype
+        if isinstance(sd, str):
+            sd = {"float32": torch.float32, "fp32": torch.float32, "bfloat16": torch.bfloat16,
+                  "bf16": torch.bfloat16}.get(sd.lower())
+        if sd not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"state_dtype must be float32 or bfloat16, got {state_dtype!r}.")
+        target_state_dtype = sd
+    else:
+        target_state_dtype = torch.float32
+    for name, t, last in (("g", g, K), ("b", b, K), ("w", w, V)):
+        if (t.ndim not in (3, 4) or t.shape[0] != B or t.shape[1] != T or t.shape[2] not in (1, Hk, Hv)
+                or (t.ndim == 4 and t.shape[3] not in (1, last))):
+            dim = "K" if name != "w" else "V"
+            raise ValueError(f"{name} shape {tuple(t.shape)} invalid for batch={B}, T={T}, Hk={Hk}, Hv={Hv}, {dim}={last}.")
+    reset_t = None
+    if reset is not None:
+        r = reset if isinstance(reset, torch.Tensor) else torch.as_tensor(np.asarray(reset))
+        r = r.to(torch.bool)
+        if r.ndim == 0:
+            r = r.reshape(1)
+        if r.ndim == 1:
+            if r.numel() not in (1, B):
+                raise ValueError(f"reset batch dimension ({r.shape[0]}) must match input batch dimension ({B}).")
+            first = torch.broadcast_to(r, (B,))
+            r = torch.zeros((B, T), dtype=torch.bool, device=r.device)
+            r[:, 0] = first
+        elif tuple(r.shape) != (B, T):
+            raise ValueError(f"reset must have shape (B,) or (B, T) = ({B}, {T}), got {tuple(r.shape)}.")
+        reset_t = r.to(torch.uint8)
+
+    dev = _require_gpu(q, k, v, g, b, w, state)
+    if reset_t is not None:
+        reset_t = reset_t.to(dev).contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(K)
+    if q.dtype not in _DT or k.dtype != q.dtype:
+        q = q.to(torch.float32)
+        k = k.to(torch.float32)
+    q, k = q.contiguous(), k.contiguous()
+    v_in = _float_arg(v)
+    # the kernel indexes every per-token tensor as (B*T, ...): fold T into B
+    fold = lambda t: t.reshape((B * T,) + tuple(t.shape[2:]))
+    g_t, g_h, g_c = _decode_gate(fold(g), B * T, Hk, Hv, K, "g")
+    b_t, b_h, b_c = _decode_gate(fold(b), B * T, Hk, Hv, K, "b")
+    w_t, w_h, w_c = _decode_gate(fold(w), B * T, Hk, Hv, V, "w")
+    s_in = state
+    if s_in.dtype not in (torch.float32, torch.bfloat16):
+        s_in = s_in.to(torch.float32)
+    s_in = s_in.contiguous()
+    if out_state is not None:
+        if tuple(out_state.shape) != (B, Hv, K, V) or out_state.dtype != target_state_dtype or not out_state.is_contiguous():
+            raise ValueError("out_state must be a contiguous (B, Hv, K, V) tensor of state_dtype.")
+        s_out = out_state
+    else:
+        s_out = torch.empty((B, Hv, K, V), dtype=target_state_dtype, device=dev)
+    out = torch.empty((B, T, Hv, V), dtype=v_in.dtype, device=dev)
+
+    a = _lib.DecodeArgs()
+    a.abi_version = _lib.DN_ABI_VERSION
+    a.B, a.Hk, a.Hv, a.K, a.V = B, Hk, Hv, K, V
+    a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v_in)
+    a.qk_dtype, a.v_dtype = _DT[q.dtype], _DT[v_in.dtype]
+    a.g, a.g_dtype, a.g_heads, a.g_chans = _ptr(g_t), _DT[g_t.dtype], g_h, g_c
+    a.b, a.b_dtype, a.b_heads, a.b_chans = _ptr(b_t), _DT[b_t.dtype], b_h, b_c
+    a.w, a.w_dtype, a.w_heads, a.w_chans = _ptr(w_t), _DT[w_t.dtype], w_h, w_c
+    a.state_in, a.state_in_dtype = _ptr(s_in), _DT[s_in.dtype]
+    a.state_out, a.state_out_dtype = _ptr(s_out), _DT[s_out.dtype]
+    a.reset = _ptr(reset_t)
+    a.out = _ptr(out)
+    a.scale = float(scale)
+    a.qk_l2norm = int(bool(qk_l2norm))
+    a.stability_guard = int(bool(stability_guard))
+    a.stability_tau = float(stability_tau)
+    lib = _lib.load_library()
+    _lib.check(lib.dn_decode_steps(ctypes.byref(a), int(T), _stream(dev)), "dn_decode_steps")
+    o = out if out.dtype == v.dtype else out.to(v.dtype)
+    return o, s_out
+

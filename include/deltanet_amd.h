@@ -118,6 +118,17 @@ typedef struct dn_decode_args {
  * reset, GQA repeat, L2-norm, decay/erase/write/readout, cap, state cast). */
 int dn_decode_step(const dn_decode_args* a, void* stream);
 
+/* T consecutive decode steps in one launch (no counterpart in the reference:
+ * the multi-token decode it lists as a next step, for speculative decoding and
+ * small-batch serving, where one state read and write per T tokens replaces T).
+ * Same arguments as dn_decode_step except that every per-token tensor carries
+ * a token axis after the batch axis: q, k (B,T,Hk,K); v, out (B,T,Hv,V); gates
+ * (B,T,Hx,Cx); reset NULL or (B,T), clearing the state before that token.  The
+ * result equals T chained dn_decode_step calls (the state is rounded to bf16
+ * after every token when state_out_dtype is bf16; stability_guard caps after
+ * every token).  T == 1 is dn_decode_step. */
+int dn_decode_steps(const dn_decode_args* a, int32_t T, void* stream);
+
 /* In-place Frobenius cap S <- S * min(1, tau / sqrt(||S||_F^2 + 1e-6)) of
  * `nmat` consecutive (rows x cols) float32 matrices (the stability_guard cap of
  * gdn2.py:2180-2188 / 2224-2226 / 2236-2238). */
@@ -127,7 +138,7 @@ int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, fl
  * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
  * every dn_prefill_fwd call on the calling thread records HIP events on its
  * stream around each of its kernels (prepass, value, chain) and every
- * dn_decode_step call around its kernel.  dn_profile_end() waits for those
+ * dn_decode_step / dn_decode_steps call around its kernel.  dn_profile_end() waits for those
  * events and writes, per kernel kind, the summed duration in milliseconds
  * and the number of launches (arrays of DN_PROFILE_KINDS entries). */
 #define DN_PROFILE_KINDS 4   /* 0 prepass, 1 value, 2 chain, 3 decode */

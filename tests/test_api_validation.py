@@ -152,3 +152,22 @@ def test_channel_wise_beta_in_variants_raises():
         kda_decode_step(qd, qd, torch.zeros(1, 4, 128), torch.zeros(1, 2, 128), torch.zeros(1, 2, 128), st)
     with pytest.raises(ValueError, match="channel-wise beta with shape"):
         delta_rule_decode_step(qd, qd, torch.zeros(1, 4, 128), torch.zeros(1, 2, 128), st)
+
+
+def test_decode_steps_validation():
+    from deltanet_tpu_amd import gdn2_decode_steps
+    B, T, Hk, Hv = 2, 3, 2, 4
+    q = torch.zeros(B, T, Hk, 128)
+    v = torch.zeros(B, T, Hv, 128)
+    g = torch.zeros(B, T, Hk, 128)
+    st = torch.zeros(B, Hv, 128, 128)
+    with pytest.raises(ValueError, match="rank 4"):
+        gdn2_decode_steps(q[:, 0], q[:, 0], v[:, 0], g, g, v, st)
+    with pytest.raises(ValueError, match="must start with"):
+        gdn2_decode_steps(q, q, v[:, :2], g, g, v, st)
+    with pytest.raises(ValueError, match="invalid for batch"):
+        gdn2_decode_steps(q, q, v, g[:, :2], g, v, st)
+    with pytest.raises(ValueError, match="reset must have shape"):
+        gdn2_decode_steps(q, q, v, g, g, v, st, reset=torch.zeros(B, T + 1, dtype=torch.bool))
+    with pytest.raises(ValueError, match="state shape"):
+        gdn2_decode_steps(q, q, v, g, g, v, st[:1])

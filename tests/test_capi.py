@@ -79,4 +79,7 @@ def test_invalid_args_rejected_without_gpu():
     d.abi_version = _lib.DN_ABI_VERSION
     d.B, d.Hk, d.Hv, d.K, d.V = 1, 2, 3, 128, 128
     assert lib.dn_decode_step(ctypes.byref(d), None) == -1
+    assert lib.dn_decode_steps(ctypes.byref(d), 4, None) == -1
+    d.Hv = 4
+    assert lib.dn_decode_steps(ctypes.byref(d), 0, None) == -1 and b"T must be positive" in lib.dn_last_error()
     assert lib.dn_state_frob_cap(None, 1, 128, 128, 1.0, None) == -1

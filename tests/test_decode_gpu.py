@@ -7,8 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from deltanet_tpu_amd import (chunk_gdn2, delta_rule_decode_step, gdn2_decode_step, gdn_decode_step,
-                              gla_decode_step, kda_decode_step)
+from deltanet_tpu_amd import (chunk_gdn2, delta_rule_decode_step, gdn2_decode_step, gdn2_decode_steps,
+                              gdn_decode_step, gla_decode_step, kda_decode_step)
 from oracle import gdn_oracle as O
 from tests._util import rel_l2, sig
 from tests.gpu_common import as_np, check, to_dev
@@ -184,3 +184,77 @@ def test_decode_variants(variant):
         o, s = delta_rule_decode_step(T(q), T(k), T(v), T(beta), T(S), qk_l2norm=True)
         ro, rs = O.decode_step(q, k, v, np.zeros((B, 1)), beta[:, 0], beta[:, 0], S, qk_l2norm=True)
     check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", f"decode {variant}")
+
+
+def steps_inputs(seed, B, T, Hk, Hv, gate_heads="hk"):
+    rng = np.random.default_rng(seed)
+    Hg = Hk if gate_heads == "hk" else Hv
+    q = rng.standard_normal((B, T, Hk, 128))
+    k = rng.standard_normal((B, T, Hk, 128))
+    v = rng.standard_normal((B, T, Hv, 128))
+    g = -np.exp(0.39 * rng.standard_normal((B, T, Hg, 128)) - 1)
+    b = sig(0.39 * rng.standard_normal((B, T, Hg, 128)))
+    w = sig(0.39 * rng.standard_normal((B, T, Hv, 128)))
+    return q, k, v, g, b, w
+
+
+@pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("guard", [False, True])
+def test_decode_steps_equal_chained_steps(state_dtype, guard):
+    # one launch over T tokens == T chained single steps (per-token resets,
+    # stability cap after every token, bf16 state rounded after every token)
+    B, T, Hk, Hv = 3, 6, 2, 4
+    q, k, v, g, b, w = steps_inputs(31, B, T, Hk, Hv)
+    S0 = 0.3 * np.random.default_rng(32).standard_normal((B, Hv, 128, 128))
+    reset = np.zeros((B, T), bool)
+    reset[1, 0] = reset[2, 3] = True
+    tb = lambda x: to_dev(x, torch.bfloat16)
+    st0 = to_dev(S0)
+    if state_dtype == "bfloat16":
+        st0 = st0.to(torch.bfloat16)
+    kw = dict(qk_l2norm=True, state_dtype=state_dtype, stability_guard=guard, stability_tau=20.0)
+    o_m, s_m = gdn2_decode_steps(tb(q), tb(k), tb(v), to_dev(g), to_dev(b), to_dev(w), st0,
+                                 reset=torch.tensor(reset), **kw)
+    st = st0
+    outs = []
+    for t in range(T):
+        o1, st = gdn2_decode_step(tb(q[:, t]), tb(k[:, t]), tb(v[:, t]), to_dev(g[:, t]), to_dev(b[:, t]),
+                                  to_dev(w[:, t]), st, reset=torch.tensor(reset[:, t]), **kw)
+        outs.append(o1)
+    o_c = torch.stack(outs, 1)
+    assert o_m.shape == (B, T, Hv, 128) and o_m.dtype == torch.bfloat16
+    assert s_m.dtype == st.dtype
+    # same arithmetic in the same order: agreement to a few fp32 rounding steps
+    assert rel_l2(as_np(o_m), as_np(o_c)) < 1e-5
+    assert rel_l2(as_np(s_m), as_np(st)) < 1e-5
+
+
+@pytest.mark.parametrize("gate_heads", ["hk", "hv"])
+def test_decode_steps_vs_oracle(gate_heads):
+    B, T, Hk, Hv = 2, 8, 2, 4
+    q, k, v, g, b, w = steps_inputs(33, B, T, Hk, Hv, gate_heads)
+    S0 = 0.1 * np.random.default_rng(34).standard_normal((B, Hv, 128, 128))
+    reset = np.zeros((B, T), bool)
+    reset[0, 5] = True
+    o, s = gdn2_decode_steps(to_dev(q), to_dev(k), to_dev(v), to_dev(g), to_dev(b), to_dev(w), to_dev(S0),
+                             reset=torch.tensor(reset), qk_l2norm=True)
+    ref_s = S0
+    ro = []
+    for t in range(T):
+        o1, ref_s = O.decode_step(q[:, t], k[:, t], v[:, t], g[:, t], b[:, t], w[:, t], ref_s,
+                                  reset=reset[:, t], qk_l2norm=True)
+        ro.append(o1)
+    ro = np.stack(ro, 1)
+    check(o.reshape(B, T * Hv, 128), ro.reshape(B, T * Hv, 128), s, ref_s, "fp32", "fp32", f"decode_steps {gate_heads}")
+
+
+def test_decode_steps_in_place_and_single_token():
+    B, Hk, Hv = 2, 2, 4
+    q, k, v, g, b, w = steps_inputs(35, B, 1, Hk, Hv)
+    S0 = 0.1 * np.random.default_rng(36).standard_normal((B, Hv, 128, 128))
+    args = [to_dev(x) for x in (q, k, v, g, b, w)]
+    o1, s1 = gdn2_decode_step(*[x[:, 0] for x in args], to_dev(S0), qk_l2norm=True)
+    st = to_dev(S0)
+    o2, s2 = gdn2_decode_steps(*args, st, qk_l2norm=True, out_state=st)
+    assert s2.data_ptr() == st.data_ptr()
+    assert torch.equal(o1, o2[:, 0]) and torch.equal(s1, s2)
