@@ -1,0 +1,940 @@
+// Training backward of the GDN-2 recurrence on gfx950 (fp32 throughout).
+//
+// Reference: the custom VJP of chunk_gdn2 (maelie-labs/deltanet-tpu v0.3.0,
+// src/deltanet_tpu/gdn2.py:1446-1769) with its backward kernels
+// (gdn2.py:243-493 analytical prepass adjoint, 496-582, 698-769 reverse state
+// scan).  The recurrence differentiated is reference.py:123-161:
+//   Sd = e^{g_t} S ; u = w v - Sd^T (b k) ; S' = Sd + k u^T ; o = S'^T q.
+//
+// Chunk form (C = 64 tokens, G_i = cumulative log-decay from the chunk start,
+// carry_i = token i continues the state entering the chunk, last_j = token j
+// is in the chunk's last document, same(i,j) = same document):
+//   A_ij = sum_r b_i k_i[r] k_j[r] e^{G_i-G_j}  (j < i, same)   T = (I + A)^-1
+//   M_ij = sum_r q_i[r] k_j[r] e^{G_i-G_j}      (j <= i, same)
+//   W = T diag(carry) (b k e^G) ; U0 = T (w v) ; U = U0 - W S_c
+//   Kc_j = last_j k_j e^{G_last-G_j} ; lam = all_carry e^{G_last}
+//   Xf = diag(carry) q e^G - M W
+//   S_{c+1} = lam * S_c + Kc^T U            O_c = Xf S_c + M U0
+// and its adjoint, the same affine map transposed and run backwards:
+//   dS_c = lam * dS_{c+1} + Xf^T dO_c - W^T (Kc dS_{c+1})
+// plus the chunk-local parameter gradients (dU = M^T dO + Kc dS_{c+1},
+// dX = T^T dU, dM = dO U^T, dA = -dX U^T, ...; see k_bw_grads).
+//
+// Every decay factor is formed as a product of factors <= 1: a pair (i, j)
+// with j <= m <= i uses e^{G_i-G_m} e^{G_m-G_j}, m = the first row of i's
+// 16-row block (or the last row of j's block); pairs inside one 16-row block
+// use e^{G_i-G_j} directly.  No factor can overflow, whatever the decay
+// (the reference's strong-decay test uses g = -150 per token).
+//
+// Kernels (one launch each, in stream order):
+//   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G
+//   k_bw_chain<false>  per (batch, head, 16-column tile): S_c for every chunk
+//   k_bw_chain<true>   same tiles, reverse: dS_{c+1} for every chunk, dS_0
+//   k_bw_grads   per (batch, head, chunk): dq, dk, dv, dg, db, dw
+#include "dn_common.h"
+#include "dn_host.h"
+
+namespace dn {
+
+namespace {
+
+constexpr int BC = 64;        // tokens per backward chunk
+constexpr int KD = 128;       // K = V = 128
+constexpr int CK = BC * KD;
+constexpr int CC = BC * BC;
+constexpr int KK = KD * KD;
+constexpr int KP = KD + 4;    // padded LDS row pitch (128-wide rows)
+constexpr int CP = BC + 4;    // padded LDS row pitch (64-wide rows)
+
+struct BW {
+  int B, L, H, NC;
+  const float *q, *k, *v, *g, *b, *w;
+  const int32_t* seg;
+  const float* init;
+  const float* dout;
+  const float* dfin;
+  float *dq, *dk, *dv, *dg, *db, *dw, *dinit;
+  // workspace, per unit u = (batch * H + head) * NC + chunk
+  float *G;    // [BC][KD] cumulative log2-decay from the chunk start
+  float *Wm;   // [BC][KD] W
+  float *WT;   // [KD][BC] W^T
+  float *Kc;   // [BC][KD]
+  float *KcT;  // [KD][BC]
+  float *XfT;  // [KD][BC]
+  float *U0;   // [BC][KD]
+  float *MT;   // [BC][BC] M^T
+  float *TT;   // [BC][BC] T^T
+  float *lam;  // [KD]
+  float *S, *ST;    // [KD][KD] state entering the chunk, and its transpose
+  float *dS, *dST;  // [KD][KD] gradient of the state leaving the chunk, and its transpose
+};
+
+__device__ __forceinline__ int64_t row_of(const BW& p, int bb, int t, int h) {
+  return (((int64_t)bb * p.L + t) * p.H + h) * KD;
+}
+
+__device__ __forceinline__ int seg_at(const BW& p, int bb, int t) {
+  if (p.seg == nullptr) return 0;
+  t = t < p.L ? t : p.L - 1;
+  return p.seg[(int64_t)bb * p.L + t];
+}
+
+// Per-token document flags of chunk c (threads 0..BC-1).  Segment ids are
+// canonical: nondecreasing, and the state entering token 0 belongs to id 0.
+__device__ __forceinline__ void chunk_docs(const BW& p, int bb, int t0, int* sseg, int* scar, int* slast) {
+  const int t = threadIdx.x;
+  const int prev = t0 == 0 ? 0 : seg_at(p, bb, t0 - 1);
+  const int s = seg_at(p, bb, t0 + t);
+  sseg[t] = s;
+  scar[t] = s == prev;
+  slast[t] = s == seg_at(p, bb, t0 + BC - 1);
+}
+
+__device__ __forceinline__ float ex2(float x) { return exp2f(fminf(x, 0.f)); }
+
+__device__ __forceinline__ float4 ld4g(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 zero_f4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+__device__ __forceinline__ float f4at(const float4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// 8 values of a 128-wide row at the fragment positions of slab s:
+// x[0..3] = row[32s + 4q .. +3], x[4..7] = row[32s + 16 + 4q .. +3]
+__device__ __forceinline__ void row8(const float* rowp, int s, int q, float* x) {
+  const float4 a = ld4g(rowp + 32 * s + 4 * q);
+  const float4 b = ld4g(rowp + 32 * s + 16 + 4 * q);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
+__device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<false>(x); }
+
+// ---------------------------------------------------------------------------
+// k_bw_intra
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_bw_intra(BW p) {
+  __shared__ float sG[BC][KP];
+  __shared__ float sA[BC][CP];   // A, then T
+  __shared__ float sM[BC][CP];
+  __shared__ float sW[BC][KP];
+  __shared__ int sseg[BC], scar[BC], slast[BC];
+
+  const int u = blockIdx.x;
+  const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
+  const int t0 = c * BC;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+  float* G = p.G + (int64_t)u * CK;
+
+  if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
+  for (int i = tid; i < BC * CP; i += 256) {
+    (&sA[0][0])[i] = 0.f;
+    (&sM[0][0])[i] = 0.f;
+  }
+  __syncthreads();
+  // ---- cumulative decay (log2 units), per channel -------------------------
+  if (tid < KD) {
+    float acc = 0.f;
+    for (int t = 0; t < BC; ++t) {
+      const int tok = t0 + t;
+      const float gv = tok < p.L ? p.g[row_of(p, bb, tok, h) + tid] : 0.f;
+      acc += gv * kLog2e;
+      sG[t][tid] = acc;
+      G[t * KD + tid] = acc;
+    }
+    p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? exp2f(acc) : 0.f;
+  }
+  __syncthreads();
+
+  // ---- A (strict) and M (with diagonal), 16x16 tiles of the lower triangle --
+  for (int task = wv; task < 20; task += 4) {
+    const bool isM = task >= 10;
+    const int tt = task % 10;
+    const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
+    const int J = tt - I * (I + 1) / 2;
+    float res[4];
+    if (J < I) {
+      const int m = 16 * I;
+      const int i = 16 * I + l16, j = 16 * J + l16;
+      const bool vi = t0 + i < p.L, vj = t0 + j < p.L;
+      const float* qi = p.q + row_of(p, bb, vi ? t0 + i : 0, h);
+      const float* ki = p.k + row_of(p, bb, vi ? t0 + i : 0, h);
+      const float* bi = p.b + row_of(p, bb, vi ? t0 + i : 0, h);
+      const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float xa[8], xb[8], x2[8], gi[8], gm[8], gj[8];
+        if (isM) {
+          row8(qi, s, q, xa);
+        } else {
+          row8(bi, s, q, xa);
+          row8(ki, s, q, x2);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xa[e] *= x2[e];
+        }
+        row8(kj, s, q, xb);
+        row8(&sG[i][0], s, q, gi);
+        row8(&sG[m][0], s, q, gm);
+        row8(&sG[j][0], s, q, gj);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xa[e] = vi ? xa[e] * ex2(gi[e] - gm[e]) : 0.f;
+          xb[e] = vj ? xb[e] * ex2(gm[e] - gj[e]) : 0.f;
+        }
+        mma(acc, fr8(xa), fr8(xb));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) res[e] = acc[e];
+    } else {
+      // diagonal block: e^{G_i - G_j} per element
+      const int j = 16 * I + l16;
+      const bool vj = t0 + j < p.L;
+      const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) res[e] = 0.f;
+      for (int r4 = 0; r4 < KD / 4; ++r4) {
+        const float4 kv = ld4g(kj + 4 * r4);
+        const float4 gjv = *reinterpret_cast<const float4*>(&sG[j][4 * r4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e;
+          const int ti = t0 + i < p.L ? t0 + i : 0;
+          float4 xv;
+          if (isM) {
+            xv = ld4g(p.q + row_of(p, bb, ti, h) + 4 * r4);
+          } else {
+            const float4 bv = ld4g(p.b + row_of(p, bb, ti, h) + 4 * r4);
+            const float4 k2 = ld4g(p.k + row_of(p, bb, ti, h) + 4 * r4);
+            xv = make_float4(bv.x * k2.x, bv.y * k2.y, bv.z * k2.z, bv.w * k2.w);
+          }
+          const float4 giv = *reinterpret_cast<const float4*>(&sG[i][4 * r4]);
+          res[e] += xv.x * kv.x * ex2(giv.x - gjv.x) + xv.y * kv.y * ex2(giv.y - gjv.y) +
+                    xv.z * kv.z * ex2(giv.z - gjv.z) + xv.w * kv.w * ex2(giv.w - gjv.w);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * I + 4 * q + e, j = 16 * J + l16;
+      const bool ok = (isM ? j <= i : j < i) && sseg[i] == sseg[j] && t0 + i < p.L && t0 + j < p.L;
+      (isM ? sM : sA)[i][j] = ok ? res[e] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- T = (I + A)^-1 by forward substitution (wave 0, lane = column) -----
+  if (wv == 0) {
+    float Tc[BC];
+#pragma unroll
+    for (int i = 0; i < BC; ++i) {
+      float t = (i == l) ? 1.f : 0.f;
+#pragma unroll
+      for (int j4 = 0; j4 < (i + 3) / 4; ++j4) {
+        const float4 a = *reinterpret_cast<const float4*>(&sA[i][4 * j4]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          if (4 * j4 + jj < i) t -= f4at(a, jj) * Tc[4 * j4 + jj];
+        }
+      }
+      Tc[i] = t;
+    }
+    float* TT = p.TT + (int64_t)u * CC + l * BC;
+#pragma unroll
+    for (int i = 0; i < BC; ++i) sA[i][l] = Tc[i];
+#pragma unroll
+    for (int i4 = 0; i4 < BC / 4; ++i4)
+      *reinterpret_cast<float4*>(TT + 4 * i4) = make_float4(Tc[4 * i4], Tc[4 * i4 + 1], Tc[4 * i4 + 2], Tc[4 * i4 + 3]);
+  } else {
+    const int t2 = tid - 64;
+    float* MT = p.MT + (int64_t)u * CC;
+    for (int idx = t2; idx < CC; idx += 192) {
+      const int j = idx / BC, i = idx % BC;
+      MT[idx] = sM[i][j];
+    }
+    float* Kc = p.Kc + (int64_t)u * CK;
+    float* KcT = p.KcT + (int64_t)u * CK;
+    for (int idx = t2; idx < CK; idx += 192) {
+      const int j = idx / KD, r = idx % KD;
+      const bool ok = slast[j] && t0 + j < p.L;
+      Kc[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
+    }
+    for (int idx = t2; idx < CK; idx += 192) {
+      const int r = idx / BC, j = idx % BC;
+      const bool ok = slast[j] && t0 + j < p.L;
+      KcT[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- W = T diag(carry) (b k e^G), U0 = T (w v) ---------------------------
+  {
+    f32x4 aw[4][2], au[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) { aw[I][R2] = zero4(); au[I][R2] = zero4(); }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Frag<false> a[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        float x[8];
+        const float* rp = &sA[16 * I + l16][32 * s];
+        const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
+        const float4 x1 = *reinterpret_cast<const float4*>(rp + 16 + 4 * q);
+        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+        a[I] = fr8(x);
+      }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int r = 16 * (2 * wv + R2) + l16;
+        float xb[8], xu[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * s + pi_k(q, e);
+          const bool vj = t0 + j < p.L;
+          const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
+          xb[e] = (vj && scar[j]) ? p.b[ro] * p.k[ro] * ex2(sG[j][r]) : 0.f;
+          xu[e] = vj ? p.w[ro] * p.v[ro] : 0.f;
+        }
+        const Frag<false> fb = fr8(xb), fu = fr8(xu);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          mma(aw[I][R2], a[I], fb);
+          mma(au[I][R2], a[I], fu);
+        }
+      }
+    }
+    float* Wm = p.Wm + (int64_t)u * CK;
+    float* WT = p.WT + (int64_t)u * CK;
+    float* U0 = p.U0 + (int64_t)u * CK;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int r = 16 * (2 * wv + R2) + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e;
+          sW[i][r] = aw[I][R2][e];
+          Wm[i * KD + r] = aw[I][R2][e];
+          U0[i * KD + r] = au[I][R2][e];
+        }
+        *reinterpret_cast<float4*>(WT + r * BC + 16 * I + 4 * q) =
+            make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
+      }
+  }
+  __syncthreads();
+
+  // ---- Xf = diag(carry) q e^G - M W ----------------------------------------
+  {
+    f32x4 ax[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) ax[I][R2] = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Frag<false> a[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        float x[8];
+        const float* rp = &sM[16 * I + l16][32 * s];
+        const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
+        const float4 x1 = *reinterpret_cast<const float4*>(rp + 16 + 4 * q);
+        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+        a[I] = fr8(x);
+      }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int r = 16 * (2 * wv + R2) + l16;
+        float xb[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xb[e] = sW[32 * s + pi_k(q, e)][r];
+        const Frag<false> fb = fr8(xb);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) mma(ax[I][R2], a[I], fb);
+      }
+    }
+    float* XfT = p.XfT + (int64_t)u * CK;
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int r = 16 * (2 * wv + R2) + l16;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e;
+          const bool vi = t0 + i < p.L && scar[i];
+          const float qe = vi ? p.q[row_of(p, bb, t0 + i, h) + r] * ex2(sG[i][r]) : 0.f;
+          o[e] = qe - ax[I][R2][e];
+        }
+        *reinterpret_cast<float4*>(XfT + r * BC + 16 * I + 4 * q) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_bw_chain: one (batch, head, 16-column tile) per workgroup; the 128 x 16
+// state tile lives in LDS in fragment order ([slab][lane][8]); wave w owns
+// rows 32w..32w+31.
+//   forward  (BWD = false):  Y = U0 - W S ;  S <- lam * S + Kc^T Y
+//   backward (BWD = true):   Z = -Kc dS  ;  dS <- lam * dS + Xf^T dO + W^T Z
+// ---------------------------------------------------------------------------
+template <bool BWD>
+__global__ __launch_bounds__(256) void k_bw_chain(BW p) {
+  __shared__ float sS[4][64][8];
+  __shared__ float sY[2][64][8];
+  const int blk = blockIdx.x;
+  const int ct = blk % (KD / 16), bh = blk / (KD / 16), h = bh % p.H, bb = bh / p.H;
+  const int col0 = 16 * ct;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+
+  f32x4 st[2];
+  const float* src = BWD ? p.dfin : p.init;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 32 * wv + 16 * tt + 4 * q + e;
+      st[tt][e] = src ? src[((int64_t)bh * KD + r) * KD + col0 + l16] : 0.f;
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sS[wv][l][e] = st[0][e];
+    sS[wv][l][4 + e] = st[1][e];
+  }
+
+  for (int it = 0; it < p.NC; ++it) {
+    const int c = BWD ? p.NC - 1 - it : it;
+    const int64_t u = (int64_t)bh * p.NC + c;
+    const int t0 = c * BC;
+    __syncthreads();
+    {
+      float* X = (BWD ? p.dS : p.S) + u * KK;
+      float* XT = (BWD ? p.dST : p.ST) + u * KK;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int r0 = 32 * wv + 16 * tt + 4 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) X[(r0 + e) * KD + col0 + l16] = st[tt][e];
+        *reinterpret_cast<float4*>(XT + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
+      }
+    }
+    // Y (or Z) tile: token rows 16w..16w+15
+    f32x4 y = zero4();
+    {
+      const float* Arow = (BWD ? p.Kc : p.Wm) + u * CK + (16 * wv + l16) * KD;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float xa[8];
+        row8(Arow, s, q, xa);
+        mma(y, fr8(xa), fr8(&sS[s][l][0]));
+      }
+    }
+    if (BWD) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = -y[e];
+    } else {
+      const float* U0 = p.U0 + u * CK;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = U0[(16 * wv + 4 * q + e) * KD + col0 + l16] - y[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
+    __syncthreads();
+    const float* lam = p.lam + u * KD;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int rA = 32 * wv + 16 * tt + l16;
+      f32x4 acc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = lam[32 * wv + 16 * tt + 4 * q + e] * st[tt][e];
+      const float* Arow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float xa[8];
+        row8(Arow, s2, q, xa);
+        mma(acc, fr8(xa), fr8(&sY[s2][l][0]));
+      }
+      if (BWD) {
+        const float* Xrow = p.XfT + u * CK + rA * BC;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          float xa[8], xb[8];
+          row8(Xrow, s2, q, xa);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int tok = t0 + 32 * s2 + pi_k(q, e);
+            xb[e] = tok < p.L ? p.dout[row_of(p, bb, tok, h) + col0 + l16] : 0.f;
+          }
+          mma(acc, fr8(xa), fr8(xb));
+        }
+      }
+      st[tt] = acc;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sS[wv][l][e] = st[0][e];
+      sS[wv][l][4 + e] = st[1][e];
+    }
+  }
+  if (BWD && p.dinit != nullptr) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 32 * wv + 16 * tt + 4 * q + e;
+        p.dinit[((int64_t)bh * KD + r) * KD + col0 + l16] = st[tt][e];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_bw_grads: chunk-local parameter gradients.  With S0 = S_c, dSC = dS_{c+1}:
+//   U = U0 - W S0 ; dU = M^T dO + Kc dSC ; dX = T^T dU
+//   dv = dX w ; dw = dX v ; dM = mask(dO U^T) ; dA = -mask(dX U^T)
+//   dq_i   = carry_i e^{G_i} (S0 dO_i) + sum_j dM_ij e^{G_i-G_j} k_j
+//   dbeta_i = -carry_i e^{G_i} (S0 dX_i) + sum_j dA_ij e^{G_i-G_j} k_j
+//   dk_j   = sum_i dM_ij e^{G_i-G_j} q_i + sum_i dA_ij e^{G_i-G_j} beta_i
+//            + last_j e^{G_last-G_j} (dSC u_j)
+//   dG_i = q_i dq_i + beta_i dbeta_i - k_i dk_i, plus at the last row
+//          sum_j k_j dk_j^(Kc) + lam * rowsum(S0 * dSC);  dg_t = sum_{i>=t} dG_i
+//   db = k dbeta ; dk += b dbeta
+// Wave w owns the state / key columns 32w..32w+31 of every C x 128 product.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_bw_grads(BW p) {
+  __shared__ float sdO[BC][KP];
+  __shared__ float sX[BC][KP];       // dU, then dX
+  __shared__ float sU[BC][KD];       // U, then dG
+  __shared__ float sdM[BC][CP];
+  __shared__ float sdA[BC][CP];
+  __shared__ int sseg[BC], scar[BC], slast[BC];
+
+  const int u = blockIdx.x;
+  const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
+  const int t0 = c * BC;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+  const float* G = p.G + (int64_t)u * CK;
+  const float* S0 = p.S + (int64_t)u * KK;
+  const float* S0T = p.ST + (int64_t)u * KK;
+  const float* dSC = p.dS + (int64_t)u * KK;
+  const float* dSCT = p.dST + (int64_t)u * KK;
+
+  if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
+  for (int i = tid; i < BC * CP; i += 256) {
+    (&sdM[0][0])[i] = 0.f;
+    (&sdA[0][0])[i] = 0.f;
+  }
+  for (int idx = tid; idx < BC * KD / 4; idx += 256) {
+    const int i = idx / (KD / 4), c4 = idx % (KD / 4);
+    const float4 v = t0 + i < p.L ? ld4g(p.dout + row_of(p, bb, t0 + i, h) + 4 * c4) : zero_f4();
+    *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
+  }
+  __syncthreads();
+
+  // ---- U = U0 - W S0 ---------------------------------------------------------
+  {
+    const float* Wm = p.Wm + (int64_t)u * CK;
+    const float* U0 = p.U0 + (int64_t)u * CK;
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      Frag<false> a[4], bfr[2];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) { float x[8]; row8(Wm + (16 * I + l16) * KD, s, q, x); a[I] = fr8(x); }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(S0T + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int vcol = 32 * wv + 16 * R2 + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e;
+          sU[i][vcol] = U0[i * KD + vcol] - acc[I][R2][e];
+        }
+      }
+  }
+  __syncthreads();
+
+  // ---- Kc part of dk: last_j e^{G_last-G_j} (U dSC^T)_j; written to dk -------
+  {
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      Frag<false> a[4], bfr[2];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) { float x[8]; row8(&sU[16 * I + l16][0], s, q, x); a[I] = fr8(x); }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(dSC + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    }
+#pragma unroll
+    for (int R2 = 0; R2 < 2; ++R2) {
+      const int r = 32 * wv + 16 * R2 + l16;
+      const float glast = G[(BC - 1) * KD + r];
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 16 * I + 4 * q + e;
+          if (t0 + j < p.L) {
+            const int64_t ro = row_of(p, bb, t0 + j, h) + r;
+            const float dkc = slast[j] ? ex2(glast - G[j * KD + r]) * acc[I][R2][e] : 0.f;
+            p.dk[ro] = dkc;               // completed below
+            p.dg[ro] = p.k[ro] * dkc;     // prefix-summed below
+          }
+        }
+    }
+  }
+
+  // ---- dU = M^T dO + Kc dSC  (into sX) --------------------------------------
+  {
+    const float* MT = p.MT + (int64_t)u * CC;
+    const float* Kc = p.Kc + (int64_t)u * CK;
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Frag<false> a[4], bfr[2];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) { float x[8]; row8(MT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int vcol = 32 * wv + 16 * R2 + l16;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
+        bfr[R2] = fr8(x);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      Frag<false> a[4], bfr[2];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) { float x[8]; row8(Kc + (16 * I + l16) * KD, s, q, x); a[I] = fr8(x); }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(dSCT + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int vcol = 32 * wv + 16 * R2 + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][R2][e];
+      }
+  }
+  __syncthreads();
+
+  // ---- dX = T^T dU ; dv = dX w ; dw = dX v ----------------------------------
+  {
+    const float* TT = p.TT + (int64_t)u * CC;
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      Frag<false> a[4], bfr[2];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) { float x[8]; row8(TT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int vcol = 32 * wv + 16 * R2 + l16;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
+        bfr[R2] = fr8(x);
+      }
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) {
+        const int vcol = 32 * wv + 16 * R2 + l16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * I + 4 * q + e;
+          const float dx = acc[I][R2][e];
+          sX[i][vcol] = dx;
+          if (t0 + i < p.L) {
+            const int64_t ro = row_of(p, bb, t0 + i, h) + vcol;
+            p.dv[ro] = dx * p.w[ro];
+            p.dw[ro] = dx * p.v[ro];
+          }
+        }
+      }
+  }
+  __syncthreads();
+
+  // ---- dM = mask(dO U^T), dA = -mask(dX U^T) --------------------------------
+  for (int task = wv; task < 20; task += 4) {
+    const bool isA = task >= 10;
+    const int tt = task % 10;
+    const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
+    const int J = tt - I * (I + 1) / 2;
+    const float* Xs = isA ? &sX[0][0] : &sdO[0][0];
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float xa[8], xb[8];
+      row8(Xs + (16 * I + l16) * KP, s, q, xa);
+      row8(&sU[16 * J + l16][0], s, q, xb);
+      mma(acc, fr8(xa), fr8(xb));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * I + 4 * q + e, j = 16 * J + l16;
+      const bool ok = (isA ? j < i : j <= i) && sseg[i] == sseg[j];
+      (isA ? sdA : sdM)[i][j] = ok ? (isA ? -acc[e] : acc[e]) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- dq, dbeta, dk per 16 x 16 tile; dG into sU ----------------------------
+  float (*sdG)[KD] = sU;
+  for (int I = 0; I < 4; ++I) {
+#pragma unroll
+    for (int R2 = 0; R2 < 2; ++R2) {
+      const int r = 32 * wv + 16 * R2 + l16;
+      // S0-side products: (dO S0^T), (dX S0^T)
+      f32x4 aq = zero4(), ab = zero4();
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float xo[8], xx[8], xs[8];
+        row8(&sdO[16 * I + l16][0], s, q, xo);
+        row8(&sX[16 * I + l16][0], s, q, xx);
+        row8(S0 + (32 * wv + 16 * R2 + l16) * KD, s, q, xs);
+        const Frag<false> fs = fr8(xs);
+        mma(aq, fr8(xo), fs);
+        mma(ab, fr8(xx), fs);
+      }
+      // off-diagonal blocks, reference row m = 16 I (rows i) ...
+      f32x4 oq = zero4(), ob = zero4();
+      if (I > 0) {
+        const int m = 16 * I;
+        const float gm = G[m * KD + r];
+        for (int s = 0; s < (I + 1) / 2; ++s) {
+          float xm[8], xa[8], xk[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int j = 32 * s + pi_k(q, e);
+            xm[e] = j < m ? sdM[16 * I + l16][j] : 0.f;
+            xa[e] = j < m ? sdA[16 * I + l16][j] : 0.f;
+            const bool vj = j < m && t0 + j < p.L;
+            xk[e] = vj ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(gm - G[j * KD + r]) : 0.f;
+          }
+          const Frag<false> fk = fr8(xk);
+          mma(oq, fr8(xm), fk);
+          mma(ob, fr8(xa), fk);
+        }
+      }
+      // ... and reference row m = 16 J + 15 (columns j, here the rows of dk)
+      f32x4 ok_ = zero4();
+      if (I < 3) {
+        const int m = 16 * I + 15;
+        const float gm = G[m * KD + r];
+        for (int s = (16 * (I + 1)) / 32; s < 2; ++s) {
+          float xm[8], xa[8], xq[8], xbeta[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 32 * s + pi_k(q, e);
+            const bool in = i > m;
+            xm[e] = in ? sdM[i][16 * I + l16] : 0.f;
+            xa[e] = in ? sdA[i][16 * I + l16] : 0.f;
+            const bool vi = in && t0 + i < p.L;
+            const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + r;
+            const float f = vi ? ex2(G[i * KD + r] - gm) : 0.f;
+            xq[e] = vi ? p.q[ro] * f : 0.f;
+            xbeta[e] = vi ? p.b[ro] * p.k[ro] * f : 0.f;
+          }
+          mma(ok_, fr8(xm), fr8(xq));
+          mma(ok_, fr8(xa), fr8(xbeta));
+        }
+      }
+      // diagonal block, per element, and the epilogue
+      const float gI0 = G[(16 * I) * KD + r];
+      const float gI15 = G[(16 * I + 15) * KD + r];
+      float kb[16], qb[16], betab[16], gb[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = 16 * I + jj;
+        const bool vj = t0 + j < p.L;
+        const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
+        kb[jj] = vj ? p.k[ro] : 0.f;
+        qb[jj] = vj ? p.q[ro] : 0.f;
+        betab[jj] = vj ? p.b[ro] * kb[jj] : 0.f;
+        gb[jj] = G[j * KD + r];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ii = 4 * q + e;            // row within the block
+        const int i = 16 * I + ii;
+        const float gi = G[i * KD + r];
+        // the pair (i, i) of M is kept apart: its factor e^0 does not depend
+        // on g, and its two dG contributions (q dq, -k dk) cancel exactly
+        float dq = 0.f, dbeta = 0.f, dk = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const float off = jj == ii ? 0.f : 1.f;
+          // i as the row: pairs (i, j), j < i inside the block
+          const float fij = ex2(gi - gb[jj]);
+          dq += off * sdM[i][16 * I + jj] * fij * kb[jj];
+          dbeta += sdA[i][16 * I + jj] * fij * kb[jj];
+          // i as the column: pairs (i2, i), i2 > i inside the block
+          const float fji = ex2(gb[jj] - gi);
+          dk += off * sdM[16 * I + jj][i] * fji * qb[jj] + sdA[16 * I + jj][i] * fji * betab[jj];
+        }
+        const float dmii = sdM[i][i];
+        const bool car = scar[i] != 0;
+        const float eg = car ? ex2(gi) : 0.f;
+        dq += eg * aq[e] + oq[e] * ex2(gi - gI0);
+        dbeta += -eg * ab[e] + ob[e] * ex2(gi - gI0);
+        dk += ok_[e] * ex2(gI15 - gi);
+        const bool vi = t0 + i < p.L;
+        float dG = 0.f;
+        if (vi) {
+          const int64_t ro = row_of(p, bb, t0 + i, h) + r;
+          const float kv = kb[ii], bv = p.b[ro];
+          dG = qb[ii] * dq + bv * kv * dbeta - kv * dk;
+          const float dkc = p.dk[ro];       // Kc part, written above
+          p.dq[ro] = dq + dmii * kv;
+          p.dk[ro] = dk + dmii * qb[ii] + dkc + bv * dbeta;
+          p.db[ro] = kv * dbeta;
+        }
+        sdG[i][r] = dG;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- dg ------------------------------------------------------------------
+  // dg_t = sum_{i >= t} dG_i + sum_{j < t} k_j dk_j^(Kc) + lam * rowsum(S0 * dSC):
+  // the Kc pair (j, last) enters every dg_t with t <= j twice with opposite
+  // signs, so it is summed forward over j < t instead (no cancellation).
+  __threadfence_block();
+  __syncthreads();
+  if (tid < KD) {
+    const int r = tid;
+    float tail = 0.f;
+    if (scar[BC - 1]) {
+      float rs = 0.f;
+      for (int v4 = 0; v4 < KD / 4; ++v4) {
+        const float4 a = ld4g(S0 + r * KD + 4 * v4);
+        const float4 d = ld4g(dSC + r * KD + 4 * v4);
+        rs += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
+      }
+      tail = exp2f(G[(BC - 1) * KD + r]) * rs;
+    }
+    float fwd = 0.f;
+    for (int t = 0; t < BC && t0 + t < p.L; ++t) {
+      float* d = p.dg + row_of(p, bb, t0 + t, h) + r;
+      const float pj = *d;
+      *d = fwd;
+      fwd += pj;
+    }
+    float acc = tail;
+    for (int t = BC - 1; t >= 0; --t) {
+      acc += sdG[t][r];
+      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + r] += acc;
+    }
+  }
+}
+
+}  // namespace
+
+}  // namespace dn
+
+using namespace dn;
+
+namespace {
+
+size_t bw_units(const dn_backward_args* a) {
+  const int NC = (a->L + BC - 1) / BC;
+  return (size_t)a->B * a->H * NC;
+}
+
+constexpr size_t kUnitFloats = 7 * (size_t)CK + 2 * (size_t)CC + KD + 4 * (size_t)KK;
+
+int bw_check(const dn_backward_args* a) {
+  if (a == nullptr) return set_error(DN_E_INVALID, "null args");
+  if (a->abi_version != DN_ABI_VERSION) return set_error(DN_E_ABI, "dn_backward_args built for another ABI version");
+  if (a->K != KD || a->V != KD) return set_error(DN_E_INVALID, "K and V must both be 128");
+  if (a->B <= 0 || a->L <= 0 || a->H <= 0) return set_error(DN_E_INVALID, "B, L and H must be positive");
+  if (!a->q || !a->k || !a->v || !a->g || !a->b || !a->w || !a->d_out)
+    return set_error(DN_E_INVALID, "missing input tensor pointer");
+  if (!a->dq || !a->dk || !a->dv || !a->dg || !a->db || !a->dw)
+    return set_error(DN_E_INVALID, "missing gradient tensor pointer");
+  if (a->d_init != nullptr && a->init_state == nullptr)
+    return set_error(DN_E_INVALID, "d_init needs init_state");
+  return DN_OK;
+}
+
+}  // namespace
+
+extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
+  if (bw_check(a) != DN_OK) return 0;
+  return bw_units(a) * kUnitFloats * sizeof(float);
+}
+
+extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = bw_check(a);
+  if (rc != DN_OK) return rc;
+  const size_t need = bw_units(a) * kUnitFloats * sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need) return set_error(DN_E_WORKSPACE, "workspace too small");
+  BW p{};
+  p.B = a->B; p.L = a->L; p.H = a->H; p.NC = (a->L + BC - 1) / BC;
+  p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
+  p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
+  p.seg = a->seg; p.init = (const float*)a->init_state;
+  p.dout = (const float*)a->d_out; p.dfin = (const float*)a->d_final;
+  p.dq = (float*)a->dq; p.dk = (float*)a->dk; p.dv = (float*)a->dv;
+  p.dg = (float*)a->dg; p.db = (float*)a->db; p.dw = (float*)a->dw; p.dinit = (float*)a->d_init;
+  const size_t units = bw_units(a);
+  float* ws = (float*)workspace;
+  auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
+  p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
+  p.XfT = take(CK); p.U0 = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
+  p.S = take(KK); p.ST = take(KK); p.dS = take(KK); p.dST = take(KK);
+
+  hipStream_t st = (hipStream_t)stream;
+  const int chains = a->B * a->H * (KD / 16);
+  prof_mark(4, st, false);
+  hipLaunchKernelGGL(k_bw_intra, dim3((unsigned)units), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_chain<false>, dim3(chains), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_chain<true>, dim3(chains), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(256), 0, st, p);
+  prof_mark(4, st, true);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
+  return DN_OK;
+}

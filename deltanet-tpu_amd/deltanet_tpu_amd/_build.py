@@ -11,7 +11,7 @@ PKG_ROOT = os.path.dirname(HERE)                      # deltanet-tpu_amd/
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 INCLUDE = os.path.join(REPO_ROOT, "include")
-SOURCES = ("dn_prefill.hip", "dn_decode.hip")
+SOURCES = ("dn_prefill.hip", "dn_decode.hip", "dn_backward.hip")
 OUT = os.path.join(HERE, "libdeltanet_amd.so")
 
 
@@ -22,7 +22,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build deltanet_tpu_amd)")
 
 
-def build(arch: str = "gfx950", out: str = OUT, extra=(), jobs: int = 2) -> str:
+def build(arch: str = "gfx950", out: str = OUT, extra=(), jobs: int = 3) -> str:
     """Compile every HIP source for `arch` and link the shared library `out`."""
     objs = []
     procs = []

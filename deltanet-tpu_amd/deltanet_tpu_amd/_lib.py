@@ -66,18 +66,36 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class BackwardArgs(ctypes.Structure):
+    """Mirror of ``dn_backward_args``."""
+
+    _fields_ = [
+        ("abi_version", _c_i32),
+        ("B", _c_i32), ("L", _c_i32), ("H", _c_i32), ("K", _c_i32), ("V", _c_i32),
+        ("q", _c_ptr), ("k", _c_ptr), ("v", _c_ptr), ("g", _c_ptr), ("b", _c_ptr), ("w", _c_ptr),
+        ("seg", _c_ptr),
+        ("init_state", _c_ptr),
+        ("d_out", _c_ptr),
+        ("d_final", _c_ptr),
+        ("dq", _c_ptr), ("dk", _c_ptr), ("dv", _c_ptr), ("dg", _c_ptr), ("db", _c_ptr), ("dw", _c_ptr),
+        ("d_init", _c_ptr),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "dn_prefill_workspace_size",
     "dn_prefill_fwd",
     "dn_decode_step",
     "dn_decode_steps",
+    "dn_prefill_bwd_workspace_size",
+    "dn_prefill_bwd",
     "dn_state_frob_cap",
     "dn_last_error",
     "dn_abi_version",
     "dn_profile_begin",
     "dn_profile_end",
 )
-PROFILE_KINDS = ("prepass", "value", "chain", "decode")
+PROFILE_KINDS = ("prepass", "value", "chain", "decode", "backward")
 
 _lock = threading.Lock()
 _lib = None
@@ -103,6 +121,10 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         lib.dn_decode_step.restype = ctypes.c_int
         lib.dn_decode_steps.argtypes = [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr]
         lib.dn_decode_steps.restype = ctypes.c_int
+        lib.dn_prefill_bwd_workspace_size.argtypes = [ctypes.POINTER(BackwardArgs)]
+        lib.dn_prefill_bwd_workspace_size.restype = ctypes.c_size_t
+        lib.dn_prefill_bwd.argtypes = [ctypes.POINTER(BackwardArgs), _c_ptr, ctypes.c_size_t, _c_ptr]
+        lib.dn_prefill_bwd.restype = ctypes.c_int
         lib.dn_state_frob_cap.argtypes = [_c_ptr, ctypes.c_int64, _c_i32, _c_i32, ctypes.c_float, _c_ptr]
         lib.dn_state_frob_cap.restype = ctypes.c_int
         lib.dn_last_error.argtypes = []

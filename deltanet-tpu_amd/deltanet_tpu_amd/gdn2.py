@@ -221,6 +221,12 @@ def chunk_gdn2(
 
     fp32 = precision_clean in ("fp32", "float32") or bool(state_fp32_matmul)
 
+    if (not is_inference) and torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v, g, b, w, initial_state)):
+        return _chunk_gdn2_train(
+            q, k, v, g, b, w, seg_t, initial_state, initial_state_segment_id, output_final_state,
+            "fp32" if fp32 else "bf16", scale, qk_l2norm, fuse_prologue, stability_guard)
+
     # ---- execution mode (gdn2.py:1992-2007) ----------------------------------
     gates_at_hv = ((g.shape[2] == Hv) or (b.shape[2] == Hv)) and (Hk < Hv)
 
@@ -315,6 +321,138 @@ def chunk_gdn2(
         return o
 
     return _maybe_guard_grad(is_inference, run, tensors)
+
+
+# ---------------------------------------------------------------------------
+# training path: autograd around the HIP backward
+# ---------------------------------------------------------------------------
+
+def _gate_to_heads(t, B, L, Hk, Hv, last):
+    """(B,L,H) / (B,L,H,1|last) with H in {1, Hk, Hv} -> (B,L,Hv,last), value
+    head j reading gate head j // (Hv // Hk) (gdn2.py:1992-2031)."""
+    if t.ndim == 3:
+        t = t.unsqueeze(-1)
+    if t.shape[2] == Hk and Hv != Hk:
+        t = torch.repeat_interleave(t, Hv // Hk, dim=2)
+    return t.expand(B, L, Hv, last)
+
+
+def _canonical_segments(seg_t, B, L, has_init, init_seg_id, dev):
+    """Canonical ids (gdn2.py:2081-2094) as int32 (B, L): nondecreasing, with
+    id 0 meaning "continues the initial state"."""
+    if seg_t is None:
+        return None
+    s = seg_t.to(torch.int64)
+    if s.ndim == 1:
+        s = s.unsqueeze(0).expand(B, L)
+    first = torch.zeros((B,), dtype=torch.int64, device=dev)
+    if has_init and init_seg_id is not None:
+        i0 = torch.as_tensor(init_seg_id, dtype=torch.int64, device=dev).reshape(-1)
+        first = (s[:, 0] != torch.broadcast_to(i0, (B,))).to(torch.int64)
+    ch = torch.cumsum((s[:, 1:] != s[:, :-1]).to(torch.int64), dim=1)
+    canon = torch.cat([torch.zeros((B, 1), dtype=torch.int64, device=dev), ch], dim=1) + first[:, None]
+    return canon.to(torch.int32).contiguous()
+
+
+class _RecurrenceFn(torch.autograd.Function):
+    """The chunked recurrence on prepared float32 inputs (all at Hv heads).
+
+    Forward: ``dn_prefill_fwd`` (the inference kernels).  Backward:
+    ``dn_prefill_bwd`` (reference custom VJP, gdn2.py:1446-1769).
+    """
+
+    @staticmethod
+    def forward(ctx, qe, ke, ve, ge, be, we, init, meta):
+        seg_t, init_seg_id, canon, precision = meta
+        with torch.no_grad():
+            out, fin = chunk_gdn2(
+                qe, ke, ve, ge, be, we, segment_ids=seg_t, initial_state=init,
+                initial_state_segment_id=init_seg_id, output_final_state=True, precision=precision,
+                scale=1.0, is_inference=True)
+        ctx.save_for_backward(qe, ke, ve, ge, be, we, init)
+        ctx.canon = canon
+        ctx.has_init = init is not None
+        return out.float(), fin
+
+    @staticmethod
+    def backward(ctx, d_out, d_fin):
+        qe, ke, ve, ge, be, we, init = ctx.saved_tensors
+        B, L, H, K = qe.shape
+        V = ve.shape[3]
+        dev = qe.device
+        d_out = torch.zeros_like(ve) if d_out is None else d_out.to(torch.float32).contiguous()
+        d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
+        grads = [torch.empty_like(x) for x in (qe, ke, ve, ge, be, we)]
+        d_init = torch.empty_like(init) if ctx.has_init else None
+        a = _lib.BackwardArgs()
+        a.abi_version = _lib.DN_ABI_VERSION
+        a.B, a.L, a.H, a.K, a.V = B, L, H, K, V
+        a.q, a.k, a.v, a.g, a.b, a.w = (_ptr(x) for x in (qe, ke, ve, ge, be, we))
+        a.seg = _ptr(ctx.canon)
+        a.init_state = _ptr(init)
+        a.d_out, a.d_final = _ptr(d_out), _ptr(d_fin)
+        a.dq, a.dk, a.dv, a.dg, a.db, a.dw = (_ptr(x) for x in grads)
+        a.d_init = _ptr(d_init)
+        lib = _lib.load_library()
+        nbytes = lib.dn_prefill_bwd_workspace_size(ctypes.byref(a))
+        if nbytes == 0:
+            _lib.check(-1, "dn_prefill_bwd_workspace_size")
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        _lib.check(lib.dn_prefill_bwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_bwd")
+        return (*grads, d_init, None)
+
+
+def _chunk_gdn2_train(q, k, v, g, b, w, seg_t, initial_state, init_seg_id, output_final_state,
+                      precision, scale, qk_l2norm, fuse_prologue, stability_guard):
+    """Training-mode chunk_gdn2 (is_inference=False, gdn2.py:2244-2286).
+
+    The wrapper's elementwise steps (gdn2.py:1970-2125) run as differentiable
+    torch ops, so autograd carries their derivatives and sums the gate / GQA
+    broadcasts; the recurrence itself is ``_RecurrenceFn``.
+    """
+    B, L, Hk, K = q.shape
+    Hv, V = v.shape[2], v.shape[3]
+    dev = q.device
+    G = Hv // Hk
+    qf, kf = q.to(torch.float32), k.to(torch.float32)
+
+    def l2(x):
+        return x * torch.rsqrt(torch.sum(x * x, dim=-1, keepdim=True) + 1e-6)
+
+    if fuse_prologue:
+        qh, kh = l2(qf) * scale, l2(kf)
+        ga = -torch.exp(torch.clamp(g.to(torch.float32), max=5.0))
+        if stability_guard:
+            ga = torch.clamp(ga, max=-1e-6)
+        ba, wa = torch.sigmoid(b.to(torch.float32)), torch.sigmoid(w.to(torch.float32))
+    else:
+        gf = g.to(torch.float32)
+        # gdn2.py:38-62: min(g, 0) with the gradient passed wherever g <= 0
+        ga = torch.where(gf <= 0.0, gf, torch.zeros_like(gf))
+        ba, wa = b.to(torch.float32), w.to(torch.float32)
+        if stability_guard:
+            ba = torch.clamp(ba, min=0.0)
+            ga = torch.clamp(ga, max=-1e-6)
+        if qk_l2norm:
+            qh, kh = l2(qf) * scale, l2(kf)
+        else:
+            qh, kh = qf * scale, kf
+        # gdn2.py:2113-2122: normalised q / k are stored back in the input dtype
+        qh, kh = qh.to(q.dtype).to(torch.float32), kh.to(k.dtype).to(torch.float32)
+    qe = torch.repeat_interleave(qh, G, dim=2) if G > 1 else qh
+    ke = torch.repeat_interleave(kh, G, dim=2) if G > 1 else kh
+    ge = _gate_to_heads(ga, B, L, Hk, Hv, K)
+    be = _gate_to_heads(ba, B, L, Hk, Hv, K)
+    we = _gate_to_heads(wa, B, L, Hk, Hv, V)
+    ve = v.to(torch.float32)
+    qe, ke, ve, ge, be, we = (x.contiguous() for x in (qe, ke, ve, ge, be, we))
+    init = initial_state.to(torch.float32).contiguous() if initial_state is not None else None
+    canon = _canonical_segments(seg_t, B, L, initial_state is not None, init_seg_id, dev)
+    out, fin = _RecurrenceFn.apply(qe, ke, ve, ge, be, we, init, (seg_t, init_seg_id, canon, precision))
+    out = out.to(v.dtype)
+    if output_final_state:
+        return out, fin
+    return out
 
 
 def _decode_gate(t, B, Hk, Hv, last, name):

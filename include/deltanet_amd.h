@@ -129,6 +129,40 @@ int dn_decode_step(const dn_decode_args* a, void* stream);
  * every token).  T == 1 is dn_decode_step. */
 int dn_decode_steps(const dn_decode_args* a, int32_t T, void* stream);
 
+/* Arguments of the training backward of the chunked recurrence.  All tensors
+ * are float32 and already prepared by the caller: q (scaled, normalised), k,
+ * g (clamped, natural-log decay) and b at H value heads with K channels each;
+ * v and w at H heads with V channels.  The wrapper's elementwise steps
+ * (prologue, L2-norm, gate broadcast, GQA repeat) are differentiated by the
+ * caller, which sums the returned gradients back to its own layouts. */
+typedef struct dn_backward_args {
+  int32_t abi_version;
+  int32_t B, L, H, K, V;        /* K == V == 128                                 */
+  const void* q;                /* (B,L,H,K) f32                                 */
+  const void* k;                /* (B,L,H,K) f32                                 */
+  const void* v;                /* (B,L,H,V) f32                                 */
+  const void* g;                /* (B,L,H,K) f32, <= 0                           */
+  const void* b;                /* (B,L,H,K) f32                                 */
+  const void* w;                /* (B,L,H,V) f32                                 */
+  const int32_t* seg;           /* NULL or (B,L) canonical segment ids: nondecreasing,
+                                   the initial state belongs to id 0              */
+  const void* init_state;       /* NULL or (B,H,K,V) f32                         */
+  const void* d_out;            /* (B,L,H,V) f32 cotangent of the output          */
+  const void* d_final;          /* NULL or (B,H,K,V) f32 cotangent of the final state */
+  void *dq, *dk, *dv, *dg, *db, *dw;  /* f32, shapes of q k v g b w            */
+  void* d_init;                 /* NULL or (B,H,K,V) f32 (needs init_state)       */
+} dn_backward_args;
+
+/* Workspace bytes dn_prefill_bwd needs (0 if the arguments are invalid):
+ * about 525 KB per (batch, head, 64-token chunk). */
+size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
+
+/* Backward of the chunked recurrence: replaces the reference's custom-VJP
+ * backward (gdn2.py:1446-1769: reverse state scan gdn2.py:698-769 and the
+ * analytical prepass adjoint gdn2.py:243-493, 496-582).  Gradients of
+ * sum(out * d_out) + sum(final * d_final) are written (not accumulated). */
+int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
 /* In-place Frobenius cap S <- S * min(1, tau / sqrt(||S||_F^2 + 1e-6)) of
  * `nmat` consecutive (rows x cols) float32 matrices (the stability_guard cap of
  * gdn2.py:2180-2188 / 2224-2226 / 2236-2238). */
@@ -138,10 +172,11 @@ int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, fl
  * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
  * every dn_prefill_fwd call on the calling thread records HIP events on its
  * stream around each of its kernels (prepass, value, chain) and every
- * dn_decode_step / dn_decode_steps call around its kernel.  dn_profile_end() waits for those
+ * dn_decode_step / dn_decode_steps call around its kernel, and every
+ * dn_prefill_bwd call around its four kernels together.  dn_profile_end() waits for those
  * events and writes, per kernel kind, the summed duration in milliseconds
  * and the number of launches (arrays of DN_PROFILE_KINDS entries). */
-#define DN_PROFILE_KINDS 4   /* 0 prepass, 1 value, 2 chain, 3 decode */
+#define DN_PROFILE_KINDS 5   /* 0 prepass, 1 value, 2 chain, 3 decode, 4 backward */
 int dn_profile_begin(void);
 int dn_profile_end(double* ms_sum, int64_t* launches);
 

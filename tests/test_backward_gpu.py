@@ -1,0 +1,190 @@
+"""GPU parity of the training backward (``chunk_gdn2(..., is_inference=False)``
+under torch.autograd, HIP kernels of ``dn_prefill_bwd``) against the gradient
+oracle (oracle/gdn_grad.py, pinned in tests/test_oracle_grad.py).
+
+Cases and tolerances follow the reference's gradient tests: rel L2 per
+gradient < 1e-5 in "fp32" mode and < 1e-2 in "bf16" mode
+(tests/test_parity.py:32-68), the L2-norm / scale / GQA case
+(test_parity.py:71-99), the fused prologue with an unaligned length, initial
+state, segment ids and a final-state cotangent (test_parity.py:160-221),
+strong decay g <= -150 (tests/test_strong_decay.py:35-69, tolerance 1e-3 /
+1e-2), gate layouts (tests/test_matrix.py) and chunk_gdn (variants.py:17-88).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn_grad as GR
+from oracle import gdn_oracle as O
+from tests._util import rel_l2, sig
+from tests.gpu_common import as_np, to_dev
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("dq", "dk", "dv", "dg", "db", "dw")
+
+
+def ref_inputs(seed, B, L, Hk, Hv, K=128, V=128):
+    """The reference tests' generator (test_parity.py:18-26), seeded NumPy."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s)
+    q = f(B, L, Hk, K) * 0.1
+    k = f(B, L, Hk, K) * 0.1
+    v = f(B, L, Hv, V) * 0.1
+    b = sig(f(B, L, Hk, K) * 0.39)
+    w = sig(f(B, L, Hv, V) * 0.39)
+    g = -np.exp(f(B, L, Hk, K) * 0.39 - 1.0)
+    return q, k, v, g, b, w
+
+
+def run_dev(q, k, v, g, b, w, do, df=None, init=None, qkv_dtype=torch.float32, fn=None, **kw):
+    ts = [to_dev(x, qkv_dtype if i < 3 else torch.float32).requires_grad_(True)
+          for i, x in enumerate((q, k, v, g, b, w))]
+    ti = to_dev(init).requires_grad_(True) if init is not None else None
+    if fn is None:
+        from deltanet_tpu_amd import chunk_gdn2 as fn
+    res = fn(*ts, initial_state=ti, output_final_state=df is not None, is_inference=False, **kw)
+    if df is not None:
+        out, fin = res
+        loss = (out.float() * to_dev(do)).sum() + (fin * to_dev(df)).sum()
+    else:
+        out = res
+        loss = (out.float() * to_dev(do)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = {n: as_np(t.grad) for n, t in zip(NAMES, ts)}
+    grads["dinit"] = as_np(ti.grad) if ti is not None else None
+    return as_np(out), grads
+
+
+def compare(got, ref, tol, tag):
+    errs = {n: rel_l2(got[n], ref[n]) for n in (*NAMES, "dinit") if ref.get(n) is not None and n in got}
+    print("[measured]", tag, " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
+    for n, e in errs.items():
+        assert np.isfinite(got[n]).all(), (tag, n, "non-finite")
+        assert e < tol, f"{tag}: gradient {n} rel L2 {e:.2e} exceeds {tol:.1e}"
+
+
+@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 1e-2)])
+@pytest.mark.parametrize("L", [128, 256, 512])
+def test_backward_parity(precision, tol, L):
+    B, Hk, Hv = 1, 2, 4
+    q, k, v, g, b, w = ref_inputs(42 + L, B, L, Hk, Hv)
+    do = np.random.default_rng(100 + L).standard_normal((B, L, Hv, 128))
+    out, got = run_dev(q, k, v, g, b, w, do, precision=precision)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+    o_ref, _ = O.chunk_gdn2(q, k, v, g, b, w, is_inference=False)
+    e_o = rel_l2(out, o_ref)
+    print(f"[measured] L={L} {precision}: out rel L2 {e_o:.2e}", flush=True)
+    assert e_o < tol
+    compare(got, ref, tol, f"parity L={L} {precision}")
+
+
+def test_backward_l2norm_scale_gqa():
+    B, L, Hk, Hv = 1, 256, 2, 4
+    q, k, v, g, b, w = ref_inputs(7, B, L, Hk, Hv)
+    do = np.random.default_rng(8).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision="fp32", qk_l2norm=True, scale=0.5)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, qk_l2norm=True, scale=0.5)
+    compare(got, ref, 1e-5, "l2norm scale=0.5 G=2")
+
+
+@pytest.mark.parametrize("L", [300, 384])
+def test_backward_fuse_prologue_unaligned(L):
+    B, Hk, Hv, K, V = 1, 2, 4, 128, 128
+    rng = np.random.default_rng(2026 + L)
+    f = lambda *s: rng.standard_normal(s)
+    q, k, v = f(B, L, Hk, K) * 0.1, f(B, L, Hk, K) * 0.1, f(B, L, Hv, V) * 0.1
+    g = f(B, L, Hk, K) * 0.39 - 1.0
+    b = f(B, L, Hk, K) * 0.39
+    w = f(B, L, Hv, V) * 0.39
+    init = f(B, Hv, K, V) * 0.05
+    seg = np.array([[0] * (L // 3) + [1] * (L // 3) + [2] * (L - 2 * (L // 3))], dtype=np.int32)
+    do, df = f(B, L, Hv, V), f(B, Hv, K, V)
+    kw = dict(qk_l2norm=True, fuse_prologue=True)
+    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32",
+                     segment_ids=torch.from_numpy(seg).cuda(), **kw)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, segment_ids=seg, **kw)
+    compare(got, ref, 1e-5, f"fuse_prologue L={L}")
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_backward_strong_decay(precision):
+    B, L, Hk, Hv = 1, 256, 2, 4
+    q, k, v, _, b, w = ref_inputs(501, B, L, Hk, Hv)
+    g = -150.0 - np.abs(np.random.default_rng(502).standard_normal((B, L, Hk, 128)) * 50.0)
+    do = np.random.default_rng(503).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision=precision)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+    compare(got, ref, 1e-3 if precision == "fp32" else 1e-2, f"strong decay {precision}")
+
+
+def test_backward_positive_decay_and_guard():
+    """Positive g is clamped (zero gradient, test_strong_decay.py:72-89);
+    stability_guard clamps b >= 0 and g <= -1e-6 (gdn2.py:1972-1974)."""
+    B, L, Hk, Hv = 1, 192, 2, 4
+    q, k, v, g, b, w = ref_inputs(9, B, L, Hk, Hv)
+    rng = np.random.default_rng(10)
+    g = np.where(rng.random(g.shape) < 0.3, np.abs(g) * 0.2 + 0.01, g)
+    b = b - 0.3
+    do = rng.standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision="fp32", stability_guard=True)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, stability_guard=True)
+    compare(got, ref, 1e-5, "guard + positive g")
+    assert np.all(got["dg"][g > 0] == 0.0)
+
+
+@pytest.mark.parametrize("layout", ["scalar_hk", "rank3_one", "gates_at_hv"])
+def test_backward_gate_layouts(layout):
+    B, L, Hk, Hv = 2, 200, 1, 2
+    rng = np.random.default_rng(11)
+    f = lambda *s: rng.standard_normal(s)
+    q, k, v = f(B, L, Hk, 128) * 0.1, f(B, L, Hk, 128) * 0.1, f(B, L, Hv, 128) * 0.1
+    if layout == "scalar_hk":
+        g, b, w = -np.exp(f(B, L, Hk, 1) * 0.39 - 1), sig(f(B, L, Hk, 1)), sig(f(B, L, Hk, 1))
+    elif layout == "rank3_one":
+        g, b, w = -np.exp(f(B, L, 1) * 0.39 - 1), sig(f(B, L, Hk, 128)), sig(f(B, L, 1))
+    else:
+        g, b, w = -np.exp(f(B, L, Hv, 128) * 0.39 - 1), sig(f(B, L, Hv, 128)), sig(f(B, L, Hv, 128))
+    seg = np.array([[0] * 70 + [1] * 130, [5] * 150 + [2] * 50])
+    init = f(B, Hv, 128, 128) * 0.05
+    do, df = f(B, L, Hv, 128), f(B, Hv, 128, 128)
+    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32",
+                     segment_ids=torch.from_numpy(seg).cuda(), initial_state_segment_id=[0, 2])
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, segment_ids=seg,
+                            initial_state_segment_id=[0, 2])
+    compare(got, ref, 1e-5, f"gates {layout}")
+    # batch 1's first document (id 5) differs from its initial_state_segment_id (2)
+    assert np.all(got["dinit"][1] == 0.0) and np.abs(got["dinit"][0]).max() > 0
+
+
+def test_backward_bf16_inputs_and_chunk_gdn():
+    from deltanet_tpu_amd import chunk_gdn
+    B, L, Hk, Hv = 1, 256, 2, 4
+    q, k, v, g, b, w = ref_inputs(12, B, L, Hk, Hv)
+    qb, kb, vb = (O.bf16_round(x).astype(np.float64) for x in (q, k, v))
+    do = np.random.default_rng(13).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, qkv_dtype=torch.bfloat16, precision="fp32", qk_l2norm=True)
+    # a bf16 output receives its cotangent in bf16 (as JAX's does), and the
+    # gradients of bf16 leaves are bf16: they carry bf16 rounding (2^-9)
+    dob = O.bf16_round(do).astype(np.float64)
+    ref = GR.chunk_gdn2_vjp(qb, kb, vb, g, b, w, dob, qk_l2norm=True, qk_bf16=True)
+    compare({n: got[n] for n in ("dg", "db", "dw")}, ref, 1e-5, "bf16 q/k/v, l2norm (f32 leaves)")
+    compare({n: got[n] for n in ("dq", "dk", "dv")}, ref, 4e-3, "bf16 q/k/v, l2norm (bf16 leaves)")
+    # chunk_gdn: scalar decay per head, b = w = beta (variants.py:17-88)
+    gs = -np.exp(np.random.default_rng(14).standard_normal((B, L, Hk)) * 0.39 - 1)
+    beta = sig(np.random.default_rng(15).standard_normal((B, L, Hk)))
+    qt, kt, vt = (to_dev(x).requires_grad_(True) for x in (q, k, v))
+    gt, bt = to_dev(gs).requires_grad_(True), to_dev(beta).requires_grad_(True)
+    out = chunk_gdn(qt, kt, vt, gt, bt, precision="fp32", is_inference=False)
+    (out.float() * to_dev(do)).sum().backward()
+    rg = GR.chunk_gdn2_vjp(q, k, v, gs, beta, beta, do)
+    # beta feeds both b and w: its gradient is the sum of both
+    got2 = {"dq": as_np(qt.grad), "dk": as_np(kt.grad), "dv": as_np(vt.grad), "dg": as_np(gt.grad)}
+    for n in got2:
+        e = rel_l2(got2[n], rg[n])
+        print(f"[measured] chunk_gdn {n}={e:.2e}", flush=True)
+        assert e < 1e-5, n
+    e = rel_l2(as_np(bt.grad), rg["db"] + rg["dw"])
+    assert e < 1e-5, e
