@@ -123,10 +123,10 @@ PROFILE_DIR = os.path.join(ROOT, "profiles")
 TRAFFIC_JSON = os.path.join(PROFILE_DIR, "pmc_traffic_cfg2_cfg4.json")
 KT_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --stats "
           "--output-format csv -d gpurun_out/kt -o run -- python3 bench.py --no-cpu-baseline --steps 50 "
-          "--warmup 5 --decode-steps 16 --copy-calibration")
+          "--warmup 5 --decode-steps 16 --train-steps 0 --copy-calibration")
 PMC_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --pmc {ctr} --output-format csv "
            "-d gpurun_out/{d} -o run -- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1 "
-           "--decode-steps 2 --copy-calibration")
+           "--decode-steps 2 --train-steps 0 --copy-calibration")
 COPY_BYTES = 256 * 32 * 128 * 128 * 4   # the --copy-calibration copy (read and write this many bytes)
 
 
@@ -214,6 +214,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--train-steps", type=int, default=10,
+                    help="forward + backward steps timed at the config-2 shape (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -313,6 +315,36 @@ def main():
                    "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"decode {sd}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[sd]['state_GBps']} GB/s)")
 
+    # ---- training step (forward + backward) at the config-2 shape ----------
+    train = None
+    if args.train_steps > 0:
+        tq, tk, tv, tg, tb, tw = (x.detach().clone().requires_grad_(True) for x in (q, k, v, g, b, w))
+        tdo = torch.randn(tv.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(9)).to(tv.dtype)
+
+        def tstep():
+            o = chunk_gdn2(tq, tk, tv, tg, tb, tw, segment_ids=seg, is_inference=False, qk_l2norm=True,
+                           precision="bf16", chunk_size=128)
+            o.backward(tdo)
+
+        for _ in range(3):
+            tstep()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.train_steps):
+            tstep()
+        torch.cuda.synchronize()
+        t_us = (time.perf_counter() - t0) * 1e6 / args.train_steps
+        _lib.profile_begin()
+        for _ in range(args.train_steps):
+            tstep()
+        torch.cuda.synchronize()
+        tprof = _lib.profile_end()
+        tk_us = {n: round(ms * 1e3 / args.train_steps, 1) for n, (ms, c) in tprof.items() if c}
+        train = {"workload": "chunk_gdn2 forward + backward (is_inference=False, autograd), config-2 shape, "
+                             "precision bf16 forward, fp32 backward", "us_per_step": round(t_us, 1),
+                 "kernels_us_per_step": tk_us}
+        log(f"training step: {t_us:.1f} us; kernels per step (us): {tk_us}")
+
     copy_gbps = None
     if args.copy_calibration:
         # a plain device copy of the decode state's size: the practical
@@ -362,6 +394,7 @@ def main():
         "roofline": roof,
         "decode": {"workload": "gdn2_decode_step, BASELINE config 4: B=256 Hk=16 Hv=32 K=V=128, bf16 qkv, "
                                "channel-wise fp32 gates, qk_l2norm", **dec},
+        "training": train,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -116,7 +116,8 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
   __shared__ float sG[BC][KP];
   __shared__ float sA[BC][CP];   // A, then T
   __shared__ float sM[BC][CP];
-  __shared__ float sW[BC][KP];
+  __shared__ float sW[BC][KP];    // b * k of the chunk, then W
+  __shared__ float sQ[BC][KP];    // q of the chunk
   __shared__ int sseg[BC], scar[BC], slast[BC];
 
   const int u = blockIdx.x;
@@ -130,14 +131,29 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
     (&sA[0][0])[i] = 0.f;
     (&sM[0][0])[i] = 0.f;
   }
-  __syncthreads();
+  // stage q and beta = b k (rows past the sequence end are zero)
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / 256; ++it) {
+    const int idx = tid + 256 * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    float4 qv = zero_f4(), bv = zero_f4();
+    if (t0 + i < p.L) {
+      const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
+      qv = ld4g(p.q + ro);
+      const float4 b4 = ld4g(p.b + ro), k4 = ld4g(p.k + ro);
+      bv = make_float4(b4.x * k4.x, b4.y * k4.y, b4.z * k4.z, b4.w * k4.w);
+    }
+    *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qv;
+    *reinterpret_cast<float4*>(&sW[i][4 * c4]) = bv;
+  }
   // ---- cumulative decay (log2 units), per channel -------------------------
   if (tid < KD) {
+    float gv[BC];
+#pragma unroll
+    for (int t = 0; t < BC; ++t) gv[t] = t0 + t < p.L ? p.g[row_of(p, bb, t0 + t, h) + tid] : 0.f;
     float acc = 0.f;
+#pragma unroll
     for (int t = 0; t < BC; ++t) {
-      const int tok = t0 + t;
-      const float gv = tok < p.L ? p.g[row_of(p, bb, tok, h) + tid] : 0.f;
-      acc += gv * kLog2e;
+      acc += gv[t] * kLog2e;
       sG[t][tid] = acc;
       G[t * KD + tid] = acc;
     }
@@ -156,22 +172,13 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
       const int m = 16 * I;
       const int i = 16 * I + l16, j = 16 * J + l16;
       const bool vi = t0 + i < p.L, vj = t0 + j < p.L;
-      const float* qi = p.q + row_of(p, bb, vi ? t0 + i : 0, h);
-      const float* ki = p.k + row_of(p, bb, vi ? t0 + i : 0, h);
-      const float* bi = p.b + row_of(p, bb, vi ? t0 + i : 0, h);
+      const float* xi = isM ? &sQ[i][0] : &sW[i][0];
       const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        float xa[8], xb[8], x2[8], gi[8], gm[8], gj[8];
-        if (isM) {
-          row8(qi, s, q, xa);
-        } else {
-          row8(bi, s, q, xa);
-          row8(ki, s, q, x2);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xa[e] *= x2[e];
-        }
+        float xa[8], xb[8], gi[8], gm[8], gj[8];
+        row8(xi, s, q, xa);
         row8(kj, s, q, xb);
         row8(&sG[i][0], s, q, gi);
         row8(&sG[m][0], s, q, gm);
@@ -192,21 +199,14 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
       const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
 #pragma unroll
       for (int e = 0; e < 4; ++e) res[e] = 0.f;
+#pragma unroll 8
       for (int r4 = 0; r4 < KD / 4; ++r4) {
         const float4 kv = ld4g(kj + 4 * r4);
         const float4 gjv = *reinterpret_cast<const float4*>(&sG[j][4 * r4]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
-          const int ti = t0 + i < p.L ? t0 + i : 0;
-          float4 xv;
-          if (isM) {
-            xv = ld4g(p.q + row_of(p, bb, ti, h) + 4 * r4);
-          } else {
-            const float4 bv = ld4g(p.b + row_of(p, bb, ti, h) + 4 * r4);
-            const float4 k2 = ld4g(p.k + row_of(p, bb, ti, h) + 4 * r4);
-            xv = make_float4(bv.x * k2.x, bv.y * k2.y, bv.z * k2.z, bv.w * k2.w);
-          }
+          const float4 xv = *reinterpret_cast<const float4*>(isM ? &sQ[i][4 * r4] : &sW[i][4 * r4]);
           const float4 giv = *reinterpret_cast<const float4*>(&sG[i][4 * r4]);
           res[e] += xv.x * kv.x * ex2(giv.x - gjv.x) + xv.y * kv.y * ex2(giv.y - gjv.y) +
                     xv.z * kv.z * ex2(giv.z - gjv.z) + xv.w * kv.w * ex2(giv.w - gjv.w);
@@ -253,11 +253,13 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
     }
     float* Kc = p.Kc + (int64_t)u * CK;
     float* KcT = p.KcT + (int64_t)u * CK;
+#pragma unroll 8
     for (int idx = t2; idx < CK; idx += 192) {
       const int j = idx / KD, r = idx % KD;
       const bool ok = slast[j] && t0 + j < p.L;
       Kc[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
     }
+#pragma unroll 8
     for (int idx = t2; idx < CK; idx += 192) {
       const int r = idx / BC, j = idx % BC;
       const bool ok = slast[j] && t0 + j < p.L;
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
           const int j = 32 * s + pi_k(q, e);
           const bool vj = t0 + j < p.L;
           const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
-          xb[e] = (vj && scar[j]) ? p.b[ro] * p.k[ro] * ex2(sG[j][r]) : 0.f;
+          xb[e] = scar[j] ? sW[j][r] * ex2(sG[j][r]) : 0.f;
           xu[e] = vj ? p.w[ro] * p.v[ro] : 0.f;
         }
         const Frag<false> fb = fr8(xb), fu = fr8(xu);
@@ -308,6 +310,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
     float* Wm = p.Wm + (int64_t)u * CK;
     float* WT = p.WT + (int64_t)u * CK;
     float* U0 = p.U0 + (int64_t)u * CK;
+    __syncthreads();   // every wave has read b k from sW
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -366,8 +369,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
-          const bool vi = t0 + i < p.L && scar[i];
-          const float qe = vi ? p.q[row_of(p, bb, t0 + i, h) + r] * ex2(sG[i][r]) : 0.f;
+          const float qe = scar[i] ? sQ[i][r] * ex2(sG[i][r]) : 0.f;
           o[e] = qe - ax[I][R2][e];
         }
         *reinterpret_cast<float4*>(XfT + r * BC + 16 * I + 4 * q) = make_float4(o[0], o[1], o[2], o[3]);
@@ -381,13 +383,71 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 // rows 32w..32w+31.
 //   forward  (BWD = false):  Y = U0 - W S ;  S <- lam * S + Kc^T Y
 //   backward (BWD = true):   Z = -Kc dS  ;  dS <- lam * dS + Xf^T dO + W^T Z
+// Every operand but the state is known before the scan, so each step loads
+// the next chunk's operands while it computes.  The 8 column tiles of a head
+// run on one XCD (xcd_block), which serves their shared rows from its L2.
 // ---------------------------------------------------------------------------
+struct ChainOps {
+  float a[4][8];        // W (forward) / Kc (backward) rows of this wave's 16 tokens
+  float b[2][2][8];     // Kc^T (forward) / W^T (backward) rows of this wave's 32 state rows
+  float x[2][2][8];     // Xf^T rows (backward)
+  float o[2][8];        // dO fragments (backward)
+  float u[4];           // U0 tile entries (forward)
+  float lm[2][4];       // lam of this lane's state rows
+};
+
+template <bool BWD>
+__device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, int c, int col0, int wv, int l,
+                                           ChainOps& o) {
+  const int q = l >> 4, l16 = l & 15;
+  const int64_t u = (int64_t)bh * p.NC + c;
+  const float* Arow = (BWD ? p.Kc : p.Wm) + u * CK + (16 * wv + l16) * KD;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) row8(Arow, s, q, o.a[s]);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int rA = 32 * wv + 16 * tt + l16;
+    const float* Brow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) row8(Brow, s2, q, o.b[tt][s2]);
+    if (BWD) {
+      const float* Xrow = p.XfT + u * CK + rA * BC;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) row8(Xrow, s2, q, o.x[tt][s2]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.lm[tt][e] = p.lam[u * KD + 32 * wv + 16 * tt + 4 * q + e];
+  }
+  if (BWD) {
+    const int t0 = c * BC;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tok = t0 + 32 * s2 + pi_k(q, e);
+        o.o[s2][e] = tok < p.L ? p.dout[row_of(p, bb, tok, h) + col0 + l16] : 0.f;
+      }
+  } else {
+    const float* U0 = p.U0 + u * CK;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.u[e] = U0[(16 * wv + 4 * q + e) * KD + col0 + l16];
+  }
+}
+
 template <bool BWD>
 __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
   __shared__ float sS[4][64][8];
   __shared__ float sY[2][64][8];
-  const int blk = blockIdx.x;
-  const int ct = blk % (KD / 16), bh = blk / (KD / 16), h = bh % p.H, bb = bh / p.H;
+  int ct, bh, zz;
+  {
+    int x = blockIdx.x, y = 0, z = 0;
+    xcd_block(x, y, z);     // 1-D grid: x = 8 * (batch * H + head) + column tile
+    ct = x % (KD / 16);
+    bh = x / (KD / 16);
+    zz = z;
+  }
+  (void)zz;
+  const int h = bh % p.H, bb = bh / p.H;
   const int col0 = 16 * ct;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
 
@@ -406,10 +466,12 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     sS[wv][l][4 + e] = st[1][e];
   }
 
+  ChainOps cur, nxt;
+  chain_load<BWD>(p, bh, bb, h, BWD ? p.NC - 1 : 0, col0, wv, l, cur);
   for (int it = 0; it < p.NC; ++it) {
     const int c = BWD ? p.NC - 1 - it : it;
     const int64_t u = (int64_t)bh * p.NC + c;
-    const int t0 = c * BC;
+    if (it + 1 < p.NC) chain_load<BWD>(p, bh, bb, h, BWD ? c - 1 : c + 1, col0, wv, l, nxt);
     __syncthreads();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;
@@ -424,53 +486,23 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     }
     // Y (or Z) tile: token rows 16w..16w+15
     f32x4 y = zero4();
-    {
-      const float* Arow = (BWD ? p.Kc : p.Wm) + u * CK + (16 * wv + l16) * KD;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float xa[8];
-        row8(Arow, s, q, xa);
-        mma(y, fr8(xa), fr8(&sS[s][l][0]));
-      }
-    }
-    if (BWD) {
+    for (int s = 0; s < 4; ++s) mma(y, fr8(cur.a[s]), fr8(&sS[s][l][0]));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = -y[e];
-    } else {
-      const float* U0 = p.U0 + u * CK;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = U0[(16 * wv + 4 * q + e) * KD + col0 + l16] - y[e];
-    }
+    for (int e = 0; e < 4; ++e) y[e] = BWD ? -y[e] : cur.u[e] - y[e];
 #pragma unroll
     for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
     __syncthreads();
-    const float* lam = p.lam + u * KD;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int rA = 32 * wv + 16 * tt + l16;
       f32x4 acc;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = lam[32 * wv + 16 * tt + 4 * q + e] * st[tt][e];
-      const float* Arow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
+      for (int e = 0; e < 4; ++e) acc[e] = cur.lm[tt][e] * st[tt][e];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float xa[8];
-        row8(Arow, s2, q, xa);
-        mma(acc, fr8(xa), fr8(&sY[s2][l][0]));
-      }
+      for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(cur.b[tt][s2]), fr8(&sY[s2][l][0]));
       if (BWD) {
-        const float* Xrow = p.XfT + u * CK + rA * BC;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          float xa[8], xb[8];
-          row8(Xrow, s2, q, xa);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int tok = t0 + 32 * s2 + pi_k(q, e);
-            xb[e] = tok < p.L ? p.dout[row_of(p, bb, tok, h) + col0 + l16] : 0.f;
-          }
-          mma(acc, fr8(xa), fr8(xb));
-        }
+        for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(cur.x[tt][s2]), fr8(cur.o[s2]));
       }
       st[tt] = acc;
     }
@@ -479,6 +511,7 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
       sS[wv][l][e] = st[0][e];
       sS[wv][l][4 + e] = st[1][e];
     }
+    cur = nxt;
   }
   if (BWD && p.dinit != nullptr) {
 #pragma unroll
@@ -723,7 +756,7 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
   // ---- dq, dbeta, dk per 16 x 16 tile; dG into sU ----------------------------
   float (*sdG)[KD] = sU;
   for (int I = 0; I < 4; ++I) {
-#pragma unroll
+#pragma unroll 1
     for (int R2 = 0; R2 < 2; ++R2) {
       const int r = 32 * wv + 16 * R2 + l16;
       // S0-side products: (dO S0^T), (dX S0^T)
@@ -740,10 +773,11 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
       }
       // off-diagonal blocks, reference row m = 16 I (rows i) ...
       f32x4 oq = zero4(), ob = zero4();
-      if (I > 0) {
+      {
         const int m = 16 * I;
         const float gm = G[m * KD + r];
-        for (int s = 0; s < (I + 1) / 2; ++s) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
           float xm[8], xa[8], xk[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -760,10 +794,11 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
       }
       // ... and reference row m = 16 J + 15 (columns j, here the rows of dk)
       f32x4 ok_ = zero4();
-      if (I < 3) {
+      {
         const int m = 16 * I + 15;
         const float gm = G[m * KD + r];
-        for (int s = (16 * (I + 1)) / 32; s < 2; ++s) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
           float xm[8], xa[8], xq[8], xbeta[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -848,6 +883,7 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
     float tail = 0.f;
     if (scar[BC - 1]) {
       float rs = 0.f;
+#pragma unroll 8
       for (int v4 = 0; v4 < KD / 4; ++v4) {
         const float4 a = ld4g(S0 + r * KD + 4 * v4);
         const float4 d = ld4g(dSC + r * KD + 4 * v4);
@@ -855,18 +891,25 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
       }
       tail = exp2f(G[(BC - 1) * KD + r]) * rs;
     }
+    float dgv[BC];
+#pragma unroll
+    for (int t = 0; t < BC; ++t) dgv[t] = t0 + t < p.L ? p.dg[row_of(p, bb, t0 + t, h) + r] : 0.f;
     float fwd = 0.f;
-    for (int t = 0; t < BC && t0 + t < p.L; ++t) {
-      float* d = p.dg + row_of(p, bb, t0 + t, h) + r;
-      const float pj = *d;
-      *d = fwd;
+#pragma unroll
+    for (int t = 0; t < BC; ++t) {
+      const float pj = dgv[t];
+      dgv[t] = fwd;
       fwd += pj;
     }
     float acc = tail;
+#pragma unroll
     for (int t = BC - 1; t >= 0; --t) {
       acc += sdG[t][r];
-      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + r] += acc;
+      dgv[t] += acc;
     }
+#pragma unroll
+    for (int t = 0; t < BC; ++t)
+      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + r] = dgv[t];
   }
 }
 

@@ -14,6 +14,8 @@
 //   cap |S'|_F at tau (guard), cast to state dtype  gdn2.py:2484-2489
 // The read-out uses o_j = sum_i q_i d_i S_ij + (q.k) vn_j, which equals
 // S'^T q exactly in real arithmetic and needs only the single pass over S.
+#include <atomic>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -32,30 +34,37 @@ int set_error(int code, const char* msg) {
 }
 
 namespace {
+// Profiling records are process-wide (a framework may launch the backward from
+// its own thread); the event opened by a launch's first mark is per thread.
 struct ProfRec { int kind; hipEvent_t a, b; };
-thread_local bool g_prof = false;
-thread_local std::vector<ProfRec> g_recs;
-thread_local std::vector<hipEvent_t> g_pool;
+std::atomic<bool> g_prof{false};
+std::mutex g_prof_mu;
+std::vector<ProfRec> g_recs;
+std::vector<hipEvent_t> g_pool;
 thread_local hipEvent_t g_open = nullptr;
 
 hipEvent_t take_event() {
-  if (!g_pool.empty()) { hipEvent_t e = g_pool.back(); g_pool.pop_back(); return e; }
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (!g_pool.empty()) { hipEvent_t e = g_pool.back(); g_pool.pop_back(); return e; }
+  }
   hipEvent_t e = nullptr;
   if (hipEventCreate(&e) != hipSuccess) return nullptr;
   return e;
 }
 }  // namespace
 
-bool profiling() { return g_prof; }
+bool profiling() { return g_prof.load(); }
 
 void prof_mark(int kind, hipStream_t st, bool after) {
-  if (!g_prof) return;
+  if (!g_prof.load()) return;
   hipEvent_t e = take_event();
   if (e == nullptr) return;
   (void)hipEventRecord(e, st);
   if (!after) {
     g_open = e;
   } else if (g_open != nullptr) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
     g_recs.push_back(ProfRec{kind, g_open, e});
     g_open = nullptr;
   }
@@ -520,19 +529,25 @@ using namespace dn;
 extern "C" const char* dn_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" int dn_profile_begin(void) {
-  g_prof = true;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
   g_recs.clear();
+  g_prof.store(true);
   return DN_OK;
 }
 
 extern "C" int dn_profile_end(double* ms_sum, int64_t* launches) {
-  g_prof = false;
+  std::vector<ProfRec> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof.store(false);
+    recs.swap(g_recs);
+  }
   for (int k = 0; k < DN_PROFILE_KINDS; ++k) {
     if (ms_sum) ms_sum[k] = 0.0;
     if (launches) launches[k] = 0;
   }
   int rc = DN_OK;
-  for (const ProfRec& r : g_recs) {
+  for (const ProfRec& r : recs) {
     float ms = 0.f;
     if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) {
       rc = set_error(DN_E_LAUNCH, "profiling event failed");
@@ -540,10 +555,12 @@ extern "C" int dn_profile_end(double* ms_sum, int64_t* launches) {
       if (ms_sum) ms_sum[r.kind] += ms;
       if (launches) launches[r.kind] += 1;
     }
+  }
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  for (const ProfRec& r : recs) {
     g_pool.push_back(r.a);
     g_pool.push_back(r.b);
   }
-  g_recs.clear();
   return rc;
 }
 

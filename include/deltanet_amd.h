@@ -170,7 +170,7 @@ int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, fl
 
 /* Kernel timing instrumentation (no counterpart in the reference; for
  * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
- * every dn_prefill_fwd call on the calling thread records HIP events on its
+ * every dn_prefill_fwd call (from any thread of the process) records HIP events on its
  * stream around each of its kernels (prepass, value, chain) and every
  * dn_decode_step / dn_decode_steps call around its kernel, and every
  * dn_prefill_bwd call around its four kernels together.  dn_profile_end() waits for those
