@@ -30,7 +30,10 @@
 //   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G
 //   k_bw_chain<false>  per (batch, head, 16-column tile): S_c for every chunk
 //   k_bw_chain<true>   same tiles, reverse: dS_{c+1} for every chunk, dS_0
-//   k_bw_grads   per (batch, head, chunk): dq, dk, dv, dg, db, dw
+//   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA and the chunk-wide
+//                products of dq, dk, db
+//   k_bw_dqk     per (batch, head, chunk, half of the key channels): dq, dk,
+//                db, dg
 #include "dn_common.h"
 #include "dn_host.h"
 
@@ -65,6 +68,7 @@ struct BW {
   float *MT;   // [BC][BC] M^T
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
+  float *dMw, *dAw; // [BC][BC] dM and dA (k_bw_grads -> k_bw_dqk)
   float *S, *ST;    // [KD][KD] state entering the chunk, and its transpose
   float *dS, *dST;  // [KD][KD] gradient of the state leaving the chunk, and its transpose
 };
@@ -90,7 +94,9 @@ __device__ __forceinline__ void chunk_docs(const BW& p, int bb, int t0, int* sse
   slast[t] = s == seg_at(p, bb, t0 + BC - 1);
 }
 
-__device__ __forceinline__ float ex2(float x) { return exp2f(fminf(x, 0.f)); }
+// 2^x for x <= 0 (v_exp_f32; results below 2^-126 flush to zero, which no
+// gradient here can resolve anyway)
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(fminf(x, 0.f)); }
 
 __device__ __forceinline__ float4 ld4g(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 zero_f4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
@@ -157,9 +163,9 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
       sG[t][tid] = acc;
       G[t * KD + tid] = acc;
     }
-    p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? exp2f(acc) : 0.f;
+    p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(acc) : 0.f;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- A (strict) and M (with diagonal), 16x16 tiles of the lower triangle --
   for (int task = wv; task < 20; task += 4) {
@@ -220,7 +226,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
       (isM ? sM : sA)[i][j] = ok ? res[e] : 0.f;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- T = (I + A)^-1 by forward substitution (wave 0, lane = column) -----
   if (wv == 0) {
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
       KcT[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- W = T diag(carry) (b k e^G), U0 = T (w v) ---------------------------
   {
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
     float* Wm = p.Wm + (int64_t)u * CK;
     float* WT = p.WT + (int64_t)u * CK;
     float* U0 = p.U0 + (int64_t)u * CK;
-    __syncthreads();   // every wave has read b k from sW
+    lds_barrier();   // every wave has read b k from sW
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -327,7 +333,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
             make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
       }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- Xf = diag(carry) q e^G - M W ----------------------------------------
   {
@@ -424,8 +430,9 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
+        // tokens past the end read a clamped row: their Xf^T columns are zero
         const int tok = t0 + 32 * s2 + pi_k(q, e);
-        o.o[s2][e] = tok < p.L ? p.dout[row_of(p, bb, tok, h) + col0 + l16] : 0.f;
+        o.o[s2][e] = p.dout[row_of(p, bb, min(tok, p.L - 1), h) + col0 + l16];
       }
   } else {
     const float* U0 = p.U0 + u * CK;
@@ -466,13 +473,10 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     sS[wv][l][4 + e] = st[1][e];
   }
 
-  ChainOps cur, nxt;
-  chain_load<BWD>(p, bh, bb, h, BWD ? p.NC - 1 : 0, col0, wv, l, cur);
-  for (int it = 0; it < p.NC; ++it) {
-    const int c = BWD ? p.NC - 1 - it : it;
+  // one scan step on chunk c with operands `o` in registers
+  auto step = [&](int c, const ChainOps& o) {
     const int64_t u = (int64_t)bh * p.NC + c;
-    if (it + 1 < p.NC) chain_load<BWD>(p, bh, bb, h, BWD ? c - 1 : c + 1, col0, wv, l, nxt);
-    __syncthreads();
+    lds_barrier();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;
       float* XT = (BWD ? p.dST : p.ST) + u * KK;
@@ -487,22 +491,22 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     // Y (or Z) tile: token rows 16w..16w+15
     f32x4 y = zero4();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) mma(y, fr8(cur.a[s]), fr8(&sS[s][l][0]));
+    for (int s = 0; s < 4; ++s) mma(y, fr8(o.a[s]), fr8(&sS[s][l][0]));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = BWD ? -y[e] : cur.u[e] - y[e];
+    for (int e = 0; e < 4; ++e) y[e] = BWD ? -y[e] : o.u[e] - y[e];
 #pragma unroll
     for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       f32x4 acc;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = cur.lm[tt][e] * st[tt][e];
+      for (int e = 0; e < 4; ++e) acc[e] = o.lm[tt][e] * st[tt][e];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(cur.b[tt][s2]), fr8(&sY[s2][l][0]));
+      for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(o.b[tt][s2]), fr8(&sY[s2][l][0]));
       if (BWD) {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(cur.x[tt][s2]), fr8(cur.o[s2]));
+        for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(o.x[tt][s2]), fr8(o.o[s2]));
       }
       st[tt] = acc;
     }
@@ -511,8 +515,23 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
       sS[wv][l][e] = st[0][e];
       sS[wv][l][4 + e] = st[1][e];
     }
-    cur = nxt;
+  };
+  // chunk visited at scan position it (clamped: the load past the end is unused)
+  auto chunk_at = [&](int it) {
+    const int itc = it < p.NC ? it : p.NC - 1;
+    return BWD ? p.NC - 1 - itc : itc;
+  };
+  // two operand sets, alternated (no register copies between steps)
+  ChainOps o0, o1;
+  chain_load<BWD>(p, bh, bb, h, chunk_at(0), col0, wv, l, o0);
+  int it = 0;
+  for (; it + 1 < p.NC; it += 2) {
+    chain_load<BWD>(p, bh, bb, h, chunk_at(it + 1), col0, wv, l, o1);
+    step(chunk_at(it), o0);
+    chain_load<BWD>(p, bh, bb, h, chunk_at(it + 2), col0, wv, l, o0);
+    step(chunk_at(it + 1), o1);
   }
+  if (it < p.NC) step(chunk_at(it), o0);
   if (BWD && p.dinit != nullptr) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -525,67 +544,78 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
 }
 
 // ---------------------------------------------------------------------------
-// k_bw_grads: chunk-local parameter gradients.  With S0 = S_c, dSC = dS_{c+1}:
-//   U = U0 - W S0 ; dU = M^T dO + Kc dSC ; dX = T^T dU
-//   dv = dX w ; dw = dX v ; dM = mask(dO U^T) ; dA = -mask(dX U^T)
-//   dq_i   = carry_i e^{G_i} (S0 dO_i) + sum_j dM_ij e^{G_i-G_j} k_j
-//   dbeta_i = -carry_i e^{G_i} (S0 dX_i) + sum_j dA_ij e^{G_i-G_j} k_j
-//   dk_j   = sum_i dM_ij e^{G_i-G_j} q_i + sum_i dA_ij e^{G_i-G_j} beta_i
-//            + last_j e^{G_last-G_j} (dSC u_j)
-//   dG_i = q_i dq_i + beta_i dbeta_i - k_i dk_i, plus at the last row
-//          sum_j k_j dk_j^(Kc) + lam * rowsum(S0 * dSC);  dg_t = sum_{i>=t} dG_i
-//   db = k dbeta ; dk += b dbeta
-// Wave w owns the state / key columns 32w..32w+31 of every C x 128 product.
+// k_bw_grads: the chunk-wide products of the parameter gradients.  With
+// S0 = S_c, dSC = dS_{c+1}:
+//   U = U0 - W S0 ; dU = M^T dO + Kc dSC ; dX = T^T dU ; dv = dX w ; dw = dX v
+//   dM = mask(dO U^T), dA = -mask(dX U^T)            -> workspace
+//   U dSC^T -> dk,  dO S0^T -> dq,  dX S0^T -> db     (raw; k_bw_dqk finishes them)
+// Wave w owns the columns 32w..32w+31 of every C x 128 product.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_raw(const BW& p, float* out, int bb, int h, int t0, int wv, int q, int l16,
+                                          const f32x4 (&acc)[4][2]) {
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int R2 = 0; R2 < 2; ++R2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * I + 4 * q + e;
+        if (t0 + i < p.L) out[row_of(p, bb, t0 + i, h) + 32 * wv + 16 * R2 + l16] = acc[I][R2][e];
+      }
+}
+
+// acc[I][R2] += X[rows 16I..][:] * Y[cols 32w + 16 R2 ..][:]^T over 128 (X rows
+// at stride xs, in LDS or global; Y rows at stride ys, global)
+__device__ __forceinline__ void nt_128(f32x4 (&acc)[4][2], const float* X, int xs, const float* Y, int ys,
+                                       int wv, int q, int l16) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    Frag<false> a[4], bfr[2];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) { float x[8]; row8(X + (16 * I + l16) * xs, s, q, x); a[I] = fr8(x); }
+#pragma unroll
+    for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(Y + (32 * wv + 16 * R2 + l16) * ys, s, q, x); bfr[R2] = fr8(x); }
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+  }
+}
+
+__device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][2]) {
+#pragma unroll
+  for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+}
+
 __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
   __shared__ float sdO[BC][KP];
   __shared__ float sX[BC][KP];       // dU, then dX
-  __shared__ float sU[BC][KD];       // U, then dG
-  __shared__ float sdM[BC][CP];
-  __shared__ float sdA[BC][CP];
+  __shared__ float sU[BC][KP];
   __shared__ int sseg[BC], scar[BC], slast[BC];
 
   const int u = blockIdx.x;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
   const int t0 = c * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
-  const float* G = p.G + (int64_t)u * CK;
   const float* S0 = p.S + (int64_t)u * KK;
   const float* S0T = p.ST + (int64_t)u * KK;
   const float* dSC = p.dS + (int64_t)u * KK;
   const float* dSCT = p.dST + (int64_t)u * KK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
-  for (int i = tid; i < BC * CP; i += 256) {
-    (&sdM[0][0])[i] = 0.f;
-    (&sdA[0][0])[i] = 0.f;
-  }
-  for (int idx = tid; idx < BC * KD / 4; idx += 256) {
-    const int i = idx / (KD / 4), c4 = idx % (KD / 4);
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / 256; ++it) {
+    const int idx = tid + 256 * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4g(p.dout + row_of(p, bb, t0 + i, h) + 4 * c4) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
   }
-  __syncthreads();
 
+  f32x4 acc[4][2];
   // ---- U = U0 - W S0 ---------------------------------------------------------
   {
-    const float* Wm = p.Wm + (int64_t)u * CK;
     const float* U0 = p.U0 + (int64_t)u * CK;
-    f32x4 acc[4][2];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      Frag<false> a[4], bfr[2];
-#pragma unroll
-      for (int I = 0; I < 4; ++I) { float x[8]; row8(Wm + (16 * I + l16) * KD, s, q, x); a[I] = fr8(x); }
-#pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(S0T + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
-    }
+    zero_acc(acc);
+    nt_128(acc, p.Wm + (int64_t)u * CK, KD, S0T, KD, wv, q, l16);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -598,51 +628,20 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
         }
       }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- Kc part of dk: last_j e^{G_last-G_j} (U dSC^T)_j; written to dk -------
-  {
-    f32x4 acc[4][2];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      Frag<false> a[4], bfr[2];
-#pragma unroll
-      for (int I = 0; I < 4; ++I) { float x[8]; row8(&sU[16 * I + l16][0], s, q, x); a[I] = fr8(x); }
-#pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(dSC + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
-    }
-#pragma unroll
-    for (int R2 = 0; R2 < 2; ++R2) {
-      const int r = 32 * wv + 16 * R2 + l16;
-      const float glast = G[(BC - 1) * KD + r];
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = 16 * I + 4 * q + e;
-          if (t0 + j < p.L) {
-            const int64_t ro = row_of(p, bb, t0 + j, h) + r;
-            const float dkc = slast[j] ? ex2(glast - G[j * KD + r]) * acc[I][R2][e] : 0.f;
-            p.dk[ro] = dkc;               // completed below
-            p.dg[ro] = p.k[ro] * dkc;     // prefix-summed below
-          }
-        }
-    }
-  }
+  // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
+  zero_acc(acc);
+  nt_128(acc, &sU[0][0], KP, dSC, KD, wv, q, l16);
+  store_raw(p, p.dk, bb, h, t0, wv, q, l16, acc);
+  zero_acc(acc);
+  nt_128(acc, &sdO[0][0], KP, S0, KD, wv, q, l16);
+  store_raw(p, p.dq, bb, h, t0, wv, q, l16, acc);
 
   // ---- dU = M^T dO + Kc dSC  (into sX) --------------------------------------
   {
     const float* MT = p.MT + (int64_t)u * CC;
-    const float* Kc = p.Kc + (int64_t)u * CK;
-    f32x4 acc[4][2];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+    zero_acc(acc);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       Frag<false> a[4], bfr[2];
@@ -661,18 +660,7 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 #pragma unroll
         for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
     }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      Frag<false> a[4], bfr[2];
-#pragma unroll
-      for (int I = 0; I < 4; ++I) { float x[8]; row8(Kc + (16 * I + l16) * KD, s, q, x); a[I] = fr8(x); }
-#pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(dSCT + (32 * wv + 16 * R2 + l16) * KD, s, q, x); bfr[R2] = fr8(x); }
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
-    }
+    nt_128(acc, p.Kc + (int64_t)u * CK, KD, dSCT, KD, wv, q, l16);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -682,14 +670,12 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
         for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][R2][e];
       }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- dX = T^T dU ; dv = dX w ; dw = dX v ----------------------------------
   {
     const float* TT = p.TT + (int64_t)u * CC;
-    f32x4 acc[4][2];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+    zero_acc(acc);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       Frag<false> a[4], bfr[2];
@@ -708,7 +694,7 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 #pragma unroll
         for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -727,189 +713,214 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
         }
       }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- dM = mask(dO U^T), dA = -mask(dX U^T) --------------------------------
-  for (int task = wv; task < 20; task += 4) {
-    const bool isA = task >= 10;
-    const int tt = task % 10;
-    const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
-    const int J = tt - I * (I + 1) / 2;
-    const float* Xs = isA ? &sX[0][0] : &sdO[0][0];
-    f32x4 acc = zero4();
+  // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
+  zero_acc(acc);
+  nt_128(acc, &sX[0][0], KP, S0, KD, wv, q, l16);
+  store_raw(p, p.db, bb, h, t0, wv, q, l16, acc);
+
+  // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
+  for (int task = wv; task < 32; task += 4) {
+    const bool isA = task >= 16;
+    const int I = (task & 15) >> 2, J = task & 3;
+    float* dst = (isA ? p.dAw : p.dMw) + (int64_t)u * CC;
+    f32x4 a = zero4();
+    if (J <= I) {
+      const float* Xs = isA ? &sX[0][0] : &sdO[0][0];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float xa[8], xb[8];
-      row8(Xs + (16 * I + l16) * KP, s, q, xa);
-      row8(&sU[16 * J + l16][0], s, q, xb);
-      mma(acc, fr8(xa), fr8(xb));
+      for (int s = 0; s < 4; ++s) {
+        float xa[8], xb[8];
+        row8(Xs + (16 * I + l16) * KP, s, q, xa);
+        row8(&sU[16 * J + l16][0], s, q, xb);
+        mma(a, fr8(xa), fr8(xb));
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * q + e, j = 16 * J + l16;
       const bool ok = (isA ? j < i : j <= i) && sseg[i] == sseg[j];
-      (isA ? sdA : sdM)[i][j] = ok ? (isA ? -acc[e] : acc[e]) : 0.f;
+      dst[i * BC + j] = ok ? (isA ? -a[e] : a[e]) : 0.f;
     }
   }
-  __syncthreads();
+}
 
-  // ---- dq, dbeta, dk per 16 x 16 tile; dG into sU ----------------------------
-  float (*sdG)[KD] = sU;
+// ---------------------------------------------------------------------------
+// k_bw_dqk: the decay-weighted parts of dq, dbeta, dk and dg, per (unit, half
+// of the key channels).  With the chunk's q, k, b, G and dM, dA in LDS:
+//   dq_i    = carry_i e^{G_i} (dO S0^T)_i + sum_j dM_ij e^{G_i-G_j} k_j
+//   dbeta_i = -carry_i e^{G_i} (dX S0^T)_i + sum_j dA_ij e^{G_i-G_j} k_j
+//   dk_j    = sum_i dM_ij e^{G_i-G_j} q_i + sum_i dA_ij e^{G_i-G_j} beta_i
+//             + last_j e^{G_last-G_j} (U dSC^T)_j
+//   dG_i    = q_i dq_i + beta_i dbeta_i - k_i dk_i   (pairs whose factor is e^0
+//             left out: they cancel), db = k dbeta, dk += b dbeta,
+//   dg_t    = sum_{i>=t} dG_i + sum_{j<t} k_j dk_j^(Kc) + lam rowsum(S0 * dSC)
+// Off-diagonal 16-row blocks use e^{G_i-G_m} e^{G_m-G_j} (both <= 1) through
+// MFMA; pairs inside a block use e^{G_i-G_j} per element.
+// Wave w owns 16 channels; lanes hold rows 4q..4q+3 of each 16-row block.
+// ---------------------------------------------------------------------------
+constexpr int HC = KD / 2;      // channels per k_bw_dqk workgroup
+constexpr int HP = HC + 4;
+
+__global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
+  __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
+  __shared__ float sdM[BC][CP], sdA[BC][CP];
+  __shared__ float sdG[BC][HP], sP[BC][HP];
+  __shared__ float sTail[HC];
+  __shared__ int scar[BC], slast[BC], sseg[BC];
+
+  const int u = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
+  const int t0 = c * BC;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+  const int ch0 = HC * half;
+  const float* G = p.G + (int64_t)u * CK;
+
+  const int rl = 16 * wv + l16, r = ch0 + rl;
+  // raw products from k_bw_grads for this lane's 16 rows, loaded up front
+  float rq[4][4], rb[4][4], rk[4][4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * I + 4 * q + e;
+      const bool vi = t0 + i < p.L;
+      const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + r;
+      rq[I][e] = vi ? p.dq[ro] : 0.f;
+      rb[I][e] = vi ? p.db[ro] : 0.f;
+      rk[I][e] = vi ? p.dk[ro] : 0.f;
+    }
+  // rowsum(S0 * dSC) of channel ch0 + tid / 4, a quarter of the row per thread
+  float rs = 0.f;
+  {
+    const int cr = ch0 + (tid >> 2), part = tid & 3;
+    const float* S0 = p.S + (int64_t)u * KK + cr * KD + 32 * part;
+    const float* dSC = p.dS + (int64_t)u * KK + cr * KD + 32 * part;
+#pragma unroll
+    for (int v4 = 0; v4 < 8; ++v4) {
+      const float4 a = ld4g(S0 + 4 * v4);
+      const float4 d = ld4g(dSC + 4 * v4);
+      rs += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
+    }
+  }
+  if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
+#pragma unroll
+  for (int it = 0; it < BC * HC / 4 / 256; ++it) {
+    const int idx = tid + 256 * it, i = idx / (HC / 4), c4 = idx % (HC / 4);
+    float4 qv = zero_f4(), kv = zero_f4(), bv = zero_f4();
+    if (t0 + i < p.L) {
+      const int64_t ro = row_of(p, bb, t0 + i, h) + ch0 + 4 * c4;
+      qv = ld4g(p.q + ro); kv = ld4g(p.k + ro); bv = ld4g(p.b + ro);
+    }
+    *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qv;
+    *reinterpret_cast<float4*>(&sK[i][4 * c4]) = kv;
+    *reinterpret_cast<float4*>(&sB[i][4 * c4]) = bv;
+    *reinterpret_cast<float4*>(&sG[i][4 * c4]) = ld4g(G + i * KD + ch0 + 4 * c4);
+  }
+#pragma unroll
+  for (int it = 0; it < CC / 4 / 256; ++it) {
+    const int idx = tid + 256 * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
+    *reinterpret_cast<float4*>(&sdM[i][4 * c4]) = ld4g(p.dMw + (int64_t)u * CC + i * BC + 4 * c4);
+    *reinterpret_cast<float4*>(&sdA[i][4 * c4]) = ld4g(p.dAw + (int64_t)u * CC + i * BC + 4 * c4);
+  }
+  lds_barrier();
+
+  rs += __shfl_xor(rs, 1);
+  rs += __shfl_xor(rs, 2);
+  if ((tid & 3) == 0) sTail[tid >> 2] = rs;
+  const float glast = sG[BC - 1][rl];
+#pragma unroll
   for (int I = 0; I < 4; ++I) {
-#pragma unroll 1
-    for (int R2 = 0; R2 < 2; ++R2) {
-      const int r = 32 * wv + 16 * R2 + l16;
-      // S0-side products: (dO S0^T), (dX S0^T)
-      f32x4 aq = zero4(), ab = zero4();
+    // off-diagonal blocks: rows i of block I against columns j < 16 I
+    f32x4 oq = zero4(), ob = zero4(), ok_ = zero4();
+    const int m = 16 * I, m2 = 16 * I + 15;
+    const float gm = sG[m][rl], gm2 = sG[m2][rl];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float xo[8], xx[8], xs[8];
-        row8(&sdO[16 * I + l16][0], s, q, xo);
-        row8(&sX[16 * I + l16][0], s, q, xx);
-        row8(S0 + (32 * wv + 16 * R2 + l16) * KD, s, q, xs);
-        const Frag<false> fs = fr8(xs);
-        mma(aq, fr8(xo), fs);
-        mma(ab, fr8(xx), fs);
+    for (int s = 0; s < 2; ++s) {
+      float xm[8], xa[8], xk[8], ym[8], ya[8], yq[8], yb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 32 * s + pi_k(q, e);
+        const bool lo = j < m, hi = j > m2;
+        xm[e] = lo ? sdM[16 * I + l16][j] : 0.f;
+        xa[e] = lo ? sdA[16 * I + l16][j] : 0.f;
+        xk[e] = lo ? sK[j][rl] * ex2(gm - sG[j][rl]) : 0.f;
+        ym[e] = hi ? sdM[j][16 * I + l16] : 0.f;
+        ya[e] = hi ? sdA[j][16 * I + l16] : 0.f;
+        const float f = hi ? ex2(sG[j][rl] - gm2) : 0.f;
+        yq[e] = sQ[j][rl] * f;
+        yb[e] = sB[j][rl] * sK[j][rl] * f;
       }
-      // off-diagonal blocks, reference row m = 16 I (rows i) ...
-      f32x4 oq = zero4(), ob = zero4();
-      {
-        const int m = 16 * I;
-        const float gm = G[m * KD + r];
+      const Frag<false> fk = fr8(xk);
+      mma(oq, fr8(xm), fk);
+      mma(ob, fr8(xa), fk);
+      mma(ok_, fr8(ym), fr8(yq));
+      mma(ok_, fr8(ya), fr8(yb));
+    }
+    // pairs inside block I, and the epilogue
+    float kb[16], qb[16], betab[16], gb[16];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          float xm[8], xa[8], xk[8];
+    for (int jj = 0; jj < 16; ++jj) {
+      const int j = 16 * I + jj;
+      kb[jj] = sK[j][rl];
+      qb[jj] = sQ[j][rl];
+      betab[jj] = sB[j][rl] * kb[jj];
+      gb[jj] = sG[j][rl];
+    }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int j = 32 * s + pi_k(q, e);
-            xm[e] = j < m ? sdM[16 * I + l16][j] : 0.f;
-            xa[e] = j < m ? sdA[16 * I + l16][j] : 0.f;
-            const bool vj = j < m && t0 + j < p.L;
-            xk[e] = vj ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(gm - G[j * KD + r]) : 0.f;
-          }
-          const Frag<false> fk = fr8(xk);
-          mma(oq, fr8(xm), fk);
-          mma(ob, fr8(xa), fk);
-        }
-      }
-      // ... and reference row m = 16 J + 15 (columns j, here the rows of dk)
-      f32x4 ok_ = zero4();
-      {
-        const int m = 16 * I + 15;
-        const float gm = G[m * KD + r];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          float xm[8], xa[8], xq[8], xbeta[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int i = 32 * s + pi_k(q, e);
-            const bool in = i > m;
-            xm[e] = in ? sdM[i][16 * I + l16] : 0.f;
-            xa[e] = in ? sdA[i][16 * I + l16] : 0.f;
-            const bool vi = in && t0 + i < p.L;
-            const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + r;
-            const float f = vi ? ex2(G[i * KD + r] - gm) : 0.f;
-            xq[e] = vi ? p.q[ro] * f : 0.f;
-            xbeta[e] = vi ? p.b[ro] * p.k[ro] * f : 0.f;
-          }
-          mma(ok_, fr8(xm), fr8(xq));
-          mma(ok_, fr8(xa), fr8(xbeta));
-        }
-      }
-      // diagonal block, per element, and the epilogue
-      const float gI0 = G[(16 * I) * KD + r];
-      const float gI15 = G[(16 * I + 15) * KD + r];
-      float kb[16], qb[16], betab[16], gb[16];
+    for (int e = 0; e < 4; ++e) {
+      const int ii = 4 * q + e;
+      const int i = 16 * I + ii;
+      const float gi = sG[i][rl];
+      float dq = 0.f, dbeta = 0.f, dk = 0.f;
 #pragma unroll
       for (int jj = 0; jj < 16; ++jj) {
-        const int j = 16 * I + jj;
-        const bool vj = t0 + j < p.L;
-        const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
-        kb[jj] = vj ? p.k[ro] : 0.f;
-        qb[jj] = vj ? p.q[ro] : 0.f;
-        betab[jj] = vj ? p.b[ro] * kb[jj] : 0.f;
-        gb[jj] = G[j * KD + r];
+        const float off = jj == ii ? 0.f : 1.f;
+        const float fij = ex2(gi - gb[jj]);
+        dq += off * sdM[i][16 * I + jj] * fij * kb[jj];
+        dbeta += sdA[i][16 * I + jj] * fij * kb[jj];
+        const float fji = ex2(gb[jj] - gi);
+        dk += off * sdM[16 * I + jj][i] * fji * qb[jj] + sdA[16 * I + jj][i] * fji * betab[jj];
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int ii = 4 * q + e;            // row within the block
-        const int i = 16 * I + ii;
-        const float gi = G[i * KD + r];
-        // the pair (i, i) of M is kept apart: its factor e^0 does not depend
-        // on g, and its two dG contributions (q dq, -k dk) cancel exactly
-        float dq = 0.f, dbeta = 0.f, dk = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-          const float off = jj == ii ? 0.f : 1.f;
-          // i as the row: pairs (i, j), j < i inside the block
-          const float fij = ex2(gi - gb[jj]);
-          dq += off * sdM[i][16 * I + jj] * fij * kb[jj];
-          dbeta += sdA[i][16 * I + jj] * fij * kb[jj];
-          // i as the column: pairs (i2, i), i2 > i inside the block
-          const float fji = ex2(gb[jj] - gi);
-          dk += off * sdM[16 * I + jj][i] * fji * qb[jj] + sdA[16 * I + jj][i] * fji * betab[jj];
-        }
-        const float dmii = sdM[i][i];
-        const bool car = scar[i] != 0;
-        const float eg = car ? ex2(gi) : 0.f;
-        dq += eg * aq[e] + oq[e] * ex2(gi - gI0);
-        dbeta += -eg * ab[e] + ob[e] * ex2(gi - gI0);
-        dk += ok_[e] * ex2(gI15 - gi);
-        const bool vi = t0 + i < p.L;
-        float dG = 0.f;
-        if (vi) {
-          const int64_t ro = row_of(p, bb, t0 + i, h) + r;
-          const float kv = kb[ii], bv = p.b[ro];
-          dG = qb[ii] * dq + bv * kv * dbeta - kv * dk;
-          const float dkc = p.dk[ro];       // Kc part, written above
-          p.dq[ro] = dq + dmii * kv;
-          p.dk[ro] = dk + dmii * qb[ii] + dkc + bv * dbeta;
-          p.db[ro] = kv * dbeta;
-        }
-        sdG[i][r] = dG;
+      const float eg = scar[i] ? ex2(gi) : 0.f;
+      dq += eg * rq[I][e] + oq[e] * ex2(gi - gm);
+      dbeta += -eg * rb[I][e] + ob[e] * ex2(gi - gm);
+      dk += ok_[e] * ex2(gm2 - gi);
+      const float dkc = slast[i] ? ex2(glast - gi) * rk[I][e] : 0.f;
+      const float kv = kb[ii], bv = sB[i][rl], dmii = sdM[i][i];
+      sdG[i][rl] = qb[ii] * dq + bv * kv * dbeta - kv * dk;
+      sP[i][rl] = kv * dkc;
+      if (t0 + i < p.L) {
+        const int64_t ro = row_of(p, bb, t0 + i, h) + r;
+        p.dq[ro] = dq + dmii * kv;
+        p.dk[ro] = dk + dmii * qb[ii] + dkc + bv * dbeta;
+        p.db[ro] = kv * dbeta;
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- dg ------------------------------------------------------------------
-  // dg_t = sum_{i >= t} dG_i + sum_{j < t} k_j dk_j^(Kc) + lam * rowsum(S0 * dSC):
-  // the Kc pair (j, last) enters every dg_t with t <= j twice with opposite
-  // signs, so it is summed forward over j < t instead (no cancellation).
-  __threadfence_block();
-  __syncthreads();
-  if (tid < KD) {
-    const int r = tid;
-    float tail = 0.f;
-    if (scar[BC - 1]) {
-      float rs = 0.f;
-#pragma unroll 8
-      for (int v4 = 0; v4 < KD / 4; ++v4) {
-        const float4 a = ld4g(S0 + r * KD + 4 * v4);
-        const float4 d = ld4g(dSC + r * KD + 4 * v4);
-        rs += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
-      }
-      tail = exp2f(G[(BC - 1) * KD + r]) * rs;
-    }
+  // ---- dg_t = sum_{i>=t} dG_i + sum_{j<t} P_j + lam rowsum(S0 * dSC) -------
+  // (the Kc pair (j, last) enters dg_t for t <= j twice with opposite signs,
+  // so it is summed forward over j < t instead)
+  if (tid < HC) {
+    const int rr = ch0 + tid;
+    const float tail = scar[BC - 1] ? ex2(sG[BC - 1][tid]) * sTail[tid] : 0.f;
+    float fwd = 0.f, acc = tail;
     float dgv[BC];
 #pragma unroll
-    for (int t = 0; t < BC; ++t) dgv[t] = t0 + t < p.L ? p.dg[row_of(p, bb, t0 + t, h) + r] : 0.f;
-    float fwd = 0.f;
-#pragma unroll
     for (int t = 0; t < BC; ++t) {
-      const float pj = dgv[t];
       dgv[t] = fwd;
-      fwd += pj;
+      fwd += sP[t][tid];
     }
-    float acc = tail;
 #pragma unroll
     for (int t = BC - 1; t >= 0; --t) {
-      acc += sdG[t][r];
+      acc += sdG[t][tid];
       dgv[t] += acc;
     }
 #pragma unroll
     for (int t = 0; t < BC; ++t)
-      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + r] = dgv[t];
+      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + rr] = dgv[t];
   }
 }
 
@@ -926,7 +937,7 @@ size_t bw_units(const dn_backward_args* a) {
   return (size_t)a->B * a->H * NC;
 }
 
-constexpr size_t kUnitFloats = 7 * (size_t)CK + 2 * (size_t)CC + KD + 4 * (size_t)KK;
+constexpr size_t kUnitFloats = 7 * (size_t)CK + 4 * (size_t)CC + KD + 4 * (size_t)KK;
 
 int bw_check(const dn_backward_args* a) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
@@ -967,6 +978,7 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
   p.XfT = take(CK); p.U0 = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
+  p.dMw = take(CC); p.dAw = take(CC);
   p.S = take(KK); p.ST = take(KK); p.dS = take(KK); p.dST = take(KK);
 
   hipStream_t st = (hipStream_t)stream;
@@ -976,6 +988,7 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   hipLaunchKernelGGL(k_bw_chain<false>, dim3(chains), dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_bw_chain<true>, dim3(chains), dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(2 * units)), dim3(256), 0, st, p);
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
