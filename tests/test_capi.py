@@ -41,6 +41,7 @@ def test_struct_layout_matches_header(tmp_path):
     fields = {
         "dn_prefill_args": _lib.PrefillArgs,
         "dn_decode_args": _lib.DecodeArgs,
+        "dn_backward_args": _lib.BackwardArgs,
     }
     src = ['#include <stdio.h>', '#include <stddef.h>', '#include "deltanet_amd.h"', "int main(void){"]
     for cname, cls in fields.items():
@@ -83,3 +84,23 @@ def test_invalid_args_rejected_without_gpu():
     d.Hv = 4
     assert lib.dn_decode_steps(ctypes.byref(d), 0, None) == -1 and b"T must be positive" in lib.dn_last_error()
     assert lib.dn_state_frob_cap(None, 1, 128, 128, 1.0, None) == -1
+    bw = _lib.BackwardArgs()
+    bw.abi_version = _lib.DN_ABI_VERSION
+    bw.B, bw.L, bw.H, bw.K, bw.V = 1, 128, 4, 128, 128
+    # missing tensor pointers: size 0 and a clear error, no HIP call
+    assert lib.dn_prefill_bwd_workspace_size(ctypes.byref(bw)) == 0
+    assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -1 and b"missing" in lib.dn_last_error()
+    bw.K = 64
+    assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -1 and b"128" in lib.dn_last_error()
+    bw.abi_version = 99
+    assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -4
+    # with (fake, never dereferenced) pointers the size is positive and a short
+    # workspace is refused before any launch
+    bw.abi_version, bw.K = _lib.DN_ABI_VERSION, 128
+    for f in ("q", "k", "v", "g", "b", "w", "d_out", "dq", "dk", "dv", "dg", "db", "dw"):
+        setattr(bw, f, 0x1000)
+    need = lib.dn_prefill_bwd_workspace_size(ctypes.byref(bw))
+    assert need == 4 * 2 * 4 * (7 * 64 * 128 + 4 * 64 * 64 + 128 + 4 * 128 * 128)   # bytes: 2 chunks x 4 heads
+    assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -2
+    bw.d_init = 0x1000
+    assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -1 and b"init_state" in lib.dn_last_error()
