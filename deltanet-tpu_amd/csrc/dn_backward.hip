@@ -230,19 +230,20 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 
   // ---- T = (I + A)^-1 by forward substitution (wave 0, lane = column) -----
   if (wv == 0) {
+    // four partial sums (j mod 4) keep the dependent FMA chain of row i at i/4
     float Tc[BC];
 #pragma unroll
     for (int i = 0; i < BC; ++i) {
-      float t = (i == l) ? 1.f : 0.f;
+      float t[4] = {(i == l) ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j4 = 0; j4 < (i + 3) / 4; ++j4) {
         const float4 a = *reinterpret_cast<const float4*>(&sA[i][4 * j4]);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          if (4 * j4 + jj < i) t -= f4at(a, jj) * Tc[4 * j4 + jj];
+          if (4 * j4 + jj < i) t[jj] -= f4at(a, jj) * Tc[4 * j4 + jj];
         }
       }
-      Tc[i] = t;
+      Tc[i] = (t[0] + t[1]) + (t[2] + t[3]);
     }
     float* TT = p.TT + (int64_t)u * CC + l * BC;
 #pragma unroll
@@ -263,13 +264,9 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
     for (int idx = t2; idx < CK; idx += 192) {
       const int j = idx / KD, r = idx % KD;
       const bool ok = slast[j] && t0 + j < p.L;
-      Kc[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
-    }
-#pragma unroll 8
-    for (int idx = t2; idx < CK; idx += 192) {
-      const int r = idx / BC, j = idx % BC;
-      const bool ok = slast[j] && t0 + j < p.L;
-      KcT[idx] = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
+      const float kc = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
+      Kc[idx] = kc;
+      KcT[r * BC + j] = kc;
     }
   }
   lds_barrier();
