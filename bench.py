@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "deltanet-tpu_amd"))
 # MI355X published peaks
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3      # dense fp32 MFMA (v_mfma_f32_*_f32)
 
 METRIC = "prefill tokens/s + %bf16 MFMA peak; decode step µs + state HBM GB/s"
 
@@ -82,6 +83,17 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128):
                 value=dict(flops=units * f_val, bytes=vw_bytes),
                 chain=dict(flops=units * f_chain, bytes=state_bytes + out_bytes),
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
+
+
+def backward_work(B=1, L=2048, H=24, K=128, V=128, C=64):
+    """Algorithmic flops of dn_prefill_bwd (multiply-adds x 2), per the chunk
+    form in dn_backward.hip (triangular products at half size):
+    intra A, M, W, U0, Xf ~ 5 C^2 K / 2 + C^3 / 6; forward and reverse scans
+    5 C K V; chunk products 5 C K V + 2 C^2 V; decay-weighted dq / dbeta / dk
+    2 C^2 K."""
+    units = B * H * ((L + C - 1) // C)
+    mac = C * C * K * 5 + C ** 3 / 6 + 10 * C * K * V + 2 * C * C * V
+    return {"flops": 2 * mac * units, "units": units}
 
 
 def cpu_baseline(max_seconds=20.0):
@@ -340,9 +352,15 @@ def main():
         torch.cuda.synchronize()
         tprof = _lib.profile_end()
         tk_us = {n: round(ms * 1e3 / args.train_steps, 1) for n, (ms, c) in tprof.items() if c}
+        bw = backward_work(H=tv.shape[2])
+        bw_s = tk_us.get("backward", 0.0) * 1e-6
         train = {"workload": "chunk_gdn2 forward + backward (is_inference=False, autograd), config-2 shape, "
                              "precision bf16 forward, fp32 backward", "us_per_step": round(t_us, 1),
-                 "kernels_us_per_step": tk_us}
+                 "kernels_us_per_step": tk_us,
+                 "backward_roofline": {"bound": "mfma", "dtype": "fp32", "flops": bw["flops"],
+                                       "achieved": round(bw["flops"] / bw_s / 1e12, 2) if bw_s else None,
+                                       "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(bw["flops"] / bw_s / 1e12 / PEAK_FP32_TFLOPS, 4) if bw_s else None}}
         log(f"training step: {t_us:.1f} us; kernels per step (us): {tk_us}")
 
     copy_gbps = None

@@ -485,28 +485,40 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
         *reinterpret_cast<float4*>(XT + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
       }
     }
-    // Y (or Z) tile: token rows 16w..16w+15
-    f32x4 y = zero4();
+    // Xf^T dO (backward) needs neither the state nor the exchanged tile
+    f32x4 acc2[2] = {zero4(), zero4()};
+    if (BWD) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) mma(y, fr8(o.a[s]), fr8(&sS[s][l][0]));
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = BWD ? -y[e] : o.u[e] - y[e];
+        for (int s2 = 0; s2 < 2; ++s2) mma(acc2[tt], fr8(o.x[tt][s2]), fr8(o.o[s2]));
+    }
+    // Y (or Z) tile: token rows 16w..16w+15; two accumulators halve the
+    // dependent MFMA chain on the sequential path
+    f32x4 y = zero4(), y2 = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      mma(y, fr8(o.a[s]), fr8(&sS[s][l][0]));
+      mma(y2, fr8(o.a[s + 2]), fr8(&sS[s + 2][l][0]));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = BWD ? -(y[e] + y2[e]) : o.u[e] - (y[e] + y2[e]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
     lds_barrier();
+    f32x4 acc[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x4 acc;
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = o.lm[tt][e] * st[tt][e];
+      for (int e = 0; e < 4; ++e) acc[tt][e] = o.lm[tt][e] * st[tt][e];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(o.b[tt][s2]), fr8(&sY[s2][l][0]));
-      if (BWD) {
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) mma(acc, fr8(o.x[tt][s2]), fr8(o.o[s2]));
-      }
-      st[tt] = acc;
-    }
+      for (int s2 = 0; s2 < 2; ++s2) mma(acc[tt], fr8(o.b[tt][s2]), fr8(&sY[s2][l][0]));
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st[tt][e] = acc[tt][e] + acc2[tt][e];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sS[wv][l][e] = st[0][e];
