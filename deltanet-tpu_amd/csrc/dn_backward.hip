@@ -48,6 +48,9 @@ constexpr int CC = BC * BC;
 constexpr int KK = KD * KD;
 constexpr int KP = KD + 4;    // padded LDS row pitch (128-wide rows)
 constexpr int CP = BC + 4;    // padded LDS row pitch (64-wide rows)
+constexpr int NWV = 8;        // waves per workgroup of the chunk-parallel kernels
+constexpr int NT = 64 * NWV;
+constexpr int TPW = 8 / NWV;  // 16-column tiles per wave in C x 128 products
 
 struct BW {
   int B, L, H, NC;
@@ -118,7 +121,7 @@ __device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<fa
 // ---------------------------------------------------------------------------
 // k_bw_intra
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_bw_intra(BW p) {
+__global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   __shared__ float sG[BC][KP];
   __shared__ float sA[BC][CP];   // A, then T
   __shared__ float sM[BC][CP];
@@ -133,14 +136,14 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
   float* G = p.G + (int64_t)u * CK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
-  for (int i = tid; i < BC * CP; i += 256) {
+  for (int i = tid; i < BC * CP; i += NT) {
     (&sA[0][0])[i] = 0.f;
     (&sM[0][0])[i] = 0.f;
   }
   // stage q and beta = b k (rows past the sequence end are zero)
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / 256; ++it) {
-    const int idx = tid + 256 * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     float4 qv = zero_f4(), bv = zero_f4();
     if (t0 + i < p.L) {
       const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
   lds_barrier();
 
   // ---- A (strict) and M (with diagonal), 16x16 tiles of the lower triangle --
-  for (int task = wv; task < 20; task += 4) {
+  for (int task = wv; task < 20; task += NWV) {
     const bool isM = task >= 10;
     const int tt = task % 10;
     const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
@@ -254,14 +257,14 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
   } else {
     const int t2 = tid - 64;
     float* MT = p.MT + (int64_t)u * CC;
-    for (int idx = t2; idx < CC; idx += 192) {
+    for (int idx = t2; idx < CC; idx += NT - 64) {
       const int j = idx / BC, i = idx % BC;
       MT[idx] = sM[i][j];
     }
     float* Kc = p.Kc + (int64_t)u * CK;
     float* KcT = p.KcT + (int64_t)u * CK;
 #pragma unroll 8
-    for (int idx = t2; idx < CK; idx += 192) {
+    for (int idx = t2; idx < CK; idx += NT - 64) {
       const int j = idx / KD, r = idx % KD;
       const bool ok = slast[j] && t0 + j < p.L;
       const float kc = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
@@ -273,11 +276,11 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 
   // ---- W = T diag(carry) (b k e^G), U0 = T (w v) ---------------------------
   {
-    f32x4 aw[4][2], au[4][2];
+    f32x4 aw[4][TPW], au[4][TPW];
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) { aw[I][R2] = zero4(); au[I][R2] = zero4(); }
+      for (int R2 = 0; R2 < TPW; ++R2) { aw[I][R2] = zero4(); au[I][R2] = zero4(); }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       Frag<false> a[4];
@@ -291,8 +294,8 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
         a[I] = fr8(x);
       }
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int r = 16 * (2 * wv + R2) + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int r = 16 * (TPW * wv + R2) + l16;
         float xb[8], xu[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -317,8 +320,8 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int r = 16 * (2 * wv + R2) + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int r = 16 * (TPW * wv + R2) + l16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
@@ -334,11 +337,11 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 
   // ---- Xf = diag(carry) q e^G - M W ----------------------------------------
   {
-    f32x4 ax[4][2];
+    f32x4 ax[4][TPW];
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) ax[I][R2] = zero4();
+      for (int R2 = 0; R2 < TPW; ++R2) ax[I][R2] = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       Frag<false> a[4];
@@ -352,8 +355,8 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
         a[I] = fr8(x);
       }
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int r = 16 * (2 * wv + R2) + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int r = 16 * (TPW * wv + R2) + l16;
         float xb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) xb[e] = sW[32 * s + pi_k(q, e)][r];
@@ -366,8 +369,8 @@ __global__ __launch_bounds__(256) void k_bw_intra(BW p) {
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int r = 16 * (2 * wv + R2) + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int r = 16 * (TPW * wv + R2) + l16;
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -561,42 +564,44 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
 // Wave w owns the columns 32w..32w+31 of every C x 128 product.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void store_raw(const BW& p, float* out, int bb, int h, int t0, int wv, int q, int l16,
-                                          const f32x4 (&acc)[4][2]) {
+                                          const f32x4 (&acc)[4][TPW]) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int R2 = 0; R2 < 2; ++R2)
+    for (int R2 = 0; R2 < TPW; ++R2)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * I + 4 * q + e;
-        if (t0 + i < p.L) out[row_of(p, bb, t0 + i, h) + 32 * wv + 16 * R2 + l16] = acc[I][R2][e];
+        if (t0 + i < p.L) out[row_of(p, bb, t0 + i, h) + 16 * (TPW * wv + R2) + l16] = acc[I][R2][e];
       }
 }
 
 // acc[I][R2] += X[rows 16I..][:] * Y[cols 32w + 16 R2 ..][:]^T over 128 (X rows
 // at stride xs, in LDS or global; Y rows at stride ys, global)
-__device__ __forceinline__ void nt_128(f32x4 (&acc)[4][2], const float* X, int xs, const float* Y, int ys,
+__device__ __forceinline__ void nt_128(f32x4 (&acc)[4][TPW], const float* X, int xs, const float* Y, int ys,
                                        int wv, int q, int l16) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    Frag<false> a[4], bfr[2];
+    Frag<false> a[4], bfr[TPW];
 #pragma unroll
     for (int I = 0; I < 4; ++I) { float x[8]; row8(X + (16 * I + l16) * xs, s, q, x); a[I] = fr8(x); }
 #pragma unroll
-    for (int R2 = 0; R2 < 2; ++R2) { float x[8]; row8(Y + (32 * wv + 16 * R2 + l16) * ys, s, q, x); bfr[R2] = fr8(x); }
+    for (int R2 = 0; R2 < TPW; ++R2) { float x[8]; row8(Y + (16 * (TPW * wv + R2) + l16) * ys, s, q, x); bfr[R2] = fr8(x); }
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+      for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
   }
 }
 
-__device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][2]) {
+__device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][TPW]) {
 #pragma unroll
-  for (int I = 0; I < 4; ++I) { acc[I][0] = zero4(); acc[I][1] = zero4(); }
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int R2 = 0; R2 < TPW; ++R2) acc[I][R2] = zero4();
 }
 
-__global__ __launch_bounds__(256) void k_bw_grads(BW p) {
+__global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   __shared__ float sdO[BC][KP];
   __shared__ float sX[BC][KP];       // dU, then dX
   __shared__ float sU[BC][KP];
@@ -613,13 +618,13 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / 256; ++it) {
-    const int idx = tid + 256 * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4g(p.dout + row_of(p, bb, t0 + i, h) + 4 * c4) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
   }
 
-  f32x4 acc[4][2];
+  f32x4 acc[4][TPW];
   // ---- U = U0 - W S0 ---------------------------------------------------------
   {
     const float* U0 = p.U0 + (int64_t)u * CK;
@@ -628,8 +633,8 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int vcol = 32 * wv + 16 * R2 + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int vcol = 16 * (TPW * wv + R2) + l16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
@@ -653,12 +658,12 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
     zero_acc(acc);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4], bfr[2];
+      Frag<false> a[4], bfr[TPW];
 #pragma unroll
       for (int I = 0; I < 4; ++I) { float x[8]; row8(MT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int vcol = 32 * wv + 16 * R2 + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int vcol = 16 * (TPW * wv + R2) + l16;
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
@@ -667,14 +672,14 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 #pragma unroll
       for (int I = 0; I < 4; ++I)
 #pragma unroll
-        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+        for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
     }
     nt_128(acc, p.Kc + (int64_t)u * CK, KD, dSCT, KD, wv, q, l16);
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int vcol = 32 * wv + 16 * R2 + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int vcol = 16 * (TPW * wv + R2) + l16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][R2][e];
       }
@@ -687,12 +692,12 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
     zero_acc(acc);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4], bfr[2];
+      Frag<false> a[4], bfr[TPW];
 #pragma unroll
       for (int I = 0; I < 4; ++I) { float x[8]; row8(TT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int vcol = 32 * wv + 16 * R2 + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int vcol = 16 * (TPW * wv + R2) + l16;
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
@@ -701,14 +706,14 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 #pragma unroll
       for (int I = 0; I < 4; ++I)
 #pragma unroll
-        for (int R2 = 0; R2 < 2; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+        for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
     }
     lds_barrier();
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < 2; ++R2) {
-        const int vcol = 32 * wv + 16 * R2 + l16;
+      for (int R2 = 0; R2 < TPW; ++R2) {
+        const int vcol = 16 * (TPW * wv + R2) + l16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
@@ -730,7 +735,7 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
   store_raw(p, p.db, bb, h, t0, wv, q, l16, acc);
 
   // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
-  for (int task = wv; task < 32; task += 4) {
+  for (int task = wv; task < 32; task += NWV) {
     const bool isA = task >= 16;
     const int I = (task & 15) >> 2, J = task & 3;
     float* dst = (isA ? p.dAw : p.dMw) + (int64_t)u * CC;
@@ -766,12 +771,13 @@ __global__ __launch_bounds__(256) void k_bw_grads(BW p) {
 //   dg_t    = sum_{i>=t} dG_i + sum_{j<t} k_j dk_j^(Kc) + lam rowsum(S0 * dSC)
 // Off-diagonal 16-row blocks use e^{G_i-G_m} e^{G_m-G_j} (both <= 1) through
 // MFMA; pairs inside a block use e^{G_i-G_j} per element.
-// Wave w owns 16 channels; lanes hold rows 4q..4q+3 of each 16-row block.
+// Wave w owns the 16 channels 16 (w % 4) .. and the 16-row blocks
+// 2 (w / 4), 2 (w / 4) + 1; lanes hold rows 4q..4q+3 of each block.
 // ---------------------------------------------------------------------------
 constexpr int HC = KD / 2;      // channels per k_bw_dqk workgroup
 constexpr int HP = HC + 4;
 
-__global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
+__global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
   __shared__ float sdG[BC][HP], sP[BC][HP];
@@ -785,28 +791,32 @@ __global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
   const int ch0 = HC * half;
   const float* G = p.G + (int64_t)u * CK;
 
-  const int rl = 16 * wv + l16, r = ch0 + rl;
-  // raw products from k_bw_grads for this lane's 16 rows, loaded up front
-  float rq[4][4], rb[4][4], rk[4][4];
+  constexpr int NB = 4 / (NWV / 4);          // 16-row blocks per wave
+  const int rl = 16 * (wv & 3) + l16, r = ch0 + rl;
+  const int I0 = NB * (wv >> 2);
+  // raw products from k_bw_grads for this lane's rows, loaded up front
+  float rq[NB][4], rb[NB][4], rk[NB][4];
 #pragma unroll
-  for (int I = 0; I < 4; ++I)
+  for (int Ib = 0; Ib < NB; ++Ib)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      const int I = I0 + Ib;
       const int i = 16 * I + 4 * q + e;
       const bool vi = t0 + i < p.L;
       const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + r;
-      rq[I][e] = vi ? p.dq[ro] : 0.f;
-      rb[I][e] = vi ? p.db[ro] : 0.f;
-      rk[I][e] = vi ? p.dk[ro] : 0.f;
+      rq[Ib][e] = vi ? p.dq[ro] : 0.f;
+      rb[Ib][e] = vi ? p.db[ro] : 0.f;
+      rk[Ib][e] = vi ? p.dk[ro] : 0.f;
     }
-  // rowsum(S0 * dSC) of channel ch0 + tid / 4, a quarter of the row per thread
+  // rowsum(S0 * dSC) of channel ch0 + tid / PARTS, 128 / PARTS entries per thread
+  constexpr int PARTS = NT / HC;
   float rs = 0.f;
   {
-    const int cr = ch0 + (tid >> 2), part = tid & 3;
-    const float* S0 = p.S + (int64_t)u * KK + cr * KD + 32 * part;
-    const float* dSC = p.dS + (int64_t)u * KK + cr * KD + 32 * part;
+    const int cr = ch0 + tid / PARTS, part = tid % PARTS;
+    const float* S0 = p.S + (int64_t)u * KK + cr * KD + (KD / PARTS) * part;
+    const float* dSC = p.dS + (int64_t)u * KK + cr * KD + (KD / PARTS) * part;
 #pragma unroll
-    for (int v4 = 0; v4 < 8; ++v4) {
+    for (int v4 = 0; v4 < KD / PARTS / 4; ++v4) {
       const float4 a = ld4g(S0 + 4 * v4);
       const float4 d = ld4g(dSC + 4 * v4);
       rs += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
@@ -814,8 +824,8 @@ __global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
   }
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
 #pragma unroll
-  for (int it = 0; it < BC * HC / 4 / 256; ++it) {
-    const int idx = tid + 256 * it, i = idx / (HC / 4), c4 = idx % (HC / 4);
+  for (int it = 0; it < BC * HC / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (HC / 4), c4 = idx % (HC / 4);
     float4 qv = zero_f4(), kv = zero_f4(), bv = zero_f4();
     if (t0 + i < p.L) {
       const int64_t ro = row_of(p, bb, t0 + i, h) + ch0 + 4 * c4;
@@ -827,19 +837,20 @@ __global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
     *reinterpret_cast<float4*>(&sG[i][4 * c4]) = ld4g(G + i * KD + ch0 + 4 * c4);
   }
 #pragma unroll
-  for (int it = 0; it < CC / 4 / 256; ++it) {
-    const int idx = tid + 256 * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
+  for (int it = 0; it < CC / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
     *reinterpret_cast<float4*>(&sdM[i][4 * c4]) = ld4g(p.dMw + (int64_t)u * CC + i * BC + 4 * c4);
     *reinterpret_cast<float4*>(&sdA[i][4 * c4]) = ld4g(p.dAw + (int64_t)u * CC + i * BC + 4 * c4);
   }
   lds_barrier();
 
-  rs += __shfl_xor(rs, 1);
-  rs += __shfl_xor(rs, 2);
-  if ((tid & 3) == 0) sTail[tid >> 2] = rs;
+#pragma unroll
+  for (int o = 1; o < PARTS; o <<= 1) rs += __shfl_xor(rs, o);
+  if (tid % PARTS == 0) sTail[tid / PARTS] = rs;
   const float glast = sG[BC - 1][rl];
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int Ib = 0; Ib < NB; ++Ib) {
+    const int I = I0 + Ib;
     // off-diagonal blocks: rows i of block I against columns j < 16 I
     f32x4 oq = zero4(), ob = zero4(), ok_ = zero4();
     const int m = 16 * I, m2 = 16 * I + 15;
@@ -892,10 +903,10 @@ __global__ __launch_bounds__(256) void k_bw_dqk(BW p) {
         dk += off * sdM[16 * I + jj][i] * fji * qb[jj] + sdA[16 * I + jj][i] * fji * betab[jj];
       }
       const float eg = scar[i] ? ex2(gi) : 0.f;
-      dq += eg * rq[I][e] + oq[e] * ex2(gi - gm);
-      dbeta += -eg * rb[I][e] + ob[e] * ex2(gi - gm);
+      dq += eg * rq[Ib][e] + oq[e] * ex2(gi - gm);
+      dbeta += -eg * rb[Ib][e] + ob[e] * ex2(gi - gm);
       dk += ok_[e] * ex2(gm2 - gi);
-      const float dkc = slast[i] ? ex2(glast - gi) * rk[I][e] : 0.f;
+      const float dkc = slast[i] ? ex2(glast - gi) * rk[Ib][e] : 0.f;
       const float kv = kb[ii], bv = sB[i][rl], dmii = sdM[i][i];
       sdG[i][rl] = qb[ii] * dq + bv * kv * dbeta - kv * dk;
       sP[i][rl] = kv * dkc;
@@ -993,11 +1004,11 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   hipStream_t st = (hipStream_t)stream;
   const int chains = a->B * a->H * (KD / 16);
   prof_mark(4, st, false);
-  hipLaunchKernelGGL(k_bw_intra, dim3((unsigned)units), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_intra, dim3((unsigned)units), dim3(NT), 0, st, p);
   hipLaunchKernelGGL(k_bw_chain<false>, dim3(chains), dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_bw_chain<true>, dim3(chains), dim3(256), 0, st, p);
-  hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(256), 0, st, p);
-  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(2 * units)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(NT), 0, st, p);
+  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(2 * units)), dim3(NT), 0, st, p);
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
