@@ -67,7 +67,7 @@ struct BW {
   float *Kc;   // [BC][KD]
   float *KcT;  // [KD][BC]
   float *XfT;  // [KD][BC]
-  float *U0;   // [BC][KD]
+  float *U0T;  // [KD][BC] U0^T
   float *MT;   // [BC][BC] M^T
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     }
     float* Wm = p.Wm + (int64_t)u * CK;
     float* WT = p.WT + (int64_t)u * CK;
-    float* U0 = p.U0 + (int64_t)u * CK;
+    float* U0T = p.U0T + (int64_t)u * CK;
     lds_barrier();   // every wave has read b k from sW
 #pragma unroll
     for (int I = 0; I < 4; ++I)
@@ -327,8 +327,9 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
           const int i = 16 * I + 4 * q + e;
           sW[i][r] = aw[I][R2][e];
           Wm[i * KD + r] = aw[I][R2][e];
-          U0[i * KD + r] = au[I][R2][e];
         }
+        *reinterpret_cast<float4*>(U0T + r * BC + 16 * I + 4 * q) =
+            make_float4(au[I][R2][0], au[I][R2][1], au[I][R2][2], au[I][R2][3]);
         *reinterpret_cast<float4*>(WT + r * BC + 16 * I + 4 * q) =
             make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
       }
@@ -397,9 +398,9 @@ struct ChainOps {
   float a[4][8];        // W (forward) / Kc (backward) rows of this wave's 16 tokens
   float b[2][2][8];     // Kc^T (forward) / W^T (backward) rows of this wave's 32 state rows
   float x[2][2][8];     // Xf^T rows (backward)
-  float o[2][8];        // dO fragments (backward)
-  float u[4];           // U0 tile entries (forward)
-  float lm[2][4];       // lam of this lane's state rows
+  float4 o4;            // one float4 of the chunk's 64 x 16 dO tile (backward), staged through LDS
+  float4 u;             // U0 tile entries of this lane (forward)
+  float4 lm[2];         // lam of this lane's state rows
 };
 
 template <bool BWD>
@@ -421,23 +422,16 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) row8(Xrow, s2, q, o.x[tt][s2]);
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o.lm[tt][e] = p.lam[u * KD + 32 * wv + 16 * tt + 4 * q + e];
+    o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
   if (BWD) {
-    const int t0 = c * BC;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // tokens past the end read a clamped row: their Xf^T columns are zero
-        const int tok = t0 + 32 * s2 + pi_k(q, e);
-        o.o[s2][e] = p.dout[row_of(p, bb, min(tok, p.L - 1), h) + col0 + l16];
-      }
+    // thread t loads columns 4 (t % 4) .. +3 of token t / 4; tokens past the
+    // end read a clamped row (their Xf^T columns are zero)
+    const int t = 64 * wv + l;
+    const int tok = c * BC + (t >> 2);
+    o.o4 = ld4g(p.dout + row_of(p, bb, min(tok, p.L - 1), h) + col0 + 4 * (t & 3));
   } else {
-    const float* U0 = p.U0 + u * CK;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o.u[e] = U0[(16 * wv + 4 * q + e) * KD + col0 + l16];
+    o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
   }
 }
 
@@ -445,6 +439,7 @@ template <bool BWD>
 __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
   __shared__ float sS[4][64][8];
   __shared__ float sY[2][64][8];
+  __shared__ float sO[BC][16 + 1];   // dO tile of the current chunk (backward)
   int ct, bh, zz;
   {
     int x = blockIdx.x, y = 0, z = 0;
@@ -476,6 +471,11 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
   // one scan step on chunk c with operands `o` in registers
   auto step = [&](int c, const ChainOps& o) {
     const int64_t u = (int64_t)bh * p.NC + c;
+    if (BWD) {
+      const int t = 64 * wv + l;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sO[t >> 2][4 * (t & 3) + j] = f4at(o.o4, j);
+    }
     lds_barrier();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;
@@ -492,9 +492,13 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     f32x4 acc2[2] = {zero4(), zero4()};
     if (BWD) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float xo[8];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) mma(acc2[tt], fr8(o.x[tt][s2]), fr8(o.o[s2]));
+        for (int e = 0; e < 8; ++e) xo[e] = sO[32 * s2 + pi_k(q, e)][l16];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) mma(acc2[tt], fr8(o.x[tt][s2]), fr8(xo));
+      }
     }
     // Y (or Z) tile: token rows 16w..16w+15; two accumulators halve the
     // dependent MFMA chain on the sequential path
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
       mma(y2, fr8(o.a[s + 2]), fr8(&sS[s + 2][l][0]));
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = BWD ? -(y[e] + y2[e]) : o.u[e] - (y[e] + y2[e]);
+    for (int e = 0; e < 4; ++e) y[e] = BWD ? -(y[e] + y2[e]) : f4at(o.u, e) - (y[e] + y2[e]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
     lds_barrier();
@@ -513,7 +517,7 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[tt][e] = o.lm[tt][e] * st[tt][e];
+      for (int e = 0; e < 4; ++e) acc[tt][e] = f4at(o.lm[tt], e) * st[tt][e];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -627,7 +631,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   f32x4 acc[4][TPW];
   // ---- U = U0 - W S0 ---------------------------------------------------------
   {
-    const float* U0 = p.U0 + (int64_t)u * CK;
+    const float* U0T = p.U0T + (int64_t)u * CK;
     zero_acc(acc);
     nt_128(acc, p.Wm + (int64_t)u * CK, KD, S0T, KD, wv, q, l16);
 #pragma unroll
@@ -635,11 +639,9 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
       for (int R2 = 0; R2 < TPW; ++R2) {
         const int vcol = 16 * (TPW * wv + R2) + l16;
+        const float4 u0 = ld4g(U0T + vcol * BC + 16 * I + 4 * q);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 16 * I + 4 * q + e;
-          sU[i][vcol] = U0[i * KD + vcol] - acc[I][R2][e];
-        }
+        for (int e = 0; e < 4; ++e) sU[16 * I + 4 * q + e][vcol] = f4at(u0, e) - acc[I][R2][e];
       }
   }
   lds_barrier();
@@ -997,7 +999,7 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   float* ws = (float*)workspace;
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
-  p.XfT = take(CK); p.U0 = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
+  p.XfT = take(CK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
   p.dMw = take(CC); p.dAw = take(CC);
   p.S = take(KK); p.ST = take(KK); p.dS = take(KK); p.dST = take(KK);
 
