@@ -80,10 +80,13 @@ class _NoGrad(torch.autograd.Function):
 
 
 def _maybe_guard_grad(is_inference, run, tensors):
-    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
+    """Inference calls whose inputs require grad get an op whose backward
+    raises (gdn2.py:1436-1441).  Training calls that need gradients never
+    reach this point (they take ``_chunk_gdn2_train``)."""
+    if is_inference and torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
         msg = ("chunk_gdn2: differentiation is not supported when is_inference=True; "
-               "set is_inference=False for training.") if is_inference else (
-            "chunk_gdn2: the backward pass is not part of the MI355X build (forward-only drop-in).")
+               "set is_inference=False for training.")
         return _NoGrad.apply(msg, run, *[t for t in tensors if isinstance(t, torch.Tensor)])
     return run()
 
@@ -113,10 +116,12 @@ def chunk_gdn2(
 ):
     """Forward pass of chunked-WY GDN-2 on MI355X (reference: gdn2.py:1772-2286).
 
-    Args and returns as the reference ``chunk_gdn2``.  Flags that only shape the
-    reference's TPU backward or fallback (``fallback_scan``, ``recompute_states``,
-    ``truncate_bwd_dT_bf16``) are accepted and have no effect on the forward
-    result.  ``state_fp32_matmul=True`` runs the call at ``precision="fp32"``.
+    Args and returns as the reference ``chunk_gdn2``.  With ``is_inference=False``
+    and inputs that require grad, the call is differentiable under torch.autograd
+    (backward: ``dn_prefill_bwd``, fp32, reference custom VJP gdn2.py:1446-1769).
+    Flags that only shape the reference's TPU backward or fallback
+    (``fallback_scan``, ``recompute_states``, ``truncate_bwd_dT_bf16``) are
+    accepted and change no result.  ``state_fp32_matmul=True`` runs the call at ``precision="fp32"``.
     ``mask_lambda_by_doc`` is accepted: the kernels never form a cumulative
     decay across a document boundary, so the flag's precision concern does
     not arise.

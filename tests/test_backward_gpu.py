@@ -188,3 +188,16 @@ def test_backward_bf16_inputs_and_chunk_gdn():
         assert e < 1e-5, n
     e = rel_l2(as_np(bt.grad), rg["db"] + rg["dw"])
     assert e < 1e-5, e
+
+
+def test_backward_cu_seqlens_batch2():
+    """cu_seqlens documents (gdn2.py:2033-2079) with B = 2 and an initial state."""
+    B, L, Hk, Hv = 2, 320, 2, 4
+    q, k, v, g, b, w = ref_inputs(31, B, L, Hk, Hv)
+    rng = np.random.default_rng(32)
+    init = rng.standard_normal((B, Hv, 128, 128)) * 0.05
+    do, df = rng.standard_normal((B, L, Hv, 128)), rng.standard_normal((B, Hv, 128, 128))
+    cu = [0, 70, 200, 201, 320]
+    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32", cu_seqlens=cu)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, cu_seqlens=cu)
+    compare(got, ref, 1e-5, "cu_seqlens B=2")
