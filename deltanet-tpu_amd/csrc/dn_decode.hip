@@ -175,6 +175,7 @@ __device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
 #define DN_DECODE_WAVES 4
 #endif
 constexpr int kDecodeWaves = DN_DECODE_WAVES;
+constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel (8 measured slower)
 
 // One workgroup of NW waves per (batch row, value head).  Lane (rg, cg)
 // holds state rows R*rg..R*rg+R-1 (R = 32/NW), 8 columns per row (Row8
@@ -471,18 +472,19 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
     float vc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) vc[e] = vn[u][RowIn::col(cg, e)];
-    float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int ii = R * rg + r;
       const float di = dd[u][ii], ki = kn[u][ii];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        S[r][e] = fmaf(di, S[r][e], ki * vc[e]);
-        ss += S[r][e] * S[r][e];
-      }
+      for (int e = 0; e < 8; ++e) S[r][e] = fmaf(di, S[r][e], ki * vc[e]);
     }
     if (p.guard) {
+      float ss = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += S[r][e] * S[r][e];
       ss = wave_sum(ss);
       if (lane == 0) gbuf[u][wid] = ss;
       __syncthreads();
@@ -605,10 +607,10 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
     else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
     else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
   } else {
-    if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kDecodeWaves>), grid, blk, 0, st, p);
-    else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kDecodeWaves>), grid, blk, 0, st, p);
-    else if (fo) hipLaunchKernelGGL((k_decode_multi<bf16, float, kDecodeWaves>), grid, blk, 0, st, p);
-    else hipLaunchKernelGGL((k_decode_multi<bf16, bf16, kDecodeWaves>), grid, blk, 0, st, p);
+    if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
+    else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
+    else if (fo) hipLaunchKernelGGL((k_decode_multi<bf16, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
+    else hipLaunchKernelGGL((k_decode_multi<bf16, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
   }
   prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
