@@ -201,3 +201,37 @@ def test_backward_cu_seqlens_batch2():
     _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32", cu_seqlens=cu)
     ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, cu_seqlens=cu)
     compare(got, ref, 1e-5, "cu_seqlens B=2")
+
+
+@pytest.mark.parametrize("variant", ["kda", "gla", "delta_rule"])
+def test_backward_variants(variant):
+    """The variants are adapters over chunk_gdn2 (variants.py:91-285), so they
+    train through the same backward: KDA (channel decay, b = w = beta), GLA
+    (b = 0, w = 1), DeltaNet (g = 0, b = w = beta)."""
+    import deltanet_tpu_amd as D
+    B, L, Hk, Hv = 1, 200, 2, 4
+    q, k, v, g, _, _ = ref_inputs(40, B, L, Hk, Hv)
+    rng = np.random.default_rng(41)
+    beta = sig(rng.standard_normal((B, L, Hk)))
+    do = rng.standard_normal((B, L, Hv, 128))
+    ones = lambda: np.ones((B, L, 1))
+    qt, kt, vt = (to_dev(x).requires_grad_(True) for x in (q, k, v))
+    gt, bt = to_dev(g).requires_grad_(True), to_dev(beta).requires_grad_(True)
+    if variant == "kda":
+        out = D.chunk_kda(qt, kt, vt, gt, bt, precision="fp32", is_inference=False)
+        ref = GR.chunk_gdn2_vjp(q, k, v, g, beta, beta, do)
+    elif variant == "gla":
+        out = D.chunk_gla(qt, kt, vt, gt, precision="fp32", is_inference=False)
+        ref = GR.chunk_gdn2_vjp(q, k, v, g, 0 * ones(), ones(), do)
+    else:
+        out = D.chunk_delta_rule(qt, kt, vt, bt, precision="fp32", is_inference=False)
+        ref = GR.chunk_gdn2_vjp(q, k, v, 0 * ones(), beta, beta, do)
+    (out.float() * to_dev(do)).sum().backward()
+    got = {"dq": as_np(qt.grad), "dk": as_np(kt.grad), "dv": as_np(vt.grad)}
+    if variant != "delta_rule":
+        got["dg"] = as_np(gt.grad)
+    if variant != "gla":
+        got["db"] = as_np(bt.grad)
+        ref = dict(ref, db=ref["db"] + ref["dw"])
+    ref = {n: ref[n] for n in got}
+    compare(got, ref, 1e-5, f"variant {variant}")
