@@ -359,52 +359,83 @@ def _canonical_segments(seg_t, B, L, has_init, init_seg_id, dev):
     return canon.to(torch.int32).contiguous()
 
 
-class _RecurrenceFn(torch.autograd.Function):
-    """The chunked recurrence on prepared float32 inputs (all at Hv heads).
+def _sum_to(grad, shape):
+    """Sum a (B, L, Hv, C) gradient back to a (B, L, H, c) input that was
+    broadcast to it (H in {1, Hk, Hv} with value head j reading head j // G;
+    c in {1, C})."""
+    B, L, Hv, C = grad.shape
+    H, c = shape[2], shape[3]
+    if H != Hv:
+        grad = grad.view(B, L, H, Hv // H, C).sum(3) if H > 1 else grad.sum(2, keepdim=True)
+    if c != C:
+        grad = grad.sum(3, keepdim=True)
+    return grad
 
-    Forward: ``dn_prefill_fwd`` (the inference kernels).  Backward:
-    ``dn_prefill_bwd`` (reference custom VJP, gdn2.py:1446-1769).
+
+class _RecurrenceFn(torch.autograd.Function):
+    """The chunked recurrence on prepared inputs: q, k at key heads, gates in
+    their own (B, L, H, C) layouts, all already activated / normalised.
+
+    Forward: ``dn_prefill_fwd`` (the inference kernels, GQA and gate broadcast
+    read in place).  Backward: ``dn_prefill_bwd`` (reference custom VJP,
+    gdn2.py:1446-1769) on float32 copies expanded to value heads; the
+    gradients are summed back to each input's layout.
     """
 
     @staticmethod
-    def forward(ctx, qe, ke, ve, ge, be, we, init, meta):
+    def forward(ctx, qh, kh, v, ga, ba, wa, init, meta):
         seg_t, init_seg_id, canon, precision = meta
         with torch.no_grad():
             out, fin = chunk_gdn2(
-                qe, ke, ve, ge, be, we, segment_ids=seg_t, initial_state=init,
+                qh, kh, v, ga, ba, wa, segment_ids=seg_t, initial_state=init,
                 initial_state_segment_id=init_seg_id, output_final_state=True, precision=precision,
                 scale=1.0, is_inference=True)
-        ctx.save_for_backward(qe, ke, ve, ge, be, we, init)
+        ctx.save_for_backward(qh, kh, v, ga, ba, wa, init)
         ctx.canon = canon
         ctx.has_init = init is not None
-        return out.float(), fin
+        return out, fin
 
     @staticmethod
     def backward(ctx, d_out, d_fin):
-        qe, ke, ve, ge, be, we, init = ctx.saved_tensors
-        B, L, H, K = qe.shape
-        V = ve.shape[3]
-        dev = qe.device
-        d_out = torch.zeros_like(ve) if d_out is None else d_out.to(torch.float32).contiguous()
-        d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
-        grads = [torch.empty_like(x) for x in (qe, ke, ve, ge, be, we)]
-        d_init = torch.empty_like(init) if ctx.has_init else None
-        a = _lib.BackwardArgs()
-        a.abi_version = _lib.DN_ABI_VERSION
-        a.B, a.L, a.H, a.K, a.V = B, L, H, K, V
-        a.q, a.k, a.v, a.g, a.b, a.w = (_ptr(x) for x in (qe, ke, ve, ge, be, we))
-        a.seg = _ptr(ctx.canon)
-        a.init_state = _ptr(init)
-        a.d_out, a.d_final = _ptr(d_out), _ptr(d_fin)
-        a.dq, a.dk, a.dv, a.dg, a.db, a.dw = (_ptr(x) for x in grads)
-        a.d_init = _ptr(d_init)
-        lib = _lib.load_library()
-        nbytes = lib.dn_prefill_bwd_workspace_size(ctypes.byref(a))
-        if nbytes == 0:
-            _lib.check(-1, "dn_prefill_bwd_workspace_size")
-        ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
-        _lib.check(lib.dn_prefill_bwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_bwd")
-        return (*grads, d_init, None)
+        qh, kh, v, ga, ba, wa, init = ctx.saved_tensors
+        B, L, Hk, K = qh.shape
+        H, V = v.shape[2], v.shape[3]
+        G = H // Hk
+        dev = qh.device
+        with torch.no_grad():
+            f32 = lambda t: t.to(torch.float32)
+            qe = torch.repeat_interleave(f32(qh), G, dim=2).contiguous() if G > 1 else f32(qh).contiguous()
+            ke = torch.repeat_interleave(f32(kh), G, dim=2).contiguous() if G > 1 else f32(kh).contiguous()
+            ge = _gate_to_heads(f32(ga), B, L, Hk, H, K).contiguous()
+            be = _gate_to_heads(f32(ba), B, L, Hk, H, K).contiguous()
+            we = _gate_to_heads(f32(wa), B, L, Hk, H, V).contiguous()
+            ve = f32(v).contiguous()
+            d_out = torch.zeros_like(ve) if d_out is None else d_out.to(torch.float32).contiguous()
+            d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
+            grads = [torch.empty_like(x) for x in (qe, ke, ve, ge, be, we)]
+            d_init = torch.empty_like(init) if ctx.has_init else None
+            a = _lib.BackwardArgs()
+            a.abi_version = _lib.DN_ABI_VERSION
+            a.B, a.L, a.H, a.K, a.V = B, L, H, K, V
+            a.q, a.k, a.v, a.g, a.b, a.w = (_ptr(x) for x in (qe, ke, ve, ge, be, we))
+            a.seg = _ptr(ctx.canon)
+            a.init_state = _ptr(init)
+            a.d_out, a.d_final = _ptr(d_out), _ptr(d_fin)
+            a.dq, a.dk, a.dv, a.dg, a.db, a.dw = (_ptr(x) for x in grads)
+            a.d_init = _ptr(d_init)
+            lib = _lib.load_library()
+            nbytes = lib.dn_prefill_bwd_workspace_size(ctypes.byref(a))
+            if nbytes == 0:
+                _lib.check(-1, "dn_prefill_bwd_workspace_size")
+            ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+            _lib.check(lib.dn_prefill_bwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_bwd")
+            dq, dk, dv, dg, db, dw = grads
+            if G > 1:
+                dq = dq.view(B, L, Hk, G, K).sum(3)
+                dk = dk.view(B, L, Hk, G, K).sum(3)
+            out = (dq.to(qh.dtype), dk.to(kh.dtype), dv.to(v.dtype), _sum_to(dg, ga.shape).to(ga.dtype),
+                   _sum_to(db, ba.shape).to(ba.dtype), _sum_to(dw, wa.shape).to(wa.dtype))
+        return (*out, d_init, None)
 
 
 def _chunk_gdn2_train(q, k, v, g, b, w, seg_t, initial_state, init_seg_id, output_final_state,
@@ -412,29 +443,30 @@ def _chunk_gdn2_train(q, k, v, g, b, w, seg_t, initial_state, init_seg_id, outpu
     """Training-mode chunk_gdn2 (is_inference=False, gdn2.py:2244-2286).
 
     The wrapper's elementwise steps (gdn2.py:1970-2125) run as differentiable
-    torch ops, so autograd carries their derivatives and sums the gate / GQA
-    broadcasts; the recurrence itself is ``_RecurrenceFn``.
+    torch ops, so autograd carries their derivatives; the recurrence itself is
+    ``_RecurrenceFn``, whose forward reads q / k at key heads and the gates in
+    their own layouts like the inference path.
     """
     B, L, Hk, K = q.shape
     Hv, V = v.shape[2], v.shape[3]
     dev = q.device
-    G = Hv // Hk
     qf, kf = q.to(torch.float32), k.to(torch.float32)
 
     def l2(x):
         return x * torch.rsqrt(torch.sum(x * x, dim=-1, keepdim=True) + 1e-6)
 
+    four = lambda t: t.unsqueeze(-1) if t.ndim == 3 else t
     if fuse_prologue:
         qh, kh = l2(qf) * scale, l2(kf)
-        ga = -torch.exp(torch.clamp(g.to(torch.float32), max=5.0))
+        ga = -torch.exp(torch.clamp(four(g).to(torch.float32), max=5.0))
         if stability_guard:
             ga = torch.clamp(ga, max=-1e-6)
-        ba, wa = torch.sigmoid(b.to(torch.float32)), torch.sigmoid(w.to(torch.float32))
+        ba, wa = torch.sigmoid(four(b).to(torch.float32)), torch.sigmoid(four(w).to(torch.float32))
     else:
-        gf = g.to(torch.float32)
+        gf = four(g).to(torch.float32)
         # gdn2.py:38-62: min(g, 0) with the gradient passed wherever g <= 0
         ga = torch.where(gf <= 0.0, gf, torch.zeros_like(gf))
-        ba, wa = b.to(torch.float32), w.to(torch.float32)
+        ba, wa = four(b).to(torch.float32), four(w).to(torch.float32)
         if stability_guard:
             ba = torch.clamp(ba, min=0.0)
             ga = torch.clamp(ga, max=-1e-6)
@@ -443,17 +475,13 @@ def _chunk_gdn2_train(q, k, v, g, b, w, seg_t, initial_state, init_seg_id, outpu
         else:
             qh, kh = qf * scale, kf
         # gdn2.py:2113-2122: normalised q / k are stored back in the input dtype
-        qh, kh = qh.to(q.dtype).to(torch.float32), kh.to(k.dtype).to(torch.float32)
-    qe = torch.repeat_interleave(qh, G, dim=2) if G > 1 else qh
-    ke = torch.repeat_interleave(kh, G, dim=2) if G > 1 else kh
-    ge = _gate_to_heads(ga, B, L, Hk, Hv, K)
-    be = _gate_to_heads(ba, B, L, Hk, Hv, K)
-    we = _gate_to_heads(wa, B, L, Hk, Hv, V)
-    ve = v.to(torch.float32)
-    qe, ke, ve, ge, be, we = (x.contiguous() for x in (qe, ke, ve, ge, be, we))
+        if q.dtype in (torch.bfloat16, torch.float16):
+            qh, kh = qh.to(q.dtype), kh.to(k.dtype)
+    qh, kh, ga, ba, wa = (x.contiguous() for x in (qh, kh, ga, ba, wa))
+    vv = v if v.dtype in (torch.float32, torch.bfloat16) else v.to(torch.float32)
     init = initial_state.to(torch.float32).contiguous() if initial_state is not None else None
     canon = _canonical_segments(seg_t, B, L, initial_state is not None, init_seg_id, dev)
-    out, fin = _RecurrenceFn.apply(qe, ke, ve, ge, be, we, init, (seg_t, init_seg_id, canon, precision))
+    out, fin = _RecurrenceFn.apply(qh, kh, vv.contiguous(), ga, ba, wa, init, (seg_t, init_seg_id, canon, precision))
     out = out.to(v.dtype)
     if output_final_state:
         return out, fin
