@@ -946,6 +946,228 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Raw-input backward: the whole training op's VJP from the forward's own
+// arguments (dn_prefill_args): segment canonicalisation, the wrapper's
+// prologue (gdn2.py:1970-2125, 133-142) recomputed per value head, the
+// recurrence backward above, and the prologue's derivatives summed back to
+// each raw layout (GQA groups, broadcast gate heads / channels).
+// ---------------------------------------------------------------------------
+struct BR {
+  int B, L, Hk, Hv, G;
+  const void *q, *k, *v;
+  int qk_dt, v_dt;
+  const float *g, *b, *w;
+  int g_h, g_c, b_h, b_c, w_h, w_c;
+  const void* seg; int seg_dt, seg_batched;
+  const int32_t* init_seg; int has_init;
+  float scale; int l2norm, fuse, guard;
+  int32_t* canon;                                 // (B, L)
+  float *qe, *ke, *ve, *ge, *be, *we;             // (B, L, Hv, 128) prepared inputs
+  const float *dqe, *dke, *dge, *dbe, *dwe;       // their gradients
+  float *dq, *dk, *dg, *db, *dw;                  // raw-layout gradients
+};
+
+__device__ __forceinline__ int gate_head(int H, int Hk, int Hv, int hv, int G) {
+  return H == Hv ? hv : (H == Hk ? hv / G : 0);
+}
+__device__ __forceinline__ float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
+// canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094)
+__global__ __launch_bounds__(256) void k_bw_canon(BR p) {
+  __shared__ int part[256];
+  const int bb = blockIdx.x, tid = threadIdx.x;
+  const int per = (p.L + 255) / 256;
+  const int t0 = tid * per, t1 = min(t0 + per, p.L);
+  const int64_t base = p.seg_batched ? (int64_t)bb * p.L : 0;
+  auto sid = [&](int t) -> int64_t { return p.seg ? ld_i(p.seg, base + t, p.seg_dt) : 0; };
+  int cnt = 0;
+  for (int t = max(t0, 1); t < t1; ++t) cnt += sid(t) != sid(t - 1);
+  part[tid] = cnt;
+  __syncthreads();
+  if (tid == 0) {
+    int acc = (p.has_init && p.init_seg != nullptr) ? (sid(0) != (int64_t)p.init_seg[bb]) : 0;
+    for (int i = 0; i < 256; ++i) { const int c = part[i]; part[i] = acc; acc += c; }
+  }
+  __syncthreads();
+  int acc = part[tid];             // first_new + changes at positions 1 .. t0-1
+  for (int t = t0; t < t1; ++t) {
+    if (t > 0) acc += sid(t) != sid(t - 1);
+    p.canon[(int64_t)bb * p.L + t] = acc;
+  }
+}
+
+// one wave per (batch, token, value head) row: the prepared inputs exactly as
+// the forward kernels form them
+__global__ __launch_bounds__(256) void k_bw_prep(BR p) {
+  const int l = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t rows = (int64_t)p.B * p.L * p.Hv;
+  if (row >= rows) return;
+  const int hv = (int)(row % p.Hv);
+  const int64_t bt = row / p.Hv;                 // batch * L + token
+  const int hk = hv / p.G;
+  const int64_t qrow = (bt * p.Hk + hk) * KD;
+  float x[2], y[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    x[e] = ld_f(p.q, qrow + l + 64 * e, p.qk_dt);
+    y[e] = ld_f(p.k, qrow + l + 64 * e, p.qk_dt);
+  }
+  float sq = x[0] * x[0] + x[1] * x[1], sk = y[0] * y[0] + y[1] * y[1];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { sq += __shfl_xor(sq, o); sk += __shfl_xor(sk, o); }
+  const bool b16 = p.qk_dt != DT_F32;
+  const int64_t orow = row * KD;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int i = l + 64 * e;
+    float qh, kh;
+    if (p.fuse) {
+      qh = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
+      kh = y[e] * rsqrtf(sk + 1e-6f);
+    } else if (p.l2norm) {
+      qh = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
+      kh = y[e] * rsqrtf(sk + 1e-6f);
+      if (b16) { qh = p.qk_dt == DT_BF16 ? round_as<bf16>(qh) : round_as<f16>(qh);
+                 kh = p.qk_dt == DT_BF16 ? round_as<bf16>(kh) : round_as<f16>(kh); }
+    } else {
+      qh = x[e] * p.scale;
+      kh = y[e];
+      if (b16) qh = p.qk_dt == DT_BF16 ? round_as<bf16>(qh) : round_as<f16>(qh);
+    }
+    const int hg = gate_head(p.g_h, p.Hk, p.Hv, hv, p.G), hb = gate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
+    const int hw = gate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+    float gv = p.g[(bt * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i)];
+    float bv = p.b[(bt * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i)];
+    float wv = p.w[(bt * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i)];
+    if (p.fuse) {
+      gv = -__expf(fminf(gv, 5.f));
+      bv = sigmoid_hw(bv);
+      wv = sigmoid_hw(wv);
+    } else {
+      gv = fminf(gv, 0.f);
+      if (p.guard) bv = fmaxf(bv, 0.f);
+    }
+    if (p.guard) gv = fminf(gv, -1e-6f);
+    p.qe[orow + i] = qh;
+    p.ke[orow + i] = kh;
+    p.ge[orow + i] = gv;
+    p.be[orow + i] = bv;
+    p.we[orow + i] = wv;
+    p.ve[orow + i] = ld_f(p.v, (bt * p.Hv + hv) * KD + i, p.v_dt);
+  }
+}
+
+// one wave per (batch, token, key head) row: dq, dk through the GQA sum and
+// the L2-norm / scale (a bf16 or f16 normalised q / k receives its cotangent
+// in that dtype, as the reference's cast back does)
+__global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
+  const int l = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)p.B * p.L * p.Hk) return;
+  const int hk = (int)(row % p.Hk);
+  const int64_t bt = row / p.Hk;
+  float dqh[2] = {0.f, 0.f}, dkh[2] = {0.f, 0.f}, x[2], y[2];
+  for (int g = 0; g < p.G; ++g) {
+    const int64_t er = (bt * p.Hv + hk * p.G + g) * KD;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      dqh[e] += p.dqe[er + l + 64 * e];
+      dkh[e] += p.dke[er + l + 64 * e];
+    }
+  }
+  const bool b16 = p.qk_dt != DT_F32 && !p.fuse;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    x[e] = ld_f(p.q, row * KD + l + 64 * e, p.qk_dt);
+    y[e] = ld_f(p.k, row * KD + l + 64 * e, p.qk_dt);
+    if (b16) {
+      dqh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(dqh[e]) : round_as<f16>(dqh[e]);
+      dkh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(dkh[e]) : round_as<f16>(dkh[e]);
+    }
+  }
+  float dq[2], dk[2];
+  if (p.fuse || p.l2norm) {
+    float sq = x[0] * x[0] + x[1] * x[1], sk = y[0] * y[0] + y[1] * y[1];
+    float xq = x[0] * dqh[0] + x[1] * dqh[1], yk = y[0] * dkh[0] + y[1] * dkh[1];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      sq += __shfl_xor(sq, o); sk += __shfl_xor(sk, o);
+      xq += __shfl_xor(xq, o); yk += __shfl_xor(yk, o);
+    }
+    // d/dx of c x / sqrt(|x|^2 + eps) = c r (dx^ - r^2 x (x . dx^))
+    const float rq = rsqrtf(sq + 1e-6f), rk = rsqrtf(sk + 1e-6f);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      dq[e] = p.scale * rq * (dqh[e] - rq * rq * x[e] * xq);
+      dk[e] = rk * (dkh[e] - rk * rk * y[e] * yk);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) { dq[e] = p.scale * dqh[e]; dk[e] = dkh[e]; }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    p.dq[row * KD + l + 64 * e] = dq[e];
+    p.dk[row * KD + l + 64 * e] = dk[e];
+  }
+}
+
+// one thread per raw gate element: the sum of the prepared gradient over the
+// value heads and channels it was broadcast to, times the prologue derivative
+template <int WHICH>   // 0 = g, 1 = b, 2 = w
+__global__ __launch_bounds__(256) void k_bw_post_gate(BR p) {
+  const int H = WHICH == 0 ? p.g_h : (WHICH == 1 ? p.b_h : p.w_h);
+  const int C = WHICH == 0 ? p.g_c : (WHICH == 1 ? p.b_c : p.w_c);
+  const float* raw = WHICH == 0 ? p.g : (WHICH == 1 ? p.b : p.w);
+  const float* dpre = WHICH == 0 ? p.dge : (WHICH == 1 ? p.dbe : p.dwe);
+  float* out = WHICH == 0 ? p.dg : (WHICH == 1 ? p.db : p.dw);
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)p.B * p.L * H * C;
+  if (idx >= n) return;
+  const int c = (int)(idx % C);
+  const int h = (int)((idx / C) % H);
+  const int64_t bt = idx / ((int64_t)C * H);
+  // value heads that read gate head h: h (H = Hv), h G .. h G + G - 1 (H = Hk), all (H = 1)
+  int h0, hn;
+  if (H == p.Hv) { h0 = h; hn = 1; }
+  else if (H == p.Hk) { h0 = h * p.G; hn = p.G; }
+  else { h0 = 0; hn = p.Hv; }
+  const float* rowp = dpre + (bt * p.Hv + h0) * KD;
+  float s = 0.f;
+  if (C == 1) {
+    for (int j = 0; j < hn; ++j, rowp += KD) {
+      float4 acc = zero_f4();
+#pragma unroll 8
+      for (int i4 = 0; i4 < KD / 4; ++i4) {
+        const float4 x4 = ld4g(rowp + 4 * i4);
+        acc.x += x4.x; acc.y += x4.y; acc.z += x4.z; acc.w += x4.w;
+      }
+      s += (acc.x + acc.y) + (acc.z + acc.w);
+    }
+  } else {
+    for (int j = 0; j < hn; ++j, rowp += KD) s += rowp[c];
+  }
+  const float x = raw[idx];
+  float d;
+  if (WHICH == 0) {
+    if (p.fuse) {
+      const float ga = -__expf(fminf(x, 5.f));
+      d = (x <= 5.f ? -__expf(x) : 0.f) * ((!p.guard || ga <= -1e-6f) ? 1.f : 0.f);
+    } else {
+      d = (x <= 0.f && (!p.guard || x <= -1e-6f)) ? 1.f : 0.f;
+    }
+  } else if (WHICH == 1) {
+    if (p.fuse) { const float sg = sigmoid_hw(x); d = sg * (1.f - sg); }
+    else d = (!p.guard || x >= 0.f) ? 1.f : 0.f;
+  } else {
+    if (p.fuse) { const float sg = sigmoid_hw(x); d = sg * (1.f - sg); }
+    else d = 1.f;
+  }
+  out[idx] = s * d;
+}
+
 }  // namespace
 
 }  // namespace dn
@@ -1013,6 +1235,108 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(2 * units)), dim3(NT), 0, st, p);
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
+  return DN_OK;
+}
+
+namespace {
+
+struct RawLayout {
+  size_t canon, pre, core;   // bytes
+};
+
+RawLayout raw_layout(const dn_prefill_args* a) {
+  RawLayout r;
+  r.canon = (((size_t)a->B * a->L * sizeof(int32_t)) + 255) & ~(size_t)255;
+  r.pre = (size_t)a->B * a->L * a->Hv * KD * sizeof(float);
+  dn_backward_args c{};
+  c.B = a->B; c.L = a->L; c.H = a->Hv;
+  r.core = bw_units(&c) * kUnitFloats * sizeof(float);
+  return r;
+}
+
+int raw_check(const dn_prefill_args* a) {
+  if (a == nullptr) return set_error(DN_E_INVALID, "null args");
+  if (a->abi_version != DN_ABI_VERSION) return set_error(DN_E_ABI, "dn_prefill_args built for another ABI version");
+  if (a->K != KD || a->V != KD) return set_error(DN_E_INVALID, "K and V must both be 128");
+  if (a->B <= 0 || a->L <= 0 || a->Hk <= 0 || a->Hv <= 0 || a->Hv % a->Hk)
+    return set_error(DN_E_INVALID, "bad batch / length / head counts");
+  if (!a->q || !a->k || !a->v || !a->g || !a->b || !a->w) return set_error(DN_E_INVALID, "missing input tensor pointer");
+  if (a->qk_dtype != DN_F32 && a->qk_dtype != DN_BF16 && a->qk_dtype != DN_F16)
+    return set_error(DN_E_INVALID, "q/k dtype must be f32, bf16 or f16");
+  if (a->v_dtype != DN_F32 && a->v_dtype != DN_BF16) return set_error(DN_E_INVALID, "v dtype must be f32 or bf16");
+  const int hs[3] = {a->g_heads, a->b_heads, a->w_heads}, cs[3] = {a->g_chans, a->b_chans, a->w_chans};
+  const int ds[3] = {a->g_dtype, a->b_dtype, a->w_dtype};
+  for (int i = 0; i < 3; ++i) {
+    if (ds[i] != DN_F32) return set_error(DN_E_INVALID, "gates must be f32");
+    if (hs[i] != 1 && hs[i] != a->Hk && hs[i] != a->Hv) return set_error(DN_E_INVALID, "gate heads must be 1, Hk or Hv");
+    if (cs[i] != 1 && cs[i] != KD) return set_error(DN_E_INVALID, "gate channels must be 1 or 128");
+  }
+  if (a->seg != nullptr && a->seg_dtype != DN_I32 && a->seg_dtype != DN_I64)
+    return set_error(DN_E_INVALID, "segment ids must be i32 or i64");
+  return DN_OK;
+}
+
+}  // namespace
+
+extern "C" size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a) {
+  if (raw_check(a) != DN_OK) return 0;
+  const RawLayout r = raw_layout(a);
+  return r.canon + 11 * r.pre + r.core;
+}
+
+extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
+                                  void* dq, void* dk, void* dv, void* dg, void* db, void* dw, void* d_init,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = raw_check(a);
+  if (rc != DN_OK) return rc;
+  if (!d_out || !dq || !dk || !dv || !dg || !db || !dw) return set_error(DN_E_INVALID, "missing gradient pointer");
+  if (d_init != nullptr && a->init_state == nullptr) return set_error(DN_E_INVALID, "d_init needs init_state");
+  const RawLayout lay = raw_layout(a);
+  if (workspace == nullptr || workspace_bytes < lay.canon + 11 * lay.pre + lay.core)
+    return set_error(DN_E_WORKSPACE, "workspace too small");
+  char* w = (char*)workspace;
+  BR r{};
+  r.B = a->B; r.L = a->L; r.Hk = a->Hk; r.Hv = a->Hv; r.G = a->Hv / a->Hk;
+  r.q = a->q; r.k = a->k; r.v = a->v; r.qk_dt = a->qk_dtype; r.v_dt = a->v_dtype;
+  r.g = (const float*)a->g; r.b = (const float*)a->b; r.w = (const float*)a->w;
+  r.g_h = a->g_heads; r.g_c = a->g_chans; r.b_h = a->b_heads; r.b_c = a->b_chans; r.w_h = a->w_heads; r.w_c = a->w_chans;
+  r.seg = a->seg; r.seg_dt = a->seg_dtype; r.seg_batched = a->seg_batched;
+  r.init_seg = a->init_seg; r.has_init = a->init_state != nullptr;
+  r.scale = a->scale; r.l2norm = a->qk_l2norm; r.fuse = a->fuse_prologue; r.guard = a->stability_guard;
+  r.canon = (int32_t*)w; w += lay.canon;
+  float* pre[11];
+  for (int i = 0; i < 11; ++i) { pre[i] = (float*)w; w += lay.pre; }
+  r.qe = pre[0]; r.ke = pre[1]; r.ve = pre[2]; r.ge = pre[3]; r.be = pre[4]; r.we = pre[5];
+  r.dqe = pre[6]; r.dke = pre[7]; r.dge = pre[8]; r.dbe = pre[9]; r.dwe = pre[10];
+  r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
+
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_bw_canon, dim3(a->B), dim3(256), 0, st, r);
+  const int64_t rows = (int64_t)a->B * a->L * a->Hv;
+  hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, r);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
+
+  dn_backward_args c{};
+  c.abi_version = DN_ABI_VERSION;
+  c.B = a->B; c.L = a->L; c.H = a->Hv; c.K = KD; c.V = KD;
+  c.q = r.qe; c.k = r.ke; c.v = r.ve; c.g = r.ge; c.b = r.be; c.w = r.we;
+  c.seg = r.canon; c.init_state = a->init_state; c.d_out = d_out; c.d_final = d_final;
+  c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
+  c.d_init = d_init;
+  rc = dn_prefill_bwd(&c, w, lay.core, stream);
+  if (rc != DN_OK) return rc;
+
+  const int64_t krows = (int64_t)a->B * a->L * a->Hk;
+  hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 3) / 4)), dim3(256), 0, st, r);
+  const int64_t ng = (int64_t)a->B * a->L * a->g_heads * a->g_chans;
+  const int64_t nb = (int64_t)a->B * a->L * a->b_heads * a->b_chans;
+  const int64_t nw = (int64_t)a->B * a->L * a->w_heads * a->w_chans;
+  hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
+  e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;
 }

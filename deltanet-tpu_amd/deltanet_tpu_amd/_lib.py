@@ -89,6 +89,8 @@ EXPORTED_SYMBOLS = (
     "dn_decode_steps",
     "dn_prefill_bwd_workspace_size",
     "dn_prefill_bwd",
+    "dn_prefill_bwd_raw_workspace_size",
+    "dn_prefill_bwd_raw",
     "dn_state_frob_cap",
     "dn_last_error",
     "dn_abi_version",
@@ -125,6 +127,10 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         lib.dn_prefill_bwd_workspace_size.restype = ctypes.c_size_t
         lib.dn_prefill_bwd.argtypes = [ctypes.POINTER(BackwardArgs), _c_ptr, ctypes.c_size_t, _c_ptr]
         lib.dn_prefill_bwd.restype = ctypes.c_int
+        lib.dn_prefill_bwd_raw_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs)]
+        lib.dn_prefill_bwd_raw_workspace_size.restype = ctypes.c_size_t
+        lib.dn_prefill_bwd_raw.argtypes = [ctypes.POINTER(PrefillArgs)] + [_c_ptr] * 9 + [_c_ptr, ctypes.c_size_t, _c_ptr]
+        lib.dn_prefill_bwd_raw.restype = ctypes.c_int
         lib.dn_state_frob_cap.argtypes = [_c_ptr, ctypes.c_int64, _c_i32, _c_i32, ctypes.c_float, _c_ptr]
         lib.dn_state_frob_cap.restype = ctypes.c_int
         lib.dn_last_error.argtypes = []

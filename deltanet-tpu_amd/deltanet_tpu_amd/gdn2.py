@@ -82,7 +82,7 @@ class _NoGrad(torch.autograd.Function):
 def _maybe_guard_grad(is_inference, run, tensors):
     """Inference calls whose inputs require grad get an op whose backward
     raises (gdn2.py:1436-1441).  Training calls that need gradients never
-    reach this point (they take ``_chunk_gdn2_train``)."""
+    reach this point (they take ``_TrainFn``)."""
     if is_inference and torch.is_grad_enabled() and any(
             isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
         msg = ("chunk_gdn2: differentiation is not supported when is_inference=True; "
@@ -226,12 +226,6 @@ def chunk_gdn2(
 
     fp32 = precision_clean in ("fp32", "float32") or bool(state_fp32_matmul)
 
-    if (not is_inference) and torch.is_grad_enabled() and any(
-            isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v, g, b, w, initial_state)):
-        return _chunk_gdn2_train(
-            q, k, v, g, b, w, seg_t, initial_state, initial_state_segment_id, output_final_state,
-            "fp32" if fp32 else "bf16", scale, qk_l2norm, fuse_prologue, stability_guard)
-
     # ---- execution mode (gdn2.py:1992-2007) ----------------------------------
     gates_at_hv = ((g.shape[2] == Hv) or (b.shape[2] == Hv)) and (Hk < Hv)
 
@@ -289,6 +283,13 @@ def chunk_gdn2(
 
     tensors = (q, k, v, g, b, w, initial_state)
 
+    if (not is_inference) and torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
+        # training op (gdn2.py:2244-2286): differentiable through dn_prefill_bwd_raw
+        out, fin = _TrainFn.apply(q, k, v_in, g_t, b_t, w_t, init, (args, seg_t, init_seg))
+        o = out if out.dtype == out_dtype else out.to(out_dtype)
+        return (o, fin) if output_final_state else o
+
     def run():
         Lp = ((L + _CHUNK - 1) // _CHUNK) * _CHUNK
         if is_inference and streaming_prefill and Lp > prefill_block_size:
@@ -329,163 +330,66 @@ def chunk_gdn2(
 
 
 # ---------------------------------------------------------------------------
-# training path: autograd around the HIP backward
+# training path: autograd around the HIP forward and backward
 # ---------------------------------------------------------------------------
 
-def _gate_to_heads(t, B, L, Hk, Hv, last):
-    """(B,L,H) / (B,L,H,1|last) with H in {1, Hk, Hv} -> (B,L,Hv,last), value
-    head j reading gate head j // (Hv // Hk) (gdn2.py:1992-2031)."""
-    if t.ndim == 3:
-        t = t.unsqueeze(-1)
-    if t.shape[2] == Hk and Hv != Hk:
-        t = torch.repeat_interleave(t, Hv // Hk, dim=2)
-    return t.expand(B, L, Hv, last)
-
-
-def _canonical_segments(seg_t, B, L, has_init, init_seg_id, dev):
-    """Canonical ids (gdn2.py:2081-2094) as int32 (B, L): nondecreasing, with
-    id 0 meaning "continues the initial state"."""
-    if seg_t is None:
-        return None
-    s = seg_t.to(torch.int64)
-    if s.ndim == 1:
-        s = s.unsqueeze(0).expand(B, L)
-    first = torch.zeros((B,), dtype=torch.int64, device=dev)
-    if has_init and init_seg_id is not None:
-        i0 = torch.as_tensor(init_seg_id, dtype=torch.int64, device=dev).reshape(-1)
-        first = (s[:, 0] != torch.broadcast_to(i0, (B,))).to(torch.int64)
-    ch = torch.cumsum((s[:, 1:] != s[:, :-1]).to(torch.int64), dim=1)
-    canon = torch.cat([torch.zeros((B, 1), dtype=torch.int64, device=dev), ch], dim=1) + first[:, None]
-    return canon.to(torch.int32).contiguous()
-
-
-def _sum_to(grad, shape):
-    """Sum a (B, L, Hv, C) gradient back to a (B, L, H, c) input that was
-    broadcast to it (H in {1, Hk, Hv} with value head j reading head j // G;
-    c in {1, C})."""
-    B, L, Hv, C = grad.shape
-    H, c = shape[2], shape[3]
-    if H != Hv:
-        grad = grad.view(B, L, H, Hv // H, C).sum(3) if H > 1 else grad.sum(2, keepdim=True)
-    if c != C:
-        grad = grad.sum(3, keepdim=True)
-    return grad
-
-
-class _RecurrenceFn(torch.autograd.Function):
-    """The chunked recurrence on prepared inputs: q, k at key heads, gates in
-    their own (B, L, H, C) layouts, all already activated / normalised.
-
-    Forward: ``dn_prefill_fwd`` (the inference kernels, GQA and gate broadcast
-    read in place).  Backward: ``dn_prefill_bwd`` (reference custom VJP,
-    gdn2.py:1446-1769) on float32 copies expanded to value heads; the
-    gradients are summed back to each input's layout.
-    """
+class _TrainFn(torch.autograd.Function):
+    """chunk_gdn2 with is_inference=False (reference custom VJP,
+    gdn2.py:1446-1769).  Forward: ``dn_prefill_fwd`` on the raw inputs (the
+    wrapper steps run inside the kernels, as in inference).  Backward:
+    ``dn_prefill_bwd_raw`` on the same argument block, which also
+    differentiates the wrapper steps (prologue, L2-norm, gate broadcast, GQA)."""
 
     @staticmethod
-    def forward(ctx, qh, kh, v, ga, ba, wa, init, meta):
-        seg_t, init_seg_id, canon, precision = meta
-        with torch.no_grad():
-            out, fin = chunk_gdn2(
-                qh, kh, v, ga, ba, wa, segment_ids=seg_t, initial_state=init,
-                initial_state_segment_id=init_seg_id, output_final_state=True, precision=precision,
-                scale=1.0, is_inference=True)
-        ctx.save_for_backward(qh, kh, v, ga, ba, wa, init)
-        ctx.canon = canon
-        ctx.has_init = init is not None
+    def _args(proto, q, k, v, g, b, w, init):
+        a = _lib.PrefillArgs.from_buffer_copy(proto)
+        a.q, a.k, a.v, a.g, a.b, a.w = (_ptr(x) for x in (q, k, v, g, b, w))
+        a.init_state = _ptr(init)
+        a.t0, a.nt = 0, a.L
+        return a
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, b, w, init, meta):
+        proto, seg_t, init_seg = meta
+        dev = q.device
+        a = _TrainFn._args(proto, q, k, v, g, b, w, init)
+        a.init_seg = _ptr(init_seg)
+        out = torch.empty((a.B, a.L, a.Hv, a.V), dtype=v.dtype, device=dev)
+        fin = torch.empty((a.B, a.Hv, a.K, a.V), dtype=torch.float32, device=dev)
+        a.out, a.final_state = _ptr(out), _ptr(fin)
+        lib = _lib.load_library()
+        nbytes = lib.dn_prefill_workspace_size(ctypes.byref(a))
+        if nbytes == 0:
+            _lib.check(-1, "dn_prefill_workspace_size")
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        _lib.check(lib.dn_prefill_fwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_fwd")
+        ctx.save_for_backward(q, k, v, g, b, w, init)
+        ctx.meta = meta
         return out, fin
 
     @staticmethod
     def backward(ctx, d_out, d_fin):
-        qh, kh, v, ga, ba, wa, init = ctx.saved_tensors
-        B, L, Hk, K = qh.shape
-        H, V = v.shape[2], v.shape[3]
-        G = H // Hk
-        dev = qh.device
-        with torch.no_grad():
-            f32 = lambda t: t.to(torch.float32)
-            qe = torch.repeat_interleave(f32(qh), G, dim=2).contiguous() if G > 1 else f32(qh).contiguous()
-            ke = torch.repeat_interleave(f32(kh), G, dim=2).contiguous() if G > 1 else f32(kh).contiguous()
-            ge = _gate_to_heads(f32(ga), B, L, Hk, H, K).contiguous()
-            be = _gate_to_heads(f32(ba), B, L, Hk, H, K).contiguous()
-            we = _gate_to_heads(f32(wa), B, L, Hk, H, V).contiguous()
-            ve = f32(v).contiguous()
-            d_out = torch.zeros_like(ve) if d_out is None else d_out.to(torch.float32).contiguous()
-            d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
-            grads = [torch.empty_like(x) for x in (qe, ke, ve, ge, be, we)]
-            d_init = torch.empty_like(init) if ctx.has_init else None
-            a = _lib.BackwardArgs()
-            a.abi_version = _lib.DN_ABI_VERSION
-            a.B, a.L, a.H, a.K, a.V = B, L, H, K, V
-            a.q, a.k, a.v, a.g, a.b, a.w = (_ptr(x) for x in (qe, ke, ve, ge, be, we))
-            a.seg = _ptr(ctx.canon)
-            a.init_state = _ptr(init)
-            a.d_out, a.d_final = _ptr(d_out), _ptr(d_fin)
-            a.dq, a.dk, a.dv, a.dg, a.db, a.dw = (_ptr(x) for x in grads)
-            a.d_init = _ptr(d_init)
-            lib = _lib.load_library()
-            nbytes = lib.dn_prefill_bwd_workspace_size(ctypes.byref(a))
-            if nbytes == 0:
-                _lib.check(-1, "dn_prefill_bwd_workspace_size")
-            ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
-            _lib.check(lib.dn_prefill_bwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_bwd")
-            dq, dk, dv, dg, db, dw = grads
-            if G > 1:
-                dq = dq.view(B, L, Hk, G, K).sum(3)
-                dk = dk.view(B, L, Hk, G, K).sum(3)
-            out = (dq.to(qh.dtype), dk.to(kh.dtype), dv.to(v.dtype), _sum_to(dg, ga.shape).to(ga.dtype),
-                   _sum_to(db, ba.shape).to(ba.dtype), _sum_to(dw, wa.shape).to(wa.dtype))
-        return (*out, d_init, None)
-
-
-def _chunk_gdn2_train(q, k, v, g, b, w, seg_t, initial_state, init_seg_id, output_final_state,
-                      precision, scale, qk_l2norm, fuse_prologue, stability_guard):
-    """Training-mode chunk_gdn2 (is_inference=False, gdn2.py:2244-2286).
-
-    The wrapper's elementwise steps (gdn2.py:1970-2125) run as differentiable
-    torch ops, so autograd carries their derivatives; the recurrence itself is
-    ``_RecurrenceFn``, whose forward reads q / k at key heads and the gates in
-    their own layouts like the inference path.
-    """
-    B, L, Hk, K = q.shape
-    Hv, V = v.shape[2], v.shape[3]
-    dev = q.device
-    qf, kf = q.to(torch.float32), k.to(torch.float32)
-
-    def l2(x):
-        return x * torch.rsqrt(torch.sum(x * x, dim=-1, keepdim=True) + 1e-6)
-
-    four = lambda t: t.unsqueeze(-1) if t.ndim == 3 else t
-    if fuse_prologue:
-        qh, kh = l2(qf) * scale, l2(kf)
-        ga = -torch.exp(torch.clamp(four(g).to(torch.float32), max=5.0))
-        if stability_guard:
-            ga = torch.clamp(ga, max=-1e-6)
-        ba, wa = torch.sigmoid(four(b).to(torch.float32)), torch.sigmoid(four(w).to(torch.float32))
-    else:
-        gf = four(g).to(torch.float32)
-        # gdn2.py:38-62: min(g, 0) with the gradient passed wherever g <= 0
-        ga = torch.where(gf <= 0.0, gf, torch.zeros_like(gf))
-        ba, wa = four(b).to(torch.float32), four(w).to(torch.float32)
-        if stability_guard:
-            ba = torch.clamp(ba, min=0.0)
-            ga = torch.clamp(ga, max=-1e-6)
-        if qk_l2norm:
-            qh, kh = l2(qf) * scale, l2(kf)
-        else:
-            qh, kh = qf * scale, kf
-        # gdn2.py:2113-2122: normalised q / k are stored back in the input dtype
-        if q.dtype in (torch.bfloat16, torch.float16):
-            qh, kh = qh.to(q.dtype), kh.to(k.dtype)
-    qh, kh, ga, ba, wa = (x.contiguous() for x in (qh, kh, ga, ba, wa))
-    vv = v if v.dtype in (torch.float32, torch.bfloat16) else v.to(torch.float32)
-    init = initial_state.to(torch.float32).contiguous() if initial_state is not None else None
-    canon = _canonical_segments(seg_t, B, L, initial_state is not None, init_seg_id, dev)
-    out, fin = _RecurrenceFn.apply(qh, kh, vv.contiguous(), ga, ba, wa, init, (seg_t, init_seg_id, canon, precision))
-    out = out.to(v.dtype)
-    if output_final_state:
-        return out, fin
-    return out
+        q, k, v, g, b, w, init = ctx.saved_tensors
+        proto, seg_t, init_seg = ctx.meta
+        dev = q.device
+        a = _TrainFn._args(proto, q, k, v, g, b, w, init)
+        a.init_seg = _ptr(init_seg)
+        f32 = lambda t: torch.empty(t.shape, dtype=torch.float32, device=dev)
+        dq, dk, dv, dg, db, dw = (f32(x) for x in (q, k, v, g, b, w))
+        d_init = f32(init) if init is not None else None
+        d_out = torch.zeros(v.shape, dtype=torch.float32, device=dev) if d_out is None \
+            else d_out.to(torch.float32).contiguous()
+        d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
+        lib = _lib.load_library()
+        nbytes = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(a))
+        if nbytes == 0:
+            _lib.check(-1, "dn_prefill_bwd_raw_workspace_size")
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        _lib.check(lib.dn_prefill_bwd_raw(ctypes.byref(a), _ptr(d_out), _ptr(d_fin), _ptr(dq), _ptr(dk), _ptr(dv),
+                                          _ptr(dg), _ptr(db), _ptr(dw), _ptr(d_init), _ptr(ws), nbytes,
+                                          _stream(dev)), "dn_prefill_bwd_raw")
+        cast = lambda d, x: d if d.dtype == x.dtype else d.to(x.dtype)
+        return (cast(dq, q), cast(dk, k), cast(dv, v), dg, db, dw, d_init, None)
 
 
 def _decode_gate(t, B, Hk, Hv, last, name):

@@ -163,6 +163,24 @@ size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
  * sum(out * d_out) + sum(final * d_final) are written (not accumulated). */
 int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes dn_prefill_bwd_raw needs (0 if the arguments are invalid):
+ * dn_prefill_bwd_workspace_size at H = Hv plus eleven (B,L,Hv,128) f32 arrays. */
+size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
+
+/* Backward of the whole training op from the forward's own arguments: the
+ * custom VJP of gdn2.py:1446-1769 together with the wrapper steps it sits
+ * behind (gdn2.py:1970-2125: nonpositive clamp with its pass-through gradient,
+ * guard clamps, fused prologue, q/k L2-norm and scale with the cast back to the
+ * input dtype, gate broadcast, GQA head mapping, segment canonicalisation).
+ * `a` is the dn_prefill_fwd argument block of the forward call (t0 = 0,
+ * nt = L; out / final_state are not read).  d_out (B,L,Hv,V) f32, d_final NULL
+ * or (B,Hv,K,V) f32.  Gradients are written as f32 in the raw layouts: dq, dk
+ * (B,L,Hk,K); dv (B,L,Hv,V); dg, db, dw (B,L,H,C) of their gate; d_init NULL or
+ * (B,Hv,K,V). */
+int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
+                       void* dq, void* dk, void* dv, void* dg, void* db, void* dw, void* d_init,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* In-place Frobenius cap S <- S * min(1, tau / sqrt(||S||_F^2 + 1e-6)) of
  * `nmat` consecutive (rows x cols) float32 matrices (the stability_guard cap of
  * gdn2.py:2180-2188 / 2224-2226 / 2236-2238). */

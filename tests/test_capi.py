@@ -104,3 +104,20 @@ def test_invalid_args_rejected_without_gpu():
     assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -2
     bw.d_init = 0x1000
     assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -1 and b"init_state" in lib.dn_last_error()
+    # raw-input backward: same argument block as the forward
+    ra = _lib.PrefillArgs()
+    ra.abi_version = _lib.DN_ABI_VERSION
+    ra.B, ra.L, ra.Hk, ra.Hv, ra.K, ra.V = 1, 128, 2, 4, 128, 128
+    assert lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra)) == 0       # no tensors
+    for f in ("q", "k", "v", "g", "b", "w"):
+        setattr(ra, f, 0x1000)
+    ra.g_heads, ra.g_chans, ra.b_heads, ra.b_chans, ra.w_heads, ra.w_chans = 2, 128, 2, 128, 4, 128
+    ra.qk_dtype, ra.v_dtype = _lib.DN_BF16, _lib.DN_BF16
+    need = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
+    core = 4 * 2 * 4 * (7 * 64 * 128 + 4 * 64 * 64 + 128 + 4 * 128 * 128)
+    assert need == 512 + 11 * 1 * 128 * 4 * 128 * 4 + core
+    fake = [0x1000] * 7
+    assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -2
+    ra.g_heads = 3
+    assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -1
+    assert b"gate heads" in lib.dn_last_error()
