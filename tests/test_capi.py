@@ -116,7 +116,7 @@ def test_invalid_args_rejected_without_gpu():
     need = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
     core = 4 * 2 * 4 * (7 * 64 * 128 + 4 * 64 * 64 + 128 + 4 * 128 * 128)
     assert need == 512 + 11 * 1 * 128 * 4 * 128 * 4 + core
-    fake = [0x1000] * 7
+    fake = [0x1000] * 6 + [None]   # dq dk dv dg db dw, no d_init
     assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -2
     ra.g_heads = 3
     assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -1
