@@ -114,20 +114,22 @@ def token_serial_vjp(qh, kh, v, g, b, w, seg, init_state, prev_seg, dout, dfinal
 def torch_token_serial(qh, kh, v, g, b, w, seg, init_state, prev_seg):
     """The token-serial forward (reference.py:123-161) in torch, for autograd.
 
-    Tensors are float64 torch tensors (qh/kh at key heads, gates at value heads);
-    returns (out (B, L, Hv, V), final state (B, Hv, K, V)).
+    Tensors are torch tensors of one dtype and device (float64 on the CPU for
+    pinning; float32 on a GPU for full-size references), qh/kh at key heads,
+    gates at value heads; returns (out (B, L, Hv, V), final state (B, Hv, K, V)).
     """
     import torch
     B, L, Hk, K = qh.shape
     Hv, V = v.shape[2], v.shape[3]
     G = Hv // Hk
-    idx = torch.arange(Hv) // G
-    S = torch.zeros((B, Hv, K, V), dtype=torch.float64) if init_state is None else init_state
-    prev = torch.as_tensor(np.full((B,), -1) if prev_seg is None else np.asarray(prev_seg)).long()
-    seg_t = torch.as_tensor(np.asarray(seg)).long()
+    dev, dt = qh.device, qh.dtype
+    idx = torch.arange(Hv, device=dev) // G
+    S = torch.zeros((B, Hv, K, V), dtype=dt, device=dev) if init_state is None else init_state
+    prev = torch.as_tensor(np.full((B,), -1) if prev_seg is None else np.asarray(prev_seg)).long().to(dev)
+    seg_t = torch.as_tensor(np.asarray(seg)).long().to(dev)
     outs = []
     for t in range(L):
-        keep = (seg_t[:, t] == prev).to(torch.float64)[:, None, None, None]
+        keep = (seg_t[:, t] == prev).to(dt)[:, None, None, None]
         S = S * keep
         prev = seg_t[:, t]
         qt = qh[:, t][:, idx]; kt = kh[:, t][:, idx]
