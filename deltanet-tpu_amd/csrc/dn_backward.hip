@@ -127,7 +127,10 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   __shared__ float sM[BC][CP];
   __shared__ float sW[BC][KP];    // b * k of the chunk, then W
   __shared__ float sQ[BC][KP];    // q of the chunk
+  __shared__ float sTot[4][KD];   // per-quarter decay totals of the scan
+  __shared__ float sX[16][17];    // one 16 x 16 block in transit (T substitution)
   __shared__ int sseg[BC], scar[BC], slast[BC];
+  __shared__ int sSafe[NWV];
 
   const int u = blockIdx.x;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
@@ -140,44 +143,94 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     (&sA[0][0])[i] = 0.f;
     (&sM[0][0])[i] = 0.f;
   }
-  // stage q and beta = b k (rows past the sequence end are zero)
+  // stage q, beta = b k and the log2-decay (rows past the sequence end are
+  // zero); k stays in registers for Kc
+  constexpr int SIT = BC * KD / 4 / NT;
+  float4 kst[SIT];
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+  for (int it = 0; it < SIT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    float4 qv = zero_f4(), bv = zero_f4();
+    float4 qv = zero_f4(), bv = zero_f4(), gv = zero_f4(), k4 = zero_f4();
     if (t0 + i < p.L) {
       const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
       qv = ld4g(p.q + ro);
-      const float4 b4 = ld4g(p.b + ro), k4 = ld4g(p.k + ro);
+      const float4 b4 = ld4g(p.b + ro);
+      k4 = ld4g(p.k + ro);
+      gv = ld4g(p.g + ro);
       bv = make_float4(b4.x * k4.x, b4.y * k4.y, b4.z * k4.z, b4.w * k4.w);
     }
+    kst[it] = k4;
     *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qv;
     *reinterpret_cast<float4*>(&sW[i][4 * c4]) = bv;
+    *reinterpret_cast<float4*>(&sG[i][4 * c4]) =
+        make_float4(gv.x * kLog2e, gv.y * kLog2e, gv.z * kLog2e, gv.w * kLog2e);
   }
-  // ---- cumulative decay (log2 units), per channel -------------------------
-  if (tid < KD) {
-    float gv[BC];
-#pragma unroll
-    for (int t = 0; t < BC; ++t) gv[t] = t0 + t < p.L ? p.g[row_of(p, bb, t0 + t, h) + tid] : 0.f;
+  lds_barrier();
+  // ---- cumulative decay (log2 units): channel tid % 128, quarter tid / 128 --
+  {
+    const int ch = tid & (KD - 1), qt = tid >> 7;
+    float part[BC / 4];
     float acc = 0.f;
 #pragma unroll
-    for (int t = 0; t < BC; ++t) {
-      acc += gv[t] * kLog2e;
-      sG[t][tid] = acc;
-      G[t * KD + tid] = acc;
+    for (int t = 0; t < BC / 4; ++t) {
+      acc += sG[16 * qt + t][ch];
+      part[t] = acc;
     }
-    p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(acc) : 0.f;
+    sTot[qt][ch] = acc;
+    lds_barrier();
+    float off = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < 3; ++s2)
+      if (s2 < qt) off += sTot[s2][ch];
+#pragma unroll
+    for (int t = 0; t < BC / 4; ++t) sG[16 * qt + t][ch] = part[t] + off;
+  }
+  lds_barrier();
+  // G (coalesced), lam, Kc / Kc^T from the staged k, and per 16-token block
+  // whether its decay span allows the factored (MFMA) diagonal tiles
+  {
+    float* Kc = p.Kc + (int64_t)u * CK;
+    float* KcT = p.KcT + (int64_t)u * CK;
+#pragma unroll
+    for (int it = 0; it < SIT; ++it) {
+      const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+      const float4 gi = *reinterpret_cast<const float4*>(&sG[i][4 * c4]);
+      const float4 gl = *reinterpret_cast<const float4*>(&sG[BC - 1][4 * c4]);
+      *reinterpret_cast<float4*>(G + i * KD + 4 * c4) = gi;
+      const bool ok = slast[i] && t0 + i < p.L;
+      const float4 k4 = kst[it];
+      const float4 kc = ok ? make_float4(k4.x * ex2(gl.x - gi.x), k4.y * ex2(gl.y - gi.y),
+                                         k4.z * ex2(gl.z - gi.z), k4.w * ex2(gl.w - gi.w))
+                           : zero_f4();
+      *reinterpret_cast<float4*>(Kc + i * KD + 4 * c4) = kc;
+      KcT[(4 * c4 + 0) * BC + i] = kc.x;
+      KcT[(4 * c4 + 1) * BC + i] = kc.y;
+      KcT[(4 * c4 + 2) * BC + i] = kc.z;
+      KcT[(4 * c4 + 3) * BC + i] = kc.w;
+    }
+    if (tid < KD) p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(sG[BC - 1][tid]) : 0.f;
+    // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128
+    const int ch = tid & (KD - 1), blk = tid >> 7;
+    const float span = sG[16 * blk][ch] - sG[16 * blk + 15][ch];
+    const bool safe = __all(span <= 64.f);
+    if (l == 0) sSafe[wv] = safe;
   }
   lds_barrier();
 
   // ---- A (strict) and M (with diagonal), 16x16 tiles of the lower triangle --
+  // A pair (i, j) with j <= m <= i is formed as (x_i e^{G_i - G_m}) (k_j e^{G_m - G_j}),
+  // m = the first row of i's block.  Off the diagonal both factors are <= 1;
+  // on the diagonal the column factor is >= 1, which is used only where the
+  // block's decay span keeps it below 2^64 -- otherwise every element takes
+  // e^{G_i - G_j} directly.
   for (int task = wv; task < 20; task += NWV) {
     const bool isM = task >= 10;
     const int tt = task % 10;
     const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
     const int J = tt - I * (I + 1) / 2;
+    const bool diag = J == I;
     float res[4];
-    if (J < I) {
+    if (!diag || (sSafe[2 * I] & sSafe[2 * I + 1])) {
       const int m = 16 * I;
       const int i = 16 * I + l16, j = 16 * J + l16;
       const bool vi = t0 + i < p.L, vj = t0 + j < p.L;
@@ -195,14 +248,15 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           xa[e] = vi ? xa[e] * ex2(gi[e] - gm[e]) : 0.f;
-          xb[e] = vj ? xb[e] * ex2(gm[e] - gj[e]) : 0.f;
+          const float fb = diag ? __builtin_amdgcn_exp2f(gm[e] - gj[e]) : ex2(gm[e] - gj[e]);
+          xb[e] = vj ? xb[e] * fb : 0.f;
         }
         mma(acc, fr8(xa), fr8(xb));
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) res[e] = acc[e];
     } else {
-      // diagonal block: e^{G_i - G_j} per element
+      // diagonal block with a large decay span: e^{G_i - G_j} per element
       const int j = 16 * I + l16;
       const bool vj = t0 + j < p.L;
       const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
@@ -229,47 +283,77 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       (isM ? sM : sA)[i][j] = ok ? res[e] : 0.f;
     }
   }
+  // w and v of this lane's W / U0 operands, loaded now and used after T
+  static_assert(TPW == 1, "one 16-column tile per wave");
+  float wvw[2][8], wvv[2][8];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = 32 * s + pi_k(q, e), r = 16 * wv + l16;
+      const bool vj = t0 + j < p.L;
+      const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
+      wvw[s][e] = vj ? p.w[ro] : 0.f;
+      wvv[s][e] = vj ? p.v[ro] : 0.f;
+    }
   lds_barrier();
 
-  // ---- T = (I + A)^-1 by forward substitution (wave 0, lane = column) -----
+  // ---- T = (I + A)^-1, blocked, by wave 0 ----------------------------------
+  // The four 16x16 diagonal blocks D_I = (I + A_II)^-1 by forward substitution
+  // (lane = block I, column c); then block rows I = 1..3 in order,
+  // T_IJ = -D_I sum_{K=J}^{I-1} A_IK T_KJ on v_mfma_f32_16x16x4f32.  Each T
+  // block overwrites the A block it replaces once no later product needs it.
   if (wv == 0) {
-    // four partial sums (j mod 4) keep the dependent FMA chain of row i at i/4
-    float Tc[BC];
+    {
+      const int I = l >> 4, cc = l & 15;
+      float t[16];
 #pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      float t[4] = {(i == l) ? 1.f : 0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 16; ++r) {
+        float acc = r == cc ? 1.f : 0.f;
 #pragma unroll
-      for (int j4 = 0; j4 < (i + 3) / 4; ++j4) {
-        const float4 a = *reinterpret_cast<const float4*>(&sA[i][4 * j4]);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          if (4 * j4 + jj < i) t[jj] -= f4at(a, jj) * Tc[4 * j4 + jj];
-        }
+        for (int s2 = 0; s2 < r; ++s2) acc -= sA[16 * I + r][16 * I + s2] * t[s2];
+        t[r] = acc;
       }
-      Tc[i] = (t[0] + t[1]) + (t[2] + t[3]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sA[16 * I + r][16 * I + cc] = t[r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int I = 1; I < 4; ++I) {
+#pragma unroll
+      for (int J = 0; J < I; ++J) {
+        f32x4 x = zero4();
+#pragma unroll
+        for (int K = J; K < I; ++K)
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(sA[16 * I + l16][16 * K + 4 * kk + q],
+                                                      sA[16 * K + 4 * kk + q][16 * J + l16], x, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sX[4 * q + e][l16] = x[e];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        f32x4 y = zero4();
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          y = __builtin_amdgcn_mfma_f32_16x16x4f32(sA[16 * I + l16][16 * I + 4 * kk + q], sX[4 * kk + q][l16], y,
+                                                    0, 0, 0);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sA[16 * I + 4 * q + e][16 * J + l16] = -y[e];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
     }
     float* TT = p.TT + (int64_t)u * CC + l * BC;
 #pragma unroll
-    for (int i = 0; i < BC; ++i) sA[i][l] = Tc[i];
-#pragma unroll
     for (int i4 = 0; i4 < BC / 4; ++i4)
-      *reinterpret_cast<float4*>(TT + 4 * i4) = make_float4(Tc[4 * i4], Tc[4 * i4 + 1], Tc[4 * i4 + 2], Tc[4 * i4 + 3]);
+      *reinterpret_cast<float4*>(TT + 4 * i4) =
+          make_float4(sA[4 * i4][l], sA[4 * i4 + 1][l], sA[4 * i4 + 2][l], sA[4 * i4 + 3][l]);
   } else {
     const int t2 = tid - 64;
     float* MT = p.MT + (int64_t)u * CC;
     for (int idx = t2; idx < CC; idx += NT - 64) {
       const int j = idx / BC, i = idx % BC;
       MT[idx] = sM[i][j];
-    }
-    float* Kc = p.Kc + (int64_t)u * CK;
-    float* KcT = p.KcT + (int64_t)u * CK;
-#pragma unroll 8
-    for (int idx = t2; idx < CK; idx += NT - 64) {
-      const int j = idx / KD, r = idx % KD;
-      const bool ok = slast[j] && t0 + j < p.L;
-      const float kc = ok ? p.k[row_of(p, bb, t0 + j, h) + r] * ex2(sG[BC - 1][r] - sG[j][r]) : 0.f;
-      Kc[idx] = kc;
-      KcT[r * BC + j] = kc;
     }
   }
   lds_barrier();
@@ -300,10 +384,8 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int j = 32 * s + pi_k(q, e);
-          const bool vj = t0 + j < p.L;
-          const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
           xb[e] = scar[j] ? sW[j][r] * ex2(sG[j][r]) : 0.f;
-          xu[e] = vj ? p.w[ro] * p.v[ro] : 0.f;
+          xu[e] = wvw[s][e] * wvv[s][e];
         }
         const Frag<false> fb = fr8(xb), fu = fr8(xu);
 #pragma unroll

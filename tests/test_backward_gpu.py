@@ -120,6 +120,26 @@ def test_backward_strong_decay(precision):
     compare(got, ref, 1e-3 if precision == "fp32" else 1e-2, f"strong decay {precision}")
 
 
+
+def test_backward_mixed_decay_spans():
+    """16-token blocks whose decay span is below 2^64 in every channel form
+    their diagonal A / M tiles as factored MFMA products, the others
+    element by element; here both kinds share chunks and channels (per-token
+    log-decay -0.05, -2.7 -- a span of about 2^58 -- and -6 in half of the
+    channels of some blocks)."""
+    B, L, Hk, Hv = 1, 256, 2, 4
+    q, k, v, _, b, w = ref_inputs(601, B, L, Hk, Hv)
+    rng = np.random.default_rng(602)
+    blk = (np.arange(L) // 16) % 4
+    per_tok = np.choose(blk, [-0.05, -2.7, -0.5, -0.05])[None, :, None, None] * np.ones((B, L, Hk, 128))
+    strong = (blk == 3)[None, :, None, None] & (np.arange(128) % 2 == 0)[None, None, None, :]
+    g = np.where(strong, -6.0, per_tok) * (1.0 + 0.01 * np.abs(rng.standard_normal((B, L, Hk, 128))))
+    do = rng.standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision="fp32")
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+    compare(got, ref, 1e-5, "mixed decay spans fp32")
+
+
 def test_backward_positive_decay_and_guard():
     """Positive g is clamped (zero gradient, test_strong_decay.py:72-89);
     stability_guard clamps b >= 0 and g <= -1e-6 (gdn2.py:1972-1974)."""
