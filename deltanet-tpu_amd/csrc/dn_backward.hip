@@ -854,7 +854,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 //             left out: they cancel), db = k dbeta, dk += b dbeta,
 //   dg_t    = sum_{i>=t} dG_i + sum_{j<t} k_j dk_j^(Kc) + lam rowsum(S0 * dSC)
 // Off-diagonal 16-row blocks use e^{G_i-G_m} e^{G_m-G_j} (both <= 1) through
-// MFMA; pairs inside a block use e^{G_i-G_j} per element.
+// MFMA; pairs inside a block join those products where the block's decay
+// span allows, else use e^{G_i-G_j} per element.
 // Wave w owns the 16 channels 16 (w % 4) .. and the 16-row blocks
 // 2 (w / 4), 2 (w / 4) + 1; lanes hold rows 4q..4q+3 of each block.
 // ---------------------------------------------------------------------------
@@ -935,23 +936,33 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
 #pragma unroll
   for (int Ib = 0; Ib < NB; ++Ib) {
     const int I = I0 + Ib;
-    // off-diagonal blocks: rows i of block I against columns j < 16 I
+    // rows i of block I against columns j < 16 I (and, for dk, rows j of the
+    // block against i > 16 I + 15) through MFMA.  Where the block's decay span
+    // stays below 2^64 in this wave's channels, the pairs inside the block
+    // join the same products: their column factor e^{G_m - G_j} (dq, dbeta)
+    // or row factor e^{G_i - G_m2} (dk) is then >= 1 and bounded.  The pair
+    // (i, i) is left out of dq and dk (its factor is e^0).
     f32x4 oq = zero4(), ob = zero4(), ok_ = zero4();
     const int m = 16 * I, m2 = 16 * I + 15;
     const float gm = sG[m][rl], gm2 = sG[m2][rl];
+    const bool inblk = __all(gm - gm2 <= 64.f);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float xm[8], xa[8], xk[8], ym[8], ya[8], yq[8], yb[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int j = 32 * s + pi_k(q, e);
-        const bool lo = j < m, hi = j > m2;
-        xm[e] = lo ? sdM[16 * I + l16][j] : 0.f;
+        const bool in = inblk && j >= m && j <= m2;
+        const bool lo = j < m || in, hi = j > m2 || in;
+        const bool self = j == 16 * I + l16;
+        const float gj = sG[j][rl];
+        xm[e] = lo && !self ? sdM[16 * I + l16][j] : 0.f;
         xa[e] = lo ? sdA[16 * I + l16][j] : 0.f;
-        xk[e] = lo ? sK[j][rl] * ex2(gm - sG[j][rl]) : 0.f;
-        ym[e] = hi ? sdM[j][16 * I + l16] : 0.f;
+        const float fk = in ? __builtin_amdgcn_exp2f(gm - gj) : ex2(gm - gj);
+        xk[e] = lo ? sK[j][rl] * fk : 0.f;
+        ym[e] = hi && !self ? sdM[j][16 * I + l16] : 0.f;
         ya[e] = hi ? sdA[j][16 * I + l16] : 0.f;
-        const float f = hi ? ex2(sG[j][rl] - gm2) : 0.f;
+        const float f = hi ? (in ? __builtin_amdgcn_exp2f(gj - gm2) : ex2(gj - gm2)) : 0.f;
         yq[e] = sQ[j][rl] * f;
         yb[e] = sB[j][rl] * sK[j][rl] * f;
       }
@@ -961,43 +972,38 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
       mma(ok_, fr8(ym), fr8(yq));
       mma(ok_, fr8(ya), fr8(yb));
     }
-    // pairs inside block I, and the epilogue
-    float kb[16], qb[16], betab[16], gb[16];
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int j = 16 * I + jj;
-      kb[jj] = sK[j][rl];
-      qb[jj] = sQ[j][rl];
-      betab[jj] = sB[j][rl] * kb[jj];
-      gb[jj] = sG[j][rl];
-    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int ii = 4 * q + e;
       const int i = 16 * I + ii;
       const float gi = sG[i][rl];
       float dq = 0.f, dbeta = 0.f, dk = 0.f;
+      if (!inblk) {
+        // pairs inside block I, e^{G_i - G_j} per element
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const float off = jj == ii ? 0.f : 1.f;
-        const float fij = ex2(gi - gb[jj]);
-        dq += off * sdM[i][16 * I + jj] * fij * kb[jj];
-        dbeta += sdA[i][16 * I + jj] * fij * kb[jj];
-        const float fji = ex2(gb[jj] - gi);
-        dk += off * sdM[16 * I + jj][i] * fji * qb[jj] + sdA[16 * I + jj][i] * fji * betab[jj];
+        for (int jj = 0; jj < 16; ++jj) {
+          const int j = 16 * I + jj;
+          const float kj = sK[j][rl], gj = sG[j][rl];
+          const float off = jj == ii ? 0.f : 1.f;
+          const float fij = ex2(gi - gj);
+          dq += off * sdM[i][j] * fij * kj;
+          dbeta += sdA[i][j] * fij * kj;
+          const float fji = ex2(gj - gi);
+          dk += off * sdM[j][i] * fji * sQ[j][rl] + sdA[j][i] * fji * (sB[j][rl] * kj);
+        }
       }
       const float eg = scar[i] ? ex2(gi) : 0.f;
       dq += eg * rq[Ib][e] + oq[e] * ex2(gi - gm);
       dbeta += -eg * rb[Ib][e] + ob[e] * ex2(gi - gm);
       dk += ok_[e] * ex2(gm2 - gi);
       const float dkc = slast[i] ? ex2(glast - gi) * rk[Ib][e] : 0.f;
-      const float kv = kb[ii], bv = sB[i][rl], dmii = sdM[i][i];
-      sdG[i][rl] = qb[ii] * dq + bv * kv * dbeta - kv * dk;
+      const float kv = sK[i][rl], qv = sQ[i][rl], bv = sB[i][rl], dmii = sdM[i][i];
+      sdG[i][rl] = qv * dq + bv * kv * dbeta - kv * dk;
       sP[i][rl] = kv * dkc;
       if (t0 + i < p.L) {
         const int64_t ro = row_of(p, bb, t0 + i, h) + r;
         p.dq[ro] = dq + dmii * kv;
-        p.dk[ro] = dk + dmii * qb[ii] + dkc + bv * dbeta;
+        p.dk[ro] = dk + dmii * qv + dkc + bv * dbeta;
         p.db[ro] = kv * dbeta;
       }
     }
