@@ -662,24 +662,6 @@ __device__ __forceinline__ void store_raw(const BW& p, float* out, int bb, int h
       }
 }
 
-// acc[I][R2] += X[rows 16I..][:] * Y[cols 32w + 16 R2 ..][:]^T over 128 (X rows
-// at stride xs, in LDS or global; Y rows at stride ys, global)
-__device__ __forceinline__ void nt_128(f32x4 (&acc)[4][TPW], const float* X, int xs, const float* Y, int ys,
-                                       int wv, int q, int l16) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    Frag<false> a[4], bfr[TPW];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) { float x[8]; row8(X + (16 * I + l16) * xs, s, q, x); a[I] = fr8(x); }
-#pragma unroll
-    for (int R2 = 0; R2 < TPW; ++R2) { float x[8]; row8(Y + (16 * (TPW * wv + R2) + l16) * ys, s, q, x); bfr[R2] = fr8(x); }
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
-  }
-}
-
 __device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][TPW]) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
@@ -687,135 +669,172 @@ __device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][TPW]) {
     for (int R2 = 0; R2 < TPW; ++R2) acc[I][R2] = zero4();
 }
 
+// this lane's rows of a product's right operand (Y rows 16 w + l16, all 128
+// columns), loaded ahead of the product
+__device__ __forceinline__ void load_y(float (&y)[4][8], const float* Y, int wv, int q, int l16) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) row8(Y + (16 * wv + l16) * KD, s, q, y[s]);
+}
+
+// acc[I] += X[rows 16I..][:] * Y^T with X in LDS (row pitch KP) and Y preloaded
+__device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, const float (&y)[4][8], int q,
+                                       int l16) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const Frag<false> b = fr8(y[s]);
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      float x[8];
+      row8(X + (16 * I + l16) * KP, s, q, x);
+      mma(acc[I][0], fr8(x), b);
+    }
+  }
+}
+
+// Every operand that comes from global memory is loaded one phase ahead of
+// its product (state rows into registers; W, Kc and M^T staged in LDS), so
+// each phase waits on at most the loads issued a phase earlier.
 __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   __shared__ float sdO[BC][KP];
   __shared__ float sX[BC][KP];       // dU, then dX
   __shared__ float sU[BC][KP];
+  __shared__ float sT[BC][KP];       // W, then Kc
+  __shared__ float sMT[BC][CP];      // M^T
   __shared__ int sseg[BC], scar[BC], slast[BC];
+  static_assert(TPW == 1, "one 16-column tile per wave");
 
   const int u = blockIdx.x;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
   const int t0 = c * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+  const int vcol = 16 * wv + l16;
   const float* S0 = p.S + (int64_t)u * KK;
   const float* S0T = p.ST + (int64_t)u * KK;
   const float* dSC = p.dS + (int64_t)u * KK;
   const float* dSCT = p.dST + (int64_t)u * KK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
+  float yA[4][8], yB[4][8], yS0[4][8];
+  load_y(yA, S0T, wv, q, l16);
+  load_y(yS0, S0, wv, q, l16);
+  float4 u0[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) u0[I] = ld4g(p.U0T + (int64_t)u * CK + vcol * BC + 16 * I + 4 * q);
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4g(p.dout + row_of(p, bb, t0 + i, h) + 4 * c4) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
+    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = ld4g(p.Wm + (int64_t)u * CK + i * KD + 4 * c4);
   }
+#pragma unroll
+  for (int it = 0; it < CC / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
+    *reinterpret_cast<float4*>(&sMT[i][4 * c4]) = ld4g(p.MT + (int64_t)u * CC + i * BC + 4 * c4);
+  }
+  lds_barrier();
 
   f32x4 acc[4][TPW];
   // ---- U = U0 - W S0 ---------------------------------------------------------
-  {
-    const float* U0T = p.U0T + (int64_t)u * CK;
-    zero_acc(acc);
-    nt_128(acc, p.Wm + (int64_t)u * CK, KD, S0T, KD, wv, q, l16);
+  zero_acc(acc);
+  nt_lds(acc, &sT[0][0], yA, q, l16);
+  load_y(yB, dSC, wv, q, l16);
+  float4 kc[BC * KD / 4 / NT];
 #pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int vcol = 16 * (TPW * wv + R2) + l16;
-        const float4 u0 = ld4g(U0T + vcol * BC + 16 * I + 4 * q);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sU[16 * I + 4 * q + e][vcol] = f4at(u0, e) - acc[I][R2][e];
-      }
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    kc[it] = ld4g(p.Kc + (int64_t)u * CK + i * KD + 4 * c4);
   }
-  lds_barrier();
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sU[16 * I + 4 * q + e][vcol] = f4at(u0[I], e) - acc[I][0][e];
+  lds_barrier();   // U complete; every wave is done with W
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = kc[it];
+  }
 
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
+  load_y(yA, dSCT, wv, q, l16);
   zero_acc(acc);
-  nt_128(acc, &sU[0][0], KP, dSC, KD, wv, q, l16);
+  nt_lds(acc, &sU[0][0], yB, q, l16);
   store_raw(p, p.dk, bb, h, t0, wv, q, l16, acc);
   zero_acc(acc);
-  nt_128(acc, &sdO[0][0], KP, S0, KD, wv, q, l16);
+  nt_lds(acc, &sdO[0][0], yS0, q, l16);
   store_raw(p, p.dq, bb, h, t0, wv, q, l16, acc);
+  // T^T rows and this lane's w, v for the dX phase
+  float tt[2][4][8];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int I = 0; I < 4; ++I) row8(p.TT + (int64_t)u * CC + (16 * I + l16) * BC, s2, q, tt[s2][I]);
+  float wq[4][4], vq[4][4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * I + 4 * q + e;
+      const bool vi = t0 + i < p.L;
+      const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + vcol;
+      wq[I][e] = vi ? p.w[ro] : 0.f;
+      vq[I][e] = vi ? p.v[ro] : 0.f;
+    }
+  lds_barrier();   // Kc staged
 
   // ---- dU = M^T dO + Kc dSC  (into sX) --------------------------------------
-  {
-    const float* MT = p.MT + (int64_t)u * CC;
-    zero_acc(acc);
+  zero_acc(acc);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4], bfr[TPW];
+  for (int s = 0; s < 2; ++s) {
+    float x[8];
 #pragma unroll
-      for (int I = 0; I < 4; ++I) { float x[8]; row8(MT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
+    for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
+    const Frag<false> bfr = fr8(x);
 #pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int vcol = 16 * (TPW * wv + R2) + l16;
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
-        bfr[R2] = fr8(x);
-      }
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
+    for (int I = 0; I < 4; ++I) {
+      float y[8];
+      row8(&sMT[16 * I + l16][0], s, q, y);
+      mma(acc[I][0], fr8(y), bfr);
     }
-    nt_128(acc, p.Kc + (int64_t)u * CK, KD, dSCT, KD, wv, q, l16);
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int vcol = 16 * (TPW * wv + R2) + l16;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][R2][e];
-      }
   }
+  nt_lds(acc, &sT[0][0], yA, q, l16);
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][0][e];
   lds_barrier();
 
   // ---- dX = T^T dU ; dv = dX w ; dw = dX v ----------------------------------
-  {
-    const float* TT = p.TT + (int64_t)u * CC;
-    zero_acc(acc);
+  zero_acc(acc);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4], bfr[TPW];
+  for (int s = 0; s < 2; ++s) {
+    float x[8];
 #pragma unroll
-      for (int I = 0; I < 4; ++I) { float x[8]; row8(TT + (16 * I + l16) * BC, s, q, x); a[I] = fr8(x); }
+    for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
+    const Frag<false> bfr = fr8(x);
 #pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int vcol = 16 * (TPW * wv + R2) + l16;
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
-        bfr[R2] = fr8(x);
-      }
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int R2 = 0; R2 < TPW; ++R2) mma(acc[I][R2], a[I], bfr[R2]);
-    }
-    lds_barrier();
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int vcol = 16 * (TPW * wv + R2) + l16;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 16 * I + 4 * q + e;
-          const float dx = acc[I][R2][e];
-          sX[i][vcol] = dx;
-          if (t0 + i < p.L) {
-            const int64_t ro = row_of(p, bb, t0 + i, h) + vcol;
-            p.dv[ro] = dx * p.w[ro];
-            p.dw[ro] = dx * p.v[ro];
-          }
-        }
-      }
+    for (int I = 0; I < 4; ++I) mma(acc[I][0], fr8(tt[s][I]), bfr);
   }
+  lds_barrier();
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * I + 4 * q + e;
+      const float dx = acc[I][0][e];
+      sX[i][vcol] = dx;
+      if (t0 + i < p.L) {
+        const int64_t ro = row_of(p, bb, t0 + i, h) + vcol;
+        p.dv[ro] = dx * wq[I][e];
+        p.dw[ro] = dx * vq[I][e];
+      }
+    }
   lds_barrier();
 
   // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
   zero_acc(acc);
-  nt_128(acc, &sX[0][0], KP, S0, KD, wv, q, l16);
+  nt_lds(acc, &sX[0][0], yS0, q, l16);
   store_raw(p, p.db, bb, h, t0, wv, q, l16, acc);
 
   // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
