@@ -350,7 +350,13 @@ def main():
         tq, tk, tv, tg, tb, tw = (x.requires_grad_(True) for x in _pack(torch, dev, (q, k, v, g, b, w)))
         tdo = torch.randn(tv.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(9)).to(tv.dtype)
 
+        leaves = (tq, tk, tv, tg, tb, tw)
+
         def tstep():
+            # gradients are cleared each step, as optimizer.zero_grad() (set_to_none) does in a
+            # training loop, so backward writes them instead of accumulating into last step's
+            for x in leaves:
+                x.grad = None
             o = chunk_gdn2(tq, tk, tv, tg, tb, tw, segment_ids=seg, is_inference=False, qk_l2norm=True,
                            precision="bf16", chunk_size=128)
             o.backward(tdo)

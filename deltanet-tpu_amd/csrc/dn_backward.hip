@@ -57,7 +57,8 @@ struct BW {
   const float *q, *k, *v, *g, *b, *w;
   const int32_t* seg;
   const float* init;
-  const float* dout;
+  const void* dout;      // cotangent of the output, element type dout_dt
+  int dout_dt, dv_dt;    // DT_F32 or DT_BF16 (dv is written in dv_dt)
   const float* dfin;
   float *dq, *dk, *dv, *dg, *db, *dw, *dinit;
   // workspace, per unit u = (batch * H + head) * NC + chunk
@@ -103,6 +104,14 @@ __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(fm
 
 __device__ __forceinline__ float4 ld4g(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 zero_f4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+// 4 consecutive elements of f32 or bf16 storage, as f32
+__device__ __forceinline__ float4 ld4_dt(const void* p, int64_t i, int dt) {
+  if (dt == DT_BF16) {
+    const bf16x4 x = *reinterpret_cast<const bf16x4*>((const bf16*)p + i);
+    return make_float4((float)x[0], (float)x[1], (float)x[2], (float)x[3]);
+  }
+  return ld4g((const float*)p + i);
+}
 __device__ __forceinline__ float f4at(const float4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -511,7 +520,7 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
     // end read a clamped row (their Xf^T columns are zero)
     const int t = 64 * wv + l;
     const int tok = c * BC + (t >> 2);
-    o.o4 = ld4g(p.dout + row_of(p, bb, min(tok, p.L - 1), h) + col0 + 4 * (t & 3));
+    o.o4 = ld4_dt(p.dout, row_of(p, bb, min(tok, p.L - 1), h) + col0 + 4 * (t & 3), p.dout_dt);
   } else {
     o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
   }
@@ -723,7 +732,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    const float4 v = t0 + i < p.L ? ld4g(p.dout + row_of(p, bb, t0 + i, h) + 4 * c4) : zero_f4();
+    const float4 v = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
     *reinterpret_cast<float4*>(&sT[i][4 * c4]) = ld4g(p.Wm + (int64_t)u * CK + i * KD + 4 * c4);
   }
@@ -826,7 +835,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
       sX[i][vcol] = dx;
       if (t0 + i < p.L) {
         const int64_t ro = row_of(p, bb, t0 + i, h) + vcol;
-        p.dv[ro] = dx * wq[I][e];
+        if (p.dv_dt == DT_BF16) reinterpret_cast<bf16*>(p.dv)[ro] = (bf16)(dx * wq[I][e]);
+        else p.dv[ro] = dx * wq[I][e];
         p.dw[ro] = dx * vq[I][e];
       }
     }
@@ -1072,7 +1082,7 @@ struct BR {
   int32_t* canon;                                 // (B, L)
   float *qe, *ke, *ve, *ge, *be, *we;             // (B, L, Hv, 128) prepared inputs
   const float *dqe, *dke, *dge, *dbe, *dwe;       // their gradients
-  float *dq, *dk, *dg, *db, *dw;                  // raw-layout gradients
+  float *dq, *dk, *dg, *db, *dw;                  // raw-layout gradients (dq, dk in qk_dt)
 };
 
 __device__ __forceinline__ int gate_head(int H, int Hk, int Hv, int hv, int G) {
@@ -1216,8 +1226,17 @@ __global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
   }
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    p.dq[row * KD + l + 64 * e] = dq[e];
-    p.dk[row * KD + l + 64 * e] = dk[e];
+    const int64_t o = row * KD + l + 64 * e;
+    if (p.qk_dt == DT_BF16) {
+      reinterpret_cast<bf16*>(p.dq)[o] = (bf16)dq[e];
+      reinterpret_cast<bf16*>(p.dk)[o] = (bf16)dk[e];
+    } else if (p.qk_dt == DT_F16) {
+      reinterpret_cast<f16*>(p.dq)[o] = (f16)dq[e];
+      reinterpret_cast<f16*>(p.dk)[o] = (f16)dk[e];
+    } else {
+      p.dq[o] = dq[e];
+      p.dk[o] = dk[e];
+    }
   }
 }
 
@@ -1311,7 +1330,9 @@ extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
   return bw_units(a) * kUnitFloats * sizeof(float);
 }
 
-extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+// the recurrence backward with the element types of d_out and dv given
+static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* workspace, size_t workspace_bytes,
+                    void* stream) {
   const int rc = bw_check(a);
   if (rc != DN_OK) return rc;
   const size_t need = bw_units(a) * kUnitFloats * sizeof(float);
@@ -1321,7 +1342,7 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
   p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
   p.seg = a->seg; p.init = (const float*)a->init_state;
-  p.dout = (const float*)a->d_out; p.dfin = (const float*)a->d_final;
+  p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.dfin = (const float*)a->d_final;
   p.dq = (float*)a->dq; p.dk = (float*)a->dk; p.dv = (float*)a->dv;
   p.dg = (float*)a->dg; p.db = (float*)a->db; p.dw = (float*)a->dw; p.dinit = (float*)a->d_init;
   const size_t units = bw_units(a);
@@ -1344,6 +1365,10 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;
+}
+
+extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  return bwd_core(a, DT_F32, DT_F32, workspace, workspace_bytes, stream);
 }
 
 namespace {
@@ -1432,7 +1457,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   c.seg = r.canon; c.init_state = a->init_state; c.d_out = d_out; c.d_final = d_final;
   c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
   c.d_init = d_init;
-  rc = dn_prefill_bwd(&c, w, lay.core, stream);
+  rc = bwd_core(&c, a->v_dtype, a->v_dtype, w, lay.core, stream);
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;

@@ -374,11 +374,15 @@ class _TrainFn(torch.autograd.Function):
         dev = q.device
         a = _TrainFn._args(proto, q, k, v, g, b, w, init)
         a.init_seg = _ptr(init_seg)
-        f32 = lambda t: torch.empty(t.shape, dtype=torch.float32, device=dev)
-        dq, dk, dv, dg, db, dw = (f32(x) for x in (q, k, v, g, b, w))
-        d_init = f32(init) if init is not None else None
-        d_out = torch.zeros(v.shape, dtype=torch.float32, device=dev) if d_out is None \
-            else d_out.to(torch.float32).contiguous()
+        # dq, dk, dv come back in the input dtypes (rounded to nearest even in
+        # the kernels), the gate gradients in f32; the output cotangent is read
+        # in the output's (v's) dtype
+        like = lambda t, dt: torch.empty(t.shape, dtype=dt, device=dev)
+        dq, dk, dv = like(q, q.dtype), like(k, k.dtype), like(v, v.dtype)
+        dg, db, dw = (like(x, torch.float32) for x in (g, b, w))
+        d_init = like(init, torch.float32) if init is not None else None
+        d_out = torch.zeros(v.shape, dtype=v.dtype, device=dev) if d_out is None \
+            else d_out.to(v.dtype).contiguous()
         d_fin = None if d_fin is None else d_fin.to(torch.float32).contiguous()
         lib = _lib.load_library()
         nbytes = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(a))

@@ -173,10 +173,12 @@ size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
  * guard clamps, fused prologue, q/k L2-norm and scale with the cast back to the
  * input dtype, gate broadcast, GQA head mapping, segment canonicalisation).
  * `a` is the dn_prefill_fwd argument block of the forward call (t0 = 0,
- * nt = L; out / final_state are not read).  d_out (B,L,Hv,V) f32, d_final NULL
- * or (B,Hv,K,V) f32.  Gradients are written as f32 in the raw layouts: dq, dk
- * (B,L,Hk,K); dv (B,L,Hv,V); dg, db, dw (B,L,H,C) of their gate; d_init NULL or
- * (B,Hv,K,V). */
+ * nt = L; out / final_state are not read).  d_out (B,L,Hv,V) in the output's
+ * element type (v_dtype), d_final NULL or (B,Hv,K,V) f32.  Gradients are written
+ * in the raw layouts, like the reference's VJP in the input dtypes: dq, dk
+ * (B,L,Hk,K) in qk_dtype and dv (B,L,Hv,V) in v_dtype (f32 results rounded to
+ * nearest even); dg, db, dw (B,L,H,C) of their gate and d_init NULL or
+ * (B,Hv,K,V) in f32. */
 int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
                        void* dq, void* dk, void* dv, void* dg, void* db, void* dw, void* d_init,
                        void* workspace, size_t workspace_bytes, void* stream);
