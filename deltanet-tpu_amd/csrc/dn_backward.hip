@@ -1242,6 +1242,24 @@ __global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
 
 // one thread per raw gate element: the sum of the prepared gradient over the
 // value heads and channels it was broadcast to, times the prologue derivative
+// derivative of the prologue step of gate WHICH at raw value x
+template <int WHICH>
+__device__ __forceinline__ float gate_deriv(const BR& p, float x) {
+  if (WHICH == 0) {
+    if (p.fuse) {
+      const float ga = -__expf(fminf(x, 5.f));
+      return (x <= 5.f ? -__expf(x) : 0.f) * ((!p.guard || ga <= -1e-6f) ? 1.f : 0.f);
+    }
+    return (x <= 0.f && (!p.guard || x <= -1e-6f)) ? 1.f : 0.f;
+  } else if (WHICH == 1) {
+    if (p.fuse) { const float sg = sigmoid_hw(x); return sg * (1.f - sg); }
+    return (!p.guard || x >= 0.f) ? 1.f : 0.f;
+  } else {
+    if (p.fuse) { const float sg = sigmoid_hw(x); return sg * (1.f - sg); }
+    return 1.f;
+  }
+}
+
 template <int WHICH>   // 0 = g, 1 = b, 2 = w
 __global__ __launch_bounds__(256) void k_bw_post_gate(BR p) {
   const int H = WHICH == 0 ? p.g_h : (WHICH == 1 ? p.b_h : p.w_h);
@@ -1276,22 +1294,37 @@ __global__ __launch_bounds__(256) void k_bw_post_gate(BR p) {
     for (int j = 0; j < hn; ++j, rowp += KD) s += rowp[c];
   }
   const float x = raw[idx];
-  float d;
-  if (WHICH == 0) {
-    if (p.fuse) {
-      const float ga = -__expf(fminf(x, 5.f));
-      d = (x <= 5.f ? -__expf(x) : 0.f) * ((!p.guard || ga <= -1e-6f) ? 1.f : 0.f);
-    } else {
-      d = (x <= 0.f && (!p.guard || x <= -1e-6f)) ? 1.f : 0.f;
-    }
-  } else if (WHICH == 1) {
-    if (p.fuse) { const float sg = sigmoid_hw(x); d = sg * (1.f - sg); }
-    else d = (!p.guard || x >= 0.f) ? 1.f : 0.f;
-  } else {
-    if (p.fuse) { const float sg = sigmoid_hw(x); d = sg * (1.f - sg); }
-    else d = 1.f;
-  }
+  const float d = gate_deriv<WHICH>(p, x);
   out[idx] = s * d;
+}
+
+// channel-wise gates (C = 128): one thread per 4 channels of one (token, head)
+// row, the row split into token and head once per thread
+template <int WHICH>
+__global__ __launch_bounds__(256) void k_bw_post_gate4(BR p) {
+  const int H = WHICH == 0 ? p.g_h : (WHICH == 1 ? p.b_h : p.w_h);
+  const float* raw = WHICH == 0 ? p.g : (WHICH == 1 ? p.b : p.w);
+  const float* dpre = WHICH == 0 ? p.dge : (WHICH == 1 ? p.dbe : p.dwe);
+  float* out = WHICH == 0 ? p.dg : (WHICH == 1 ? p.db : p.dw);
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int c4 = threadIdx.x & 31;
+  if (row >= (int64_t)p.B * p.L * H) return;
+  const int h = (int)(row % H);
+  const int64_t bt = row / H;
+  int h0, hn;
+  if (H == p.Hv) { h0 = h; hn = 1; }
+  else if (H == p.Hk) { h0 = h * p.G; hn = p.G; }
+  else { h0 = 0; hn = p.Hv; }
+  const float* rowp = dpre + (bt * p.Hv + h0) * KD + 4 * c4;
+  float4 s = zero_f4();
+  for (int j = 0; j < hn; ++j, rowp += KD) {
+    const float4 x4 = ld4g(rowp);
+    s.x += x4.x; s.y += x4.y; s.z += x4.z; s.w += x4.w;
+  }
+  const float4 x = ld4g(raw + row * KD + 4 * c4);
+  *reinterpret_cast<float4*>(out + row * KD + 4 * c4) =
+      make_float4(s.x * gate_deriv<WHICH>(p, x.x), s.y * gate_deriv<WHICH>(p, x.y), s.z * gate_deriv<WHICH>(p, x.z),
+                  s.w * gate_deriv<WHICH>(p, x.w));
 }
 
 }  // namespace
@@ -1465,9 +1498,13 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   const int64_t ng = (int64_t)a->B * a->L * a->g_heads * a->g_chans;
   const int64_t nb = (int64_t)a->B * a->L * a->b_heads * a->b_chans;
   const int64_t nw = (int64_t)a->B * a->L * a->w_heads * a->w_chans;
-  hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
-  hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
-  hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
+  // channel-wise gates take the float4 kernel (8 rows of 128 channels per block)
+  if (a->g_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<0>, dim3((unsigned)((ng / KD + 7) / 8)), dim3(256), 0, st, r);
+  else hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
+  if (a->b_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<1>, dim3((unsigned)((nb / KD + 7) / 8)), dim3(256), 0, st, r);
+  else hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
+  if (a->w_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<2>, dim3((unsigned)((nw / KD + 7) / 8)), dim3(256), 0, st, r);
+  else hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
   e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;
