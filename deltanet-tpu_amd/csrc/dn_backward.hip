@@ -32,7 +32,7 @@
 //   k_bw_chain<true>   same tiles, reverse: dS_{c+1} for every chunk, dS_0
 //   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA and the chunk-wide
 //                products of dq, dk, db
-//   k_bw_dqk     per (batch, head, chunk, half of the key channels): dq, dk,
+//   k_bw_dqk     per (batch, head, chunk, quarter of the key channels): dq, dk,
 //                db, dg
 #include "dn_common.h"
 #include "dn_host.h"
@@ -873,8 +873,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 }
 
 // ---------------------------------------------------------------------------
-// k_bw_dqk: the decay-weighted parts of dq, dbeta, dk and dg, per (unit, half
-// of the key channels).  With the chunk's q, k, b, G and dM, dA in LDS:
+// k_bw_dqk: the decay-weighted parts of dq, dbeta, dk and dg, per (unit,
+// quarter of the key channels).  With the chunk's q, k, b, G and dM, dA in LDS:
 //   dq_i    = carry_i e^{G_i} (dO S0^T)_i + sum_j dM_ij e^{G_i-G_j} k_j
 //   dbeta_i = -carry_i e^{G_i} (dX S0^T)_i + sum_j dA_ij e^{G_i-G_j} k_j
 //   dk_j    = sum_i dM_ij e^{G_i-G_j} q_i + sum_i dA_ij e^{G_i-G_j} beta_i
@@ -885,29 +885,30 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 // Off-diagonal 16-row blocks use e^{G_i-G_m} e^{G_m-G_j} (both <= 1) through
 // MFMA; pairs inside a block join those products where the block's decay
 // span allows, else use e^{G_i-G_j} per element.
-// Wave w owns the 16 channels 16 (w % 4) .. and the 16-row blocks
-// 2 (w / 4), 2 (w / 4) + 1; lanes hold rows 4q..4q+3 of each block.
+// Wave w owns the 16 channels 16 (w % 2) .. and the 16-row block w / 2;
+// lanes hold rows 4q..4q+3 of it.  About 73 KB of LDS: two workgroups per CU.
 // ---------------------------------------------------------------------------
-constexpr int HC = KD / 2;      // channels per k_bw_dqk workgroup
+constexpr int HC = KD / 4;      // channels per k_bw_dqk workgroup
+constexpr int NQ = KD / HC;     // k_bw_dqk workgroups per unit
 constexpr int HP = HC + 4;
 
-__global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_bw_dqk(BW p) {
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
-  __shared__ float sdG[BC][HP], sP[BC][HP];
   __shared__ float sTail[HC];
   __shared__ int scar[BC], slast[BC], sseg[BC];
 
-  const int u = blockIdx.x >> 1, half = blockIdx.x & 1;
+  const int u = blockIdx.x / NQ, part = blockIdx.x % NQ;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
   const int t0 = c * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
-  const int ch0 = HC * half;
+  const int ch0 = HC * part;
   const float* G = p.G + (int64_t)u * CK;
 
-  constexpr int NB = 4 / (NWV / 4);          // 16-row blocks per wave
-  const int rl = 16 * (wv & 3) + l16, r = ch0 + rl;
-  const int I0 = NB * (wv >> 2);
+  constexpr int CG = HC / 16;                // 16-channel groups
+  constexpr int NB = 4 * CG / NWV;           // 16-row blocks per wave
+  const int rl = 16 * (wv % CG) + l16, r = ch0 + rl;
+  const int I0 = NB * (wv / CG);
   // raw products from k_bw_grads for this lane's rows, loaded up front
   float rq[NB][4], rb[NB][4], rk[NB][4];
 #pragma unroll
@@ -962,6 +963,7 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
   for (int o = 1; o < PARTS; o <<= 1) rs += __shfl_xor(rs, o);
   if (tid % PARTS == 0) sTail[tid / PARTS] = rs;
   const float glast = sG[BC - 1][rl];
+  float rdg[NB][4], rpp[NB][4];   // dG and P of this lane's rows
 #pragma unroll
   for (int Ib = 0; Ib < NB; ++Ib) {
     const int I = I0 + Ib;
@@ -1027,8 +1029,8 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
       dk += ok_[e] * ex2(gm2 - gi);
       const float dkc = slast[i] ? ex2(glast - gi) * rk[Ib][e] : 0.f;
       const float kv = sK[i][rl], qv = sQ[i][rl], bv = sB[i][rl], dmii = sdM[i][i];
-      sdG[i][rl] = qv * dq + bv * kv * dbeta - kv * dk;
-      sP[i][rl] = kv * dkc;
+      rdg[Ib][e] = qv * dq + bv * kv * dbeta - kv * dk;
+      rpp[Ib][e] = kv * dkc;
       if (t0 + i < p.L) {
         const int64_t ro = row_of(p, bb, t0 + i, h) + r;
         p.dq[ro] = dq + dmii * kv;
@@ -1037,6 +1039,18 @@ __global__ __launch_bounds__(NT) void k_bw_dqk(BW p) {
       }
     }
   }
+  // dG and P rows replace q and k in LDS once every wave is done with them
+  lds_barrier();
+  float (*sdG)[HP] = sQ;
+  float (*sP)[HP] = sK;
+#pragma unroll
+  for (int Ib = 0; Ib < NB; ++Ib)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * (I0 + Ib) + 4 * q + e;
+      sdG[i][rl] = rdg[Ib][e];
+      sP[i][rl] = rpp[Ib][e];
+    }
   lds_barrier();
 
   // ---- dg_t = sum_{i>=t} dG_i + sum_{j<t} P_j + lam rowsum(S0 * dSC) -------
@@ -1393,7 +1407,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
   hipLaunchKernelGGL(k_bw_chain<false>, dim3(chains), dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_bw_chain<true>, dim3(chains), dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(NT), 0, st, p);
-  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(2 * units)), dim3(NT), 0, st, p);
+  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * units)), dim3(NT), 0, st, p);
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
