@@ -73,8 +73,8 @@ struct BW {
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
   float *dMw, *dAw; // [BC][BC] dM and dA (k_bw_grads -> k_bw_dqk)
-  float *S, *ST;    // [KD][KD] state entering the chunk, and its transpose
-  float *dS, *dST;  // [KD][KD] gradient of the state leaving the chunk, and its transpose
+  float *S;         // [KD][KD] state entering the chunk
+  float *dS;        // [KD][KD] gradient of the state leaving the chunk
 };
 
 __device__ __forceinline__ int64_t row_of(const BW& p, int bb, int t, int h) {
@@ -570,13 +570,11 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     lds_barrier();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;
-      float* XT = (BWD ? p.dST : p.ST) + u * KK;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int r0 = 32 * wv + 16 * tt + 4 * q;
 #pragma unroll
         for (int e = 0; e < 4; ++e) X[(r0 + e) * KD + col0 + l16] = st[tt][e];
-        *reinterpret_cast<float4*>(XT + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
       }
     }
     // Xf^T dO (backward) needs neither the state nor the exchanged tile
@@ -685,6 +683,15 @@ __device__ __forceinline__ void load_y(float (&y)[4][8], const float* Y, int wv,
   for (int s = 0; s < 4; ++s) row8(Y + (16 * wv + l16) * KD, s, q, y[s]);
 }
 
+// the same operand rows of Y = X^T, read from row-major X: column 16 w + l16
+// of X, rows 32 s + pi_k(q, e)
+__device__ __forceinline__ void load_yT(float (&y)[4][8], const float* X, int wv, int q, int l16) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[s][e] = X[(32 * s + pi_k(q, e)) * KD + 16 * wv + l16];
+}
+
 // acc[I] += X[rows 16I..][:] * Y^T with X in LDS (row pitch KP) and Y preloaded
 __device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, const float (&y)[4][8], int q,
                                        int l16) {
@@ -718,13 +725,11 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   const int vcol = 16 * wv + l16;
   const float* S0 = p.S + (int64_t)u * KK;
-  const float* S0T = p.ST + (int64_t)u * KK;
   const float* dSC = p.dS + (int64_t)u * KK;
-  const float* dSCT = p.dST + (int64_t)u * KK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
   float yA[4][8], yB[4][8], yS0[4][8];
-  load_y(yA, S0T, wv, q, l16);
+  load_yT(yA, S0, wv, q, l16);
   load_y(yS0, S0, wv, q, l16);
   float4 u0[4];
 #pragma unroll
@@ -766,7 +771,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   }
 
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
-  load_y(yA, dSCT, wv, q, l16);
+  load_yT(yA, dSC, wv, q, l16);
   zero_acc(acc);
   nt_lds(acc, &sU[0][0], yB, q, l16);
   store_raw(p, p.dk, bb, h, t0, wv, q, l16, acc);
@@ -1354,7 +1359,7 @@ size_t bw_units(const dn_backward_args* a) {
   return (size_t)a->B * a->H * NC;
 }
 
-constexpr size_t kUnitFloats = 7 * (size_t)CK + 4 * (size_t)CC + KD + 4 * (size_t)KK;
+constexpr size_t kUnitFloats = 7 * (size_t)CK + 4 * (size_t)CC + KD + 2 * (size_t)KK;
 
 int bw_check(const dn_backward_args* a) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
@@ -1398,7 +1403,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
   p.XfT = take(CK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
   p.dMw = take(CC); p.dAw = take(CC);
-  p.S = take(KK); p.ST = take(KK); p.dS = take(KK); p.dST = take(KK);
+  p.S = take(KK); p.dS = take(KK);
 
   hipStream_t st = (hipStream_t)stream;
   const int chains = a->B * a->H * (KD / 16);
