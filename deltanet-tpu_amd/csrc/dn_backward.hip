@@ -73,8 +73,8 @@ struct BW {
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
   float *dMw, *dAw; // [BC][BC] dM and dA (k_bw_grads -> k_bw_dqk)
-  float *S;         // [KD][KD] state entering the chunk
-  float *dS;        // [KD][KD] gradient of the state leaving the chunk
+  float *S;         // [KD][KD] state entering the chunk, transposed: element (v, k) at v * KD + k
+  float *dS;        // [KD][KD] gradient of the state leaving the chunk, transposed likewise
 };
 
 __device__ __forceinline__ int64_t row_of(const BW& p, int bb, int t, int h) {
@@ -569,12 +569,11 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
     }
     lds_barrier();
     {
-      float* X = (BWD ? p.dS : p.S) + u * KK;
+      float* X = (BWD ? p.dS : p.S) + u * KK;   // transposed: 4 consecutive k per lane
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int r0 = 32 * wv + 16 * tt + 4 * q;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) X[(r0 + e) * KD + col0 + l16] = st[tt][e];
+        *reinterpret_cast<float4*>(X + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
       }
     }
     // Xf^T dO (backward) needs neither the state nor the exchanged tile
@@ -729,8 +728,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
   float yA[4][8], yB[4][8], yS0[4][8];
-  load_yT(yA, S0, wv, q, l16);
-  load_y(yS0, S0, wv, q, l16);
+  load_y(yA, S0, wv, q, l16);
+  load_yT(yS0, S0, wv, q, l16);
   float4 u0[4];
 #pragma unroll
   for (int I = 0; I < 4; ++I) u0[I] = ld4g(p.U0T + (int64_t)u * CK + vcol * BC + 16 * I + 4 * q);
@@ -752,7 +751,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   // ---- U = U0 - W S0 ---------------------------------------------------------
   zero_acc(acc);
   nt_lds(acc, &sT[0][0], yA, q, l16);
-  load_y(yB, dSC, wv, q, l16);
+  load_yT(yB, dSC, wv, q, l16);
   float4 kc[BC * KD / 4 / NT];
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
@@ -771,7 +770,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   }
 
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
-  load_yT(yA, dSC, wv, q, l16);
+  load_y(yA, dSC, wv, q, l16);
   zero_acc(acc);
   nt_lds(acc, &sU[0][0], yB, q, l16);
   store_raw(p, p.dk, bb, h, t0, wv, q, l16, acc);
@@ -900,7 +899,7 @@ constexpr int HP = HC + 4;
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_bw_dqk(BW p) {
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
-  __shared__ float sTail[HC];
+  __shared__ float sRS[NT / HC][HC];   // partial rowsums of S0 * dSC
   __shared__ int scar[BC], slast[BC], sseg[BC];
 
   const int u = blockIdx.x / NQ, part = blockIdx.x % NQ;
@@ -928,18 +927,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       rb[Ib][e] = vi ? p.db[ro] : 0.f;
       rk[Ib][e] = vi ? p.dk[ro] : 0.f;
     }
-  // rowsum(S0 * dSC) of channel ch0 + tid / PARTS, 128 / PARTS entries per thread
+  // rowsum(S0 * dSC) of channel ch0 + tid % HC over the value range of part
+  // tid / HC (the states are stored transposed: channel k of row v at v * KD + k,
+  // so a wave reads consecutive channels)
   constexpr int PARTS = NT / HC;
   float rs = 0.f;
   {
-    const int cr = ch0 + tid / PARTS, part = tid % PARTS;
-    const float* S0 = p.S + (int64_t)u * KK + cr * KD + (KD / PARTS) * part;
-    const float* dSC = p.dS + (int64_t)u * KK + cr * KD + (KD / PARTS) * part;
+    const int cr = ch0 + tid % HC, part = tid / HC;
+    const float* S0 = p.S + (int64_t)u * KK + cr;
+    const float* dSC = p.dS + (int64_t)u * KK + cr;
 #pragma unroll
-    for (int v4 = 0; v4 < KD / PARTS / 4; ++v4) {
-      const float4 a = ld4g(S0 + 4 * v4);
-      const float4 d = ld4g(dSC + 4 * v4);
-      rs += a.x * d.x + a.y * d.y + a.z * d.z + a.w * d.w;
+    for (int vv = 0; vv < KD / PARTS; ++vv) {
+      const int v = (KD / PARTS) * part + vv;
+      rs += S0[v * KD] * dSC[v * KD];
     }
   }
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
@@ -964,9 +964,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   }
   lds_barrier();
 
-#pragma unroll
-  for (int o = 1; o < PARTS; o <<= 1) rs += __shfl_xor(rs, o);
-  if (tid % PARTS == 0) sTail[tid / PARTS] = rs;
+  sRS[tid / HC][tid % HC] = rs;
   const float glast = sG[BC - 1][rl];
   float rdg[NB][4], rpp[NB][4];   // dG and P of this lane's rows
 #pragma unroll
@@ -1063,7 +1061,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   // so it is summed forward over j < t instead)
   if (tid < HC) {
     const int rr = ch0 + tid;
-    const float tail = scar[BC - 1] ? ex2(sG[BC - 1][tid]) * sTail[tid] : 0.f;
+    float rsum = 0.f;
+#pragma unroll
+    for (int pp = 0; pp < NT / HC; ++pp) rsum += sRS[pp][tid];
+    const float tail = scar[BC - 1] ? ex2(sG[BC - 1][tid]) * rsum : 0.f;
     float fwd = 0.f, acc = tail;
     float dgv[BC];
 #pragma unroll
