@@ -27,7 +27,8 @@
 // (the reference's strong-decay test uses g = -150 per token).
 //
 // Kernels (one launch each, in stream order):
-//   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G
+//   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G and
+//                the reverse scan's state-free term Xf^T dO
 //   k_bw_chain<false>  per (batch, head, 16-column tile): S_c for every chunk
 //   k_bw_chain<true>   same tiles, reverse: dS_{c+1} for every chunk, dS_0
 //   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA and the chunk-wide
@@ -67,7 +68,7 @@ struct BW {
   float *WT;   // [KD][BC] W^T
   float *Kc;   // [BC][KD]
   float *KcT;  // [KD][BC]
-  float *XfT;  // [KD][BC]
+  float *PT;   // [KD][KD] (Xf^T dO)^T: element (v, k) at v * KD + k
   float *U0T;  // [KD][BC] U0^T
   float *MT;   // [BC][BC] M^T
   float *TT;   // [BC][BC] T^T
@@ -427,8 +428,15 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   }
   lds_barrier();
 
-  // ---- Xf = diag(carry) q e^G - M W ----------------------------------------
+  // ---- Xf = diag(carry) q e^G - M W, then P^T = (Xf^T dO)^T ------------------
   {
+    // the chunk's dO (rows past the sequence end zero), used after Xf
+    float4 dov[BC * KD / 4 / NT];
+#pragma unroll
+    for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+      const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+      dov[it] = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
+    }
     f32x4 ax[4][TPW];
 #pragma unroll
     for (int I = 0; I < 4; ++I)
@@ -457,21 +465,49 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         for (int I = 0; I < 4; ++I) mma(ax[I][R2], a[I], fb);
       }
     }
-    float* XfT = p.XfT + (int64_t)u * CK;
+    float xf[4][4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int r = 16 * wv + l16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * I + 4 * q + e;
+        const float qe = scar[i] ? sQ[i][r] * ex2(sG[i][r]) : 0.f;
+        xf[I][e] = qe - ax[I][0][e];
+      }
+    }
+    // Xf replaces W in sW and dO replaces q in sQ once every wave is done with them
+    lds_barrier();
 #pragma unroll
     for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int r = 16 * (TPW * wv + R2) + l16;
-        float o[4];
+      for (int e = 0; e < 4; ++e) sW[16 * I + 4 * q + e][16 * wv + l16] = xf[I][e];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 16 * I + 4 * q + e;
-          const float qe = scar[i] ? sQ[i][r] * ex2(sG[i][r]) : 0.f;
-          o[e] = qe - ax[I][R2][e];
-        }
-        *reinterpret_cast<float4*>(XfT + r * BC + 16 * I + 4 * q) = make_float4(o[0], o[1], o[2], o[3]);
+    for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+      const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+      *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = dov[it];
+    }
+    lds_barrier();
+    // P^T rows v = 16 w .. 16 w + 15, all 128 k: P[k][v] = sum_i Xf[i][k] dO[i][v]
+    // is the state-free term of the reverse scan's step
+    float xb[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xb[s][e] = sQ[32 * s + pi_k(q, e)][16 * wv + l16];
+    float* PT = p.PT + (int64_t)u * KK;
+#pragma unroll
+    for (int kt = 0; kt < KD / 16; ++kt) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float xa[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[e] = sW[32 * s + pi_k(q, e)][16 * kt + l16];
+        mma(acc, fr8(xa), fr8(xb[s]));
       }
+      *reinterpret_cast<float4*>(PT + (16 * wv + l16) * KD + 16 * kt + 4 * q) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
   }
 }
 
@@ -488,8 +524,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 struct ChainOps {
   float a[4][8];        // W (forward) / Kc (backward) rows of this wave's 16 tokens
   float b[2][2][8];     // Kc^T (forward) / W^T (backward) rows of this wave's 32 state rows
-  float x[2][2][8];     // Xf^T rows (backward)
-  float4 o4;            // one float4 of the chunk's 64 x 16 dO tile (backward), staged through LDS
+  float4 pp[2];         // (Xf^T dO) entries of this lane's state rows (backward)
   float4 u;             // U0 tile entries of this lane (forward)
   float4 lm[2];         // lam of this lane's state rows
 };
@@ -508,38 +543,22 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
     const float* Brow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) row8(Brow, s2, q, o.b[tt][s2]);
-    if (BWD) {
-      const float* Xrow = p.XfT + u * CK + rA * BC;
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) row8(Xrow, s2, q, o.x[tt][s2]);
-    }
+    if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + (col0 + l16) * KD + 32 * wv + 16 * tt + 4 * q);
     o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
-  if (BWD) {
-    // thread t loads columns 4 (t % 4) .. +3 of token t / 4; tokens past the
-    // end read a clamped row (their Xf^T columns are zero)
-    const int t = 64 * wv + l;
-    const int tok = c * BC + (t >> 2);
-    o.o4 = ld4_dt(p.dout, row_of(p, bb, min(tok, p.L - 1), h) + col0 + 4 * (t & 3), p.dout_dt);
-  } else {
-    o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
-  }
+  if (!BWD) o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
 }
 
 template <bool BWD>
 __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
   __shared__ float sS[4][64][8];
   __shared__ float sY[2][64][8];
-  __shared__ float sO[BC][16 + 1];   // dO tile of the current chunk (backward)
-  int ct, bh, zz;
-  {
-    int x = blockIdx.x, y = 0, z = 0;
-    xcd_block(x, y, z);     // 1-D grid: x = 8 * (batch * H + head) + column tile
-    ct = x % (KD / 16);
-    bh = x / (KD / 16);
-    zz = z;
-  }
-  (void)zz;
+  const int chains = p.B * p.H * (KD / 16);
+  // chain x = 8 * (batch * H + head) + column tile; blocks b and b + 8 k share
+  // an XCD, so the 8 column tiles of a head run on one XCD, whose L2 serves
+  // their shared rows
+  const int x = ((int)blockIdx.x & 7) * (chains >> 3) + ((int)blockIdx.x >> 3);
+  const int ct = x % (KD / 16), bh = x / (KD / 16);
   const int h = bh % p.H, bb = bh / p.H;
   const int col0 = 16 * ct;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
@@ -562,11 +581,6 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
   // one scan step on chunk c with operands `o` in registers
   auto step = [&](int c, const ChainOps& o) {
     const int64_t u = (int64_t)bh * p.NC + c;
-    if (BWD) {
-      const int t = 64 * wv + l;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sO[t >> 2][4 * (t & 3) + j] = f4at(o.o4, j);
-    }
     lds_barrier();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;   // transposed: 4 consecutive k per lane
@@ -574,18 +588,6 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
       for (int tt = 0; tt < 2; ++tt) {
         const int r0 = 32 * wv + 16 * tt + 4 * q;
         *reinterpret_cast<float4*>(X + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
-      }
-    }
-    // Xf^T dO (backward) needs neither the state nor the exchanged tile
-    f32x4 acc2[2] = {zero4(), zero4()};
-    if (BWD) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float xo[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xo[e] = sO[32 * s2 + pi_k(q, e)][l16];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) mma(acc2[tt], fr8(o.x[tt][s2]), fr8(xo));
       }
     }
     // Y (or Z) tile: token rows 16w..16w+15; two accumulators halve the
@@ -613,7 +615,7 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) st[tt][e] = acc[tt][e] + acc2[tt][e];
+      for (int e = 0; e < 4; ++e) st[tt][e] = acc[tt][e] + (BWD ? f4at(o.pp[tt], e) : 0.f);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       sS[wv][l][e] = st[0][e];
@@ -1360,7 +1362,7 @@ size_t bw_units(const dn_backward_args* a) {
   return (size_t)a->B * a->H * NC;
 }
 
-constexpr size_t kUnitFloats = 7 * (size_t)CK + 4 * (size_t)CC + KD + 2 * (size_t)KK;
+constexpr size_t kUnitFloats = 6 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
 
 int bw_check(const dn_backward_args* a) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
@@ -1402,7 +1404,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
   float* ws = (float*)workspace;
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
-  p.XfT = take(CK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
+  p.PT = take(KK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
   p.dMw = take(CC); p.dAw = take(CC);
   p.S = take(KK); p.dS = take(KK);
 
