@@ -368,6 +368,14 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   }
   lds_barrier();
 
+  // the chunk's dO (rows past the sequence end zero), loaded now for the P^T
+  // phase at the end
+  float4 dov[BC * KD / 4 / NT];
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    dov[it] = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
+  }
   // ---- W = T diag(carry) (b k e^G), U0 = T (w v) ---------------------------
   {
     f32x4 aw[4][TPW], au[4][TPW];
@@ -430,13 +438,6 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 
   // ---- Xf = diag(carry) q e^G - M W, then P^T = (Xf^T dO)^T ------------------
   {
-    // the chunk's dO (rows past the sequence end zero), used after Xf
-    float4 dov[BC * KD / 4 / NT];
-#pragma unroll
-    for (int it = 0; it < BC * KD / 4 / NT; ++it) {
-      const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-      dov[it] = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
-    }
     f32x4 ax[4][TPW];
 #pragma unroll
     for (int I = 0; I < 4; ++I)
