@@ -121,6 +121,19 @@ def test_backward_strong_decay(precision):
 
 
 
+@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 1e-2)])
+def test_backward_odd_heads_two_batches(precision, tol):
+    """B = 2, three value heads on one key head (G = 3) and an unaligned length:
+    24 chain workgroups per direction (not a multiple of 8 heads per XCD) and a
+    partial last chunk in every kernel's index mapping."""
+    B, L, Hk, Hv = 2, 130, 1, 3
+    q, k, v, g, b, w = ref_inputs(701, B, L, Hk, Hv)
+    do = np.random.default_rng(702).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision=precision)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+    compare(got, ref, tol, f"B=2 Hk=1 Hv=3 L=130 {precision}")
+
+
 def test_backward_mixed_decay_spans():
     """16-token blocks whose decay span is below 2^64 in every channel form
     their diagonal A / M tiles as factored MFMA products, the others
