@@ -786,17 +786,17 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
     for (int I = 0; I < 4; ++I) row8(p.TT + (int64_t)u * CC + (16 * I + l16) * BC, s2, q, tt[s2][I]);
-  float wq[4][4], vq[4][4];
+  // w, v of the coalesced dv / dw pass: float4s tid + NT it of the chunk's
+  // row-major 64 x 128 tiles
+  float4 wq[BC * KD / 4 / NT], vq[BC * KD / 4 / NT];
 #pragma unroll
-  for (int I = 0; I < 4; ++I)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * I + 4 * q + e;
-      const bool vi = t0 + i < p.L;
-      const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + vcol;
-      wq[I][e] = vi ? p.w[ro] : 0.f;
-      vq[I][e] = vi ? p.v[ro] : 0.f;
-    }
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    const bool vi = t0 + i < p.L;
+    const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + 4 * c4;
+    wq[it] = vi ? ld4g(p.w + ro) : zero_f4();
+    vq[it] = vi ? ld4g(p.v + ro) : zero_f4();
+  }
   lds_barrier();   // Kc staged
 
   // ---- dU = M^T dO + Kc dSC  (into sX) --------------------------------------
@@ -836,18 +836,27 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * I + 4 * q + e;
-      const float dx = acc[I][0][e];
-      sX[i][vcol] = dx;
-      if (t0 + i < p.L) {
-        const int64_t ro = row_of(p, bb, t0 + i, h) + vcol;
-        if (p.dv_dt == DT_BF16) reinterpret_cast<bf16*>(p.dv)[ro] = (bf16)(dx * wq[I][e]);
-        else p.dv[ro] = dx * wq[I][e];
-        p.dw[ro] = dx * vq[I][e];
-      }
-    }
+    for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][0][e];
   lds_barrier();
+  // dv = dX w, dw = dX v, row-major and coalesced
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    if (t0 + i < p.L) {
+      const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
+      const float4 dx = *reinterpret_cast<const float4*>(&sX[i][4 * c4]);
+      const float4 a = wq[it], v4 = vq[it];
+      const float4 dv = make_float4(dx.x * a.x, dx.y * a.y, dx.z * a.z, dx.w * a.w);
+      if (p.dv_dt == DT_BF16) {
+        bf16x4 hb;
+        hb[0] = (bf16)dv.x; hb[1] = (bf16)dv.y; hb[2] = (bf16)dv.z; hb[3] = (bf16)dv.w;
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(p.dv) + ro) = hb;
+      } else {
+        *reinterpret_cast<float4*>(p.dv + ro) = dv;
+      }
+      *reinterpret_cast<float4*>(p.dw + ro) = make_float4(dx.x * v4.x, dx.y * v4.y, dx.z * v4.z, dx.w * v4.w);
+    }
+  }
 
   // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
   zero_acc(acc);
