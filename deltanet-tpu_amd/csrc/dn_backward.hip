@@ -74,6 +74,8 @@ struct BW {
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
   float *dMw, *dAw; // [BC][BC] dM and dA (k_bw_grads -> k_bw_dqk)
+  float *Rq, *Rk, *Rb; // raw dO S0^T, U dSC^T, dX S0^T (k_bw_grads -> k_bw_dqk), in
+                       // MFMA accumulator order: [column tile][row block][lane][4]
   float *S;         // [KD][KD] state entering the chunk, transposed: element (v, k) at v * KD + k
   float *dS;        // [KD][KD] gradient of the state leaving the chunk, transposed likewise
 };
@@ -655,20 +657,15 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
 // S0 = S_c, dSC = dS_{c+1}:
 //   U = U0 - W S0 ; dU = M^T dO + Kc dSC ; dX = T^T dU ; dv = dX w ; dw = dX v
 //   dM = mask(dO U^T), dA = -mask(dX U^T)            -> workspace
-//   U dSC^T -> dk,  dO S0^T -> dq,  dX S0^T -> db     (raw; k_bw_dqk finishes them)
-// Wave w owns the columns 32w..32w+31 of every C x 128 product.
+//   U dSC^T, dO S0^T, dX S0^T -> workspace (Rk, Rq, Rb; k_bw_dqk finishes dk, dq, db)
+// Wave w owns the columns 16w..16w+15 of every C x 128 product.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void store_raw(const BW& p, float* out, int bb, int h, int t0, int wv, int q, int l16,
-                                          const f32x4 (&acc)[4][TPW]) {
+// a 64 x 16 product tile of wave wv in accumulator order: one 16-byte
+// vector per lane and row block
+__device__ __forceinline__ void store_frag(float* R, int wv, int l, const f32x4 (&acc)[4][TPW]) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
-#pragma unroll
-    for (int R2 = 0; R2 < TPW; ++R2)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * I + 4 * q + e;
-        if (t0 + i < p.L) out[row_of(p, bb, t0 + i, h) + 16 * (TPW * wv + R2) + l16] = acc[I][R2][e];
-      }
+    *reinterpret_cast<float4*>(R + ((wv * 4 + I) * 64 + l) * 4) = make_float4(acc[I][0][0], acc[I][0][1], acc[I][0][2], acc[I][0][3]);
 }
 
 __device__ __forceinline__ void zero_acc(f32x4 (&acc)[4][TPW]) {
@@ -776,10 +773,10 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   load_y(yA, dSC, wv, q, l16);
   zero_acc(acc);
   nt_lds(acc, &sU[0][0], yB, q, l16);
-  store_raw(p, p.dk, bb, h, t0, wv, q, l16, acc);
+  store_frag(p.Rk + (int64_t)u * CK, wv, l, acc);
   zero_acc(acc);
   nt_lds(acc, &sdO[0][0], yS0, q, l16);
-  store_raw(p, p.dq, bb, h, t0, wv, q, l16, acc);
+  store_frag(p.Rq + (int64_t)u * CK, wv, l, acc);
   // T^T rows and this lane's w, v for the dX phase
   float tt[2][4][8];
 #pragma unroll
@@ -861,7 +858,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
   zero_acc(acc);
   nt_lds(acc, &sX[0][0], yS0, q, l16);
-  store_raw(p, p.db, bb, h, t0, wv, q, l16, acc);
+  store_frag(p.Rb + (int64_t)u * CK, wv, l, acc);
 
   // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
   for (int task = wv; task < 32; task += NWV) {
@@ -926,19 +923,22 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   const int rl = 16 * (wv % CG) + l16, r = ch0 + rl;
   const int I0 = NB * (wv / CG);
   // raw products from k_bw_grads for this lane's rows, loaded up front
+  // (k_bw_grads stored them in accumulator order: column tile r / 16, the
+  // same lane, rows 16 I + 4 q + e; rows past the sequence end count as zero)
   float rq[NB][4], rb[NB][4], rk[NB][4];
 #pragma unroll
-  for (int Ib = 0; Ib < NB; ++Ib)
+  for (int Ib = 0; Ib < NB; ++Ib) {
+    const int I = I0 + Ib;
+    const int64_t fo = (int64_t)u * CK + (((r >> 4) * 4 + I) * 64 + l) * 4;
+    const float4 fq = ld4g(p.Rq + fo), fb = ld4g(p.Rb + fo), fk = ld4g(p.Rk + fo);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int I = I0 + Ib;
-      const int i = 16 * I + 4 * q + e;
-      const bool vi = t0 + i < p.L;
-      const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + r;
-      rq[Ib][e] = vi ? p.dq[ro] : 0.f;
-      rb[Ib][e] = vi ? p.db[ro] : 0.f;
-      rk[Ib][e] = vi ? p.dk[ro] : 0.f;
+      const bool vi = t0 + 16 * I + 4 * q + e < p.L;
+      rq[Ib][e] = vi ? f4at(fq, e) : 0.f;
+      rb[Ib][e] = vi ? f4at(fb, e) : 0.f;
+      rk[Ib][e] = vi ? f4at(fk, e) : 0.f;
     }
+  }
   // rowsum(S0 * dSC) of channel ch0 + tid % HC over the value range of part
   // tid / HC (the states are stored transposed: channel k of row v at v * KD + k,
   // so a wave reads consecutive channels)
@@ -1372,7 +1372,7 @@ size_t bw_units(const dn_backward_args* a) {
   return (size_t)a->B * a->H * NC;
 }
 
-constexpr size_t kUnitFloats = 6 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
+constexpr size_t kUnitFloats = 9 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
 
 int bw_check(const dn_backward_args* a) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
@@ -1415,7 +1415,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
   p.PT = take(KK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
-  p.dMw = take(CC); p.dAw = take(CC);
+  p.dMw = take(CC); p.dAw = take(CC); p.Rq = take(CK); p.Rk = take(CK); p.Rb = take(CK);
   p.S = take(KK); p.dS = take(KK);
 
   hipStream_t st = (hipStream_t)stream;

@@ -154,7 +154,7 @@ typedef struct dn_backward_args {
 } dn_backward_args;
 
 /* Workspace bytes dn_prefill_bwd needs (0 if the arguments are invalid):
- * about 449 KB per (batch, head, 64-token chunk). */
+ * about 545 KB per (batch, head, 64-token chunk). */
 size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
 
 /* Backward of the chunked recurrence: replaces the reference's custom-VJP
