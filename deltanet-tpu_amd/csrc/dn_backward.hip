@@ -60,6 +60,7 @@ struct BW {
   const float* init;
   const void* dout;      // cotangent of the output, element type dout_dt
   int dout_dt, dv_dt;    // DT_F32 or DT_BF16 (dv is written in dv_dt)
+  int v_dt;              // element type of v (DT_F32 or DT_BF16)
   const float* dfin;
   float *dq, *dk, *dv, *dg, *db, *dw, *dinit;
   // workspace, per unit u = (batch * H + head) * NC + chunk
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const bool vj = t0 + j < p.L;
       const int64_t ro = row_of(p, bb, vj ? t0 + j : 0, h) + r;
       wvw[s][e] = vj ? p.w[ro] : 0.f;
-      wvv[s][e] = vj ? p.v[ro] : 0.f;
+      wvv[s][e] = vj ? ld_f(p.v, ro, p.v_dt) : 0.f;
     }
   lds_barrier();
 
@@ -792,7 +793,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     const bool vi = t0 + i < p.L;
     const int64_t ro = row_of(p, bb, vi ? t0 + i : 0, h) + 4 * c4;
     wq[it] = vi ? ld4g(p.w + ro) : zero_f4();
-    vq[it] = vi ? ld4g(p.v + ro) : zero_f4();
+    vq[it] = vi ? ld4_dt(p.v, ro, p.v_dt) : zero_f4();
   }
   lds_barrier();   // Kc staged
 
@@ -1113,6 +1114,7 @@ struct BR {
   float scale; int l2norm, fuse, guard;
   int32_t* canon;                                 // (B, L)
   float *qe, *ke, *ve, *ge, *be, *we;             // (B, L, Hv, 128) prepared inputs
+  int w_alias;                                    // w's prologue step is the identity: we unused
   const float *dqe, *dke, *dge, *dbe, *dwe;       // their gradients
   float *dq, *dk, *dg, *db, *dw;                  // raw-layout gradients (dq, dk in qk_dt)
 };
@@ -1203,7 +1205,7 @@ __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
     p.ke[orow + i] = kh;
     p.ge[orow + i] = gv;
     p.be[orow + i] = bv;
-    p.we[orow + i] = wv;
+    if (!p.w_alias) p.we[orow + i] = wv;
     p.ve[orow + i] = ld_f(p.v, (bt * p.Hv + hv) * KD + i, p.v_dt);
   }
 }
@@ -1396,7 +1398,7 @@ extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
 }
 
 // the recurrence backward with the element types of d_out and dv given
-static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* workspace, size_t workspace_bytes,
+static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt, void* workspace, size_t workspace_bytes,
                     void* stream) {
   const int rc = bw_check(a);
   if (rc != DN_OK) return rc;
@@ -1407,7 +1409,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
   p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
   p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
   p.seg = a->seg; p.init = (const float*)a->init_state;
-  p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.dfin = (const float*)a->d_final;
+  p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.v_dt = v_dt; p.dfin = (const float*)a->d_final;
   p.dq = (float*)a->dq; p.dk = (float*)a->dk; p.dv = (float*)a->dv;
   p.dg = (float*)a->dg; p.db = (float*)a->db; p.dw = (float*)a->dw; p.dinit = (float*)a->d_init;
   const size_t units = bw_units(a);
@@ -1433,7 +1435,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, void* wor
 }
 
 extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  return bwd_core(a, DT_F32, DT_F32, workspace, workspace_bytes, stream);
+  return bwd_core(a, DT_F32, DT_F32, DT_F32, workspace, workspace_bytes, stream);
 }
 
 namespace {
@@ -1506,6 +1508,9 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   for (int i = 0; i < 11; ++i) { pre[i] = (float*)w; w += lay.pre; }
   r.qe = pre[0]; r.ke = pre[1]; r.ve = pre[2]; r.ge = pre[3]; r.be = pre[4]; r.we = pre[5];
   r.dqe = pre[6]; r.dke = pre[7]; r.dge = pre[8]; r.dbe = pre[9]; r.dwe = pre[10];
+  // the recurrence kernels read w in place when its prologue step is the
+  // identity on a per-value-head, channel-wise layout
+  r.w_alias = !a->fuse_prologue && !a->stability_guard && a->w_heads == a->Hv && a->w_chans == KD;
   r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
 
   hipStream_t st = (hipStream_t)stream;
@@ -1518,11 +1523,11 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   dn_backward_args c{};
   c.abi_version = DN_ABI_VERSION;
   c.B = a->B; c.L = a->L; c.H = a->Hv; c.K = KD; c.V = KD;
-  c.q = r.qe; c.k = r.ke; c.v = r.ve; c.g = r.ge; c.b = r.be; c.w = r.we;
+  c.q = r.qe; c.k = r.ke; c.v = r.ve; c.g = r.ge; c.b = r.be; c.w = r.w_alias ? a->w : r.we;
   c.seg = r.canon; c.init_state = a->init_state; c.d_out = d_out; c.d_final = d_final;
   c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
   c.d_init = d_init;
-  rc = bwd_core(&c, a->v_dtype, a->v_dtype, w, lay.core, stream);
+  rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, w, lay.core, stream);
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;
