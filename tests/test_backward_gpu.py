@@ -192,6 +192,23 @@ def test_backward_gate_layouts(layout):
     assert np.all(got["dinit"][1] == 0.0) and np.abs(got["dinit"][0]).max() > 0
 
 
+def test_backward_f16_inputs():
+    """f16 q, k, v: dq and dk come back in f16 from the kernel (v is carried in
+    f32 and its gradient cast back by autograd); scale 1 and no L2-norm, so the
+    forward sees the f16 values exactly and the oracle runs on them."""
+    B, L, Hk, Hv = 1, 200, 2, 4
+    q, k, v, g, b, w = ref_inputs(31, B, L, Hk, Hv)
+    qh, kh, vh = (x.astype(np.float16).astype(np.float64) for x in (q, k, v))
+    do = np.random.default_rng(32).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, qkv_dtype=torch.float16, precision="fp32", scale=1.0)
+    doh = do.astype(np.float16).astype(np.float64)   # the f16 output's cotangent is f16
+    ref = GR.chunk_gdn2_vjp(qh, kh, vh, g, b, w, doh, scale=1.0)
+    # scale 1 instead of 1/sqrt(K) makes the scores ~11x larger than in the
+    # reference's cases, and the fp32 rounding of the gate gradients with them
+    compare({n: got[n] for n in ("dg", "db", "dw")}, ref, 5e-5, "f16 q/k/v (f32 leaves)")
+    compare({n: got[n] for n in ("dq", "dk", "dv")}, ref, 2e-3, "f16 q/k/v (f16 leaves)")
+
+
 def test_backward_bf16_inputs_and_chunk_gdn():
     from deltanet_tpu_amd import chunk_gdn
     B, L, Hk, Hv = 1, 256, 2, 4
