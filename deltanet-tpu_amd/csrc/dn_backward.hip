@@ -29,8 +29,9 @@
 // Kernels (one launch each, in stream order):
 //   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G and
 //                the reverse scan's state-free term Xf^T dO
-//   k_bw_chain<false>  per (batch, head, 16-column tile): S_c for every chunk
-//   k_bw_chain<true>   same tiles, reverse: dS_{c+1} for every chunk, dS_0
+//   k_bw_chains  per (batch, head, 16-column tile) and direction, both scans in
+//                one launch: forward S_c for every chunk;
+//                reverse dS_{c+1} for every chunk, dS_0
 //   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA and the chunk-wide
 //                products of dq, dk, db
 //   k_bw_dqk     per (batch, head, chunk, quarter of the key channels): dq, dk,
@@ -516,7 +517,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 }
 
 // ---------------------------------------------------------------------------
-// k_bw_chain: one (batch, head, 16-column tile) per workgroup; the 128 x 16
+// chain_run: one (batch, head, 16-column tile) per workgroup; the 128 x 16
 // state tile lives in LDS in fragment order ([slab][lane][8]); wave w owns
 // rows 32w..32w+31.
 //   forward  (BWD = false):  Y = U0 - W S ;  S <- lam * S + Kc^T Y
@@ -553,15 +554,11 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
   if (!BWD) o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
 }
 
+// one scan over chain x = 8 * (batch * H + head) + column tile
 template <bool BWD>
-__global__ __launch_bounds__(256) void k_bw_chain(BW p) {
+__device__ __forceinline__ void chain_run(const BW& p, int x) {
   __shared__ float sS[4][64][8];
   __shared__ float sY[2][64][8];
-  const int chains = p.B * p.H * (KD / 16);
-  // chain x = 8 * (batch * H + head) + column tile; blocks b and b + 8 k share
-  // an XCD, so the 8 column tiles of a head run on one XCD, whose L2 serves
-  // their shared rows
-  const int x = ((int)blockIdx.x & 7) * (chains >> 3) + ((int)blockIdx.x >> 3);
   const int ct = x % (KD / 16), bh = x / (KD / 16);
   const int h = bh % p.H, bb = bh / p.H;
   const int col0 = 16 * ct;
@@ -651,6 +648,19 @@ __global__ __launch_bounds__(256) void k_bw_chain(BW p) {
         p.dinit[((int64_t)bh * KD + r) * KD + col0 + l16] = st[tt][e];
       }
   }
+}
+
+// Both scans in one launch: they are independent (both read only
+// k_bw_intra's products) and each waits mostly on its next chunk's operands,
+// so a forward and a reverse workgroup share each CU.  Blocks b and b + 8 n
+// land on the same XCD; each XCD runs C / 8 chains of each direction
+// (C = chains per direction, a multiple of 8), the 8 column tiles of a head
+// together.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_bw_chains(BW p, int C) {
+  const int b = blockIdx.x, per = C >> 3, s = b >> 3;
+  const int x = (b & 7) * per + s % per;
+  if (s < per) chain_run<false>(p, x);
+  else chain_run<true>(p, x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1424,8 +1434,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   const int chains = a->B * a->H * (KD / 16);
   prof_mark(4, st, false);
   hipLaunchKernelGGL(k_bw_intra, dim3((unsigned)units), dim3(NT), 0, st, p);
-  hipLaunchKernelGGL(k_bw_chain<false>, dim3(chains), dim3(256), 0, st, p);
-  hipLaunchKernelGGL(k_bw_chain<true>, dim3(chains), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_bw_chains, dim3(2 * chains), dim3(256), 0, st, p, chains);
   hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(NT), 0, st, p);
   hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * units)), dim3(NT), 0, st, p);
   prof_mark(4, st, true);
