@@ -1136,25 +1136,29 @@ __device__ __forceinline__ float sigmoid_hw(float x) { return __builtin_amdgcn_r
 
 // canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094)
 __global__ __launch_bounds__(256) void k_bw_canon(BR p) {
-  __shared__ int part[256];
-  const int bb = blockIdx.x, tid = threadIdx.x;
-  const int per = (p.L + 255) / 256;
-  const int t0 = tid * per, t1 = min(t0 + per, p.L);
+  __shared__ int wsum[4];
+  const int bb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t base = p.seg_batched ? (int64_t)bb * p.L : 0;
   auto sid = [&](int t) -> int64_t { return p.seg ? ld_i(p.seg, base + t, p.seg_dt) : 0; };
-  int cnt = 0;
-  for (int t = max(t0, 1); t < t1; ++t) cnt += sid(t) != sid(t - 1);
-  part[tid] = cnt;
-  __syncthreads();
-  if (tid == 0) {
-    int acc = (p.has_init && p.init_seg != nullptr) ? (sid(0) != (int64_t)p.init_seg[bb]) : 0;
-    for (int i = 0; i < 256; ++i) { const int c = part[i]; part[i] = acc; acc += c; }
-  }
-  __syncthreads();
-  int acc = part[tid];             // first_new + changes at positions 1 .. t0-1
-  for (int t = t0; t < t1; ++t) {
-    if (t > 0) acc += sid(t) != sid(t - 1);
-    p.canon[(int64_t)bb * p.L + t] = acc;
+  // tiles of 256 tokens: thread tid flags token ts + tid as a change from the
+  // token before it; a block-wide inclusive scan of the flags gives the ids
+  int run = (p.has_init && p.init_seg != nullptr) ? (sid(0) != (int64_t)p.init_seg[bb]) : 0;
+  for (int ts = 0; ts < p.L; ts += 256) {
+    const int t = ts + tid;
+    int f = (t > 0 && t < p.L) ? (sid(t) != sid(t - 1)) : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int x = __shfl_up(f, o);
+      if (lane >= o) f += x;
+    }
+    if (lane == 63) wsum[wid] = f;
+    __syncthreads();
+    int before = run;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) before += w < wid ? wsum[w] : 0;
+    if (t < p.L) p.canon[(int64_t)bb * p.L + t] = before + f;
+    run += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();   // wsum is rewritten by the next tile
   }
 }
 
