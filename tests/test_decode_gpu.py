@@ -139,10 +139,25 @@ def test_decode_stability_guard():
     B, Hk, Hv = 2, 2, 4
     q, k, v, g, b, w = dec_inputs(5, B, Hk, Hv)
     S = 10.0 * np.random.default_rng(4).standard_normal((B, Hv, 128, 128))
+    S[:, 1] *= 0.01   # value head 1 stays below the cap
     T = lambda x: to_dev(x)
     tau = 100.0
     o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), stability_guard=True, stability_tau=tau)
-    assert bool((torch.linalg.vector_norm(s, dim=(-2, -1)) <= tau * 1.001).all())
+    # independently: the guard's gate clamps by hand, no guard, then the cap
+    # must put capped heads on ||S||_F = tau along the uncapped direction and
+    # leave the others bit-identical (gdn2.py:2484-2487)
+    o_unc, s_unc = gdn2_decode_step(T(q), T(k), T(v), T(np.minimum(g, -1e-6)), T(np.maximum(b, 0.0)), T(w), T(S))
+    n_unc = torch.linalg.vector_norm(s_unc.double(), dim=(-2, -1))
+    norms = torch.linalg.vector_norm(s.double(), dim=(-2, -1))
+    capped = n_unc > tau
+    assert bool(capped.any()) and bool((~capped).any())
+    assert torch.allclose(norms[capped], torch.full_like(norms[capped], tau), rtol=1e-5, atol=0)
+    scale = tau / torch.sqrt(n_unc ** 2 + 1e-6)
+    assert torch.allclose(s.double()[capped], (s_unc.double() * scale[..., None, None])[capped], rtol=1e-5,
+                          atol=1e-6 * tau / 128)
+    assert torch.equal(s[~capped], s_unc[~capped])
+    # the step's output uses the uncapped state
+    assert torch.equal(o, o_unc)
     ro, rs = O.decode_step(q, k, v, g, b, w, S, stability_guard=True, stability_tau=tau)
     check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", "decode guard")
 

@@ -236,3 +236,106 @@ def test_bf16_round_matches_torch():
     x[:4] = [0.0, -0.0, 1.00390625, 1.01171875]  # exact ties: round to even
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(O.bf16_round(x), ref)
+
+
+# ----------------------------------------------------------------------------
+# frob_cap (gdn2.py:2180-2188 streaming cap, 2224-2226 final cap, 2484-2487
+# decode cap): pinned by what the cap must do, not by its formula
+# ----------------------------------------------------------------------------
+
+def test_frob_cap_properties():
+    rng = np.random.default_rng(30)
+    tau = 7.5
+    # a batch of matrices: some far above tau, some below, one exactly zero
+    S = rng.standard_normal((6, 16, 24))
+    S[0] *= 50.0          # ||S|| ~ 1000 >> tau
+    S[1] *= 3.0           # ||S|| ~ 60 > tau
+    S[2] *= 0.1           # ||S|| ~ 2 < tau
+    S[3] = 0.0
+    S[4] *= tau / np.linalg.norm(S[4]) * 0.999   # just below tau
+    S[5] *= tau / np.linalg.norm(S[5]) * 1.001   # just above tau
+    out = O.frob_cap(S, tau)
+    nrm = np.linalg.norm(S.reshape(6, -1), axis=1)
+    onrm = np.linalg.norm(out.reshape(6, -1), axis=1)
+    for i in range(6):
+        if nrm[i] > tau:
+            # capped: the Frobenius norm lands on tau (the 1e-6 inside the
+            # square root moves it by tau * 5e-7 / ||S||^2 at most)
+            assert abs(onrm[i] - tau) <= tau * 1e-6, (i, onrm[i])
+            # the direction is kept: a positive multiple of S
+            c = out[i] / S[i]
+            assert np.allclose(c, c.flat[0], rtol=1e-13) and c.flat[0] > 0
+        else:
+            # below the cap the matrix comes back bit-identical
+            assert np.array_equal(out[i], S[i]), i
+    # each matrix is capped on its own norm: capping one alone gives the same
+    for i in range(6):
+        assert np.array_equal(O.frob_cap(S[i:i + 1], tau)[0], out[i])
+    # idempotent up to the 1e-6 inside the square root (a relative change of
+    # 5e-7 / tau^2), and the cap of a scaled matrix does not depend on the scale
+    assert np.allclose(O.frob_cap(out, tau), out, rtol=1e-8, atol=0)
+    assert np.allclose(O.frob_cap(S[:2] * 10.0, tau), out[:2], rtol=1e-9)
+
+
+# ----------------------------------------------------------------------------
+# fused prologue (gdn2.py:133-142): pinned by inverse functions.  Raw inputs
+# built as graw = log(-g), braw = logit(b), wraw = logit(w) from activated
+# targets must reproduce the unfused result on the targets; graw above 5
+# saturates at g = -e^5.
+# ----------------------------------------------------------------------------
+
+def test_fused_prologue_by_inverse_functions():
+    B, L, Hk, Hv, K = 1, 24, 1, 2, K_SMALL
+    rng = np.random.default_rng(31)
+    q, k = rng.standard_normal((2, B, L, Hk, K))
+    v = rng.standard_normal((B, L, Hv, K))
+    g_t = -rng.uniform(0.05, 3.0, (B, L, Hk, K))          # target decay in (-e^5, 0)
+    b_t = rng.uniform(0.02, 0.98, (B, L, Hk, K))
+    w_t = rng.uniform(0.02, 0.98, (B, L, Hv, K))
+    graw = np.log(-g_t)
+    braw = np.log(b_t) - np.log1p(-b_t)
+    wraw = np.log(w_t) - np.log1p(-w_t)
+    o1, s1 = O.chunk_gdn2(q, k, v, graw, braw, wraw, fuse_prologue=True, qk_l2norm=True, output_final_state=True)
+    o2, s2 = O.chunk_gdn2(q, k, v, g_t, b_t, w_t, qk_l2norm=True, output_final_state=True)
+    # the fused path normalises q / k in fp32 (gdn2.py:133-137)
+    assert rel_l2(o1, o2) < 1e-6 and rel_l2(s1, s2) < 1e-6
+    # saturation: every raw decay above 5 acts as 5, i.e. g = -e^5
+    g_hi = graw.copy()
+    g_hi[:, ::3] = 5.0 + rng.uniform(0.0, 40.0, g_hi[:, ::3].shape)
+    g_5 = graw.copy()
+    g_5[:, ::3] = 5.0
+    oh, _ = O.chunk_gdn2(q, k, v, g_hi, braw, wraw, fuse_prologue=True, qk_l2norm=True)
+    o5, _ = O.chunk_gdn2(q, k, v, g_5, braw, wraw, fuse_prologue=True, qk_l2norm=True)
+    assert np.array_equal(oh, o5)
+    g_t5 = g_t.copy()
+    g_t5[:, ::3] = -np.exp(5.0)
+    ot, _ = O.chunk_gdn2(q, k, v, g_t5, b_t, w_t, qk_l2norm=True)
+    assert rel_l2(o5, ot) < 1e-6
+    # large raw gates saturate the sigmoids at 0 / 1: braw -> -inf erases
+    # nothing, wraw -> +inf writes the whole value
+    o_sat, _ = O.chunk_gdn2(q, k, v, graw, np.full_like(braw, -60.0), np.full_like(wraw, 60.0),
+                            fuse_prologue=True, qk_l2norm=True)
+    o_ref, _ = O.chunk_gdn2(q, k, v, g_t, np.zeros_like(b_t), np.ones_like(w_t), qk_l2norm=True)
+    assert rel_l2(o_sat, o_ref) < 1e-6
+
+
+def test_fused_prologue_decay_saturation_level():
+    # The saturated decay -e^5 is observable only through a state that is read
+    # after it: write k0 v0^T at token 0 (w = 1, no erase), decay with a raw
+    # gate above 5 at token 1, write nothing there (v1 = 0), and read.  Then
+    # o1 / o0 = e^{-e^5} (q1 . k0) / (q0 . k0) per column, in float64.
+    K = K_SMALL
+    rng = np.random.default_rng(32)
+    q, k = rng.standard_normal((2, 1, 2, 1, K))
+    v = rng.standard_normal((1, 2, 1, K))
+    v[:, 1] = 0.0
+    graw = np.full((1, 2, 1, K), 7.0)
+    braw = np.full((1, 2, 1, K), -np.inf)
+    wraw = np.full((1, 2, 1, K), np.inf)
+    o, _ = O.chunk_gdn2(q, k, v, graw, braw, wraw, fuse_prologue=True, qk_l2norm=True)
+    q32, k32 = q.astype(np.float32).astype(np.float64), k.astype(np.float32).astype(np.float64)
+    qn = q32[0, :, 0] / np.sqrt((q32[0, :, 0] ** 2).sum(-1, keepdims=True) + 1e-6)
+    kn = k32[0, :, 0] / np.sqrt((k32[0, :, 0] ** 2).sum(-1, keepdims=True) + 1e-6)
+    ratio = o[0, 1, 0] / o[0, 0, 0]
+    expect = np.exp(-np.exp(5.0)) * (qn[1] @ kn[0]) / (qn[0] @ kn[0])
+    assert np.allclose(ratio, expect, rtol=1e-9, atol=0)

@@ -152,12 +152,26 @@ def test_stability_guard_caps_state():
     # test_streaming_and_stability.py:93-112
     q, k, v, g, b, w = make_inputs(9, 1, 512, 2, 4, qscale=10.0)
     v = v * 100.0
+    v[:, :, 1] *= 1e-3   # value head 1 stays below the cap
     T = lambda x: to_dev(x)
     tau = 50.0
     o, s = chunk_gdn2(T(q), T(k), T(v), T(g), T(b), T(w), is_inference=True, output_final_state=True,
                       qk_l2norm=True, stability_guard=True, stability_tau=tau, precision="fp32")
-    norms = torch.linalg.vector_norm(s, dim=(-2, -1))
-    assert bool((norms <= tau * (1 + 1e-2)).all())
+    # The uncapped state, independently: the guard's input clamps applied by
+    # hand (gdn2.py:1972-1974) and no guard.  Capped heads must land on
+    # ||S||_F = tau along the uncapped direction (gdn2.py:2224-2226); heads
+    # below tau must come back bit-identical.
+    _, s_unc = chunk_gdn2(T(q), T(k), T(v), T(np.minimum(g, -1e-6)), T(np.maximum(b, 0.0)), T(w),
+                          is_inference=True, output_final_state=True, qk_l2norm=True, precision="fp32")
+    n_unc = torch.linalg.vector_norm(s_unc.double(), dim=(-2, -1))
+    norms = torch.linalg.vector_norm(s.double(), dim=(-2, -1))
+    capped = n_unc > tau
+    assert bool(capped.any()) and bool((~capped).any())
+    assert torch.allclose(norms[capped], torch.full_like(norms[capped], tau), rtol=1e-5, atol=0)
+    scale = tau / torch.sqrt(n_unc ** 2 + 1e-6)
+    assert torch.allclose(s.double()[capped], (s_unc.double() * scale[..., None, None])[capped], rtol=1e-5,
+                          atol=1e-6 * tau / 128)
+    assert torch.equal(s[~capped], s_unc[~capped])
     ro, rs = O.chunk_gdn2(q, k, v, g, b, w, output_final_state=True, qk_l2norm=True, stability_guard=True,
                           stability_tau=tau)
     check(o, ro, s, rs, "fp32", "fp32", "guard")
