@@ -42,13 +42,6 @@ constexpr int XP = 132;
 #endif
 constexpr int kValueWaves = DN_VALUE_WAVES;
 constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
-// 16-column tiles per chain workgroup.  One tile measured fastest: more tiles
-// share each chunk's Pn and X loads but lengthen the per-chunk MFMA work of
-// the recurrence and output waves.
-#ifndef DN_CHAIN_TILES
-#define DN_CHAIN_TILES 1
-#endif
-constexpr int kChainTiles = DN_CHAIN_TILES;
    // fp32 LDS pitch (floats): conflict-free 16-lane column groups
 
 // diag blocks whose in-block log2-decay span exceeds this use the
@@ -1183,201 +1176,198 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
 
 // ===========================================================================
 // k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c, and the output
-// O_c = X_c S_c + Oi_c of every chunk.
-// One workgroup of 12 waves per (NCT 16-column tiles, exec head, batch), in
-// two roles that meet at one LDS barrier per chunk:
-//   waves 0-3 (recurrence): wave w owns state rows 32w..32w+31 of the NCT
-//     column tiles (fp32, in VGPRs) and publishes them to LDS as slab w of
-//     each tile's S_c^T fragment (split high / low bf16 in bf16 mode); after
-//     the barrier it reads the fragments to form S_{c+1}.  Only 8 MFMAs per
-//     wave and tile sit on the sequential path.
-//   waves 4-11 (output): after the same barrier, wave 4+t reads the S_c^T
-//     fragments and computes token tile t of the NCT column tiles as
-//     O^T = S^T X^T + (M U)^T, beside the recurrence on the other wave
-//     slots of each SIMD.
-// Each role prefetches its next chunk's operands while the current one
-// computes.  The role is a scalar (wave-uniform) branch, and both roles
-// execute exactly one barrier per chunk.
+// O_c = X_c S_c + Oi_c of every chunk, for one 16-column value tile of one
+// exec head.  One workgroup of 8 waves in two roles that meet at one LDS
+// barrier per chunk:
+//   waves 0-3 (recurrence): wave w owns state rows 32w..32w+31 (fp32, in
+//     VGPRs) and publishes them to LDS as slab w of the S_c^T fragment
+//     (split high / low bf16 in bf16 mode); after the barrier it reads the
+//     whole fragment and forms S_{c+1}: two independent chains of 4 MFMAs
+//     on the sequential path.
+//   waves 4-7 (output): wave 4 + t computes token tiles 2t and 2t + 1 of the
+//     chunk as O^T = S^T X^T + (M U)^T from the same fragments, beside the
+//     recurrence on the other wave slot of each SIMD.
+// A chunk step is short next to the latency of its operand loads, so each
+// role keeps several chunks of operands in flight in VGPRs (ChainSets: the
+// number of operand sets; a chunk's loads are issued that many steps minus
+// one ahead).  Two waves per SIMD leave each wave 256 VGPRs for them.
+// The role is a scalar (wave-uniform) branch, and both roles execute exactly
+// one barrier per chunk.  Loop trips run whole groups of chunks and the
+// remainder runs after the loop: an exit in the middle of a trip would make
+// the loop head wait for every outstanding load, the prefetches included.
 // ===========================================================================
-template <bool BF, int NCT, class TO>
-__global__ __launch_bounds__(768) void k_chain(const PF p) {
+template <bool BF> struct ChainSets {
+  static constexpr int rec = 4, out = 3;
+};
+template <> struct ChainSets<false> {   // fp32 fragments are twice as wide
+  static constexpr int rec = 2, out = 3;
+};
+
+template <bool BF, class TO>
+__global__ __launch_bounds__(512) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
-  constexpr int NT = 768;
+  constexpr int NT = 512;
   constexpr int FR = 4 * 64 * 8;   // elements of one tile's S^T fragment
-  // S_c^T fragments per column tile, high and low words, double-buffered
-  __shared__ __align__(16) ST Sh_s[2][NCT * FR];
-  __shared__ __align__(16) ST Sl_s[2][BF ? NCT * FR : 1];
+  // S_c^T fragment, high and low words, double-buffered
+  __shared__ __align__(16) ST Sh_s[2][FR];
+  __shared__ __align__(16) ST Sl_s[2][BF ? FR : 1];
   __shared__ int flg[2 * kMaxBlockChunks];   // is_new_doc, all_same_doc per chunk
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, r16 = l & 15, q = l >> 4;
-  int cg, h, b;
-  xcd_block(cg, h, b);
-  const int ct0 = NCT * cg;
+  int ct, h, b;
+  xcd_block(ct, h, b);
+  const int hv = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
+  const int vc = (16 * ct) % KD;   // first column of the tile inside head hv
   auto frag_lo = [&](int buf) -> ST* { return BF ? &Sl_s[buf][0] : &Sh_s[buf][0]; };
   // chunk flags into LDS once, so testing them never waits on vector loads
   for (int i = tid; i < 2 * p.NCb; i += NT) flg[i] = p.flags[(int64_t)b * p.NCb * 2 + i];
   __syncthreads();
 
   if (wid < 4) {
-    // ---------------- recurrence: rows 32w.. of all NCT column tiles ----------------
+    // ---------------- recurrence: state rows 32w.. ----------------
+    constexpr int RS = ChainSets<BF>::rec;
     const int w = wid;
-    f32x4 S[2][NCT];
+    const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + vc + r16;
+    f32x4 S[2];
 #pragma unroll
-    for (int j = 0; j < NCT; ++j) {
-      const int n = 16 * (ct0 + j) + r16;
-      const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-      const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          S[r][j][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
-    }
+      for (int ii = 0; ii < 4; ++ii)
+        S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
     struct Ops {
       F1 pf[2][4];
-      f32x4 qc[2][NCT], dv[2];
+      f32x4 qc[2], dv[2];
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
       const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
       const ST* Pn = (const ST*)p.PnA + u * (KD * KD);
       const float* Qc = p.QC + u * (int64_t)(KD * p.Vp);
-      const float* dvp = p.dvec + u * KD;
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
-#pragma unroll
-        for (int j = 0; j < NCT; ++j) o.qc[r][j] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct0 + j, p.nct, l));
-        o.dv[r] = *reinterpret_cast<const f32x4*>(dvp + 32 * w + 16 * r + 4 * q);
+        o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
+        o.dv[r] = *reinterpret_cast<const f32x4*>(p.dvec + u * KD + 32 * w + 16 * r + 4 * q);
       }
     };
     auto step = [&](int c, const Ops& o) {
       const int is_new = flg[2 * c], same = flg[2 * c + 1];
-#pragma unroll
-      for (int j = 0; j < NCT; ++j) {
-        if (is_new) { S[0][j] = zero4(); S[1][j] = zero4(); }
-        // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
-        const float x[8] = {S[0][j][0], S[0][j][1], S[0][j][2], S[0][j][3],
-                            S[1][j][0], S[1][j][1], S[1][j][2], S[1][j][3]};
-        const int fo = j * FR + (w * 64 + l) * 8;
-        SS::st8s(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo, x);
-      }
+      if (is_new) { S[0] = zero4(); S[1] = zero4(); }
+      // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
+      const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
+      const int fo = (w * 64 + l) * 8;
+      SS::st8s(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo, x);
       lds_barrier();
+      F1 Sf[4];
 #pragma unroll
-      for (int j = 0; j < NCT; ++j) {
-        F1 Sf[4];
+      for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][(s * 64 + l) * 8]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][j * FR + (s * 64 + l) * 8]);
+      for (int r = 0; r < 2; ++r) {
+        f32x4 acc = o.qc[r];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          f32x4 acc = o.qc[r][j];
+        for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
 #pragma unroll
-          for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) S[r][j][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][j][ii] : 0.f);
-        }
+        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][ii] : 0.f);
       }
     };
-    Ops o0, o1;
-    load_ops(0, o0);
+    Ops o[RS];
+#pragma unroll
+    for (int j = 0; j + 1 < RS; ++j) load_ops(j, o[j]);
+    const int ntrip = p.NCb / RS;
 #pragma unroll 1
-    for (int c = 0; c < p.NCb; c += 2) {
-      load_ops(c + 1, o1);
-      step(c, o0);
-      if (c + 1 >= p.NCb) break;
-      load_ops(c + 2, o0);
-      step(c + 1, o1);
+    for (int k = 0; k < ntrip; ++k) {
+#pragma unroll
+      for (int j = 0; j < RS; ++j) {
+        load_ops(RS * k + j + RS - 1, o[(j + RS - 1) % RS]);
+        step(RS * k + j, o[j]);
+      }
     }
+    const int rem = p.NCb - RS * ntrip;   // < RS; their operands are loaded
 #pragma unroll
-    for (int j = 0; j < NCT; ++j) {
-      const int n = 16 * (ct0 + j) + r16;
-      const int hv = p.gates_at_hv ? h : h * p.G + n / KD;
-      const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + n % KD;
+    for (int j = 0; j + 1 < RS; ++j)
+      if (j < rem) step(RS * ntrip + j, o[j]);
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][j][ii];
-    }
+      for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
   } else {
-    // ---------------- output: token tile rt of all NCT column tiles ----------------
-    const int rt = wid - 4;
+    // ---------------- output: token tiles 2t, 2t + 1 ----------------
+    constexpr int OS = ChainSets<BF>::out;
+    const int t2 = 2 * (wid - 4);
     struct Ops {
-      F3 xb[4];      // X fragments of token tile rt
-      f32x4 oi[NCT]; // (M U)^T tiles of token tile rt
+      F3 xb[2][4];   // X fragments of the two token tiles
+      f32x4 oi[2];   // (M U)^T tiles of the two token tiles
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
       const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + cc;
       const ST* Xh = (const ST*)p.XAh + u * (CH * KD);
       const ST* Xl = (const ST*)p.XAl + u * (CH * KD);
-      const float* Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o.xb[s] = SS::fa3(Xh + fofs(rt, s, l), Xl + fofs(rt, s, l));
+      for (int r = 0; r < 2; ++r) {
 #pragma unroll
-      for (int j = 0; j < NCT; ++j) o.oi[j] = *reinterpret_cast<const f32x4*>(Oi + cofs(rt, ct0 + j, p.nct, l));
-    };
-    f32x4 res[NCT];
-    auto step = [&](int c, const Ops& o) {
-      lds_barrier();
-#pragma unroll
-      for (int j = 0; j < NCT; ++j) {
-        f32x4 acc = o.oi[j];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int fo = j * FR + (s * 64 + l) * 8;
-          P::m33(acc, SS::fa3(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo), o.xb[s]);
-        }
-        res[j] = acc;
+        for (int s = 0; s < 4; ++s) o.xb[r][s] = SS::fa3(Xh + fofs(t2 + r, s, l), Xl + fofs(t2 + r, s, l));
+        o.oi[r] = *reinterpret_cast<const f32x4*>(p.OiT + u * (int64_t)(CH * p.Vp) + cofs(t2 + r, ct, p.nct, l));
       }
     };
-    // lane (t, q) holds O[token 16rt + t][column 16ct + 4q + ii].  Every
-    // lane stores (tokens past the end into the workspace's sink): a store
-    // skipped under a branch would leave the compiler unsure how many
+    f32x4 res[2];
+    auto step = [&](int c, const Ops& o) {
+      lds_barrier();
+      res[0] = o.oi[0];
+      res[1] = o.oi[1];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int fs = (s * 64 + l) * 8;
+        const F3 sf = SS::fa3(&Sh_s[c & 1][fs], frag_lo(c & 1) + fs);
+        P::m33(res[0], sf, o.xb[0][s]);
+        P::m33(res[1], sf, o.xb[1][s]);
+      }
+    };
+    // lane (t, q) holds O[token 16 (t2 + r) + t][column 16ct + 4q + ii].
+    // Every lane stores (tokens past the end into the workspace's sink): a
+    // store skipped under a branch would leave the compiler unsure how many
     // vector-memory operations are pending at the loop head, and it would
     // then wait for all of them (the prefetches included).
     auto store = [&](int c) {
-      const int t = p.t0 + c * CH + 16 * rt + r16;
-      const bool tv = t < min(p.t0 + p.nt, p.L);
 #pragma unroll
-      for (int j = 0; j < NCT; ++j) {
-        const int ct = ct0 + j;
-        const int hvo = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
-        const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hvo) * KD + (16 * ct) % KD + 4 * q;
+      for (int r = 0; r < 2; ++r) {
+        const int t = p.t0 + c * CH + 16 * (t2 + r) + r16;
+        const bool tv = t < min(p.t0 + p.nt, p.L);
+        const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hv) * KD + vc + 4 * q;
         TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
-        const float x[4] = {res[j][0], res[j][1], res[j][2], res[j][3]};
+        const float x[4] = {res[r][0], res[r][1], res[r][2], res[r][3]};
         st4<TO>(dst, x);
       }
     };
     // Each chunk's prefetch is issued before its output store: the wait for
     // a prefetched operand then never covers a store (the vector-memory
     // counter counts stores too and drains in order).
-    Ops o0, o1;
-    load_ops(0, o0);
-    load_ops(1, o1);
-    // whole pairs of chunks in the loop, an odd last chunk after it (an exit
-    // in the middle of the loop body costs a full vector-memory drain at the
-    // loop head)
-    const int npair = p.NCb / 2;
+    Ops o[OS];
+#pragma unroll
+    for (int j = 0; j + 1 < OS; ++j) load_ops(j, o[j]);
+    const int ntrip = p.NCb / OS;
 #pragma unroll 1
-    for (int k = 0; k < npair; ++k) {
-      const int c = 2 * k;
-      step(c, o0);
-      load_ops(c + 2, o0);
-      store(c);
-      step(c + 1, o1);
-      load_ops(c + 3, o1);
-      store(c + 1);
+    for (int k = 0; k < ntrip; ++k) {
+#pragma unroll
+      for (int j = 0; j < OS; ++j) {
+        step(OS * k + j, o[j]);
+        load_ops(OS * k + j + OS - 1, o[(j + OS - 1) % OS]);
+        store(OS * k + j);
+      }
     }
-    if (p.NCb & 1) {
-      step(p.NCb - 1, o0);
-      store(p.NCb - 1);
-    }
+    const int rem = p.NCb - OS * ntrip;
+#pragma unroll
+    for (int j = 0; j + 1 < OS; ++j)
+      if (j < rem) {
+        step(OS * ntrip + j, o[j]);
+        store(OS * ntrip + j);
+      }
   }
 }
 
@@ -1490,7 +1480,7 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF, kChainTiles, TV>), dim3(p.Vp / (16 * kChainTiles), p.Hx, p.B), dim3(768), 0, st, p);
+  hipLaunchKernelGGL((k_chain<BF, TV>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
   prof_mark(2, st, true);
   return hipGetLastError();
 }
