@@ -38,7 +38,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def prefill_inputs(torch, dev, B=1, L=2048, Hk=12, Hv=24, K=128, seed=2):
+def prefill_inputs(torch, dev, B=1, L=2048, Hk=12, Hv=24, K=128, seed=2, packed=True):
+    """BASELINE config 2 inputs.  packed=False leaves each input in its own
+    allocation (wherever the caching allocator puts it)."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     rn = lambda *s: torch.randn(*s, device=dev, generator=g)
@@ -49,7 +51,52 @@ def prefill_inputs(torch, dev, B=1, L=2048, Hk=12, Hv=24, K=128, seed=2):
     w = torch.sigmoid(0.39 * rn(B, L, Hv, K))
     gg = -torch.exp(0.39 * rn(B, L, Hk, K) - 1.0)
     seg = (torch.arange(L, device=dev) >= 1024).to(torch.int32)[None].repeat(B, 1)
-    return _pack(torch, dev, (q, k, v, gg, b, w, seg))
+    t = (q, k, v, gg, b, w, seg)
+    return _pack(torch, dev, t) if packed else t
+
+
+def geometric_segments(torch, dev, gen, B, L, mean, lo=16):
+    """segment_ids of documents with geometric(1/mean) lengths clipped to [lo, L]."""
+    import numpy as np
+
+    rng = np.random.default_rng(gen)
+    seg = np.zeros((B, L), np.int32)
+    for b in range(B):
+        t, d = 0, 0
+        while t < L:
+            n = int(np.clip(rng.geometric(1.0 / mean), lo, L))
+            seg[b, t:t + n] = d
+            t += n
+            d += 1
+    return torch.from_numpy(seg).to(dev)
+
+
+def config3_inputs(torch, dev, B=4, L=8192, Hk=16, Hv=32, K=128, seed=3):
+    """BASELINE config 3 (chunk_gdn, Qwen3-Next scalar decay, packed documents)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = rn(B, L, Hk, K).to(torch.bfloat16)
+    k = rn(B, L, Hk, K).to(torch.bfloat16)
+    v = rn(B, L, Hv, K).to(torch.bfloat16)
+    a_log = math.log(1.0) + (math.log(16.0) - math.log(1.0)) * torch.rand(Hv, device=dev, generator=g)
+    gg = -torch.exp(a_log) * torch.nn.functional.softplus(rn(B, L, Hv))
+    beta = torch.sigmoid(rn(B, L, Hv))
+    seg = geometric_segments(torch, dev, seed, B, L, 1024)
+    return _pack(torch, dev, (q, k, v, gg, beta, seg))
+
+
+def config5_inputs(torch, dev, B=1, L=65536, Hk=16, Hv=32, K=128, seed=5):
+    """BASELINE config 5 (streaming prefill, fused prologue: raw gates)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = rn(B, L, Hk, K).to(torch.bfloat16)
+    k = rn(B, L, Hk, K).to(torch.bfloat16)
+    v = rn(B, L, Hv, K).to(torch.bfloat16)
+    gr, br, wr = rn(B, L, Hk, K), rn(B, L, Hk, K), rn(B, L, Hv, K)
+    seg = geometric_segments(torch, dev, seed, B, L, 8192)
+    return _pack(torch, dev, (q, k, v, gr, br, wr, seg))
 
 
 def _pack(torch, dev, tensors):
@@ -83,16 +130,24 @@ def decode_inputs(torch, dev, B=256, Hk=16, Hv=32, K=128, seed=4):
     return _pack(torch, dev, (q, k, v, gg, b, w, state))
 
 
-def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128):
-    """Algorithmic flops / bytes of config 2, split by kernel (per-(head, chunk)
-    figures of the chunked WY algorithm x the units one launch processes)."""
-    Vp = (Hv // Hk) * K
-    units = B * Hk * math.ceil(L / C)
+def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128, gates="channel"):
+    """Algorithmic flops / bytes of one prefill call, split by kernel
+    (per-(exec head, chunk) figures of the chunked WY algorithm x the units one
+    launch processes).  gates="channel": g, b of shape (B, L, Hk, K) and w of
+    shape (B, L, Hv, K), fp32 (chunk_gdn2); gates="scalar": g and beta of shape
+    (B, L, Hv), fp32 (chunk_gdn), so every value head is its own exec head."""
+    Hx = Hv if gates == "scalar" else Hk
+    Vp = (Hv // Hx) * K
+    units = B * Hx * math.ceil(L / C)
     f_pre = 6 * C * C * K + C ** 3 / 3                        # A, M, W = T be ; T
     f_val = 2 * C * C * Vp                                    # U = T (w*v)
     f_chain = 4 * C * K * Vp + 2 * C * K * Vp + 2 * C * C * Vp   # W S ; ke^T Vnew ; qe S ; M Vnew
-    qkgb_bytes = B * L * (2 * Hk * K * 2 + 2 * Hk * K * 4) + 4 * B * L
-    vw_bytes = B * L * (Hv * K * 2 + Hv * K * 4)
+    if gates == "scalar":
+        gate_k, gate_v = B * L * Hv * 4 * 2, 0                # g, beta (beta is also the write gate)
+    else:
+        gate_k, gate_v = 2 * B * L * Hk * K * 4, B * L * Hv * K * 4
+    qkgb_bytes = B * L * 2 * Hk * K * 2 + gate_k + 4 * B * L
+    vw_bytes = B * L * Hv * K * 2 + gate_v
     out_bytes = B * L * Hv * K * 2
     state_bytes = B * Hv * K * K * 4
     return dict(units=units, flops_total=units * (f_pre + f_val + f_chain),
@@ -100,6 +155,62 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128):
                 value=dict(flops=units * f_val, bytes=vw_bytes),
                 chain=dict(flops=units * f_chain, bytes=state_bytes + out_bytes),
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
+
+
+def kernel_times(torch, fn, n):
+    """Average device duration (us) per launch of each library kernel over n
+    calls of fn, from the profiler's activity trace (the same per-dispatch
+    timestamps rocprofv3 --kernel-trace reports; nothing is inserted into the
+    stream).  None if the profiler is unavailable (e.g. under rocprofv3)."""
+    try:
+        from torch.profiler import ProfilerActivity, profile
+
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for _ in range(n):
+                fn()
+            torch.cuda.synchronize()
+        out = {}
+        for e in prof.key_averages():
+            k = _kname(e.key)
+            if k and e.device_time_total > 0:
+                tot, cnt = out.get(k, (0.0, 0))
+                out[k] = (tot + e.device_time_total, cnt + e.count)
+        return {k: t / c for k, (t, c) in out.items()} or None
+    except Exception as ex:  # noqa: BLE001 - the bench line stands without it
+        log(f"kernel trace unavailable: {ex}")
+        return None
+
+
+def time_calls(torch, fn, steps, warmup):
+    """Wall time per call (ms), with a device synchronisation on both sides."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def roofline_of(work, t_us, name):
+    """Roofline entry of kernel `name` ("prepass" | "value" | "chain") at t_us per launch."""
+    wk = work[name]
+    t = t_us * 1e-6
+    if wk["bytes"] / (PEAK_HBM_GBPS * 1e9) >= wk["flops"] / (PEAK_BF16_TFLOPS * 1e12):
+        r = {"bound": "hbm", "achieved": wk["bytes"] / t / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
+    else:
+        r = {"bound": "mfma", "achieved": wk["flops"] / t / 1e12, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s"}
+    r["frac"] = r["achieved"] / r["peak"]
+    return r
+
+
+def step_roofline(work, ms):
+    t_roof = max(work["bytes_total"] / (PEAK_HBM_GBPS * 1e9), work["flops_total"] / (PEAK_BF16_TFLOPS * 1e12))
+    return {"t_roof_us": round(t_roof * 1e6, 2), "frac": round(t_roof / (ms * 1e-3), 4),
+            "bytes": work["bytes_total"], "flops": work["flops_total"],
+            "mfma_pct_peak": round(work["flops_total"] / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12) * 100, 3)}
 
 
 def backward_work(B=1, L=2048, H=24, K=128, V=128, C=64):
@@ -113,39 +224,50 @@ def backward_work(B=1, L=2048, H=24, K=128, V=128, C=64):
     return {"flops": 2 * mac * units, "units": units}
 
 
-def cpu_baseline(max_seconds=20.0):
+def cpu_baseline(inputs, gpu_out, gpu_state, max_seconds=20.0):
     """The C token-serial restatement (oracle/gdn_serial.c, fp32, OpenMP over
-    (batch, value head)) on this host's cores, on config 2 repeated."""
+    (batch, value head)) on this host's cores, on the bench's own config-2
+    inputs, repeated for about max_seconds.  The same leg checks the bench's
+    GPU output against one float64 run of the restatement on those inputs
+    (max |out - ref| / rms(ref), raw and net of the half-ulp rounding a bf16
+    output cannot avoid; relative Frobenius error of the final state)."""
     import numpy as np
 
     from oracle import c_oracle as C
     from oracle import gdn_oracle as O
 
-    rng = np.random.default_rng(0)
-    B, L, Hk, Hv, K = 1, 2048, 12, 24, 128
-    q = O.bf16_round(rng.standard_normal((B, L, Hk, K)))
-    k = O.bf16_round(rng.standard_normal((B, L, Hk, K)))
-    v = O.bf16_round(rng.standard_normal((B, L, Hv, K)))
-    b = 1 / (1 + np.exp(-0.39 * rng.standard_normal((B, L, Hk, K))))
-    w = 1 / (1 + np.exp(-0.39 * rng.standard_normal((B, L, Hv, K))))
-    g = -np.exp(0.39 * rng.standard_normal((B, L, Hk, K)) - 1)
-    seg = (np.arange(L) >= 1024).astype(np.int64)[None]
+    q, k, v, g, b, w, seg = (x.detach().float().cpu().numpy().astype(np.float64) for x in inputs)
+    B, L = q.shape[:2]
     threads = min(os.cpu_count() or 1, 16)
+    sg = O.canonical_segments(seg.astype(np.int64), B, L)
+    prep = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, qk_dtype="bf16", broadcast=False)
+    ref_o, ref_s = C.serial(*prep, sg, nthreads=threads, dtype=np.float64)
+    o = gpu_out.float().cpu().numpy().astype(np.float64)
+    s = gpu_state.float().cpu().numpy().astype(np.float64)
+    rms = float(np.sqrt(np.mean(ref_o ** 2)))
+    a = np.abs(ref_o).astype(np.float32).view(np.uint32)
+    half_ulp = 0.5 * (a & 0x7F800000).view(np.float32).astype(np.float64) * 2.0 ** -7
+    parity = {"out_maxabs_over_rms_raw": float(np.abs(o - ref_o).max() / rms),
+              "out_maxabs_over_rms_net_of_bf16_rounding": float(np.maximum(np.abs(o - ref_o) - half_ulp, 0).max() / rms),
+              "out_maxabs_over_rms_of_bf16_rounded_reference": float(np.abs(O.bf16_round(ref_o) - ref_o).max() / rms),
+              "state_rel_frob": float(np.linalg.norm(s - ref_s) / np.linalg.norm(ref_s)),
+              "bar": "north_star bf16: out max-abs <= 2e-2 of rms, final state rel Frobenius <= 1e-2",
+              "reference": "float64 token-serial restatement (oracle/gdn_serial.c) on the same inputs"}
     t0 = time.perf_counter()
     # the wrapper work (L2-norm, gate activation) is part of the measured CPU path
     reps, tok = 0, 0
     while True:
-        qh, kh, vv, ga, ba, wa = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, qk_dtype="bf16",
-                                                   broadcast=False)
-        C.serial(qh, kh, vv, ga, ba, wa, O.canonical_segments(seg, B, L), nthreads=threads, dtype=np.float32)
+        prep = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, qk_dtype="bf16", broadcast=False)
+        C.serial(*prep, sg, nthreads=threads, dtype=np.float32)
         reps += 1
         tok += B * L
         if time.perf_counter() - t0 >= max_seconds or reps >= 200:
             break
     dt = time.perf_counter() - t0
-    return {"value": tok / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 (B=1, L=2048, Hk=12, Hv=24) x {reps} full prefills, fp32 token-serial C "
-                      f"(oracle/gdn_serial.c, OpenMP over 24 (batch, value-head) chains), {dt:.1f} s"}
+    return ({"value": tok / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+             "sample": f"config 2 (B=1, L=2048, Hk=12, Hv=24, the bench's own inputs) x {reps} full prefills, "
+                       f"fp32 token-serial C (oracle/gdn_serial.c, OpenMP over 24 (batch, value-head) chains), "
+                       f"{dt:.1f} s"}, parity)
 
 
 PROFILE_DIR = os.path.join(ROOT, "profiles")
@@ -245,6 +367,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--train-steps", type=int, default=10,
                     help="forward + backward steps timed at the config-2 shape (0 = skip)")
+    ap.add_argument("--config-steps", type=int, default=12,
+                    help="calls timed for configs 3 and 5 (config 5 runs a quarter of them; 0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -257,7 +381,7 @@ def main():
 
     import torch
 
-    from deltanet_tpu_amd import _lib, chunk_gdn2, gdn2_decode_step
+    from deltanet_tpu_amd import _lib, chunk_gdn, chunk_gdn2, gdn2_decode_step
 
     dev = torch.device("cuda:0")
     q, k, v, g, b, w, seg = prefill_inputs(torch, dev)
@@ -267,40 +391,28 @@ def main():
         return chunk_gdn2(q, k, v, g, b, w, segment_ids=seg, is_inference=True, output_final_state=True,
                           qk_l2norm=True, precision="bf16", chunk_size=128)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    # per-kernel durations from HIP events on the launch stream, in a separate
-    # pass (the events themselves add inter-kernel gaps)
-    _lib.profile_begin()
-    for _ in range(args.steps):
-        step()
-    prof = _lib.profile_end()
+    ms_step = time_calls(torch, step, args.steps, args.warmup)
     tok_s = 2048 / (ms_step * 1e-3)
-    kern = {name: (ms / max(n, 1)) for name, (ms, n) in prof.items() if n}
+    # per-kernel device durations from the activity trace (uninstrumented);
+    # the HIP-event pass is only the fallback where the trace is unavailable
+    kern = kernel_times(torch, step, min(args.steps, 50))
+    kern_src = "profiler activity trace (per-dispatch device timestamps, as rocprofv3 --kernel-trace)"
+    if kern is None:
+        _lib.profile_begin()
+        for _ in range(args.steps):
+            step()
+        prof = _lib.profile_end()
+        kern = {f"k_{name}": ms * 1e3 / n for name, (ms, n) in prof.items() if n}
+        kern_src = "HIP events around each launch (instrumented: adds inter-kernel gaps)"
     log(f"prefill: {ms_step * 1e3:.1f} us/step; kernels (us): " +
-        ", ".join(f"{k_}={v_ * 1e3:.1f}" for k_, v_ in kern.items()))
+        ", ".join(f"{k_}={v_:.1f}" for k_, v_ in kern.items()))
 
     # dominant kernel and its roofline
-    dom = max(("prepass", "value", "chain"), key=lambda n: kern.get(n, 0.0))
-    t_dom = kern[dom] * 1e-3
-    wk = work[dom]
-    t_hbm = wk["bytes"] / (PEAK_HBM_GBPS * 1e9)
-    t_mfma = wk["flops"] / (PEAK_BF16_TFLOPS * 1e12)
-    if t_hbm >= t_mfma:
-        roof = {"bound": "hbm", "achieved": wk["bytes"] / t_dom / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
-    else:
-        roof = {"bound": "mfma", "achieved": wk["flops"] / t_dom / 1e12, "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s"}
-    roof["frac"] = roof["achieved"] / roof["peak"]
+    dom = max(("prepass", "value", "chain"), key=lambda n: kern.get(f"k_{n}", 0.0))
+    roof = roofline_of(work, kern[f"k_{dom}"], dom)
     roof["kernel"] = f"k_{dom}"
-    roof["avg_launch_us"] = kern[dom] * 1e3
+    roof["avg_launch_us"] = round(kern[f"k_{dom}"], 2)
+    roof["avg_launch_source"] = kern_src
     roof["traffic"] = None
     if os.path.exists(TRAFFIC_JSON):
         # HBM bytes per launch from the committed rocprofv3 --pmc summary
@@ -308,10 +420,56 @@ def main():
         if t:
             roof["traffic"] = round(t["traffic_bytes"])
             roof["traffic_source"] = os.path.relpath(TRAFFIC_JSON, ROOT)
+    sroof = step_roofline(work, ms_step)
 
-    # whole-step roofline (HBM-bound at this arithmetic intensity)
-    t_roof = max(work["bytes_total"] / (PEAK_HBM_GBPS * 1e9), work["flops_total"] / (PEAK_BF16_TFLOPS * 1e12))
-    mfma_pct = work["flops_total"] / (ms_step * 1e-3) / (PEAK_BF16_TFLOPS * 1e12) * 100
+    # the same workload with every input in its own allocation (the headline
+    # packs them into one arena, as a fused input projection would write them)
+    sq, sk, sv, sg, sb, sw, sseg = prefill_inputs(torch, dev, packed=False)
+    ms_scat = time_calls(torch, lambda: chunk_gdn2(sq, sk, sv, sg, sb, sw, segment_ids=sseg, is_inference=True,
+                                                   output_final_state=True, qk_l2norm=True, precision="bf16",
+                                                   chunk_size=128), args.steps, args.warmup)
+    del sq, sk, sv, sg, sb, sw, sseg
+    scattered = {"ms_per_step": round(ms_scat, 5), "tokens_per_s": round(2048 / (ms_scat * 1e-3), 1),
+                 "note": "config 2 with q, k, v, g, b, w, segment_ids each in a separate allocation"}
+    log(f"prefill, scattered inputs: {ms_scat * 1e3:.1f} us/step")
+
+    # ---- configs 3 and 5 (timed lines beside the headline) ------------------
+    others = {}
+    if args.config_steps > 0:
+        c3 = config3_inputs(torch, dev)
+        w3 = prefill_work(B=4, L=8192, Hk=16, Hv=32, gates="scalar")
+
+        def step3():
+            return chunk_gdn(c3[0], c3[1], c3[2], c3[3], c3[4], segment_ids=c3[5], is_inference=True,
+                             output_final_state=True, qk_l2norm=True, precision="bf16")
+
+        ms3 = time_calls(torch, step3, args.config_steps, 2)
+        others["config3"] = {"workload": "chunk_gdn prefill, BASELINE config 3: B=4 L=8192 Hk=16 Hv=32 K=V=128, "
+                                         "bf16 qkv, scalar fp32 g/beta per value head, geometric(1024) packed "
+                                         "documents, precision bf16, qk_l2norm, is_inference, chunk 128",
+                             "ms_per_call": round(ms3, 4), "tokens_per_s": round(4 * 8192 / (ms3 * 1e-3), 1),
+                             "step_roofline": step_roofline(w3, ms3),
+                             "kernels_us": {k_: round(v_, 2) for k_, v_ in (kernel_times(torch, step3, 3) or {}).items()}}
+        del c3
+        log(f"config 3: {ms3 * 1e3:.1f} us/call")
+        c5 = config5_inputs(torch, dev)
+        w5 = prefill_work(B=1, L=65536, Hk=16, Hv=32)
+
+        def step5():
+            return chunk_gdn2(c5[0], c5[1], c5[2], c5[3], c5[4], c5[5], segment_ids=c5[6], is_inference=True,
+                              output_final_state=True, qk_l2norm=True, fuse_prologue=True, precision="bf16",
+                              streaming_prefill=True, prefill_block_size=8192)
+
+        ms5 = time_calls(torch, step5, max(1, args.config_steps // 4), 1)
+        others["config5"] = {"workload": "chunk_gdn2 streaming prefill, BASELINE config 5: B=1 L=65536 Hk=16 Hv=32 "
+                                         "K=V=128, bf16 qkv, raw fp32 gates with fuse_prologue, geometric(8192) "
+                                         "documents, prefill_block_size 8192, precision bf16, qk_l2norm",
+                             "ms_per_call": round(ms5, 4), "tokens_per_s": round(65536 / (ms5 * 1e-3), 1),
+                             "step_roofline": step_roofline(w5, ms5),
+                             "kernels_us": {k_: round(v_, 2) for k_, v_ in (kernel_times(torch, step5, 1) or {}).items()}}
+        del c5
+        log(f"config 5: {ms5 * 1e3:.1f} us/call")
+        torch.cuda.empty_cache()
 
     # ---- decode (config 4) ------------------------------------------------
     dq, dk, dv, dg, db, dw, st = decode_inputs(torch, dev)
@@ -403,11 +561,13 @@ def main():
         copy_gbps = round(2 * src.numel() * 4 / dt / 1e9, 1)
         log(f"device copy of {src.numel() * 4 >> 20} MiB: {dt * 1e6:.1f} us, {copy_gbps} GB/s (read + write)")
 
-    cpu = None
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         try:
-            cpu = cpu_baseline(args.cpu_seconds)
-            log(f"cpu baseline: {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
+            o_gpu, s_gpu = step()
+            torch.cuda.synchronize()
+            cpu, parity = cpu_baseline((q, k, v, g, b, w, seg), o_gpu, s_gpu, args.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']:.1f} tokens/s on {cpu['cores']} threads; parity {parity}")
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline unavailable: {e}")
 
@@ -428,15 +588,18 @@ def main():
                                "bf16 qkv, fp32 gates, 2 segments, chunk 128, precision bf16, qk_l2norm, "
                                "is_inference, fp32 final state",
                    "B": 1, "L": 2048, "Hk": 12, "Hv": 24, "K": 128, "V": 128},
-        "mfma_pct_peak": round(mfma_pct, 3),
-        "step_roofline": {"t_roof_us": round(t_roof * 1e6, 2), "frac": round(t_roof / (ms_step * 1e-3), 4),
-                          "bytes": work["bytes_total"], "flops": work["flops_total"]},
-        "kernels_us": {k_: round(v_ * 1e3, 2) for k_, v_ in kern.items()},
+        "mfma_pct_peak": sroof["mfma_pct_peak"],
+        "step_roofline": sroof,
+        "kernels_us": {k_: round(v_, 2) for k_, v_ in kern.items()},
+        "kernels_us_source": kern_src,
+        "prefill_scattered_inputs": scattered,
+        "other_configs": others,
         "roofline": roof,
         "decode": {"workload": "gdn2_decode_step, BASELINE config 4: B=256 Hk=16 Hv=32 K=V=128, bf16 qkv, "
                                "channel-wise fp32 gates, qk_l2norm", **dec},
         "training": train,
         "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
     }
     print(json.dumps(line), flush=True)
 
