@@ -55,15 +55,18 @@ constexpr int NT = 64 * NWV;
 constexpr int TPW = 8 / NWV;  // 16-column tiles per wave in C x 128 products
 
 struct BW {
-  int B, L, H, NC;
+  int B, L, H, NC;       // NC: chunks of this launch's token block
+  int c0;                // first chunk of the block (token c0 * BC)
   const float *q, *k, *v, *g, *b, *w;
   const int32_t* seg;
-  const float* init;
+  const float* init;     // state entering the block's first chunk (NULL: zero)
+  float* sfin;           // NULL or: the forward scan's state leaving the block
   const void* dout;      // cotangent of the output, element type dout_dt
   int dout_dt, dv_dt;    // DT_F32 or DT_BF16 (dv is written in dv_dt)
   int v_dt;              // element type of v (DT_F32 or DT_BF16)
-  const float* dfin;
-  float *dq, *dk, *dv, *dg, *db, *dw, *dinit;
+  const float* dfin;     // gradient of the state leaving the block (NULL: zero)
+  float *dq, *dk, *dv, *dg, *db, *dw;
+  float* dinit;          // NULL or: the reverse scan's gradient of the state entering the block
   // workspace, per unit u = (batch * H + head) * NC + chunk
   float *G;    // [BC][KD] cumulative log2-decay from the chunk start
   float *Wm;   // [BC][KD] W
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 
   const int u = blockIdx.x;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
-  const int t0 = c * BC;
+  const int t0 = (p.c0 + c) * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   float* G = p.G + (int64_t)u * CK;
 
@@ -639,13 +642,14 @@ __device__ __forceinline__ void chain_run(const BW& p, int x) {
     step(chunk_at(it + 1), o1);
   }
   if (it < p.NC) step(chunk_at(it), o0);
-  if (BWD && p.dinit != nullptr) {
+  float* dst = BWD ? p.dinit : p.sfin;
+  if (dst != nullptr) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 32 * wv + 16 * tt + 4 * q + e;
-        p.dinit[((int64_t)bh * KD + r) * KD + col0 + l16] = st[tt][e];
+        dst[((int64_t)bh * KD + r) * KD + col0 + l16] = st[tt][e];
       }
   }
 }
@@ -655,7 +659,7 @@ __device__ __forceinline__ void chain_run(const BW& p, int x) {
 // so a forward and a reverse workgroup share each CU.  Blocks b and b + 8 n
 // land on the same XCD; each XCD runs C / 8 chains of each direction
 // (C = chains per direction, a multiple of 8), the 8 column tiles of a head
-// together.
+// together.  A launch of C blocks runs the forward scans only.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_bw_chains(BW p, int C) {
   const int b = blockIdx.x, per = C >> 3, s = b >> 3;
   const int x = (b & 7) * per + s % per;
@@ -731,7 +735,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 
   const int u = blockIdx.x;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
-  const int t0 = c * BC;
+  const int t0 = (p.c0 + c) * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   const int vcol = 16 * wv + l16;
   const float* S0 = p.S + (int64_t)u * KK;
@@ -924,7 +928,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
 
   const int u = blockIdx.x / NQ, part = blockIdx.x % NQ;
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
-  const int t0 = c * BC;
+  const int t0 = (p.c0 + c) * BC;
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   const int ch0 = HC * part;
   const float* G = p.G + (int64_t)u * CK;
@@ -1383,12 +1387,28 @@ using namespace dn;
 
 namespace {
 
-size_t bw_units(const dn_backward_args* a) {
+constexpr size_t kUnitFloats = 9 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
+
+// Chunks per token block: the whole sequence, or with recompute_states the
+// smallest number of chunks that still gives kRecomputeUnits (batch, head,
+// chunk) units per launch.
+constexpr int kRecomputeUnits = 1024;
+int bw_block_chunks(const dn_backward_args* a) {
   const int NC = (a->L + BC - 1) / BC;
-  return (size_t)a->B * a->H * NC;
+  if (!a->recompute_states) return NC;
+  const int bh = a->B * a->H;
+  return std::min(NC, std::max(1, (kRecomputeUnits + bh - 1) / bh));
 }
 
-constexpr size_t kUnitFloats = 9 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
+size_t bw_workspace_bytes(const dn_backward_args* a) {
+  const int NC = (a->L + BC - 1) / BC, ncb = bw_block_chunks(a);
+  const int nblk = (NC + ncb - 1) / ncb;
+  const size_t bh = (size_t)a->B * a->H;
+  // + the states at the nblk - 1 interior boundaries and one state gradient
+  // carried between blocks
+  const size_t extra = nblk > 1 ? (size_t)nblk * bh * KK : 0;
+  return (bh * ncb * kUnitFloats + extra) * sizeof(float);
+}
 
 int bw_check(const dn_backward_args* a) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
@@ -1408,7 +1428,7 @@ int bw_check(const dn_backward_args* a) {
 
 extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
   if (bw_check(a) != DN_OK) return 0;
-  return bw_units(a) * kUnitFloats * sizeof(float);
+  return bw_workspace_bytes(a);
 }
 
 // the recurrence backward with the element types of d_out and dv given
@@ -1416,31 +1436,64 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
                     void* stream) {
   const int rc = bw_check(a);
   if (rc != DN_OK) return rc;
-  const size_t need = bw_units(a) * kUnitFloats * sizeof(float);
+  const size_t need = bw_workspace_bytes(a);
   if (workspace == nullptr || workspace_bytes < need) return set_error(DN_E_WORKSPACE, "workspace too small");
+  const int NC = (a->L + BC - 1) / BC, ncb = bw_block_chunks(a);
+  const int nblk = (NC + ncb - 1) / ncb;
   BW p{};
-  p.B = a->B; p.L = a->L; p.H = a->H; p.NC = (a->L + BC - 1) / BC;
+  p.B = a->B; p.L = a->L; p.H = a->H;
   p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
   p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
-  p.seg = a->seg; p.init = (const float*)a->init_state;
-  p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.v_dt = v_dt; p.dfin = (const float*)a->d_final;
+  p.seg = a->seg;
+  p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.v_dt = v_dt;
   p.dq = (float*)a->dq; p.dk = (float*)a->dk; p.dv = (float*)a->dv;
-  p.dg = (float*)a->dg; p.db = (float*)a->db; p.dw = (float*)a->dw; p.dinit = (float*)a->d_init;
-  const size_t units = bw_units(a);
+  p.dg = (float*)a->dg; p.db = (float*)a->db; p.dw = (float*)a->dw;
+  const size_t bh = (size_t)a->B * a->H;
+  const size_t units = bh * ncb;   // per launch, at most
   float* ws = (float*)workspace;
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
   p.PT = take(KK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
   p.dMw = take(CC); p.dAw = take(CC); p.Rq = take(CK); p.Rk = take(CK); p.Rb = take(CK);
   p.S = take(KK); p.dS = take(KK);
+  // the state entering block j (j >= 1), (B, H, K, V) each, then the carried
+  // state gradient
+  float* ckpt = ws;
+  auto boundary = [&](int j) { return ckpt + (size_t)(j - 1) * bh * KK; };
+  float* dcarry = nblk > 1 ? boundary(nblk) : nullptr;
 
   hipStream_t st = (hipStream_t)stream;
   const int chains = a->B * a->H * (KD / 16);
+  auto block = [&](int j) {
+    p.c0 = j * ncb;
+    p.NC = std::min(ncb, NC - p.c0);
+    return (unsigned)(bh * p.NC);
+  };
   prof_mark(4, st, false);
-  hipLaunchKernelGGL(k_bw_intra, dim3((unsigned)units), dim3(NT), 0, st, p);
-  hipLaunchKernelGGL(k_bw_chains, dim3(2 * chains), dim3(256), 0, st, p, chains);
-  hipLaunchKernelGGL(k_bw_grads, dim3((unsigned)units), dim3(NT), 0, st, p);
-  hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * units)), dim3(NT), 0, st, p);
+  // forward pass: the states at the block boundaries (the only states kept)
+  for (int j = 0; j + 1 < nblk; ++j) {
+    const unsigned n = block(j);
+    p.init = j == 0 ? (const float*)a->init_state : boundary(j);
+    p.sfin = boundary(j + 1);
+    p.dfin = nullptr; p.dinit = nullptr;
+    hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL(k_bw_chains, dim3(chains), dim3(256), 0, st, p, chains);
+  }
+  // blocks from the last to the first: chunk products, both scans (the
+  // forward one from the block's boundary state), gradients; the reverse
+  // scan's state gradient at the block start carries into the block before
+  // it (read and written in place by the same lanes)
+  for (int j = nblk - 1; j >= 0; --j) {
+    const unsigned n = block(j);
+    p.init = j == 0 ? (const float*)a->init_state : boundary(j);
+    p.sfin = nullptr;
+    p.dfin = j == nblk - 1 ? (const float*)a->d_final : dcarry;
+    p.dinit = j == 0 ? (float*)a->d_init : dcarry;
+    hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL(k_bw_chains, dim3(2 * chains), dim3(256), 0, st, p, chains);
+    hipLaunchKernelGGL(k_bw_grads, dim3(n), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * n)), dim3(NT), 0, st, p);
+  }
   prof_mark(4, st, true);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
@@ -1463,7 +1516,8 @@ RawLayout raw_layout(const dn_prefill_args* a) {
   r.pre = (size_t)a->B * a->L * a->Hv * KD * sizeof(float);
   dn_backward_args c{};
   c.B = a->B; c.L = a->L; c.H = a->Hv;
-  r.core = bw_units(&c) * kUnitFloats * sizeof(float);
+  c.recompute_states = a->recompute_states;
+  r.core = bw_workspace_bytes(&c);
   return r;
 }
 
@@ -1540,6 +1594,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   c.seg = r.canon; c.init_state = a->init_state; c.d_out = d_out; c.d_final = d_final;
   c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
   c.d_init = d_init;
+  c.recompute_states = a->recompute_states;
   rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, w, lay.core, stream);
   if (rc != DN_OK) return rc;
 

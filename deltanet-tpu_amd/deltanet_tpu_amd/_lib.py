@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libdeltanet_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-DN_ABI_VERSION = 1
+DN_ABI_VERSION = 2
 DN_F32, DN_BF16, DN_F16, DN_I32, DN_I64 = 0, 1, 2, 3, 4
 
 _c_i32 = ctypes.c_int32
@@ -40,7 +40,7 @@ class PrefillArgs(ctypes.Structure):
         ("final_state", _c_ptr),
         ("scale", ctypes.c_float),
         ("qk_l2norm", _c_i32), ("fuse_prologue", _c_i32), ("stability_guard", _c_i32),
-        ("precision", _c_i32), ("gates_at_hv", _c_i32), ("block_tokens", _c_i32),
+        ("precision", _c_i32), ("gates_at_hv", _c_i32), ("block_tokens", _c_i32), ("recompute_states", _c_i32),
     ]
 
 
@@ -79,6 +79,7 @@ class BackwardArgs(ctypes.Structure):
         ("d_final", _c_ptr),
         ("dq", _c_ptr), ("dk", _c_ptr), ("dv", _c_ptr), ("dg", _c_ptr), ("db", _c_ptr), ("dw", _c_ptr),
         ("d_init", _c_ptr),
+        ("recompute_states", _c_i32),
     ]
 
 

@@ -119,9 +119,12 @@ def chunk_gdn2(
     Args and returns as the reference ``chunk_gdn2``.  With ``is_inference=False``
     and inputs that require grad, the call is differentiable under torch.autograd
     (backward: ``dn_prefill_bwd``, fp32, reference custom VJP gdn2.py:1446-1769).
-    Flags that only shape the reference's TPU backward or fallback
-    (``fallback_scan``, ``recompute_states``, ``truncate_bwd_dT_bf16``) are
-    accepted and change no result.  ``state_fp32_matmul=True`` runs the call at ``precision="fp32"``.
+    ``recompute_states=True`` runs that backward in token blocks, keeping only
+    the states at block boundaries and recomputing each block's chunk states
+    (reference gdn2.py:655-695, 1614-1630): less workspace, bit-identical
+    gradients.  Flags that only shape the reference's TPU fallback
+    (``fallback_scan``, ``truncate_bwd_dT_bf16``) are accepted and change no
+    result.  ``state_fp32_matmul=True`` runs the call at ``precision="fp32"``.
     ``mask_lambda_by_doc`` is accepted: the kernels never form a cumulative
     decay across a document boundary, so the flag's precision concern does
     not arise.
@@ -280,6 +283,7 @@ def chunk_gdn2(
     args.precision = 1 if fp32 else 0
     args.gates_at_hv = int(gates_at_hv)
     args.block_tokens = 0
+    args.recompute_states = int(bool(recompute_states))
 
     tensors = (q, k, v, g, b, w, initial_state)
 

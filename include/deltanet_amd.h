@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define DN_ABI_VERSION 1
+#define DN_ABI_VERSION 2
 
 /* element types */
 enum { DN_F32 = 0, DN_BF16 = 1, DN_F16 = 2, DN_I32 = 3, DN_I64 = 4 };
@@ -81,6 +81,11 @@ typedef struct dn_prefill_args {
   int32_t precision;            /* 0 = "bf16", 1 = "fp32"                        */
   int32_t gates_at_hv;          /* 1: execute per value head (g or b has Hv heads) */
   int32_t block_tokens;         /* internal token block (multiple of 128), 0=auto */
+  int32_t recompute_states;     /* training backward (dn_prefill_bwd_raw): keep only
+                                   token-block boundary states and recompute the
+                                   per-chunk states block by block, as
+                                   recompute_states=True (gdn2.py:1614-1630); the
+                                   gradients are bit-identical, the workspace smaller */
 } dn_prefill_args;
 
 /* Bytes of device workspace dn_prefill_fwd needs for these arguments. */
@@ -151,10 +156,22 @@ typedef struct dn_backward_args {
   const void* d_final;          /* NULL or (B,H,K,V) f32 cotangent of the final state */
   void *dq, *dk, *dv, *dg, *db, *dw;  /* f32, shapes of q k v g b w            */
   void* d_init;                 /* NULL or (B,H,K,V) f32 (needs init_state)       */
+  int32_t recompute_states;     /* 0: one pass over the whole sequence, every chunk's
+                                   state in the workspace.  1: token blocks, the
+                                   workspace holding one block's chunk products plus
+                                   the state at each block boundary; a forward pass
+                                   stores those states, then the blocks run from the
+                                   last to the first, each recomputing its chunk
+                                   states from the boundary state before it (the
+                                   reference's _recompute_chunk_states_kernel,
+                                   gdn2.py:655-695).  Bit-identical gradients. */
 } dn_backward_args;
 
 /* Workspace bytes dn_prefill_bwd needs (0 if the arguments are invalid):
- * about 545 KB per (batch, head, 64-token chunk). */
+ * about 545 KB per (batch, head, 64-token chunk); with recompute_states, 545 KB
+ * per (batch, head, chunk of one token block) plus 64 KB per (batch, head,
+ * interior block boundary).  The block is the smallest whole number of chunks
+ * giving at least 1024 (batch, head, chunk) units per launch. */
 size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
 
 /* Backward of the chunked recurrence: replaces the reference's custom-VJP
@@ -164,7 +181,8 @@ size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
 int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes dn_prefill_bwd_raw needs (0 if the arguments are invalid):
- * dn_prefill_bwd_workspace_size at H = Hv plus eleven (B,L,Hv,128) f32 arrays. */
+ * dn_prefill_bwd_workspace_size at H = Hv (with a->recompute_states) plus eleven
+ * (B,L,Hv,128) f32 arrays. */
 size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
 
 /* Backward of the whole training op from the forward's own arguments: the
@@ -178,7 +196,11 @@ size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
  * in the raw layouts, like the reference's VJP in the input dtypes: dq, dk
  * (B,L,Hk,K) in qk_dtype and dv (B,L,Hv,V) in v_dtype (f32 results rounded to
  * nearest even); dg, db, dw (B,L,H,C) of their gate and d_init NULL or
- * (B,Hv,K,V) in f32. */
+ * (B,Hv,K,V) in f32.  Every tensor must be dense row-major in the layout and
+ * element type the header gives (strides are implied, never passed): a
+ * channel-wise write gate at Hv heads with neither fuse_prologue nor
+ * stability_guard is read in place by the recurrence kernels, every other
+ * gate layout is first staged into the workspace. */
 int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
                        void* dq, void* dk, void* dv, void* dg, void* db, void* dw, void* d_init,
                        void* workspace, size_t workspace_bytes, void* stream);

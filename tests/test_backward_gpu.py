@@ -318,3 +318,101 @@ def test_backward_full_size_cfg2_vs_torch_fp32():
     print("[measured] cfg2 full size grads", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
     for n, e in errs.items():
         assert e < 1e-4, (n, e)
+
+
+@pytest.mark.parametrize("saturate, tol", [(False, 1e-5), (True, 1e-3)])
+def test_backward_fuse_prologue_with_guard(saturate, tol):
+    """fuse_prologue + stability_guard: raw g below ln(1e-6) (decay clamped to
+    -1e-6, zero gradient: gdn2.py:133-142, 1972-1974) and, with `saturate`,
+    above 5 (decay saturated at -e^5 per token, zero gradient), beside
+    ordinary values; raw b logits of both signs.  A per-token decay of -e^5 is
+    the strong-decay regime, checked at the reference's strong-decay
+    tolerance (tests/test_strong_decay.py: 1e-3 in fp32).  Exact ties (raw
+    g == 5) are avoided: the reference's minimum passes half the gradient
+    there, a measure-zero case."""
+    B, L, Hk, Hv, K, V = 1, 320, 2, 4, 128, 128
+    rng = np.random.default_rng(4242)
+    f = lambda *s: rng.standard_normal(s)
+    q, k, v = f(B, L, Hk, K) * 0.1, f(B, L, Hk, K) * 0.1, f(B, L, Hv, V) * 0.1
+    g = f(B, L, Hk, K) * 0.39 - 1.0
+    sel = rng.random(g.shape)
+    g = np.where(sel < 0.15, -16.0 - np.abs(f(B, L, Hk, K)), g)           # -exp(g) > -1e-6: clamped
+    if saturate:
+        g = np.where(sel > 0.9, 5.5 + np.abs(f(B, L, Hk, K)), g)          # saturated at -e^5
+    b = f(B, L, Hk, K) * 0.8
+    w = f(B, L, Hv, V) * 0.39
+    init = f(B, Hv, K, V) * 0.05
+    seg = np.array([[0] * 100 + [1] * 220], dtype=np.int32)
+    do, df = f(B, L, Hv, V), f(B, Hv, K, V)
+    kw = dict(qk_l2norm=True, fuse_prologue=True, stability_guard=True)
+    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32",
+                     segment_ids=torch.from_numpy(seg).cuda(), **kw)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, segment_ids=seg, **kw)
+    compare(got, ref, tol, f"fuse_prologue + guard, saturate={saturate}")
+    assert np.all(got["dg"][g < -14.0] == 0.0) and np.all(got["dg"][g > 5.0] == 0.0)
+    assert np.abs(got["dg"][(g > -3) & (g < 0)]).max() > 0
+
+
+@pytest.mark.parametrize("with_init", [False, True])
+def test_backward_recompute_states_bit_identical(with_init):
+    """recompute_states=True (token blocks, only block-boundary states kept,
+    chunk states recomputed per block: reference gdn2.py:655-695, 1614-1630)
+    gives gradients bit-identical to the single-pass backward.  B * Hv = 64
+    (batch, head) pairs make a block 16 chunks (1024 tokens), so L = 3000 runs
+    three blocks; document boundaries sit inside and across block edges."""
+    from deltanet_tpu_amd import chunk_gdn2
+
+    B, L, Hk, Hv = 2, 3000, 16, 32
+    rng = np.random.default_rng(77)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    q, k, v = f(B, L, Hk, 128), f(B, L, Hk, 128), f(B, L, Hv, 128)
+    g = -np.exp(0.39 * f(B, L, Hk, 128) - 1.0)
+    b, w = sig(0.39 * f(B, L, Hk, 128)), sig(0.39 * f(B, L, Hv, 128))
+    seg = np.zeros((B, L), np.int32)
+    seg[0, 1000:] = 1
+    seg[0, 1024:] = 2        # a document starting exactly at the first block edge
+    seg[1, 2100:] = 1
+    init = (0.05 * f(B, Hv, 128, 128)) if with_init else None
+    do, df = f(B, L, Hv, 128), f(B, Hv, 128, 128)
+    res = {}
+    for rc in (False, True):
+        ts = [to_dev(x, torch.bfloat16 if i < 3 else torch.float32).requires_grad_(True)
+              for i, x in enumerate((q, k, v, g, b, w))]
+        ti = to_dev(init).requires_grad_(True) if with_init else None
+        out, fin = chunk_gdn2(*ts, initial_state=ti, output_final_state=True, is_inference=False,
+                              segment_ids=torch.from_numpy(seg).cuda(), qk_l2norm=True, precision="bf16",
+                              recompute_states=rc)
+        ((out.float() * to_dev(do)).sum() + (fin * to_dev(df)).sum()).backward()
+        torch.cuda.synchronize()
+        res[rc] = {n: as_np(t.grad) for n, t in zip(NAMES, ts)}
+        if with_init:
+            res[rc]["dinit"] = as_np(ti.grad)
+    for n in res[False]:
+        a, c = res[False][n], res[True][n]
+        assert np.isfinite(a).all(), n
+        assert np.array_equal(a, c), f"{n}: max diff {np.abs(a.astype(np.float64) - c).max():.3e}"
+    print(f"[measured] recompute_states bit-identical over {len(res[False])} gradients", flush=True)
+
+
+def test_backward_w_in_place_and_staged_agree():
+    """dn_prefill_bwd_raw reads a per-value-head channel-wise w in place (no
+    staged copy) and stages every other layout.  The same write gate given
+    at Hv heads (read in place) and at Hk heads (staged, broadcast over the G
+    value heads of a key head) must give the same gradients: dq, dk, dv, dg,
+    db bit-identical, dw at Hk equal to the sum over each key head's G value
+    heads of dw at Hv."""
+    from deltanet_tpu_amd import chunk_gdn2
+
+    B, L, Hk, Hv = 2, 200, 2, 4
+    G = Hv // Hk
+    q, k, v, g, b, _ = ref_inputs(91, B, L, Hk, Hv)
+    w_hk = sig(np.random.default_rng(92).standard_normal((B, L, Hk, 128)) * 0.39)
+    w_hv = np.repeat(w_hk, G, axis=2)
+    do = np.random.default_rng(93).standard_normal((B, L, Hv, 128))
+    grads = {}
+    for name, w in (("in_place", w_hv), ("staged", w_hk)):
+        _, grads[name] = run_dev(q, k, v, g, b, w, do, precision="fp32")
+    for n in ("dq", "dk", "dv", "dg", "db"):
+        assert np.array_equal(grads["in_place"][n], grads["staged"][n]), n
+    dw_sum = grads["in_place"]["dw"].reshape(B, L, Hk, G, 128).sum(axis=3)
+    assert rel_l2(grads["staged"]["dw"], dw_sum) < 1e-6

@@ -121,3 +121,46 @@ def test_invalid_args_rejected_without_gpu():
     ra.g_heads = 3
     assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -1
     assert b"gate heads" in lib.dn_last_error()
+
+
+def test_recompute_states_workspace_size():
+    """recompute_states sizes the backward workspace for one token block (the
+    smallest whole number of 64-token chunks giving >= 1024 (batch, head,
+    chunk) units) plus one (B,H,128,128) f32 state per block boundary and one
+    carried state gradient; without it, every chunk of the sequence."""
+    lib = _lib.load_library()
+    unit = 4 * (9 * 64 * 128 + 4 * 64 * 64 + 128 + 3 * 128 * 128)   # bytes per (batch, head, chunk)
+    kk = 4 * 128 * 128
+    bw = _lib.BackwardArgs()
+    bw.abi_version = _lib.DN_ABI_VERSION
+    for f in ("q", "k", "v", "g", "b", "w", "d_out", "dq", "dk", "dv", "dg", "db", "dw"):
+        setattr(bw, f, 0x1000)
+    bw.K = bw.V = 128
+    for B, L, H in ((2, 3000, 32), (4, 8192, 32), (1, 2048, 24), (1, 128, 4)):
+        bw.B, bw.L, bw.H = B, L, H
+        NC = -(-L // 64)
+        bw.recompute_states = 0
+        full = lib.dn_prefill_bwd_workspace_size(ctypes.byref(bw))
+        assert full == B * H * NC * unit
+        bw.recompute_states = 1
+        rec = lib.dn_prefill_bwd_workspace_size(ctypes.byref(bw))
+        ncb = min(NC, max(1, -(-1024 // (B * H))))
+        nblk = -(-NC // ncb)
+        assert rec == B * H * ncb * unit + (nblk * B * H * kk if nblk > 1 else 0)
+        assert rec <= full
+        if nblk > 2:
+            assert rec < full / 2
+    # the raw entry sizes its core the same way
+    ra = _lib.PrefillArgs()
+    ra.abi_version = _lib.DN_ABI_VERSION
+    ra.B, ra.L, ra.Hk, ra.Hv, ra.K, ra.V = 4, 8192, 16, 32, 128, 128
+    for f in ("q", "k", "v", "g", "b", "w"):
+        setattr(ra, f, 0x1000)
+    ra.g_heads, ra.g_chans, ra.b_heads, ra.b_chans, ra.w_heads, ra.w_chans = 16, 128, 16, 128, 32, 128
+    ra.qk_dtype, ra.v_dtype = _lib.DN_BF16, _lib.DN_BF16
+    full = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
+    ra.recompute_states = 1
+    rec = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
+    pre = 11 * 4 * 8192 * 32 * 128 * 4
+    assert full - rec == (4 * 32 * 128 * unit) - (4 * 32 * 8 * unit + 16 * 4 * 32 * kk)
+    assert rec > pre
