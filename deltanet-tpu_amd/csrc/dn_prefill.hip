@@ -28,6 +28,8 @@
 // Intermediates live in a caller-provided workspace sized for one token
 // block, small enough to stay resident in the 256 MB Infinity Cache; every
 // array is stored in the MFMA lane order of its consumer.
+#include <mutex>
+
 #include "dn_common.h"
 #include "dn_host.h"
 
@@ -1428,12 +1430,19 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
 
 constexpr size_t kAutoBudget = size_t(160) << 20;
 
-int block_chunks(const dn_prefill_args* a, int Hx, int Vp) {
+// Chunks per token block: block_tokens when given, else the most that keep
+// the workspace within kAutoBudget.  A hard budget (the allocation-free entry
+// point's scratch) also caps a given block_tokens.
+int block_chunks(const dn_prefill_args* a, int Hx, int Vp, size_t budget = 0) {
   const int nct = (a->nt + CH - 1) / CH;
-  if (a->block_tokens > 0) return std::max(1, std::min(std::min(nct, kMaxBlockChunks), a->block_tokens / CH));
-  const bool bf = a->precision == 0;
   int ncb = std::min(nct, kMaxBlockChunks);
-  while (ncb > 1 && ws_layout(a, Hx, Vp, ncb, bf).total > kAutoBudget) ncb = (ncb + 1) / 2;
+  if (a->block_tokens > 0) {
+    ncb = std::max(1, std::min(ncb, a->block_tokens / CH));
+    if (budget == 0) return ncb;
+  }
+  if (budget == 0) budget = kAutoBudget;
+  const bool bf = a->precision == 0;
+  while (ncb > 1 && ws_layout(a, Hx, Vp, ncb, bf).total > budget) ncb = (ncb + 1) / 2;
   return std::max(1, ncb);
 }
 
@@ -1515,18 +1524,16 @@ extern "C" size_t dn_prefill_workspace_size(const dn_prefill_args* a) {
   return ws_layout(a, Hx, Vp, block_chunks(a, Hx, Vp), a->precision == 0).total;
 }
 
-extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  const int rc = check_args(a);
-  if (rc != DN_OK) return rc;
+namespace {
+
+// One dn_prefill_fwd call in token blocks of ncb chunks over the workspace ws.
+int prefill_run(const dn_prefill_args* a, char* ws, size_t workspace_bytes, int ncb, hipStream_t st) {
   const int G = a->Hv / a->Hk;
   const int Hx = a->gates_at_hv ? a->Hv : a->Hk;
   const int Vp = a->gates_at_hv ? KD : G * KD;
-  if (Vp % 64 != 0 || Vp > 1024) return set_error(DN_E_INVALID, "value width per execution head must be 64..1024");
   const bool bf = a->precision == 0;
-  const int ncb = block_chunks(a, Hx, Vp);
   const WsLayout Lw = ws_layout(a, Hx, Vp, ncb, bf);
-  if (workspace == nullptr || workspace_bytes < Lw.total) return set_error(DN_E_WORKSPACE, "workspace too small");
-  char* ws = (char*)workspace;
+  if (ws == nullptr || workspace_bytes < Lw.total) return set_error(DN_E_WORKSPACE, "workspace too small");
 
   PF p{};
   p.B = a->B; p.L = a->L; p.Hk = a->Hk; p.Hv = a->Hv; p.G = G; p.Hx = Hx; p.Vp = Vp;
@@ -1559,7 +1566,6 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
   p.WVl = bf ? ws + Lw.WVl : p.WVh;
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
 
-  hipStream_t st = (hipStream_t)stream;
   const int t_stop = a->t0 + a->nt;
   for (int tb = a->t0; tb < t_stop; tb += ncb * CH) {
     p.t0 = tb;
@@ -1578,4 +1584,77 @@ extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t 
     if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   }
   return DN_OK;
+}
+
+int prefill_shape_ok(const dn_prefill_args* a) {
+  const int rc = check_args(a);
+  if (rc != DN_OK) return rc;
+  const int G = a->Hv / a->Hk;
+  const int Vp = a->gates_at_hv ? KD : G * KD;
+  if (Vp % 64 != 0 || Vp > 1024) return set_error(DN_E_INVALID, "value width per execution head must be 64..1024");
+  return DN_OK;
+}
+
+}  // namespace
+
+extern "C" int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = prefill_shape_ok(a);
+  if (rc != DN_OK) return rc;
+  const int Hx = a->gates_at_hv ? a->Hv : a->Hk;
+  const int Vp = a->gates_at_hv ? KD : (a->Hv / a->Hk) * KD;
+  return prefill_run(a, (char*)workspace, workspace_bytes, block_chunks(a, Hx, Vp), (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free prefill: dn_prefill_fwd over a file-scope device scratch
+// array instead of a caller workspace.  Each GPU holds its own copy of
+// `scratch` (DN_NOALLOC_SCRATCH_BYTES) from the library's first use on it
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): the device
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and is the only handle used afterwards.
+// ---------------------------------------------------------------------------
+namespace {
+
+static __device__ __align__(256) char scratch[DN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// the current device's address of `scratch` (nullptr and an error set on failure)
+char* scratch_address() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(DN_E_LAUNCH, "no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error(DN_E_LAUNCH, e != hipSuccess ? hipGetErrorString(e) : "null scratch address");
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = (char*)ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int dn_prefill_fwd_noalloc(const dn_prefill_args* a, void* stream) {
+  const int rc = prefill_shape_ok(a);
+  if (rc != DN_OK) return rc;
+  const int Hx = a->gates_at_hv ? a->Hv : a->Hk;
+  const int Vp = a->gates_at_hv ? KD : (a->Hv / a->Hk) * KD;
+  const int ncb = block_chunks(a, Hx, Vp, DN_NOALLOC_SCRATCH_BYTES);
+  if (ws_layout(a, Hx, Vp, ncb, a->precision == 0).total > DN_NOALLOC_SCRATCH_BYTES)
+    return set_error(DN_E_WORKSPACE,
+                     "dn_prefill_fwd_noalloc: one 128-token chunk of every (batch, head) needs more than "
+                     "DN_NOALLOC_SCRATCH_BYTES of scratch; use dn_prefill_fwd with a workspace");
+  char* ws = scratch_address();
+  if (ws == nullptr) return DN_E_LAUNCH;
+  return prefill_run(a, ws, DN_NOALLOC_SCRATCH_BYTES, ncb, (hipStream_t)stream);
 }

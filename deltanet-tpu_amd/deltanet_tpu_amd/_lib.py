@@ -86,6 +86,7 @@ class BackwardArgs(ctypes.Structure):
 EXPORTED_SYMBOLS = (
     "dn_prefill_workspace_size",
     "dn_prefill_fwd",
+    "dn_prefill_fwd_noalloc",
     "dn_decode_step",
     "dn_decode_steps",
     "dn_prefill_bwd_workspace_size",
@@ -120,6 +121,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         lib.dn_prefill_workspace_size.restype = ctypes.c_size_t
         lib.dn_prefill_fwd.argtypes = [ctypes.POINTER(PrefillArgs), _c_ptr, ctypes.c_size_t, _c_ptr]
         lib.dn_prefill_fwd.restype = ctypes.c_int
+        lib.dn_prefill_fwd_noalloc.argtypes = [ctypes.POINTER(PrefillArgs), _c_ptr]
+        lib.dn_prefill_fwd_noalloc.restype = ctypes.c_int
         lib.dn_decode_step.argtypes = [ctypes.POINTER(DecodeArgs), _c_ptr]
         lib.dn_decode_step.restype = ctypes.c_int
         lib.dn_decode_steps.argtypes = [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr]

@@ -98,6 +98,20 @@ size_t dn_prefill_workspace_size(const dn_prefill_args* a);
  * (a hipStream_t; NULL = default stream); never synchronises. */
 int dn_prefill_fwd(const dn_prefill_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free prefill (no counterpart in the reference: for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, results and
+ * errors as dn_prefill_fwd, but the scratch is a file-scope device array of
+ * DN_NOALLOC_SCRATCH_BYTES that each GPU holds from the library's first use on
+ * it until the process ends; the call allocates nothing.  The token range is
+ * processed in blocks small enough for that scratch (bit-identical results);
+ * a shape whose single 128-token block of every (batch, head) does not fit is
+ * rejected with DN_E_WORKSPACE.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race, so the
+ * caller serialises them (one stream, or events between streams). */
+#define DN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int dn_prefill_fwd_noalloc(const dn_prefill_args* a, void* stream);
+
 /* Arguments of one single-token decode step (gdn2_decode_step, gdn2.py:2289-2490). */
 typedef struct dn_decode_args {
   int32_t abi_version;

@@ -164,3 +164,24 @@ def test_recompute_states_workspace_size():
     pre = 11 * 4 * 8192 * 32 * 128 * 4
     assert full - rec == (4 * 32 * 128 * unit) - (4 * 32 * 8 * unit + 16 * 4 * 32 * kk)
     assert rec > pre
+
+
+def test_noalloc_entry_refuses_oversized_shape():
+    """dn_prefill_fwd_noalloc refuses, before any launch, a shape whose single
+    128-token block of every (batch, head) needs more scratch than
+    DN_NOALLOC_SCRATCH_BYTES (64 MiB), and accepts the size check of one that
+    fits (then it would launch, so only the refusal runs here)."""
+    lib = _lib.load_library()
+    a = _lib.PrefillArgs()
+    a.abi_version = _lib.DN_ABI_VERSION
+    a.B, a.L, a.Hk, a.Hv, a.K, a.V = 64, 128, 16, 32, 128, 128
+    a.t0, a.nt = 0, 128
+    for f in ("q", "k", "v", "g", "b", "w", "out"):
+        setattr(a, f, 0x1000)
+    a.qk_dtype = a.v_dtype = _lib.DN_BF16
+    a.g_heads, a.g_chans, a.b_heads, a.b_chans, a.w_heads, a.w_chans = 16, 128, 16, 128, 32, 128
+    a.scale = 128 ** -0.5
+    assert lib.dn_prefill_fwd_noalloc(ctypes.byref(a), None) == -2
+    assert b"DN_NOALLOC_SCRATCH_BYTES" in lib.dn_last_error()
+    a.K = 64
+    assert lib.dn_prefill_fwd_noalloc(ctypes.byref(a), None) == -1
