@@ -157,11 +157,12 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128, gates="channel"):
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
 
 
-def kernel_times(torch, fn, n):
+def kernel_times(torch, fn, n, per_call=False):
     """Average device duration (us) per launch of each library kernel over n
-    calls of fn, from the profiler's activity trace (the same per-dispatch
-    timestamps rocprofv3 --kernel-trace reports; nothing is inserted into the
-    stream).  None if the profiler is unavailable (e.g. under rocprofv3)."""
+    calls of fn (per_call: the summed duration per call of fn), from the
+    profiler's activity trace (the same per-dispatch timestamps rocprofv3
+    --kernel-trace reports; nothing is inserted into the stream).  None if the
+    profiler is unavailable (e.g. under rocprofv3)."""
     try:
         from torch.profiler import ProfilerActivity, profile
 
@@ -176,7 +177,7 @@ def kernel_times(torch, fn, n):
             if k and e.device_time_total > 0:
                 tot, cnt = out.get(k, (0.0, 0))
                 out[k] = (tot + e.device_time_total, cnt + e.count)
-        return {k: t / c for k, (t, c) in out.items()} or None
+        return {k: t / (n if per_call else c) for k, (t, c) in out.items()} or None
     except Exception as ex:  # noqa: BLE001 - the bench line stands without it
         log(f"kernel trace unavailable: {ex}")
         return None
@@ -282,14 +283,18 @@ COPY_BYTES = 256 * 32 * 128 * 128 * 4   # the --copy-calibration copy (read and 
 
 
 def _kname(n):
+    """Short name of a library kernel from its (mangled) symbol, None for others."""
     if "copyBuffer" in n:
         return "copy (calibration)"
-    for k in ("k_prepass", "k_value", "k_chain", "k_output", "k_decode", "k_frob_cap"):
-        if k in n:
-            if k == "k_decode":
-                return "k_decode<bf16>" if ("DF16b" in n or "bf16" in n) else "k_decode<f32>"
-            return k
-    return None
+    import re
+
+    m = re.search(r"(k_[a-z0-9_]+)", n)
+    if not m or "dn" not in n:
+        return None
+    k = m.group(1)
+    if k == "k_decode":
+        return "k_decode<bf16>" if ("DF16b" in n or "bf16" in n) else "k_decode<f32>"
+    return k
 
 
 def rocprof_summary(kt_dir, f_dir, w_dir):
@@ -482,20 +487,22 @@ def main():
         def dstep(a, bb):
             return gdn2_decode_step(dq, dk, dv, dg, db, dw, a, qk_l2norm=True, state_dtype=sd, out_state=bb)
 
-        for _ in range(5):
-            dstep(s_in, s_out)
-        torch.cuda.synchronize()
-        _lib.profile_begin()
-        t0 = time.perf_counter()
-        a_, b_ = s_in, s_out
-        for _ in range(n):
-            dstep(a_, b_)
-            a_, b_ = b_, a_
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        dprof = _lib.profile_end()
-        us = (t1 - t0) * 1e6 / n
-        kus = dprof["decode"][0] * 1e3 / max(dprof["decode"][1], 1)
+        pair = [s_in, s_out]
+
+        def dstep2():
+            dstep(pair[0], pair[1])
+            pair.reverse()
+
+        us = time_calls(torch, dstep2, n, 5) * 1e3
+        kt = kernel_times(torch, dstep2, n)
+        if kt:
+            kus = next(v_ for k_, v_ in kt.items() if k_.startswith("k_decode"))
+        else:
+            _lib.profile_begin()
+            for _ in range(n):
+                dstep2()
+            dprof = _lib.profile_end()
+            kus = dprof["decode"][0] * 1e3 / max(dprof["decode"][1], 1)
         sbytes = 2 * st.numel() * elt
         dec[sd] = {"us_per_step": round(us, 2), "kernel_us": round(kus, 2),
                    "state_GBps": round(sbytes / (kus * 1e-6) / 1e9, 1),
@@ -527,14 +534,21 @@ def main():
             tstep()
         torch.cuda.synchronize()
         t_us = (time.perf_counter() - t0) * 1e6 / args.train_steps
-        _lib.profile_begin()
-        for _ in range(args.train_steps):
-            tstep()
-        torch.cuda.synchronize()
-        tprof = _lib.profile_end()
-        tk_us = {n: round(ms * 1e3 / args.train_steps, 1) for n, (ms, c) in tprof.items() if c}
+        tk_us = kernel_times(torch, tstep, args.train_steps, per_call=True)
+        if tk_us:
+            tk_us = {n: round(v_, 1) for n, v_ in tk_us.items()}
+            # the recurrence backward proper (the raw entry's prep / post kernels aside)
+            bw_us = sum(tk_us.get(n, 0.0) for n in ("k_bw_intra", "k_bw_chains", "k_bw_grads", "k_bw_dqk"))
+        else:
+            _lib.profile_begin()
+            for _ in range(args.train_steps):
+                tstep()
+            torch.cuda.synchronize()
+            tprof = _lib.profile_end()
+            tk_us = {n: round(ms * 1e3 / args.train_steps, 1) for n, (ms, c) in tprof.items() if c}
+            bw_us = tk_us.get("backward", 0.0)
         bw = backward_work(H=tv.shape[2])
-        bw_s = tk_us.get("backward", 0.0) * 1e-6
+        bw_s = bw_us * 1e-6
         train = {"workload": "chunk_gdn2 forward + backward (is_inference=False, autograd), config-2 shape, "
                              "precision bf16 forward, fp32 backward", "us_per_step": round(t_us, 1),
                  "kernels_us_per_step": tk_us,

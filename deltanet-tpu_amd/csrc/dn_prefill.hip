@@ -39,10 +39,8 @@ constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
 constexpr int XP = 132;
 // waves per k_value workgroup (each owns 32 value columns); 2 measured fastest
-#ifndef DN_VALUE_WAVES
-#define DN_VALUE_WAVES 2
-#endif
-constexpr int kValueWaves = DN_VALUE_WAVES;
+// at config 2 (more waves per group serialise on the shared T rows)
+constexpr int kValueWaves = 2;
 constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
    // fp32 LDS pitch (floats): conflict-free 16-lane column groups
 
@@ -198,15 +196,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   const int units = p.B * p.Hx * p.NCb;
   if ((int)blockIdx.x >= units) {
     // Spare workgroup (one per CU the chunk units leave idle): the value
-    // kernel's (w*v)^T fragments.  It first sleeps ~3 us, through most of
-    // the chunk units' HBM-bound entry loads (a fixed delay, not a wait on
-    // other workgroups: nothing here depends on another workgroup).  Measured
-    // at config 2: value 25.3 -> 21.2 us, prepass +1 us, step 88.4 -> 85.2 us.
-#ifndef DN_WV_SLEEP
-#define DN_WV_SLEEP 1
-#endif
-#pragma unroll
-    for (int i = 0; i < DN_WV_SLEEP; ++i) __builtin_amdgcn_s_sleep(127);
+    // kernel's (w*v)^T fragments, so k_value only reads them.
     const int groups = p.Vp / 32;
     const int nwave = (gridDim.x - units) * 8;
     for (int it = (blockIdx.x - units) * 8 + w; it < units * groups; it += nwave) {
