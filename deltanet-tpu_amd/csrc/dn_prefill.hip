@@ -1050,10 +1050,11 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 
-  // the 20 nonzero T fragments (lower slabs), loaded first so their latency
-  // overlaps the w*v loads from HBM
-  F1 Tf[20];
-  {
+  // the 20 nonzero T fragments (lower slabs).  bf16: loaded first so their
+  // latency overlaps the w*v loads from HBM.  fp32 (fragments twice as wide):
+  // loaded where they are used, which keeps the kernel out of scratch.
+  F1 Tf[BF ? 20 : 1];
+  if constexpr (BF) {
     int k = 0;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
@@ -1089,8 +1090,9 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
     for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
       for (int s = 0; s <= rt / 2; ++s) {
-        P::m13(Uc[0][rt], Tf[k], Bwv[0][s]);
-        P::m13(Uc[1][rt], Tf[k], Bwv[1][s]);
+        const F1 t = BF ? Tf[BF ? k : 0] : SS::fa(g_T + fofs(rt, s, l));
+        P::m13(Uc[0][rt], t, Bwv[0][s]);
+        P::m13(Uc[1][rt], t, Bwv[1][s]);
         ++k;
       }
     }
@@ -1418,7 +1420,12 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   return L;
 }
 
-constexpr size_t kAutoBudget = size_t(160) << 20;
+// Workspace budget of one call (token blocks beyond it run one after another).
+// Larger blocks mean fewer launches and longer chains per launch: at BASELINE
+// config 3 (8192 units) a 4 GiB budget measured 2.64 ms per call against
+// 2.91 ms at 160 MiB, and config 5's 8192-token streaming blocks run in one
+// launch each (4.15 ms against 5.47 ms); config 2 (147 MB) is unaffected.
+constexpr size_t kAutoBudget = size_t(4096) << 20;
 
 // Chunks per token block: block_tokens when given, else the most that keep
 // the workspace within kAutoBudget.  A hard budget (the allocation-free entry
