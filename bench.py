@@ -157,12 +157,17 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128, gates="channel"):
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
 
 
+_TRACE = {"on": True}
+
+
 def kernel_times(torch, fn, n, per_call=False):
     """Average device duration (us) per launch of each library kernel over n
     calls of fn (per_call: the summed duration per call of fn), from the
     profiler's activity trace (the same per-dispatch timestamps rocprofv3
     --kernel-trace reports; nothing is inserted into the stream).  None if the
     profiler is unavailable (e.g. under rocprofv3)."""
+    if not _TRACE["on"]:
+        return None
     try:
         from torch.profiler import ProfilerActivity, profile
 
@@ -275,10 +280,10 @@ PROFILE_DIR = os.path.join(ROOT, "profiles")
 TRAFFIC_JSON = os.path.join(PROFILE_DIR, "pmc_traffic_cfg2_cfg4.json")
 KT_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --stats "
           "--output-format csv -d gpurun_out/kt -o run -- python3 bench.py --no-cpu-baseline --steps 50 "
-          "--warmup 5 --decode-steps 16 --train-steps 0 --copy-calibration")
+          "--warmup 5 --decode-steps 16 --train-steps 0 --config-steps 0 --no-kernel-trace --copy-calibration")
 PMC_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --pmc {ctr} --output-format csv "
            "-d gpurun_out/{d} -o run -- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1 "
-           "--decode-steps 2 --train-steps 0 --copy-calibration")
+           "--decode-steps 2 --train-steps 0 --config-steps 0 --no-kernel-trace --copy-calibration")
 COPY_BYTES = 256 * 32 * 128 * 128 * 4   # the --copy-calibration copy (read and write this many bytes)
 
 
@@ -361,9 +366,102 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
     print("\n".join(lines))
 
 
+CFG_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --output-format csv "
+           "-d gpurun_out/ktc -o run -- python3 bench.py --no-cpu-baseline --steps 2 --warmup 1 --decode-steps 0 "
+           "--train-steps 0 --config-steps 4 --no-kernel-trace")
+
+
+def rocprof_configs_summary(kt_dir):
+    """profiles/prefill_cfg3_cfg5_rocprof.md from the CFG_CMD kernel trace: the
+    library kernels of configs 3 and 5, told apart by their launch grids."""
+    import csv
+    import collections
+
+    rows = collections.defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))):
+        k = _kname(r["Kernel_Name"])
+        if not k or k.startswith("copy"):
+            continue
+        grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"])) for a in "XYZ")
+        rows[(k, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    # config 2's grids (B=1, Hk=12, 16 chunks) are the few dispatches of the warm-up and timed cfg-2 calls
+    lines = ["# rocprofv3 kernel trace, configs 3 and 5 (bench.py other_configs)", "",
+             "Command:", "    " + CFG_CMD, "summarised by:", "    python bench.py --rocprof-configs-summary gpurun_out/ktc", "",
+             "Dispatches are grouped by kernel and launch grid (workgroups).  Config 3 (chunk_gdn, B=4, L=8192, "
+             "Hv=32 exec heads) and config 5 (L=65536 streamed in 8192-token blocks, Hk=16) launch distinct grids; "
+             "the config-2 calls of the same run are the 12-head grids.", "",
+             "| kernel | grid (workgroups) | dispatches | avg us | total us |", "|---|---|---|---|---|"]
+    for (k, grid), v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {k} | {grid[0]} x {grid[1]} x {grid[2]} | {len(v)} | {sum(v) / len(v):.1f} | {sum(v):.0f} |")
+    with open(os.path.join(PROFILE_DIR, "prefill_cfg3_cfg5_rocprof.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+BW_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --output-format csv "
+          "-d gpurun_out/bwkt -o run -- python3 bench.py --no-cpu-baseline --steps 2 --warmup 1 --decode-steps 0 "
+          "--train-steps 10 --config-steps 0 --no-kernel-trace")
+
+
+def rocprof_backward_summary(kt_dir):
+    """profiles/backward_cfg2_rocprof.md from the BW_CMD kernel trace."""
+    import csv
+    import collections
+    import re
+
+    dur = collections.defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))):
+        m = re.search(r"(k_bw_[a-z0-9_]+(?:<\d>)?)", r["Kernel_Name"])
+        if m:
+            dur[m.group(1)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    core = ("k_bw_intra", "k_bw_chains", "k_bw_grads", "k_bw_dqk")
+    bw = backward_work()
+    t_core = sum(sum(dur[k]) / len(dur[k]) for k in core if dur.get(k))
+    t_rest = sum(sum(v) / len(v) for k, v in dur.items() if k not in core)
+    lines = ["# rocprofv3 kernel trace: training backward (dn_prefill_bwd_raw), config-2 shape", "",
+             "Command (from the repository root on the GPU box):", "", "    " + BW_CMD, "",
+             "summarised by:", "", "    python bench.py --rocprof-backward-summary gpurun_out/bwkt", "",
+             "Workload: chunk_gdn2(is_inference=False) forward + backward under torch.autograd, B=1 L=2048 Hk=12 "
+             "Hv=24 K=V=128 (bf16 q/k/v, fp32 gates, 2 segments, qk_l2norm); the backward runs at H=24 value heads, "
+             "32 chunks of 64 tokens (768 (head, chunk) units), fp32 arithmetic (v_mfma_f32_16x16x4_f32).  The "
+             "first four kernels are the recurrence backward (dn_prefill_bwd's kernels); the rest are the raw-input "
+             "prologue recompute and the gradient sums back to the raw layouts.", "",
+             "| kernel | dispatches | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for k in sorted(dur, key=lambda k_: (k_ not in core, core.index(k_) if k_ in core else 0, k_)):
+        v = dur[k]
+        lines.append(f"| {k} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
+    lines += ["", f"Sum of the averages: {t_core:.0f} us for the recurrence backward (k_bw_chains runs the forward "
+              f"and the reverse state scans in one launch), {t_rest:.0f} us for the prologue and layout kernels.",
+              f"Algorithmic work of the recurrence backward (bench.py backward_work): {bw['flops'] / 1e9:.1f} GFLOP, "
+              f"i.e. {bw['flops'] / (t_core * 1e-6) / 1e12:.1f} TFLOP/s = "
+              f"{bw['flops'] / (t_core * 1e-6) / 1e12 / PEAK_FP32_TFLOPS * 100:.1f} % of the {PEAK_FP32_TFLOPS} "
+              f"TFLOP/s dense fp32 MFMA peak (floor {bw['flops'] / (PEAK_FP32_TFLOPS * 1e12) * 1e6:.0f} us)."]
+    with open(os.path.join(PROFILE_DIR, "backward_cfg2_rocprof.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def time_scattered(torch, dev, chunk_gdn2, args):
+    """Config 2 with every input in its own allocation (the headline packs them
+    into one arena, as a fused input projection would write them)."""
+    sq, sk, sv, sg, sb, sw, sseg = prefill_inputs(torch, dev, packed=False)
+    ms = time_calls(torch, lambda: chunk_gdn2(sq, sk, sv, sg, sb, sw, segment_ids=sseg, is_inference=True,
+                                              output_final_state=True, qk_l2norm=True, precision="bf16",
+                                              chunk_size=128), args.steps, args.warmup)
+    log(f"prefill, scattered inputs: {ms * 1e3:.1f} us/step")
+    return {"ms_per_step": round(ms, 5), "tokens_per_s": round(2048 / (ms * 1e-3), 1),
+            "note": "config 2 with q, k, v, g, b, w, segment_ids each in a separate allocation"}
+
+
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--rocprof-backward-summary":
+        rocprof_backward_summary(sys.argv[2])
+        return
     if len(sys.argv) == 5 and sys.argv[1] == "--rocprof-summary":
         rocprof_summary(*sys.argv[2:5])
+        return
+    if len(sys.argv) == 3 and sys.argv[1] == "--rocprof-configs-summary":
+        rocprof_configs_summary(sys.argv[2])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -375,6 +473,8 @@ def main():
     ap.add_argument("--config-steps", type=int, default=12,
                     help="calls timed for configs 3 and 5 (config 5 runs a quarter of them; 0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-trace", action="store_true",
+                    help="skip the profiler activity trace (for runs under rocprofv3, which traces itself)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC byte-counter scaling)")
@@ -387,6 +487,8 @@ def main():
     import torch
 
     from deltanet_tpu_amd import _lib, chunk_gdn, chunk_gdn2, gdn2_decode_step
+
+    _TRACE["on"] = not args.no_kernel_trace
 
     dev = torch.device("cuda:0")
     q, k, v, g, b, w, seg = prefill_inputs(torch, dev)
@@ -429,14 +531,9 @@ def main():
 
     # the same workload with every input in its own allocation (the headline
     # packs them into one arena, as a fused input projection would write them)
-    sq, sk, sv, sg, sb, sw, sseg = prefill_inputs(torch, dev, packed=False)
-    ms_scat = time_calls(torch, lambda: chunk_gdn2(sq, sk, sv, sg, sb, sw, segment_ids=sseg, is_inference=True,
-                                                   output_final_state=True, qk_l2norm=True, precision="bf16",
-                                                   chunk_size=128), args.steps, args.warmup)
-    del sq, sk, sv, sg, sb, sw, sseg
-    scattered = {"ms_per_step": round(ms_scat, 5), "tokens_per_s": round(2048 / (ms_scat * 1e-3), 1),
-                 "note": "config 2 with q, k, v, g, b, w, segment_ids each in a separate allocation"}
-    log(f"prefill, scattered inputs: {ms_scat * 1e3:.1f} us/step")
+    scattered = None
+    if not args.no_kernel_trace:   # (profiling runs keep to the headline layout)
+        scattered = time_scattered(torch, dev, chunk_gdn2, args)
 
     # ---- configs 3 and 5 (timed lines beside the headline) ------------------
     others = {}
@@ -479,7 +576,7 @@ def main():
     # ---- decode (config 4) ------------------------------------------------
     dq, dk, dv, dg, db, dw, st = decode_inputs(torch, dev)
     dec = {}
-    for sd, elt in (("float32", 4), ("bfloat16", 2)):
+    for sd, elt in (("float32", 4), ("bfloat16", 2)) if args.decode_steps > 0 else ():
         s_in = st if sd == "float32" else st.to(torch.bfloat16)
         s_out = torch.empty_like(s_in)
         n = args.decode_steps
