@@ -276,6 +276,85 @@ def cpu_baseline(inputs, gpu_out, gpu_state, max_seconds=20.0):
                        f"{dt:.1f} s"}, parity)
 
 
+def cpu_baselines_more(max_seconds=8.0):
+    """Further CPU legs on this host, each a bounded sample (about max_seconds):
+    config 1 (the reference's CPU-plumbing shape) with the C token-serial
+    restatement; config 2 with the float64 NumPy chunked-WY restatement
+    (oracle/gdn_oracle.py chunked_wy, one head at a time); the config-4 decode
+    step with the float64 NumPy restatement on a slice of the batch."""
+    import numpy as np
+
+    from oracle import c_oracle as C
+    from oracle import gdn_oracle as O
+
+    out = []
+    rng = np.random.default_rng(1)
+    threads = min(os.cpu_count() or 1, 16)
+
+    def timed(fn, unit_count):
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= max_seconds or reps >= 1000:
+                break
+        dt = time.perf_counter() - t0
+        return reps, dt, reps * unit_count / dt
+
+    # config 1: B=1, L=256, Hk=2, Hv=4, K=V=64, fp32
+    B, L, Hk, Hv, K = 1, 256, 2, 4, 64
+    f = lambda *s: rng.standard_normal(s)
+    q, k, v = f(B, L, Hk, K), f(B, L, Hk, K), f(B, L, Hv, K)
+    b, w = 1 / (1 + np.exp(-0.39 * f(B, L, Hk, K))), 1 / (1 + np.exp(-0.39 * f(B, L, Hv, K)))
+    g = -np.exp(0.39 * f(B, L, Hk, K) - 1)
+    seg = O.canonical_segments((np.arange(L) >= L // 2).astype(np.int64)[None], B, L)
+
+    def c1():
+        prep = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, broadcast=False)
+        C.serial(*prep, seg, nthreads=1, dtype=np.float32)
+
+    reps, dt, rate = timed(c1, B * L)
+    out.append({"config": 1, "value": rate, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"config 1 (B=1 L=256 Hk=2 Hv=4 K=V=64, fp32) x {reps}, C token-serial, {dt:.1f} s"})
+
+    # config 2, NumPy chunked WY (float64), heads in turn
+    B, L, Hk, Hv, K = 1, 2048, 12, 24, 128
+    q, k, v = (O.bf16_round(f(*s)) for s in ((B, L, Hk, K), (B, L, Hk, K), (B, L, Hv, K)))
+    b, w = 1 / (1 + np.exp(-0.39 * f(B, L, Hk, K))), 1 / (1 + np.exp(-0.39 * f(B, L, Hv, K)))
+    g = -np.exp(0.39 * f(B, L, Hk, K) - 1)
+    seg = O.canonical_segments((np.arange(L) >= 1024).astype(np.int64)[None], B, L)
+    qh, kh, vv, ga, ba, wa = O.prepare_prefill(q, k, v, g, b, w, qk_l2norm=True, qk_dtype="bf16")
+    heads = {"n": 0}
+
+    def c2():
+        h = heads["n"] % Hv
+        heads["n"] += 1
+        O.chunked_wy(qh[0, :, h], kh[0, :, h], vv[0, :, h], ga[0, :, h], ba[0, :, h], wa[0, :, h], seg[0])
+
+    reps, dt, rate = timed(c2, B * L / Hv)
+    out.append({"config": 2, "value": rate, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"config 2 (B=1 L=2048 Hk=12 Hv=24) NumPy float64 chunked WY, {reps} (head) "
+                          f"calls of the 24 a full prefill needs, {dt:.1f} s; tokens/s = reps / 24 x 2048 / s"})
+
+    # config 4 decode, NumPy float64, 16 of the 256 batch rows per call
+    Bs, Hk, Hv, K = 16, 16, 32, 128
+    st = 0.02 * f(Bs, Hv, K, K)
+    q, k, v = f(Bs, 1, Hk, K), f(Bs, 1, Hk, K), f(Bs, 1, Hv, K)
+    b, w = 1 / (1 + np.exp(-0.39 * f(Bs, 1, Hk, K))), 1 / (1 + np.exp(-0.39 * f(Bs, 1, Hv, K)))
+    g = -np.exp(0.39 * f(Bs, 1, Hk, K) - 1)
+
+    def c4():
+        O.decode_step(q, k, v, g, b, w, st, qk_l2norm=True)
+
+    reps, dt, rate = timed(c4, Bs / 256)
+    out.append({"config": 4, "value": 1e6 / rate, "unit": "us per full (B=256) decode step", "cores": 1,
+                "kind": "port", "higher_is_better": False,
+                "sample": f"config 4 decode step (Hk=16 Hv=32 K=V=128, fp32 state) NumPy float64 on 16 of the 256 "
+                          f"batch rows x {reps}, {dt:.1f} s; scaled to the full batch"})
+    return out
+
+
 PROFILE_DIR = os.path.join(ROOT, "profiles")
 TRAFFIC_JSON = os.path.join(PROFILE_DIR, "pmc_traffic_cfg2_cfg4.json")
 KT_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --stats "
@@ -679,6 +758,8 @@ def main():
             torch.cuda.synchronize()
             cpu, parity = cpu_baseline((q, k, v, g, b, w, seg), o_gpu, s_gpu, args.cpu_seconds)
             log(f"cpu baseline: {cpu['value']:.1f} tokens/s on {cpu['cores']} threads; parity {parity}")
+            cpu["more"] = cpu_baselines_more()
+            log(f"cpu baselines, other legs: {cpu['more']}")
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline unavailable: {e}")
 
