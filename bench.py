@@ -150,9 +150,9 @@ def prefill_work(B=1, L=2048, Hk=12, Hv=24, K=128, C=128, gates="channel"):
     vw_bytes = B * L * Hv * K * 2 + gate_v
     out_bytes = B * L * Hv * K * 2
     state_bytes = B * Hv * K * K * 4
+    # k_prepass computes the value products too (U, Q, M U) and reads v and w
     return dict(units=units, flops_total=units * (f_pre + f_val + f_chain),
-                prepass=dict(flops=units * f_pre, bytes=qkgb_bytes),
-                value=dict(flops=units * f_val, bytes=vw_bytes),
+                prepass=dict(flops=units * (f_pre + f_val), bytes=qkgb_bytes + vw_bytes),
                 chain=dict(flops=units * f_chain, bytes=state_bytes + out_bytes),
                 bytes_total=qkgb_bytes + vw_bytes + out_bytes + state_bytes)
 
@@ -201,7 +201,7 @@ def time_calls(torch, fn, steps, warmup):
 
 
 def roofline_of(work, t_us, name):
-    """Roofline entry of kernel `name` ("prepass" | "value" | "chain") at t_us per launch."""
+    """Roofline entry of kernel `name` ("prepass" | "chain") at t_us per launch."""
     wk = work[name]
     t = t_us * 1e-6
     if wk["bytes"] / (PEAK_HBM_GBPS * 1e9) >= wk["flops"] / (PEAK_BF16_TFLOPS * 1e12):
@@ -421,11 +421,10 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
              "| kernel | dispatches | avg us | min us | max us | fetch MB | write MB | algorithmic MB | "
              "traffic / algorithmic |",
              "|---|---|---|---|---|---|---|---|---|"]
-    alg = {"k_prepass": work["prepass"]["bytes"], "k_value": work["value"]["bytes"],
-           "k_chain": work["chain"]["bytes"],
+    alg = {"k_prepass": work["prepass"]["bytes"], "k_chain": work["chain"]["bytes"],
            "k_decode<f32>": 2 * 256 * 32 * 128 * 128 * 4, "k_decode<bf16>": 2 * 256 * 32 * 128 * 128 * 2,
            "copy (calibration)": 2 * COPY_BYTES}
-    for k in ("k_prepass", "k_value", "k_chain", "k_output", "k_decode<f32>", "k_decode<bf16>",
+    for k in ("k_prepass", "k_chain", "k_decode<f32>", "k_decode<bf16>",
               "copy (calibration)"):
         if k not in dur:
             continue
@@ -437,7 +436,7 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
         lines.append(f"| {k} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
                      f"{fb / 1e6:.1f} | {wb / 1e6:.1f} | {alg.get(k, 0) / 1e6:.1f} | "
                      f"{(fb + wb) / alg[k]:.2f} |")
-    lines += ["", "Prefill intermediates (workspace) travel between the three launches; their round trips "
+    lines += ["", "Prefill intermediates (workspace) travel between the two launches; their round trips "
               "are the traffic above the algorithmic bytes."]
     with open(os.path.join(PROFILE_DIR, "prefill_cfg2_decode_cfg4_rocprof.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -595,7 +594,7 @@ def main():
         ", ".join(f"{k_}={v_:.1f}" for k_, v_ in kern.items()))
 
     # dominant kernel and its roofline
-    dom = max(("prepass", "value", "chain"), key=lambda n: kern.get(f"k_{n}", 0.0))
+    dom = max(("prepass", "chain"), key=lambda n: kern.get(f"k_{n}", 0.0))
     roof = roofline_of(work, kern[f"k_{dom}"], dom)
     roof["kernel"] = f"k_{dom}"
     roof["avg_launch_us"] = round(kern[f"k_{dom}"], 2)

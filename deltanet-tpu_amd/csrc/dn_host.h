@@ -43,11 +43,7 @@ struct PF {
   void *KeBh, *KeBl;         // F  [8][4]      ST : (k e^{Lend - Lambda})^T, last document
   void *MAh, *MAl;           // F  [8][4]      ST : M, rows = token
   float* QeA;                // F  [8][4]      f32: q e^Lambda, first document
-  void* TA;                  // F  [8][4]      ST : T = (I + A)^-1
-  void *WVh, *WVl;           // F  [Vp/16][4]  ST : (w*v)^T, rows = value column (k_value B operand)
   void* sink;                // 1 KB the chain's output lanes past the last token store into
-  int wv_pre;                // WVh / WVl are produced by the prepass launch's spare workgroups
-  int wv_wgs;                // number of those spare workgroups
 };
 
 // Records the message for dn_last_error() and returns `code`.

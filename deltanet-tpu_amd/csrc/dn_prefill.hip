@@ -8,20 +8,18 @@
 //   wrapper   gdn2.py:1970-2125 (clamps, scale, L2-norm, gate broadcast,
 //                                segment canonicalisation, padding)
 //
-// The MI355X design splits the work into three launches per token block so
+// The MI355X design splits the work into two launches per token block so
 // that only a 128x128-by-128x16 product sits on the sequential critical path.
 // With Vnew = U - W S the reference's per-chunk update and output become
 //     S_next = [same doc] diag(e^Lend) S + Pn S + Q,  Pn = -ke^T W,  Q = ke^T U
 //     O      = X S + Oi,                              X = qe - M W,  Oi = M U
 // so:
 //   k_prepass (grid: one workgroup of 8 waves per (batch, exec head, chunk)
-//       unit, plus one spare workgroup per CU the units leave idle)
-//       fused prologue, Lambda, A and M on MFMA, T by blocked substitution
-//       on fp32 MFMA, W, and the chunk operators Pn and X; the spare
-//       workgroups form k_value's (w*v)^T fragments meanwhile.
-//   k_value   (grid: 64-column group x chunk x exec-head, 2 waves)
-//       U = T (w*v), Q = ke^T U and Oi = M U.
-//   k_chain   (grid: 16-column tile x exec-head x batch, 4 waves)
+//       unit) fused prologue, Lambda, A and M on MFMA, T by blocked
+//       substitution on fp32 MFMA, W, the chunk operators Pn and X, and
+//       then, from the T, ke^T and M it still holds in LDS, U = T (w*v),
+//       Q = ke^T U and Oi = M U (value_cols).
+//   k_chain   (grid: 16-column tile x exec-head x batch, 8 waves)
 //       the sequential scan over chunks with the fp32 state in VGPRs, and
 //       each chunk's output O = X S_c + Oi from the same S_c fragments.
 //
@@ -38,9 +36,6 @@ namespace dn {
 constexpr int CH = 128;   // chunk size (gdn2.py:1869)
 constexpr int KD = 128;   // key / value head dim (gdn2.py:1897)
 constexpr int XP = 132;
-// waves per k_value workgroup (each owns 32 value columns); 2 measured fastest
-// at config 2 (more waves per group serialise on the shared T rows)
-constexpr int kValueWaves = 2;
 constexpr int kMaxBlockChunks = 1024;   // chunks per token block (chain's LDS flag table)
    // fp32 LDS pitch (floats): conflict-free 16-lane column groups
 
@@ -158,7 +153,7 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
 // workgroup of 8 waves per (chunk, execution head, batch); wave w owns token
 // block w in the per-row phases and key tile w in phase 5): chunk flags,
 // Lambda, A and M, T = (I + A)^-1, W = T (b k e^Lambda), Pn = -ke^T W and
-// X = qe - M W; it also leaves T, ke^T and M for k_value.
+// X = qe - M W; then U, Q and (M U)^T of every value column (value_cols).
 //
 // Lambda is kept block-local: X[i] = sum of g over the 16-token block of i up
 // to and including i (log2 units, double-float hi in X / lo in Y), so a
@@ -171,7 +166,13 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
 // that puts the result directly in its consumer's fragment layout (M^T, Pn^T,
 // X^T); (b k e^Lambda)^T and ke^T are transposed by an identity product.
 // ===========================================================================
-template <bool BF, class TIn>
+template <bool BF, class TV, bool PRE_T>
+__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
+                                           const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
+                                           const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
+                                           const typename Store<BF>::ST* g_Ml);
+
+template <bool BF, class TIn, class TV>
 __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
@@ -194,31 +195,8 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
   const int units = p.B * p.Hx * p.NCb;
-  if ((int)blockIdx.x >= units) {
-    // Spare workgroup (one per CU the chunk units leave idle): the value
-    // kernel's (w*v)^T fragments, so k_value only reads them.
-    const int groups = p.Vp / 32;
-    const int nwave = (gridDim.x - units) * 8;
-    for (int it = (blockIdx.x - units) * 8 + w; it < units * groups; it += nwave) {
-      const int u = it / groups, col0 = 32 * (it % groups);
-      const int uc = u % p.NCb, uh = (u / p.NCb) % p.Hx, ub = u / (p.NCb * p.Hx);
-      F3 Bwv[2][4];
-      if (p.v_dt == DT_BF16) wv_frags<BF, bf16>(p, ub, uh, uc, col0, l, Bwv);
-      else wv_frags<BF, float>(p, ub, uh, uc, col0, l, Bwv);
-      const int64_t uw = (int64_t)u * (CH * p.Vp);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int o = fofs(col0 / 16 + nt, s, l);
-          SS::stf((ST*)p.WVh + uw + o, P::hi(Bwv[nt][s]));
-          if constexpr (BF) SS::stf((ST*)p.WVl + uw + o, Bwv[nt][s].lo);
-        }
-    }
-    return;
-  }
-  // chunk unit: the XCD-aware remap over the units only (the hardware deals
-  // linear block ids to the 8 XCDs round-robin; the spare workgroups come last)
+  // chunk unit: XCD-aware remap (the hardware deals linear block ids to the 8
+  // XCDs round-robin; consecutive chunks of a head share one XCD's L2)
   int c, h, b;
   {
     int id = blockIdx.x;
@@ -242,7 +220,6 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   ST* g_kel = (ST*)p.KeBl + uf;
   ST* g_Mh = (ST*)p.MAh + uf;
   ST* g_Ml = (ST*)p.MAl + uf;
-  ST* g_T = (ST*)p.TA + uf;
   float* g_qe = p.QeA + uf;
   float* g_dv = p.dvec + u * KD;
 
@@ -899,7 +876,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     }
     __syncthreads();
   }
-  // T in fragment-native layout: Y (LDS) for W here, global for k_value
+  // T in fragment-native layout in Y (LDS), for W and the value columns
   ST* Ts = reinterpret_cast<ST*>(Y);
   for (int idx = w; idx < 32; idx += 8) {
     const int rt = idx >> 2, s = idx & 3;
@@ -907,7 +884,6 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     float x[8];
     row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
     SS::st8(Ts + fofs(rt, s, l), x);
-    SS::st8(g_T + fofs(rt, s, l), x);
   }
   __syncthreads();
   // X (T in fp32) is free now: M high / low words there, ke^T high words
@@ -1019,42 +995,42 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
       x_tile(rt + 1, xb);
     }
   }
+  // ---- phase 6: U, Q and (M U)^T of value columns 32g.. (wave w: g = w, w + 8, ..)
+  // from the copies of T, M (and in bf16 mode ke^T's high words) phase 5
+  // read from LDS; ke^T's low words from the workspace (written in phase 2).
+  // One workgroup holding T, ke and M on chip replaces a separate launch
+  // that reloaded them once per 32 columns (config 2: 91 vs 94 µs per step,
+  // config 5: 3.7 vs 4.2 ms).
+  for (int g = w; g < p.Vp / 32; g += 8) value_cols<BF, TV, false>(p, b, h, c, 32 * g, l, Ts, keA, g_kel, Mh_s, Ml_s);
 }
 
 // ===========================================================================
-// k_value: U = T (w*v), Q = ke^T U and (M U)^T for one chunk and 32 x
-// kValueWaves value columns (wave w owns value tiles 2w, 2w+1 of its group).
-// Small workgroups spread the work evenly over the CUs (3 per CU at config 2).
+// value_cols: U = T (w*v), Q = ke^T U and (M U)^T for value columns
+// [col0, col0 + 32) of one chunk unit -- one wave's share, the last phase of
+// k_prepass.  The (w*v)^T fragments are formed here from v and w; T, ke^T
+// (high / low words) and M (high / low words) are the unit's fragment-native
+// arrays (LDS or workspace pointers).
 // ===========================================================================
-template <bool BF, class TV>
-__global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_eu(2))) void k_value(const PF p) {
+template <bool BF, class TV, bool PRE_T>
+__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
+                                           const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
+                                           const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
+                                           const typename Store<BF>::ST* g_Ml) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
   using SS = Store<BF>;
   using ST = typename SS::ST;
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
-  int c, pass, zh;
-  xcd_block(pass, c, zh);   // column passes of one chunk adjacent: one XCD's L2 serves T, ke, M
-  const int h = zh % p.Hx, b = zh / p.Hx;
-  const int tb = p.t0 + c * CH;
-  const int t_end = min(p.t0 + p.nt, p.L);
   const int64_t u = ((int64_t)b * p.Hx + h) * p.NCb + c;
-  const int64_t uf = u * (CH * KD);
-  const ST* g_T = (const ST*)p.TA + uf;
-  const ST* g_keh = (const ST*)p.KeBh + uf;
-  const ST* g_kel = (const ST*)p.KeBl + uf;
-  const ST* g_Mh = (const ST*)p.MAh + uf;
-  const ST* g_Ml = (const ST*)p.MAl + uf;
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 
-  // the 20 nonzero T fragments (lower slabs).  bf16: loaded first so their
-  // latency overlaps the w*v loads from HBM.  fp32 (fragments twice as wide):
-  // loaded where they are used, which keeps the kernel out of scratch.
-  F1 Tf[BF ? 20 : 1];
-  if constexpr (BF) {
+  // the 20 nonzero T fragments (lower slabs).  PRE_T: loaded first so their
+  // latency overlaps the w*v loads from HBM.  Otherwise (fp32 fragments are
+  // twice as wide; the prepass tail has T in L2) loaded where they are used,
+  // which keeps the kernel out of scratch.
+  F1 Tf[PRE_T ? 20 : 1];
+  if constexpr (PRE_T) {
     int k = 0;
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
@@ -1065,20 +1041,7 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
   // (w*v)^T fragments of this wave's 32 value columns (rows = column, k =
   // token): produced by the prepass launch's spare workgroups, or here
   F3 Bwv[2][4];
-  {
-    const int col0 = 32 * (kValueWaves * pass + w);   // first of this wave's 32 columns
-    if (p.wv_pre) {
-      const int64_t uw = u * (int64_t)(CH * p.Vp);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          Bwv[nt][s] = SS::fa3((const ST*)p.WVh + uw + fofs(col0 / 16 + nt, s, l),
-                               (const ST*)p.WVl + uw + fofs(col0 / 16 + nt, s, l));
-    } else {
-      wv_frags<BF, TV>(p, b, h, c, col0, l, Bwv);
-    }
-  }
+  wv_frags<BF, TV>(p, b, h, c, col0, l, Bwv);
   f32x4 Uc[2][8];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt)
@@ -1090,11 +1053,14 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
     for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
       for (int s = 0; s <= rt / 2; ++s) {
-        const F1 t = BF ? Tf[BF ? k : 0] : SS::fa(g_T + fofs(rt, s, l));
+        const F1 t = PRE_T ? Tf[PRE_T ? k : 0] : SS::fa(g_T + fofs(rt, s, l));
         P::m13(Uc[0][rt], t, Bwv[0][s]);
         P::m13(Uc[1][rt], t, Bwv[1][s]);
         ++k;
       }
+      // T read where it is used: keep the scheduler from hoisting every
+      // row's fragment reads ahead (that would need them all live at once)
+      if constexpr (!PRE_T) __builtin_amdgcn_sched_barrier(0);
     }
   }
   // U^T fragments (rows = value column, k = token)
@@ -1107,7 +1073,7 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
                           Uc[nt][2 * s + 1][0], Uc[nt][2 * s + 1][1], Uc[nt][2 * s + 1][2], Uc[nt][2 * s + 1][3]};
       U3[nt][s] = P::f3(x);
     }
-  const int ct0 = 2 * (kValueWaves * pass + w);   // value tile of nt = 0 within the execution head
+  const int ct0 = col0 / 16;   // value tile of nt = 0 within the execution head
   // Q tiles (rows = key, columns = value), the chain's accumulator layout
   auto q_tile = [&](int m, const F3 (&ka)[4]) {
     f32x4 Q0 = zero4(), Q1 = zero4();
@@ -1167,6 +1133,7 @@ __global__ __launch_bounds__(64 * kValueWaves) __attribute__((amdgpu_waves_per_e
     }
   }
 }
+
 
 // ===========================================================================
 // k_chain: S_{c+1} = [same doc] D_c S_c + Pn_c S_c + Q_c, and the output
@@ -1371,23 +1338,10 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
 namespace {
 
 struct WsLayout {
-  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, TA, WVh, WVl, sink, carry, total;
+  size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, sink, carry, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-// compute units of the current device (queried once per device)
-int num_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = -1;
-    cache[dev] = n > 0 ? n : -1;
-  }
-  return cache[dev] > 0 ? cache[dev] : 0;
-}
 
 // Split operands (X, St, ke^T, M) have a low-word array in bf16 mode only.
 WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
@@ -1411,9 +1365,6 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   L.MAh = take(units * sq * es);
   L.MAl = take(units * sq * ls);
   L.QeA = take(units * sq * 4);
-  L.TA = take(units * sq * es);
-  L.WVh = take(units * CH * Vp * es);
-  L.WVl = take(units * CH * Vp * ls);
   L.sink = take(64 * 16);
   L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
   L.total = off;
@@ -1475,15 +1426,9 @@ int check_args(const dn_prefill_args* a) {
 template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_prepass<BF, TIn>), dim3(p.B * p.Hx * p.NCb + p.wv_wgs), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((k_prepass<BF, TIn, TV>), dim3(p.B * p.Hx * p.NCb), dim3(512), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  prof_mark(1, st, false);
-  hipLaunchKernelGGL((k_value<BF, TV>), dim3(p.Vp / (32 * kValueWaves), p.NCb, p.Hx * p.B), dim3(64 * kValueWaves), 0,
-                     st, p);
-  prof_mark(1, st, true);
-  e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
   hipLaunchKernelGGL((k_chain<BF, TV>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
@@ -1557,10 +1502,7 @@ int prefill_run(const dn_prefill_args* a, char* ws, size_t workspace_bytes, int 
   p.MAh = ws + Lw.MAh;
   p.MAl = bf ? ws + Lw.MAl : p.MAh;
   p.QeA = (float*)(ws + Lw.QeA);
-  p.TA = ws + Lw.TA;
   p.sink = ws + Lw.sink;
-  p.WVh = ws + Lw.WVh;
-  p.WVl = bf ? ws + Lw.WVl : p.WVh;
   float* carry = a->final_state ? a->final_state : (float*)(ws + Lw.carry);
 
   const int t_stop = a->t0 + a->nt;
@@ -1568,11 +1510,6 @@ int prefill_run(const dn_prefill_args* a, char* ws, size_t workspace_bytes, int 
     p.t0 = tb;
     p.nt = std::min(ncb * CH, t_stop - tb);
     p.NCb = (p.nt + CH - 1) / CH;
-    // CUs the chunk units leave idle during the prepass (one unit per CU)
-    // take the (w*v)^T fragments off the value kernel
-    const int units = p.B * p.Hx * p.NCb;
-    p.wv_wgs = units < num_cus() ? num_cus() - units : 0;
-    p.wv_pre = p.wv_wgs > 0;
     const bool first = tb == a->t0;
     p.has_init = first ? (a->init_state != nullptr) : 1;
     p.init = first ? a->init_state : carry;
