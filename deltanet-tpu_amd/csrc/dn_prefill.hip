@@ -166,7 +166,7 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
 // that puts the result directly in its consumer's fragment layout (M^T, Pn^T,
 // X^T); (b k e^Lambda)^T and ke^T are transposed by an identity product.
 // ===========================================================================
-template <bool BF, class TV, bool PRE_T>
+template <bool BF, class TV>
 __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
                                            const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
                                            const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
@@ -1001,7 +1001,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   // One workgroup holding T, ke and M on chip replaces a separate launch
   // that reloaded them once per 32 columns (config 2: 91 vs 94 µs per step,
   // config 5: 3.7 vs 4.2 ms).
-  for (int g = w; g < p.Vp / 32; g += 8) value_cols<BF, TV, false>(p, b, h, c, 32 * g, l, Ts, keA, g_kel, Mh_s, Ml_s);
+  for (int g = w; g < p.Vp / 32; g += 8) value_cols<BF, TV>(p, b, h, c, 32 * g, l, Ts, keA, g_kel, Mh_s, Ml_s);
 }
 
 // ===========================================================================
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
 // (high / low words) and M (high / low words) are the unit's fragment-native
 // arrays (LDS or workspace pointers).
 // ===========================================================================
-template <bool BF, class TV, bool PRE_T>
+template <bool BF, class TV>
 __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
                                            const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
                                            const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
@@ -1025,21 +1025,7 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 
-  // the 20 nonzero T fragments (lower slabs).  PRE_T: loaded first so their
-  // latency overlaps the w*v loads from HBM.  Otherwise (fp32 fragments are
-  // twice as wide; the prepass tail has T in L2) loaded where they are used,
-  // which keeps the kernel out of scratch.
-  F1 Tf[PRE_T ? 20 : 1];
-  if constexpr (PRE_T) {
-    int k = 0;
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-      for (int s = 0; s <= rt / 2; ++s) Tf[k++] = SS::fa(g_T + fofs(rt, s, l));
-  }
-
-  // (w*v)^T fragments of this wave's 32 value columns (rows = column, k =
-  // token): produced by the prepass launch's spare workgroups, or here
+  // (w*v)^T fragments of this wave's 32 value columns (rows = column, k = token)
   F3 Bwv[2][4];
   wv_frags<BF, TV>(p, b, h, c, col0, l, Bwv);
   f32x4 Uc[2][8];
@@ -1047,21 +1033,17 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
   for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
-  {
-    int k = 0;
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
+  for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
-      for (int s = 0; s <= rt / 2; ++s) {
-        const F1 t = PRE_T ? Tf[PRE_T ? k : 0] : SS::fa(g_T + fofs(rt, s, l));
-        P::m13(Uc[0][rt], t, Bwv[0][s]);
-        P::m13(Uc[1][rt], t, Bwv[1][s]);
-        ++k;
-      }
-      // T read where it is used: keep the scheduler from hoisting every
-      // row's fragment reads ahead (that would need them all live at once)
-      if constexpr (!PRE_T) __builtin_amdgcn_sched_barrier(0);
+    for (int s = 0; s <= rt / 2; ++s) {
+      const F1 t = SS::fa(g_T + fofs(rt, s, l));
+      P::m13(Uc[0][rt], t, Bwv[0][s]);
+      P::m13(Uc[1][rt], t, Bwv[1][s]);
     }
+    // T read where it is used: keep the scheduler from hoisting every row's
+    // fragment reads ahead (that would need them all live at once)
+    __builtin_amdgcn_sched_barrier(0);
   }
   // U^T fragments (rows = value column, k = token)
   F3 U3[2][4];
