@@ -56,6 +56,7 @@ constexpr int TPW = 8 / NWV;  // 16-column tiles per wave in C x 128 products
 
 struct BW {
   int B, L, H, NC;       // NC: chunks of this launch's token block
+  int bf;                // precision "bf16": split-bf16 products in k_bw_grads
   int c0;                // first chunk of the block (token c0 * BC)
   const float *q, *k, *v, *g, *b, *w;
   const int32_t* seg;
@@ -134,6 +135,22 @@ __device__ __forceinline__ void row8(const float* rowp, int s, int q, float* x) 
 }
 
 __device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<false>(x); }
+
+// A 16 x 32 product operand from 8 fp32 values in fragment order: fp32 mode
+// keeps them (v_mfma_f32_16x16x4_f32), bf16 mode splits them into high and
+// low bf16 words (x = hi + lo to 16 significant bits) for the split product
+// hi*hi + hi*lo + lo*hi on v_mfma_f32_16x16x32_bf16.
+template <bool BF> struct Op;
+template <> struct Op<false> {
+  using F = Frag<false>;
+  static __device__ __forceinline__ F make(const float* x) { return make_frag<false>(x); }
+  static __device__ __forceinline__ void mac(f32x4& acc, const F& a, const F& b) { mma(acc, a, b); }
+};
+template <> struct Op<true> {
+  using F = Pol<true>::F3;
+  static __device__ __forceinline__ F make(const float* x) { return Pol<true>::f3(x); }
+  static __device__ __forceinline__ void mac(f32x4& acc, const F& a, const F& b) { Pol<true>::m33(acc, a, b); }
+};
 
 // ---------------------------------------------------------------------------
 // k_bw_intra
@@ -551,6 +568,7 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
     const float* Brow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) row8(Brow, s2, q, o.b[tt][s2]);
+    }
     if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + (col0 + l16) * KD + 32 * wv + 16 * tt + 4 * q);
     o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
@@ -707,16 +725,18 @@ __device__ __forceinline__ void load_yT(float (&y)[4][8], const float* X, int wv
 }
 
 // acc[I] += X[rows 16I..][:] * Y^T with X in LDS (row pitch KP) and Y preloaded
+template <bool BF>
 __device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, const float (&y)[4][8], int q,
                                        int l16) {
+  using O = Op<BF>;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const Frag<false> b = fr8(y[s]);
+    const typename O::F b = O::make(y[s]);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       float x[8];
       row8(X + (16 * I + l16) * KP, s, q, x);
-      mma(acc[I][0], fr8(x), b);
+      O::mac(acc[I][0], O::make(x), b);
     }
   }
 }
@@ -724,7 +744,9 @@ __device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, con
 // Every operand that comes from global memory is loaded one phase ahead of
 // its product (state rows into registers; W, Kc and M^T staged in LDS), so
 // each phase waits on at most the loads issued a phase earlier.
+template <bool BF>
 __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
+  using O = Op<BF>;
   __shared__ float sdO[BC][KP];
   __shared__ float sX[BC][KP];       // dU, then dX
   __shared__ float sU[BC][KP];
@@ -765,7 +787,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   f32x4 acc[4][TPW];
   // ---- U = U0 - W S0 ---------------------------------------------------------
   zero_acc(acc);
-  nt_lds(acc, &sT[0][0], yA, q, l16);
+  nt_lds<BF>(acc, &sT[0][0], yA, q, l16);
   load_yT(yB, dSC, wv, q, l16);
   float4 kc[BC * KD / 4 / NT];
 #pragma unroll
@@ -787,10 +809,10 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
   load_y(yA, dSC, wv, q, l16);
   zero_acc(acc);
-  nt_lds(acc, &sU[0][0], yB, q, l16);
+  nt_lds<BF>(acc, &sU[0][0], yB, q, l16);
   store_frag(p.Rk + (int64_t)u * CK, wv, l, acc);
   zero_acc(acc);
-  nt_lds(acc, &sdO[0][0], yS0, q, l16);
+  nt_lds<BF>(acc, &sdO[0][0], yS0, q, l16);
   store_frag(p.Rq + (int64_t)u * CK, wv, l, acc);
   // T^T rows and this lane's w, v for the dX phase
   float tt[2][4][8];
@@ -818,15 +840,15 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
-    const Frag<false> bfr = fr8(x);
+    const typename O::F bfr = O::make(x);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       float y[8];
       row8(&sMT[16 * I + l16][0], s, q, y);
-      mma(acc[I][0], fr8(y), bfr);
+      O::mac(acc[I][0], O::make(y), bfr);
     }
   }
-  nt_lds(acc, &sT[0][0], yA, q, l16);
+  nt_lds<BF>(acc, &sT[0][0], yA, q, l16);
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
@@ -840,9 +862,9 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
-    const Frag<false> bfr = fr8(x);
+    const typename O::F bfr = O::make(x);
 #pragma unroll
-    for (int I = 0; I < 4; ++I) mma(acc[I][0], fr8(tt[s][I]), bfr);
+    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], O::make(tt[s][I]), bfr);
   }
   lds_barrier();
 #pragma unroll
@@ -872,7 +894,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 
   // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
   zero_acc(acc);
-  nt_lds(acc, &sX[0][0], yS0, q, l16);
+  nt_lds<BF>(acc, &sX[0][0], yS0, q, l16);
   store_frag(p.Rb + (int64_t)u * CK, wv, l, acc);
 
   // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
@@ -888,7 +910,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
         float xa[8], xb[8];
         row8(Xs + (16 * I + l16) * KP, s, q, xa);
         row8(&sU[16 * J + l16][0], s, q, xb);
-        mma(a, fr8(xa), fr8(xb));
+        O::mac(a, O::make(xa), O::make(xb));
       }
     }
 #pragma unroll
@@ -1432,8 +1454,8 @@ extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
 }
 
 // the recurrence backward with the element types of d_out and dv given
-static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt, bool bf, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   const int rc = bw_check(a);
   if (rc != DN_OK) return rc;
   const size_t need = bw_workspace_bytes(a);
@@ -1442,6 +1464,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   const int nblk = (NC + ncb - 1) / ncb;
   BW p{};
   p.B = a->B; p.L = a->L; p.H = a->H;
+  p.bf = bf;
   p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
   p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
   p.seg = a->seg;
@@ -1491,7 +1514,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.dinit = j == 0 ? (float*)a->d_init : dcarry;
     hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
     hipLaunchKernelGGL(k_bw_chains, dim3(2 * chains), dim3(256), 0, st, p, chains);
-    hipLaunchKernelGGL(k_bw_grads, dim3(n), dim3(NT), 0, st, p);
+    if (p.bf) hipLaunchKernelGGL(k_bw_grads<true>, dim3(n), dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(k_bw_grads<false>, dim3(n), dim3(NT), 0, st, p);
     hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * n)), dim3(NT), 0, st, p);
   }
   prof_mark(4, st, true);
@@ -1501,7 +1525,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
 }
 
 extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  return bwd_core(a, DT_F32, DT_F32, DT_F32, workspace, workspace_bytes, stream);
+  return bwd_core(a, DT_F32, DT_F32, DT_F32, false, workspace, workspace_bytes, stream);
 }
 
 namespace {
@@ -1595,7 +1619,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
   c.d_init = d_init;
   c.recompute_states = a->recompute_states;
-  rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, w, lay.core, stream);
+  rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, a->precision == 0, w, lay.core, stream);
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;
