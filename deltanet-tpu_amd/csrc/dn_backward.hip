@@ -70,7 +70,7 @@ struct BW {
   float* dinit;          // NULL or: the reverse scan's gradient of the state entering the block
   // workspace, per unit u = (batch * H + head) * NC + chunk
   float *G;    // [BC][KD] cumulative log2-decay from the chunk start
-  float *Wm;   // [BC][KD] W
+  float *Wm;   // [BC][KD] W          (these four in gofs order)
   float *WT;   // [KD][BC] W^T
   float *Kc;   // [BC][KD]
   float *KcT;  // [KD][BC]
@@ -135,6 +135,25 @@ __device__ __forceinline__ void row8(const float* rowp, int s, int q, float* x) 
 }
 
 __device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<false>(x); }
+
+// The scan operands Wm, Kc (chunk x 128) and WT, KcT (128 x chunk) are kept
+// in the order the scans' fragments read them: a 16-row block and 32-column
+// slab is two runs of 64 lanes x 4 floats, lane q * 16 + r holding row r,
+// columns 4q..4q+3 of the slab's first (run 0) or second (run 1) 16 columns.
+// One fragment load is one contiguous 1 KB run; four consecutive columns
+// from a multiple of 4 stay contiguous.  ns = 32-column slabs per row.
+__device__ __forceinline__ int gofs(int i, int c, int ns) {
+  const int cc = c & 31;
+  return ((((i >> 4) * ns + (c >> 5)) * 2 + (cc >> 4)) * 64 + ((cc & 15) >> 2) * 16 + (i & 15)) * 4 + (c & 3);
+}
+// the 8 fragment values of lane l in run pair (blk, s) of a gofs array
+__device__ __forceinline__ void frag_run(const float* arr, int blk, int s, int ns, int l, float* x) {
+  const float* b = arr + ((blk * ns + s) * 2) * 256 + 4 * l;
+  const float4 a = ld4g(b);
+  const float4 c = ld4g(b + 256);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+}
 
 // A 16 x 32 product operand from 8 fp32 values in fragment order: fp32 mode
 // keeps them (v_mfma_f32_16x16x4_f32), bf16 mode splits them into high and
@@ -236,11 +255,11 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const float4 kc = ok ? make_float4(k4.x * ex2(gl.x - gi.x), k4.y * ex2(gl.y - gi.y),
                                          k4.z * ex2(gl.z - gi.z), k4.w * ex2(gl.w - gi.w))
                            : zero_f4();
-      *reinterpret_cast<float4*>(Kc + i * KD + 4 * c4) = kc;
-      KcT[(4 * c4 + 0) * BC + i] = kc.x;
-      KcT[(4 * c4 + 1) * BC + i] = kc.y;
-      KcT[(4 * c4 + 2) * BC + i] = kc.z;
-      KcT[(4 * c4 + 3) * BC + i] = kc.w;
+      *reinterpret_cast<float4*>(Kc + gofs(i, 4 * c4, KD / 32)) = kc;
+      KcT[gofs(4 * c4 + 0, i, BC / 32)] = kc.x;
+      KcT[gofs(4 * c4 + 1, i, BC / 32)] = kc.y;
+      KcT[gofs(4 * c4 + 2, i, BC / 32)] = kc.z;
+      KcT[gofs(4 * c4 + 3, i, BC / 32)] = kc.w;
     }
     if (tid < KD) p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(sG[BC - 1][tid]) : 0.f;
     // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128
@@ -450,11 +469,11 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
           sW[i][r] = aw[I][R2][e];
-          Wm[i * KD + r] = aw[I][R2][e];
+          Wm[gofs(i, r, KD / 32)] = aw[I][R2][e];
         }
         *reinterpret_cast<float4*>(U0T + r * BC + 16 * I + 4 * q) =
             make_float4(au[I][R2][0], au[I][R2][1], au[I][R2][2], au[I][R2][3]);
-        *reinterpret_cast<float4*>(WT + r * BC + 16 * I + 4 * q) =
+        *reinterpret_cast<float4*>(WT + gofs(r, 16 * I + 4 * q, BC / 32)) =
             make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
       }
   }
@@ -559,16 +578,14 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
                                            ChainOps& o) {
   const int q = l >> 4, l16 = l & 15;
   const int64_t u = (int64_t)bh * p.NC + c;
-  const float* Arow = (BWD ? p.Kc : p.Wm) + u * CK + (16 * wv + l16) * KD;
+  const float* Aarr = (BWD ? p.Kc : p.Wm) + u * CK;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) row8(Arow, s, q, o.a[s]);
+  for (int s = 0; s < 4; ++s) frag_run(Aarr, wv, s, KD / 32, l, o.a[s]);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const int rA = 32 * wv + 16 * tt + l16;
-    const float* Brow = (BWD ? p.WT : p.KcT) + u * CK + rA * BC;
+    const float* Barr = (BWD ? p.WT : p.KcT) + u * CK;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) row8(Brow, s2, q, o.b[tt][s2]);
-    }
+    for (int s2 = 0; s2 < 2; ++s2) frag_run(Barr, 2 * wv + tt, s2, BC / 32, l, o.b[tt][s2]);
     if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + (col0 + l16) * KD + 32 * wv + 16 * tt + 4 * q);
     o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
@@ -775,7 +792,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
-    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = ld4g(p.Wm + (int64_t)u * CK + i * KD + 4 * c4);
+    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = ld4g(p.Wm + (int64_t)u * CK + gofs(i, 4 * c4, KD / 32));
   }
 #pragma unroll
   for (int it = 0; it < CC / 4 / NT; ++it) {
@@ -793,7 +810,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    kc[it] = ld4g(p.Kc + (int64_t)u * CK + i * KD + 4 * c4);
+    kc[it] = ld4g(p.Kc + (int64_t)u * CK + gofs(i, 4 * c4, KD / 32));
   }
 #pragma unroll
   for (int I = 0; I < 4; ++I)
