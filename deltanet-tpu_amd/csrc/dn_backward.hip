@@ -74,8 +74,8 @@ struct BW {
   float *WT;   // [KD][BC] W^T
   float *Kc;   // [BC][KD]
   float *KcT;  // [KD][BC]
-  float *PT;   // [KD][KD] (Xf^T dO)^T: element (v, k) at v * KD + k
-  float *U0T;  // [KD][BC] U0^T
+  float *PT;   // [KD][KD] (Xf^T dO)^T, element (v, k) at aofs(v, k)
+  float *U0T;  // [KD][BC] U0^T, aofs order
   float *MT;   // [BC][BC] M^T
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
@@ -145,6 +145,12 @@ __device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<fa
 __device__ __forceinline__ int gofs(int i, int c, int ns) {
   const int cc = c & 31;
   return ((((i >> 4) * ns + (c >> 5)) * 2 + (cc >> 4)) * 64 + ((cc & 15) >> 2) * 16 + (i & 15)) * 4 + (c & 3);
+}
+// PT (128 x 128) and U0T (128 x chunk) in accumulator order: a 16 x 16 tile
+// is one run of 64 lanes x 4 floats, lane q * 16 + r holding row r, columns
+// 4q..4q+3.  nt = 16-column tiles per row.
+__device__ __forceinline__ int aofs(int r, int c, int nt) {
+  return (((r >> 4) * nt + (c >> 4)) * 64 + ((c & 15) >> 2) * 16 + (r & 15)) * 4 + (c & 3);
 }
 // the 8 fragment values of lane l in run pair (blk, s) of a gofs array
 __device__ __forceinline__ void frag_run(const float* arr, int blk, int s, int ns, int l, float* x) {
@@ -471,7 +477,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
           sW[i][r] = aw[I][R2][e];
           Wm[gofs(i, r, KD / 32)] = aw[I][R2][e];
         }
-        *reinterpret_cast<float4*>(U0T + r * BC + 16 * I + 4 * q) =
+        *reinterpret_cast<float4*>(U0T + aofs(r, 16 * I + 4 * q, BC / 16)) =
             make_float4(au[I][R2][0], au[I][R2][1], au[I][R2][2], au[I][R2][3]);
         *reinterpret_cast<float4*>(WT + gofs(r, 16 * I + 4 * q, BC / 32)) =
             make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
@@ -550,7 +556,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         for (int e = 0; e < 8; ++e) xa[e] = sW[32 * s + pi_k(q, e)][16 * kt + l16];
         mma(acc, fr8(xa), fr8(xb[s]));
       }
-      *reinterpret_cast<float4*>(PT + (16 * wv + l16) * KD + 16 * kt + 4 * q) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4*>(PT + aofs(16 * wv + l16, 16 * kt + 4 * q, KD / 16)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
   }
 }
@@ -586,10 +592,10 @@ __device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, i
     const float* Barr = (BWD ? p.WT : p.KcT) + u * CK;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) frag_run(Barr, 2 * wv + tt, s2, BC / 32, l, o.b[tt][s2]);
-    if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + (col0 + l16) * KD + 32 * wv + 16 * tt + 4 * q);
+    if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + aofs(col0 + l16, 32 * wv + 16 * tt + 4 * q, KD / 16));
     o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
-  if (!BWD) o.u = ld4g(p.U0T + u * CK + (col0 + l16) * BC + 16 * wv + 4 * q);
+  if (!BWD) o.u = ld4g(p.U0T + u * CK + aofs(col0 + l16, 16 * wv + 4 * q, BC / 16));
 }
 
 // one scan over chain x = 8 * (batch * H + head) + column tile
@@ -786,7 +792,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   load_yT(yS0, S0, wv, q, l16);
   float4 u0[4];
 #pragma unroll
-  for (int I = 0; I < 4; ++I) u0[I] = ld4g(p.U0T + (int64_t)u * CK + vcol * BC + 16 * I + 4 * q);
+  for (int I = 0; I < 4; ++I) u0[I] = ld4g(p.U0T + (int64_t)u * CK + aofs(vcol, 16 * I + 4 * q, BC / 16));
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
