@@ -70,7 +70,7 @@ struct BW {
   float* dinit;          // NULL or: the reverse scan's gradient of the state entering the block
   // workspace, per unit u = (batch * H + head) * NC + chunk
   float *G;    // [BC][KD] cumulative log2-decay from the chunk start
-  float *Wm;   // [BC][KD] W          (these four in gofs order)
+  float *Wm;   // [BC][KD] W          (these four in gofs / bofs order)
   float *WT;   // [KD][BC] W^T
   float *Kc;   // [BC][KD]
   float *KcT;  // [KD][BC]
@@ -145,6 +145,43 @@ __device__ __forceinline__ Frag<false> fr8(const float* x) { return make_frag<fa
 __device__ __forceinline__ int gofs(int i, int c, int ns) {
   const int cc = c & 31;
   return ((((i >> 4) * ns + (c >> 5)) * 2 + (cc >> 4)) * 64 + ((cc & 15) >> 2) * 16 + (i & 15)) * 4 + (c & 3);
+}
+// bf16 mode keeps the four scan operands split: run pair (blk, s) is 64
+// lanes x 8 high bf16 words, then 64 lanes x 8 low words, element (i, c) at
+// index e = 4 * (run) + (c & 3) of its lane (the same bytes as the fp32
+// pair).  op_put4 / op_get4 store and load either form.
+__device__ __forceinline__ int bofs(int i, int c, int ns) {
+  const int cc = c & 31;
+  return ((i >> 4) * ns + (c >> 5)) * 1024 + (((cc & 15) >> 2) * 16 + (i & 15)) * 8 + (cc >> 4) * 4 + (c & 3);
+}
+// four consecutive columns c..c+3, c a multiple of 4
+__device__ __forceinline__ void op_put4(bool bf, float* arr, int i, int c, int ns, float4 v) {
+  if (bf) {
+    bf16* b = reinterpret_cast<bf16*>(arr) + bofs(i, c, ns);
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    bf16x4 h, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = (bf16)x[e];
+      lo[e] = (bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x4*>(b) = h;
+    *reinterpret_cast<bf16x4*>(b + 512) = lo;
+  } else {
+    *reinterpret_cast<float4*>(arr + gofs(i, c, ns)) = v;
+  }
+}
+template <bool BF>
+__device__ __forceinline__ float4 op_get4(const float* arr, int i, int c, int ns) {
+  if constexpr (BF) {
+    const bf16* b = reinterpret_cast<const bf16*>(arr) + bofs(i, c, ns);
+    const bf16x4 h = *reinterpret_cast<const bf16x4*>(b);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(b + 512);
+    return make_float4((float)h[0] + (float)lo[0], (float)h[1] + (float)lo[1], (float)h[2] + (float)lo[2],
+                       (float)h[3] + (float)lo[3]);
+  } else {
+    return ld4g(arr + gofs(i, c, ns));
+  }
 }
 // PT (128 x 128) and U0T (128 x chunk) in accumulator order: a 16 x 16 tile
 // is one run of 64 lanes x 4 floats, lane q * 16 + r holding row r, columns
@@ -261,11 +298,24 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const float4 kc = ok ? make_float4(k4.x * ex2(gl.x - gi.x), k4.y * ex2(gl.y - gi.y),
                                          k4.z * ex2(gl.z - gi.z), k4.w * ex2(gl.w - gi.w))
                            : zero_f4();
-      *reinterpret_cast<float4*>(Kc + gofs(i, 4 * c4, KD / 32)) = kc;
-      KcT[gofs(4 * c4 + 0, i, BC / 32)] = kc.x;
-      KcT[gofs(4 * c4 + 1, i, BC / 32)] = kc.y;
-      KcT[gofs(4 * c4 + 2, i, BC / 32)] = kc.z;
-      KcT[gofs(4 * c4 + 3, i, BC / 32)] = kc.w;
+      op_put4(p.bf, Kc, i, 4 * c4, KD / 32, kc);
+    }
+    // Kc^T: channel tid % 128, four consecutive tokens per (vector) store;
+    // k again from memory (its rows were just read, so from the cache)
+    {
+      const int ch = tid & (KD - 1);
+      const float gl = sG[BC - 1][ch];
+#pragma unroll 2
+      for (int m = tid / KD; m < BC / 4; m += NT / KD) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * m + e;
+          const bool ok = slast[i] && t0 + i < p.L;
+          v[e] = ok ? p.k[row_of(p, bb, t0 + i, h) + ch] * ex2(gl - sG[i][ch]) : 0.f;
+        }
+        op_put4(p.bf, KcT, ch, 4 * m, BC / 32, make_float4(v[0], v[1], v[2], v[3]));
+      }
     }
     if (tid < KD) p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(sG[BC - 1][tid]) : 0.f;
     // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128
@@ -462,7 +512,6 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         }
       }
     }
-    float* Wm = p.Wm + (int64_t)u * CK;
     float* WT = p.WT + (int64_t)u * CK;
     float* U0T = p.U0T + (int64_t)u * CK;
     lds_barrier();   // every wave has read b k from sW
@@ -475,15 +524,24 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
           sW[i][r] = aw[I][R2][e];
-          Wm[gofs(i, r, KD / 32)] = aw[I][R2][e];
         }
         *reinterpret_cast<float4*>(U0T + aofs(r, 16 * I + 4 * q, BC / 16)) =
             make_float4(au[I][R2][0], au[I][R2][1], au[I][R2][2], au[I][R2][3]);
-        *reinterpret_cast<float4*>(WT + gofs(r, 16 * I + 4 * q, BC / 32)) =
-            make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]);
+        op_put4(p.bf, WT, r, 16 * I + 4 * q, BC / 32, make_float4(aw[I][R2][0], aw[I][R2][1], aw[I][R2][2], aw[I][R2][3]));
       }
   }
   lds_barrier();
+  // W in the scan operand order from sW: per task one lane's run pair (rows
+  // of 16-row block blk, slab s), two 4-column vector stores
+  {
+    float* Wm = p.Wm + (int64_t)u * CK;
+    for (int task = tid; task < BC * KD / 8; task += NT) {
+      const int ln = task & 63, pr = task >> 6, blk = pr / (KD / 32), s = pr % (KD / 32);
+      const int i = 16 * blk + (ln & 15), cc = 32 * s + 4 * (ln >> 4);
+      op_put4(p.bf, Wm, i, cc, KD / 32, *reinterpret_cast<const float4*>(&sW[i][cc]));
+      op_put4(p.bf, Wm, i, cc + 16, KD / 32, *reinterpret_cast<const float4*>(&sW[i][cc + 16]));
+    }
+  }
 
   // ---- Xf = diag(carry) q e^G - M W, then P^T = (Xf^T dO)^T ------------------
   {
@@ -562,109 +620,206 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 }
 
 // ---------------------------------------------------------------------------
-// chain_run: one (batch, head, 16-column tile) per workgroup; the 128 x 16
-// state tile lives in LDS in fragment order ([slab][lane][8]); wave w owns
-// rows 32w..32w+31.
+// chain_run: one (batch, head, block of 16 CT state columns) per workgroup;
+// wave w owns state rows 32w..32w+31 of the CT column tiles, so every operand
+// fragment it loads serves CT tiles.  The 128 x 16 CT state block lives in
+// LDS in fragment order ([tile][slab][lane][8]).
 //   forward  (BWD = false):  Y = U0 - W S ;  S <- lam * S + Kc^T Y
 //   backward (BWD = true):   Z = -Kc dS  ;  dS <- lam * dS + Xf^T dO + W^T Z
 // Every operand but the state is known before the scan, so each step loads
-// the next chunk's operands while it computes.  The 8 column tiles of a head
-// run on one XCD (xcd_block), which serves their shared rows from its L2.
+// the next chunk's operands while it computes.  The loads bound the step:
+// the operand rows are the same for every column block of a head, so wider
+// blocks (CT = 2 in bf16 mode, where the split-bf16 products keep the MFMA
+// time per step small) divide the bytes per column.  bf16 mode reads the
+// operands split (k_bw_intra stores them so) and keeps the state in LDS split.
 // ---------------------------------------------------------------------------
+template <bool BF> constexpr int chain_tiles() { return BF ? 2 : 1; }
+
+template <bool BF>
 struct ChainOps {
-  float a[4][8];        // W (forward) / Kc (backward) rows of this wave's 16 tokens
-  float b[2][2][8];     // Kc^T (forward) / W^T (backward) rows of this wave's 32 state rows
-  float4 pp[2];         // (Xf^T dO) entries of this lane's state rows (backward)
-  float4 u;             // U0 tile entries of this lane (forward)
-  float4 lm[2];         // lam of this lane's state rows
+  static constexpr int CT = chain_tiles<BF>();
+  typename Op<BF>::F a[4];      // W (forward) / Kc (backward): this wave's 16 tokens, 4 slabs
+  typename Op<BF>::F b[2][2];   // Kc^T (forward) / W^T (backward): this wave's 32 state rows, 2 slabs
+  float4 pp[CT][2];             // (Xf^T dO) entries of this lane's state rows (backward)
+  float4 u[CT];                 // U0 tile entries of this lane (forward)
+  float4 lm[2];                 // lam of this lane's state rows
 };
 
-template <bool BWD>
-__device__ __forceinline__ void chain_load(const BW& p, int bh, int bb, int h, int c, int col0, int wv, int l,
-                                           ChainOps& o) {
+// run pair (blk, s) of an operand array as an MFMA fragment of lane l
+template <bool BF>
+__device__ __forceinline__ typename Op<BF>::F op_frag(const float* arr, int blk, int s, int ns, int l) {
+  if constexpr (BF) {
+    const bf16* b = reinterpret_cast<const bf16*>(arr) + (blk * ns + s) * 1024 + 8 * l;
+    typename Op<true>::F f;
+    f.hi.v = *reinterpret_cast<const bf16x8*>(b);
+    f.lo.v = *reinterpret_cast<const bf16x8*>(b + 512);
+    return f;
+  } else {
+    float x[8];
+    frag_run(arr, blk, s, ns, l, x);
+    return fr8(x);
+  }
+}
+
+template <bool BWD, bool BF>
+__device__ __forceinline__ void chain_load(const BW& p, int bh, int c, int col0, int wv, int l, ChainOps<BF>& o) {
+  constexpr int CT = ChainOps<BF>::CT;
   const int q = l >> 4, l16 = l & 15;
   const int64_t u = (int64_t)bh * p.NC + c;
   const float* Aarr = (BWD ? p.Kc : p.Wm) + u * CK;
+  const float* Barr = (BWD ? p.WT : p.KcT) + u * CK;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) frag_run(Aarr, wv, s, KD / 32, l, o.a[s]);
+  for (int s = 0; s < 4; ++s) o.a[s] = op_frag<BF>(Aarr, wv, s, KD / 32, l);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const float* Barr = (BWD ? p.WT : p.KcT) + u * CK;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) frag_run(Barr, 2 * wv + tt, s2, BC / 32, l, o.b[tt][s2]);
-    if (BWD) o.pp[tt] = ld4g(p.PT + u * KK + aofs(col0 + l16, 32 * wv + 16 * tt + 4 * q, KD / 16));
+    for (int s2 = 0; s2 < 2; ++s2) o.b[tt][s2] = op_frag<BF>(Barr, 2 * wv + tt, s2, BC / 32, l);
+#pragma unroll
+    for (int j = 0; j < CT; ++j)
+      if (BWD) o.pp[j][tt] = ld4g(p.PT + u * KK + aofs(col0 + 16 * j + l16, 32 * wv + 16 * tt + 4 * q, KD / 16));
     o.lm[tt] = ld4g(p.lam + u * KD + 32 * wv + 16 * tt + 4 * q);
   }
-  if (!BWD) o.u = ld4g(p.U0T + u * CK + aofs(col0 + l16, 16 * wv + 4 * q, BC / 16));
+#pragma unroll
+  for (int j = 0; j < CT; ++j)
+    if (!BWD) o.u[j] = ld4g(p.U0T + u * CK + aofs(col0 + 16 * j + l16, 16 * wv + 4 * q, BC / 16));
 }
 
-// one scan over chain x = 8 * (batch * H + head) + column tile
-template <bool BWD>
-__device__ __forceinline__ void chain_run(const BW& p, int x) {
-  __shared__ float sS[4][64][8];
-  __shared__ float sY[2][64][8];
-  const int ct = x % (KD / 16), bh = x / (KD / 16);
-  const int h = bh % p.H, bb = bh / p.H;
-  const int col0 = 16 * ct;
-  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
-
-  f32x4 st[2];
-  const float* src = BWD ? p.dfin : p.init;
+// LDS copy of the state (S) and of the Y / Z tile, in fragment order; split
+// into bf16 words in bf16 mode
+template <bool BF, int CT> struct ChainLds;
+template <int CT> struct ChainLds<false, CT> {
+  float S[CT][4][64][8];
+  float Y[CT][2][64][8];
+  __device__ __forceinline__ void put_s(int j, int wv, int l, const f32x4& s0, const f32x4& s1) {
+    *reinterpret_cast<float4*>(&S[j][wv][l][0]) = make_float4(s0[0], s0[1], s0[2], s0[3]);
+    *reinterpret_cast<float4*>(&S[j][wv][l][4]) = make_float4(s1[0], s1[1], s1[2], s1[3]);
+  }
+  __device__ __forceinline__ void put_y(int j, int wv, int l, const f32x4& y) {
+    *reinterpret_cast<float4*>(&Y[j][wv >> 1][l][4 * (wv & 1)]) = make_float4(y[0], y[1], y[2], y[3]);
+  }
+  __device__ __forceinline__ Frag<false> s_frag(int j, int s, int l) const { return fr8(&S[j][s][l][0]); }
+  __device__ __forceinline__ Frag<false> y_frag(int j, int s, int l) const { return fr8(&Y[j][s][l][0]); }
+};
+template <int CT> struct ChainLds<true, CT> {
+  bf16x8 S[2][CT][4][64];   // [hi, lo]
+  bf16x4 Y[2][CT][2][64][2];
+  __device__ __forceinline__ void put_s(int j, int wv, int l, const f32x4& s0, const f32x4& s1) {
+    bf16x8 h, lo;
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
+    for (int e = 0; e < 8; ++e) {
+      const float x = e < 4 ? s0[e] : s1[e - 4];
+      h[e] = (bf16)x;
+      lo[e] = (bf16)(x - (float)h[e]);
+    }
+    S[0][j][wv][l] = h;
+    S[1][j][wv][l] = lo;
+  }
+  __device__ __forceinline__ void put_y(int j, int wv, int l, const f32x4& y) {
+    bf16x4 h, lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int r = 32 * wv + 16 * tt + 4 * q + e;
-      st[tt][e] = src ? src[((int64_t)bh * KD + r) * KD + col0 + l16] : 0.f;
+      h[e] = (bf16)y[e];
+      lo[e] = (bf16)(y[e] - (float)h[e]);
     }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    sS[wv][l][e] = st[0][e];
-    sS[wv][l][4 + e] = st[1][e];
+    Y[0][j][wv >> 1][l][wv & 1] = h;
+    Y[1][j][wv >> 1][l][wv & 1] = lo;
   }
+  __device__ __forceinline__ Pol<true>::F3 s_frag(int j, int s, int l) const {
+    Pol<true>::F3 f;
+    f.hi.v = S[0][j][s][l];
+    f.lo.v = S[1][j][s][l];
+    return f;
+  }
+  __device__ __forceinline__ Pol<true>::F3 y_frag(int j, int s, int l) const {
+    Pol<true>::F3 f;
+    const bf16x4 h0 = Y[0][j][s][l][0], h1 = Y[0][j][s][l][1], l0 = Y[1][j][s][l][0], l1 = Y[1][j][s][l][1];
+    f.hi.v = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+    f.lo.v = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+    return f;
+  }
+};
+
+// one scan over chain x = (batch * H + head) * (8 / CT) + column block
+template <bool BWD, bool BF>
+__device__ __forceinline__ void chain_run(const BW& p, int x) {
+  using O = Op<BF>;
+  constexpr int CT = chain_tiles<BF>();
+  constexpr int NB = KD / (16 * CT);
+  __shared__ ChainLds<BF, CT> sm;
+  const int cb = x % NB, bh = x / NB;
+  const int col0 = 16 * CT * cb;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+
+  f32x4 st[CT][2];
+  const float* src = BWD ? p.dfin : p.init;
+#pragma unroll
+  for (int j = 0; j < CT; ++j)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 32 * wv + 16 * tt + 4 * q + e;
+        st[j][tt][e] = src ? src[((int64_t)bh * KD + r) * KD + col0 + 16 * j + l16] : 0.f;
+      }
+#pragma unroll
+  for (int j = 0; j < CT; ++j) sm.put_s(j, wv, l, st[j][0], st[j][1]);
 
   // one scan step on chunk c with operands `o` in registers
-  auto step = [&](int c, const ChainOps& o) {
+  auto step = [&](int c, const ChainOps<BF>& o) {
     const int64_t u = (int64_t)bh * p.NC + c;
     lds_barrier();
     {
       float* X = (BWD ? p.dS : p.S) + u * KK;   // transposed: 4 consecutive k per lane
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int r0 = 32 * wv + 16 * tt + 4 * q;
-        *reinterpret_cast<float4*>(X + (col0 + l16) * KD + r0) = make_float4(st[tt][0], st[tt][1], st[tt][2], st[tt][3]);
+      for (int j = 0; j < CT; ++j)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int r0 = 32 * wv + 16 * tt + 4 * q;
+          *reinterpret_cast<float4*>(X + (col0 + 16 * j + l16) * KD + r0) =
+              make_float4(st[j][tt][0], st[j][tt][1], st[j][tt][2], st[j][tt][3]);
+        }
+    }
+    // Y (or Z) tiles: token rows 16w..16w+15; with one tile, two accumulators
+    // halve the dependent MFMA chain on the sequential path
+    f32x4 y[CT], y2[CT];
+#pragma unroll
+    for (int j = 0; j < CT; ++j) y[j] = y2[j] = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        O::mac(y[j], o.a[s], sm.s_frag(j, s, l));
+        O::mac(y2[j], o.a[s + 2], sm.s_frag(j, s + 2, l));
       }
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[j][e] = BWD ? -(y[j][e] + y2[j][e]) : f4at(o.u[j], e) - (y[j][e] + y2[j][e]);
+      sm.put_y(j, wv, l, y[j]);
     }
-    // Y (or Z) tile: token rows 16w..16w+15; two accumulators halve the
-    // dependent MFMA chain on the sequential path
-    f32x4 y = zero4(), y2 = zero4();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      mma(y, fr8(o.a[s]), fr8(&sS[s][l][0]));
-      mma(y2, fr8(o.a[s + 2]), fr8(&sS[s + 2][l][0]));
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = BWD ? -(y[e] + y2[e]) : f4at(o.u, e) - (y[e] + y2[e]);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sY[wv >> 1][l][4 * (wv & 1) + e] = y[e];
     lds_barrier();
-    f32x4 acc[2];
+    f32x4 acc[CT][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int j = 0; j < CT; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[tt][e] = f4at(o.lm[tt], e) * st[tt][e];
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+        for (int e = 0; e < 4; ++e) acc[j][tt][e] = f4at(o.lm[tt], e) * st[j][tt][e];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) mma(acc[tt], fr8(o.b[tt][s2]), fr8(&sY[s2][l][0]));
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+      for (int j = 0; j < CT; ++j) {
+        const auto fy = sm.y_frag(j, s2, l);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) st[tt][e] = acc[tt][e] + (BWD ? f4at(o.pp[tt], e) : 0.f);
+        for (int tt = 0; tt < 2; ++tt) O::mac(acc[j][tt], o.b[tt][s2], fy);
+      }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      sS[wv][l][e] = st[0][e];
-      sS[wv][l][4 + e] = st[1][e];
+    for (int j = 0; j < CT; ++j) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[j][tt][e] = acc[j][tt][e] + (BWD ? f4at(o.pp[j][tt], e) : 0.f);
+      sm.put_s(j, wv, l, st[j][0], st[j][1]);
     }
   };
   // chunk visited at scan position it (clamped: the load past the end is unused)
@@ -673,39 +828,47 @@ __device__ __forceinline__ void chain_run(const BW& p, int x) {
     return BWD ? p.NC - 1 - itc : itc;
   };
   // two operand sets, alternated (no register copies between steps)
-  ChainOps o0, o1;
-  chain_load<BWD>(p, bh, bb, h, chunk_at(0), col0, wv, l, o0);
+  ChainOps<BF> o0, o1;
+  chain_load<BWD>(p, bh, chunk_at(0), col0, wv, l, o0);
   int it = 0;
   for (; it + 1 < p.NC; it += 2) {
-    chain_load<BWD>(p, bh, bb, h, chunk_at(it + 1), col0, wv, l, o1);
+    chain_load<BWD>(p, bh, chunk_at(it + 1), col0, wv, l, o1);
     step(chunk_at(it), o0);
-    chain_load<BWD>(p, bh, bb, h, chunk_at(it + 2), col0, wv, l, o0);
+    chain_load<BWD>(p, bh, chunk_at(it + 2), col0, wv, l, o0);
     step(chunk_at(it + 1), o1);
   }
   if (it < p.NC) step(chunk_at(it), o0);
   float* dst = BWD ? p.dinit : p.sfin;
   if (dst != nullptr) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int j = 0; j < CT; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 32 * wv + 16 * tt + 4 * q + e;
-        dst[((int64_t)bh * KD + r) * KD + col0 + l16] = st[tt][e];
-      }
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 32 * wv + 16 * tt + 4 * q + e;
+          dst[((int64_t)bh * KD + r) * KD + col0 + 16 * j + l16] = st[j][tt][e];
+        }
   }
 }
 
+// Chains per direction of a launch (B * H heads, 8 / CT column blocks each).
+__host__ __device__ constexpr int chains_per_head(bool bf) { return KD / (16 * (bf ? 2 : 1)); }
+
 // Both scans in one launch: they are independent (both read only
-// k_bw_intra's products) and each waits mostly on its next chunk's operands,
-// so a forward and a reverse workgroup share each CU.  Blocks b and b + 8 n
-// land on the same XCD; each XCD runs C / 8 chains of each direction
-// (C = chains per direction, a multiple of 8), the 8 column tiles of a head
-// together.  A launch of C blocks runs the forward scans only.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_bw_chains(BW p, int C) {
-  const int b = blockIdx.x, per = C >> 3, s = b >> 3;
-  const int x = (b & 7) * per + s % per;
-  if (s < per) chain_run<false>(p, x);
-  else chain_run<true>(p, x);
+// k_bw_intra's products) and each waits mostly on its next chunk's operands.
+// nb chains (forward ones first, then the reverse ones when nb = 2 C) over a
+// grid of 8 * per blocks: block b runs chain (b % 8) * per + b / 8, so
+// consecutive chains -- the column blocks of one head, which read the same
+// operand rows -- run on one XCD and share its L2; blocks past nb return at
+// once.  C = chains per direction.
+template <bool BF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_bw_chains(BW p, int C, int nb) {
+  const int per = gridDim.x >> 3;
+  const int x = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (x >= nb) return;
+  if (x < C) chain_run<false, BF>(p, x);
+  else chain_run<true, BF>(p, x - C);
 }
 
 // ---------------------------------------------------------------------------
@@ -798,7 +961,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
-    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = ld4g(p.Wm + (int64_t)u * CK + gofs(i, 4 * c4, KD / 32));
+    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = op_get4<BF>(p.Wm + (int64_t)u * CK, i, 4 * c4, KD / 32);
   }
 #pragma unroll
   for (int it = 0; it < CC / 4 / NT; ++it) {
@@ -816,7 +979,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    kc[it] = ld4g(p.Kc + (int64_t)u * CK + gofs(i, 4 * c4, KD / 32));
+    kc[it] = op_get4<BF>(p.Kc + (int64_t)u * CK, i, 4 * c4, KD / 32);
   }
 #pragma unroll
   for (int I = 0; I < 4; ++I)
@@ -1509,7 +1672,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   float* dcarry = nblk > 1 ? boundary(nblk) : nullptr;
 
   hipStream_t st = (hipStream_t)stream;
-  const int chains = a->B * a->H * (KD / 16);
+  const int chains = a->B * a->H * chains_per_head(p.bf);
+  auto chain_grid = [](int nb) { return dim3((unsigned)(8 * ((nb + 7) / 8))); };
   auto block = [&](int j) {
     p.c0 = j * ncb;
     p.NC = std::min(ncb, NC - p.c0);
@@ -1523,7 +1687,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.sfin = boundary(j + 1);
     p.dfin = nullptr; p.dinit = nullptr;
     hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
-    hipLaunchKernelGGL(k_bw_chains, dim3(chains), dim3(256), 0, st, p, chains);
+    if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
+    else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
   }
   // blocks from the last to the first: chunk products, both scans (the
   // forward one from the block's boundary state), gradients; the reverse
@@ -1536,7 +1701,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.dfin = j == nblk - 1 ? (const float*)a->d_final : dcarry;
     p.dinit = j == 0 ? (float*)a->d_init : dcarry;
     hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
-    hipLaunchKernelGGL(k_bw_chains, dim3(2 * chains), dim3(256), 0, st, p, chains);
+    if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
+    else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
     if (p.bf) hipLaunchKernelGGL(k_bw_grads<true>, dim3(n), dim3(NT), 0, st, p);
     else hipLaunchKernelGGL(k_bw_grads<false>, dim3(n), dim3(NT), 0, st, p);
     hipLaunchKernelGGL(k_bw_dqk, dim3((unsigned)(NQ * n)), dim3(NT), 0, st, p);
