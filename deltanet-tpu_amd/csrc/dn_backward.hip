@@ -171,6 +171,24 @@ __device__ __forceinline__ void op_put4(bool bf, float* arr, int i, int c, int n
     *reinterpret_cast<float4*>(arr + gofs(i, c, ns)) = v;
   }
 }
+// the 8 values of one lane of a run pair: columns c..c+3 and c+16..c+19 of
+// row i (c = 32 s + 4 q); neighbouring lanes store neighbouring 16 bytes
+__device__ __forceinline__ void op_put8(bool bf, float* arr, int i, int c, int ns, const float* x) {
+  if (bf) {
+    bf16* b = reinterpret_cast<bf16*>(arr) + bofs(i, c, ns);
+    bf16x8 h, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      h[e] = (bf16)x[e];
+      lo[e] = (bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x8*>(b) = h;
+    *reinterpret_cast<bf16x8*>(b + 512) = lo;
+  } else {
+    *reinterpret_cast<float4*>(arr + gofs(i, c, ns)) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(arr + gofs(i, c + 16, ns)) = make_float4(x[4], x[5], x[6], x[7]);
+  }
+}
 template <bool BF>
 __device__ __forceinline__ float4 op_get4(const float* arr, int i, int c, int ns) {
   if constexpr (BF) {
@@ -235,17 +253,15 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   float* G = p.G + (int64_t)u * CK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
-  for (int i = tid; i < BC * CP; i += NT) {
-    (&sA[0][0])[i] = 0.f;
-    (&sM[0][0])[i] = 0.f;
-  }
   // stage q, beta = b k and the log2-decay (rows past the sequence end are
   // zero); k stays in registers for Kc
   constexpr int SIT = BC * KD / 4 / NT;
+  static_assert(SIT == 4 && NT == 16 * (KD / 4) && BC == 64, "token mapping of the staging loop");
   float4 kst[SIT];
 #pragma unroll
   for (int it = 0; it < SIT; ++it) {
-    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    // a thread holds 4 consecutive tokens x 4 channels
+    const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
     float4 qv = zero_f4(), bv = zero_f4(), gv = zero_f4(), k4 = zero_f4();
     if (t0 + i < p.L) {
       const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
@@ -282,14 +298,13 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     for (int t = 0; t < BC / 4; ++t) sG[16 * qt + t][ch] = part[t] + off;
   }
   lds_barrier();
-  // G (coalesced), lam, Kc / Kc^T from the staged k, and per 16-token block
+  // G (coalesced), lam, Kc from the staged k into LDS (channels 0..63 in sA,
+  // 64..127 in sM: both are free until A and M), and per 16-token block
   // whether its decay span allows the factored (MFMA) diagonal tiles
   {
-    float* Kc = p.Kc + (int64_t)u * CK;
-    float* KcT = p.KcT + (int64_t)u * CK;
 #pragma unroll
     for (int it = 0; it < SIT; ++it) {
-      const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+      const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
       const float4 gi = *reinterpret_cast<const float4*>(&sG[i][4 * c4]);
       const float4 gl = *reinterpret_cast<const float4*>(&sG[BC - 1][4 * c4]);
       *reinterpret_cast<float4*>(G + i * KD + 4 * c4) = gi;
@@ -298,24 +313,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const float4 kc = ok ? make_float4(k4.x * ex2(gl.x - gi.x), k4.y * ex2(gl.y - gi.y),
                                          k4.z * ex2(gl.z - gi.z), k4.w * ex2(gl.w - gi.w))
                            : zero_f4();
-      op_put4(p.bf, Kc, i, 4 * c4, KD / 32, kc);
-    }
-    // Kc^T: channel tid % 128, four consecutive tokens per (vector) store;
-    // k again from memory (its rows were just read, so from the cache)
-    {
-      const int ch = tid & (KD - 1);
-      const float gl = sG[BC - 1][ch];
-#pragma unroll 2
-      for (int m = tid / KD; m < BC / 4; m += NT / KD) {
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * m + e;
-          const bool ok = slast[i] && t0 + i < p.L;
-          v[e] = ok ? p.k[row_of(p, bb, t0 + i, h) + ch] * ex2(gl - sG[i][ch]) : 0.f;
-        }
-        op_put4(p.bf, KcT, ch, 4 * m, BC / 32, make_float4(v[0], v[1], v[2], v[3]));
-      }
+      *reinterpret_cast<float4*>(c4 < KD / 8 ? &sA[i][4 * c4] : &sM[i][4 * c4 - KD / 2]) = kc;
     }
     if (tid < KD) p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(sG[BC - 1][tid]) : 0.f;
     // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128
@@ -325,6 +323,44 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     if (l == 0) sSafe[wv] = safe;
   }
   lds_barrier();
+  // Kc and Kc^T in the scan operand order: per task one lane's run pair
+  {
+    float* Kc = p.Kc + (int64_t)u * CK;
+    float* KcT = p.KcT + (int64_t)u * CK;
+    auto kc_at = [&](int i, int ch) { return ch < KD / 2 ? sA[i][ch] : sM[i][ch - KD / 2]; };
+    for (int task = tid; task < BC * KD / 8; task += NT) {
+      const int ln = task & 63, pr = task >> 6;
+      float x[8];
+      {
+        const int blk = pr / (KD / 32), s = pr % (KD / 32);
+        const int i = 16 * blk + (ln & 15), cc = 32 * s + 4 * (ln >> 4);
+        const float* rp = cc < KD / 2 ? &sA[i][cc] : &sM[i][cc - KD / 2];
+        const float4 x0 = *reinterpret_cast<const float4*>(rp);
+        const float4 x1 = *reinterpret_cast<const float4*>(rp + 16);
+        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+        op_put8(p.bf, Kc, i, cc, KD / 32, x);
+      }
+      {
+        const int blk = pr / (BC / 32), s = pr % (BC / 32);
+        const int ch = 16 * blk + (ln & 15), tc = 32 * s + 4 * (ln >> 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = kc_at(tc + e, ch);
+          x[4 + e] = kc_at(tc + 16 + e, ch);
+        }
+        op_put8(p.bf, KcT, ch, tc, BC / 32, x);
+      }
+    }
+  }
+  lds_barrier();
+  // A and M write their lower-triangle 16 x 16 tiles whole; the six tiles
+  // above the diagonal stay zero
+  for (int idx = tid; idx < 6 * 256; idx += NT) {
+    const int t = idx >> 8, e = idx & 255;
+    const int I = t < 3 ? 0 : (t < 5 ? 1 : 2), J = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+    sA[16 * I + (e >> 4)][16 * J + (e & 15)] = 0.f;
+    sM[16 * I + (e >> 4)][16 * J + (e & 15)] = 0.f;
+  }
 
   // ---- A (strict) and M (with diagonal), 16x16 tiles of the lower triangle --
   // A pair (i, j) with j <= m <= i is formed as (x_i e^{G_i - G_m}) (k_j e^{G_m - G_j}),
@@ -532,14 +568,16 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   }
   lds_barrier();
   // W in the scan operand order from sW: per task one lane's run pair (rows
-  // of 16-row block blk, slab s), two 4-column vector stores
+  // of 16-row block blk, slab s)
   {
     float* Wm = p.Wm + (int64_t)u * CK;
     for (int task = tid; task < BC * KD / 8; task += NT) {
       const int ln = task & 63, pr = task >> 6, blk = pr / (KD / 32), s = pr % (KD / 32);
       const int i = 16 * blk + (ln & 15), cc = 32 * s + 4 * (ln >> 4);
-      op_put4(p.bf, Wm, i, cc, KD / 32, *reinterpret_cast<const float4*>(&sW[i][cc]));
-      op_put4(p.bf, Wm, i, cc + 16, KD / 32, *reinterpret_cast<const float4*>(&sW[i][cc + 16]));
+      const float4 x0 = *reinterpret_cast<const float4*>(&sW[i][cc]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&sW[i][cc + 16]);
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      op_put8(p.bf, Wm, i, cc, KD / 32, x);
     }
   }
 
