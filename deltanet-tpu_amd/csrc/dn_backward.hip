@@ -1170,6 +1170,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
   __shared__ float sRS[NT / HC][HC];   // partial rowsums of S0 * dSC
+  __shared__ float sSegP[NT / HC][HC], sSegG[NT / HC][HC];   // 4-token segment sums of P and dG
   __shared__ int scar[BC], slast[BC], sseg[BC];
 
   const int u = blockIdx.x / NQ, part = blockIdx.x % NQ;
@@ -1332,27 +1333,46 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   // ---- dg_t = sum_{i>=t} dG_i + sum_{j<t} P_j + lam rowsum(S0 * dSC) -------
   // (the Kc pair (j, last) enters dg_t for t <= j twice with opposite signs,
   // so it is summed forward over j < t instead)
-  if (tid < HC) {
-    const int rr = ch0 + tid;
+  // Every thread: channel tid % HC, tokens 4 sg .. 4 sg + 3; the segment
+  // sums go through LDS, then each thread scans its own four tokens.
+  {
+    constexpr int NSG = NT / HC;
+    static_assert(4 * NSG == BC, "one 4-token segment per thread");
+    const int ch = tid % HC, sg = tid / HC;
+    float pl[4], gl[4], ps = 0.f, gs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pl[e] = sP[4 * sg + e][ch];
+      gl[e] = sdG[4 * sg + e][ch];
+      ps += pl[e];
+      gs += gl[e];
+    }
+    sSegP[sg][ch] = ps;
+    sSegG[sg][ch] = gs;
     float rsum = 0.f;
 #pragma unroll
-    for (int pp = 0; pp < NT / HC; ++pp) rsum += sRS[pp][tid];
-    const float tail = scar[BC - 1] ? ex2(sG[BC - 1][tid]) * rsum : 0.f;
-    float fwd = 0.f, acc = tail;
-    float dgv[BC];
+    for (int pp = 0; pp < NSG; ++pp) rsum += sRS[pp][ch];
+    lds_barrier();
+    float fwd = 0.f, acc = scar[BC - 1] ? ex2(sG[BC - 1][ch]) * rsum : 0.f;
 #pragma unroll
-    for (int t = 0; t < BC; ++t) {
-      dgv[t] = fwd;
-      fwd += sP[t][tid];
+    for (int s2 = 0; s2 < NSG; ++s2) {
+      if (s2 < sg) fwd += sSegP[s2][ch];
+      if (s2 > sg) acc += sSegG[s2][ch];
+    }
+    float dgv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dgv[e] = fwd;
+      fwd += pl[e];
     }
 #pragma unroll
-    for (int t = BC - 1; t >= 0; --t) {
-      acc += sdG[t][tid];
-      dgv[t] += acc;
+    for (int e = 3; e >= 0; --e) {
+      acc += gl[e];
+      dgv[e] += acc;
     }
 #pragma unroll
-    for (int t = 0; t < BC; ++t)
-      if (t0 + t < p.L) p.dg[row_of(p, bb, t0 + t, h) + rr] = dgv[t];
+    for (int e = 0; e < 4; ++e)
+      if (t0 + 4 * sg + e < p.L) p.dg[row_of(p, bb, t0 + 4 * sg + e, h) + ch0 + ch] = dgv[e];
   }
 }
 
