@@ -246,36 +246,53 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   __shared__ int sseg[BC], scar[BC], slast[BC];
   __shared__ int sSafe[NWV];
 
-  const int u = blockIdx.x;
+  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
+  // Persistent: workgroup blockIdx.x takes units blockIdx.x, + gridDim.x, ...
+  // and loads the next unit's k and g (a thread's 4 tokens x 4 channels)
+  // during the current one's last phase, so only its first unit waits on
+  // them; q and b are loaded at the unit's start and staged after Kc.
+  constexpr int SIT = BC * KD / 4 / NT;
+  static_assert(SIT == 4 && NT == 16 * (KD / 4) && BC == 64, "token mapping of the staging loop");
+  const int nu = p.B * p.H * p.NC;
+  float4 nk[SIT], ng[SIT];
+  auto stage_load = [&](int un) {
+    const int c = un % p.NC, bh = un / p.NC, h = bh % p.H, bb = bh / p.H;
+    const int t0 = (p.c0 + c) * BC;
+#pragma unroll
+    for (int it = 0; it < SIT; ++it) {
+      const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
+      nk[it] = ng[it] = zero_f4();
+      if (t0 + i < p.L) {
+        const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
+        nk[it] = ld4g(p.k + ro);
+        ng[it] = ld4g(p.g + ro);
+      }
+    }
+  };
+  if (blockIdx.x < (unsigned)nu) stage_load(blockIdx.x);
+  for (int u = blockIdx.x; u < nu; u += gridDim.x) {
   const int c = u % p.NC, bh = u / p.NC, h = bh % p.H, bb = bh / p.H;
   const int t0 = (p.c0 + c) * BC;
-  const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   float* G = p.G + (int64_t)u * CK;
 
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
-  // stage q, beta = b k and the log2-decay (rows past the sequence end are
-  // zero); k stays in registers for Kc
-  constexpr int SIT = BC * KD / 4 / NT;
-  static_assert(SIT == 4 && NT == 16 * (KD / 4) && BC == 64, "token mapping of the staging loop");
-  float4 kst[SIT];
+  // stage the log2-decay (rows past the sequence end are zero); k stays in
+  // registers for Kc and beta = b k; q and b arrive during the decay scan
+  float4 kst[SIT], qst[SIT], bst[SIT];
 #pragma unroll
   for (int it = 0; it < SIT; ++it) {
     // a thread holds 4 consecutive tokens x 4 channels
     const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
-    float4 qv = zero_f4(), bv = zero_f4(), gv = zero_f4(), k4 = zero_f4();
-    if (t0 + i < p.L) {
-      const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
-      qv = ld4g(p.q + ro);
-      const float4 b4 = ld4g(p.b + ro);
-      k4 = ld4g(p.k + ro);
-      gv = ld4g(p.g + ro);
-      bv = make_float4(b4.x * k4.x, b4.y * k4.y, b4.z * k4.z, b4.w * k4.w);
-    }
-    kst[it] = k4;
-    *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qv;
-    *reinterpret_cast<float4*>(&sW[i][4 * c4]) = bv;
+    const float4 gv = ng[it];
+    kst[it] = nk[it];
     *reinterpret_cast<float4*>(&sG[i][4 * c4]) =
         make_float4(gv.x * kLog2e, gv.y * kLog2e, gv.z * kLog2e, gv.w * kLog2e);
+    qst[it] = bst[it] = zero_f4();
+    if (t0 + i < p.L) {
+      const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
+      qst[it] = ld4g(p.q + ro);
+      bst[it] = ld4g(p.b + ro);
+    }
   }
   lds_barrier();
   // ---- cumulative decay (log2 units): channel tid % 128, quarter tid / 128 --
@@ -321,6 +338,14 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     const float span = sG[16 * blk][ch] - sG[16 * blk + 15][ch];
     const bool safe = __all(span <= 64.f);
     if (l == 0) sSafe[wv] = safe;
+  }
+  // q and beta = b k
+#pragma unroll
+  for (int it = 0; it < SIT; ++it) {
+    const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
+    const float4 k4 = kst[it], b4 = bst[it];
+    *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qst[it];
+    *reinterpret_cast<float4*>(&sW[i][4 * c4]) = make_float4(b4.x * k4.x, b4.y * k4.y, b4.z * k4.z, b4.w * k4.w);
   }
   lds_barrier();
   // Kc and Kc^T in the scan operand order: per task one lane's run pair
@@ -581,6 +606,8 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     }
   }
 
+  if (u + (int)gridDim.x < nu) stage_load(u + gridDim.x);   // the next unit's inputs
+
   // ---- Xf = diag(carry) q e^G - M W, then P^T = (Xf^T dO)^T ------------------
   {
     f32x4 ax[4][TPW];
@@ -654,6 +681,8 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       }
       *reinterpret_cast<float4*>(PT + aofs(16 * wv + l16, 16 * kt + 4 * q, KD / 16)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
+  }
+  lds_barrier();   // the next unit reuses the LDS
   }
 }
 
@@ -1730,6 +1759,12 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   float* dcarry = nblk > 1 ? boundary(nblk) : nullptr;
 
   hipStream_t st = (hipStream_t)stream;
+  // k_bw_intra is persistent: at most one workgroup per CU (its LDS allows one)
+  int dev = 0, ncu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      ncu <= 0)
+    ncu = 256;
+  auto intra_grid = [&](unsigned n) { return dim3(std::min(n, (unsigned)ncu)); };
   const int chains = a->B * a->H * chains_per_head(p.bf);
   auto chain_grid = [](int nb) { return dim3((unsigned)(8 * ((nb + 7) / 8))); };
   auto block = [&](int j) {
@@ -1744,7 +1779,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.init = j == 0 ? (const float*)a->init_state : boundary(j);
     p.sfin = boundary(j + 1);
     p.dfin = nullptr; p.dinit = nullptr;
-    hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL(k_bw_intra, intra_grid(n), dim3(NT), 0, st, p);
     if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
     else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
   }
@@ -1758,7 +1793,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.sfin = nullptr;
     p.dfin = j == nblk - 1 ? (const float*)a->d_final : dcarry;
     p.dinit = j == 0 ? (float*)a->d_init : dcarry;
-    hipLaunchKernelGGL(k_bw_intra, dim3(n), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL(k_bw_intra, intra_grid(n), dim3(NT), 0, st, p);
     if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
     else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
     if (p.bf) hipLaunchKernelGGL(k_bw_grads<true>, dim3(n), dim3(NT), 0, st, p);
