@@ -149,7 +149,7 @@ __device__ __forceinline__ int gofs(int i, int c, int ns) {
 // bf16 mode keeps the four scan operands split: run pair (blk, s) is 64
 // lanes x 8 high bf16 words, then 64 lanes x 8 low words, element (i, c) at
 // index e = 4 * (run) + (c & 3) of its lane (the same bytes as the fp32
-// pair).  op_put4 / op_get4 store and load either form.
+// pair).  op_put4 / op_put8 / op_get8 store and load either form.
 __device__ __forceinline__ int bofs(int i, int c, int ns) {
   const int cc = c & 31;
   return ((i >> 4) * ns + (c >> 5)) * 1024 + (((cc & 15) >> 2) * 16 + (i & 15)) * 8 + (cc >> 4) * 4 + (c & 3);
@@ -189,16 +189,18 @@ __device__ __forceinline__ void op_put8(bool bf, float* arr, int i, int c, int n
     *reinterpret_cast<float4*>(arr + gofs(i, c + 16, ns)) = make_float4(x[4], x[5], x[6], x[7]);
   }
 }
+// the 8 values op_put8 stores for one lane of a run pair
 template <bool BF>
-__device__ __forceinline__ float4 op_get4(const float* arr, int i, int c, int ns) {
+__device__ __forceinline__ void op_get8(const float* arr, int i, int c, int ns, float* x) {
   if constexpr (BF) {
     const bf16* b = reinterpret_cast<const bf16*>(arr) + bofs(i, c, ns);
-    const bf16x4 h = *reinterpret_cast<const bf16x4*>(b);
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(b + 512);
-    return make_float4((float)h[0] + (float)lo[0], (float)h[1] + (float)lo[1], (float)h[2] + (float)lo[2],
-                       (float)h[3] + (float)lo[3]);
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(b);
+    const bf16x8 lo = *reinterpret_cast<const bf16x8*>(b + 512);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)h[e] + (float)lo[e];
   } else {
-    return ld4g(arr + gofs(i, c, ns));
+    const float4 a = ld4g(arr + gofs(i, c, ns)), d = ld4g(arr + gofs(i, c + 16, ns));
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = d.x; x[5] = d.y; x[6] = d.z; x[7] = d.w;
   }
 }
 // PT (128 x 128) and U0T (128 x chunk) in accumulator order: a 16 x 16 tile
@@ -1028,8 +1030,19 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
     *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
-    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = op_get4<BF>(p.Wm + (int64_t)u * CK, i, 4 * c4, KD / 32);
   }
+  // W (then Kc below) from the scan operand order: per task one lane's run pair
+  auto stage_op = [&](const float* arr, float (*dstT)[KP]) {
+    for (int task = tid; task < BC * KD / 8; task += NT) {
+      const int ln = task & 63, pr = task >> 6, blk = pr / (KD / 32), s = pr % (KD / 32);
+      const int i = 16 * blk + (ln & 15), cc = 32 * s + 4 * (ln >> 4);
+      float x[8];
+      op_get8<BF>(arr, i, cc, KD / 32, x);
+      *reinterpret_cast<float4*>(&dstT[i][cc]) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(&dstT[i][cc + 16]) = make_float4(x[4], x[5], x[6], x[7]);
+    }
+  };
+  stage_op(p.Wm + (int64_t)u * CK, sT);
 #pragma unroll
   for (int it = 0; it < CC / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
@@ -1042,11 +1055,19 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   zero_acc(acc);
   nt_lds<BF>(acc, &sT[0][0], yA, q, l16);
   load_yT(yB, dSC, wv, q, l16);
-  float4 kc[BC * KD / 4 / NT];
+  // Kc: this thread's two run-pair lanes, staged once W is done
+  static_assert(BC * KD / 8 == 2 * NT, "two run-pair lanes per thread");
+  float kcx[2][8];
+  auto kc_pos = [&](int t2, int& i, int& cc) {
+    const int task = tid + NT * t2, ln = task & 63, pr = task >> 6;
+    i = 16 * (pr / (KD / 32)) + (ln & 15);
+    cc = 32 * (pr % (KD / 32)) + 4 * (ln >> 4);
+  };
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
-    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    kc[it] = op_get4<BF>(p.Kc + (int64_t)u * CK, i, 4 * c4, KD / 32);
+  for (int t2 = 0; t2 < 2; ++t2) {
+    int i, cc;
+    kc_pos(t2, i, cc);
+    op_get8<BF>(p.Kc + (int64_t)u * CK, i, cc, KD / 32, kcx[t2]);
   }
 #pragma unroll
   for (int I = 0; I < 4; ++I)
@@ -1054,9 +1075,11 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     for (int e = 0; e < 4; ++e) sU[16 * I + 4 * q + e][vcol] = f4at(u0[I], e) - acc[I][0][e];
   lds_barrier();   // U complete; every wave is done with W
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
-    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    *reinterpret_cast<float4*>(&sT[i][4 * c4]) = kc[it];
+  for (int t2 = 0; t2 < 2; ++t2) {
+    int i, cc;
+    kc_pos(t2, i, cc);
+    *reinterpret_cast<float4*>(&sT[i][cc]) = make_float4(kcx[t2][0], kcx[t2][1], kcx[t2][2], kcx[t2][3]);
+    *reinterpret_cast<float4*>(&sT[i][cc + 16]) = make_float4(kcx[t2][4], kcx[t2][5], kcx[t2][6], kcx[t2][7]);
   }
 
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
