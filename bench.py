@@ -502,8 +502,8 @@ def rocprof_backward_summary(kt_dir):
              "summarised by:", "", "    python bench.py --rocprof-backward-summary gpurun_out/bwkt", "",
              "Workload: chunk_gdn2(is_inference=False) forward + backward under torch.autograd, B=1 L=2048 Hk=12 "
              "Hv=24 K=V=128 (bf16 q/k/v, fp32 gates, 2 segments, qk_l2norm); the backward runs at H=24 value heads, "
-             "32 chunks of 64 tokens (768 (head, chunk) units), precision bf16: the state scans (k_bw_chains) and k_bw_intra in fp32 (v_mfma_f32_16x16x4_f32), k_bw_grads and "
-             "k_bw_dqk's products in split bf16 (hi/lo words, 3 v_mfma_f32_16x16x32_bf16 per product).  The "
+             "32 chunks of 64 tokens (768 (head, chunk) units), precision bf16: k_bw_chains (state scans, 32-column blocks) and k_bw_grads run their products as split bf16 "
+             "(hi/lo words, 3 v_mfma_f32_16x16x32_bf16 per product), k_bw_intra and k_bw_dqk on v_mfma_f32_16x16x4_f32.  The "
              "first four kernels are the recurrence backward (dn_prefill_bwd's kernels); the rest are the raw-input "
              "prologue recompute and the gradient sums back to the raw layouts.", "",
              "| kernel | dispatches | avg us | min us | max us |", "|---|---|---|---|---|"]
@@ -727,7 +727,7 @@ def main():
         bw = backward_work(H=tv.shape[2])
         bw_s = bw_us * 1e-6
         train = {"workload": "chunk_gdn2 forward + backward (is_inference=False, autograd), config-2 shape, "
-                             "precision bf16 (backward: fp32 scans, split-bf16 gradient products)", "us_per_step": round(t_us, 1),
+                             "precision bf16 (backward: split-bf16 scans and gradient products)", "us_per_step": round(t_us, 1),
                  "kernels_us_per_step": tk_us,
                  "backward_roofline": {"bound": "mfma", "dtype": "fp32", "flops": bw["flops"],
                                        "achieved": round(bw["flops"] / bw_s / 1e12, 2) if bw_s else None,
