@@ -66,7 +66,9 @@ def compare(got, ref, tol, tag):
         assert e < tol, f"{tag}: gradient {n} rel L2 {e:.2e} exceeds {tol:.1e}"
 
 
-@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 1e-2)])
+# bf16 mode: split-bf16 products (16 significant bits) measure ~5e-6; the bound
+# leaves 10x headroom
+@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 5e-5)])
 @pytest.mark.parametrize("L", [128, 256, 512])
 def test_backward_parity(precision, tol, L):
     B, Hk, Hv = 1, 2, 4
@@ -77,7 +79,8 @@ def test_backward_parity(precision, tol, L):
     o_ref, _ = O.chunk_gdn2(q, k, v, g, b, w, is_inference=False)
     e_o = rel_l2(out, o_ref)
     print(f"[measured] L={L} {precision}: out rel L2 {e_o:.2e}", flush=True)
-    assert e_o < tol
+    # the forward's bf16 mode runs its plain products on bf16 MFMA: ~9e-5
+    assert e_o < (tol if precision == "fp32" else 5e-4)
     compare(got, ref, tol, f"parity L={L} {precision}")
 
 
@@ -117,11 +120,12 @@ def test_backward_strong_decay(precision):
     do = np.random.default_rng(503).standard_normal((B, L, Hv, 128))
     _, got = run_dev(q, k, v, g, b, w, do, precision=precision)
     ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
-    compare(got, ref, 1e-3 if precision == "fp32" else 1e-2, f"strong decay {precision}")
+    # measured 2e-7 (fp32) and 4e-6 (bf16)
+    compare(got, ref, 1e-5 if precision == "fp32" else 5e-5, f"strong decay {precision}")
 
 
 
-@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 1e-2)])
+@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 5e-5)])
 def test_backward_odd_heads_two_batches(precision, tol):
     """B = 2, three value heads on one key head (G = 3) and an unaligned length:
     24 chain workgroups per direction (not a multiple of 8 heads per XCD) and a
@@ -353,16 +357,20 @@ def test_backward_fuse_prologue_with_guard(saturate, tol):
     assert np.abs(got["dg"][(g > -3) & (g < 0)]).max() > 0
 
 
-@pytest.mark.parametrize("with_init", [False, True])
-def test_backward_recompute_states_bit_identical(with_init):
+@pytest.mark.parametrize("with_init, shape", [(False, (2, 3000, 16, 32)), (True, (2, 3000, 16, 32)),
+                                               (True, (1, 3000, 11, 33))])
+def test_backward_recompute_states_bit_identical(with_init, shape):
     """recompute_states=True (token blocks, only block-boundary states kept,
     chunk states recomputed per block: reference gdn2.py:655-695, 1614-1630)
     gives gradients bit-identical to the single-pass backward.  B * Hv = 64
     (batch, head) pairs make a block 16 chunks (1024 tokens), so L = 3000 runs
-    three blocks; document boundaries sit inside and across block edges."""
+    three blocks; document boundaries sit inside and across block edges.  With
+    B * Hv = 33 a block is 32 chunks (two blocks), and the forward-only scan
+    launch has 132 column-block chains, not a multiple of the 8 XCDs (its
+    padding blocks exit at once)."""
     from deltanet_tpu_amd import chunk_gdn2
 
-    B, L, Hk, Hv = 2, 3000, 16, 32
+    B, L, Hk, Hv = shape
     rng = np.random.default_rng(77)
     f = lambda *s: rng.standard_normal(s).astype(np.float32)
     q, k, v = f(B, L, Hk, 128), f(B, L, Hk, 128), f(B, L, Hv, 128)
@@ -371,7 +379,8 @@ def test_backward_recompute_states_bit_identical(with_init):
     seg = np.zeros((B, L), np.int32)
     seg[0, 1000:] = 1
     seg[0, 1024:] = 2        # a document starting exactly at the first block edge
-    seg[1, 2100:] = 1
+    if B > 1:
+        seg[1, 2100:] = 1
     init = (0.05 * f(B, Hv, 128, 128)) if with_init else None
     do, df = f(B, L, Hv, 128), f(B, Hv, 128, 128)
     res = {}
