@@ -80,6 +80,7 @@ struct BW {
   float *TT;   // [BC][BC] T^T
   float *lam;  // [KD]
   float *dMw, *dAw; // [BC][BC] dM and dA (k_bw_grads -> k_bw_dqk)
+  float *RS;   // [KD] rowsum over v of S_c * dS_{c+1} per channel (k_bw_grads -> k_bw_dqk)
   float *Rq, *Rk, *Rb; // raw dO S0^T, U dSC^T, dX S0^T (k_bw_grads -> k_bw_dqk), in
                        // MFMA accumulator order: [column tile][row block][lane][4]
   float *S;         // [KD][KD] state entering the chunk, transposed: element (v, k) at v * KD + k
@@ -1082,6 +1083,18 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     *reinterpret_cast<float4*>(&sT[i][cc + 16]) = make_float4(kcx[t2][4], kcx[t2][5], kcx[t2][6], kcx[t2][7]);
   }
 
+  // rowsum over v of S0 * dSC for channel 16 wv + l16 (the lane's S0 and dSC
+  // columns hold the same (k, v) pairs; the 4 lanes of a channel split v)
+  {
+    float rs = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rs += yS0[s][e] * yB[s][e];
+    rs += __shfl_xor(rs, 16);
+    rs += __shfl_xor(rs, 32);
+    if (q == 0) p.RS[(int64_t)u * KD + vcol] = rs;
+  }
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
   load_y(yA, dSC, wv, q, l16);
   zero_acc(acc);
@@ -1221,7 +1234,6 @@ constexpr int HP = HC + 4;
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_bw_dqk(BW p) {
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
-  __shared__ float sRS[NT / HC][HC];   // partial rowsums of S0 * dSC
   __shared__ float sSegP[NT / HC][HC], sSegG[NT / HC][HC];   // 4-token segment sums of P and dG
   __shared__ int scar[BC], slast[BC], sseg[BC];
 
@@ -1253,21 +1265,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       rk[Ib][e] = vi ? f4at(fk, e) : 0.f;
     }
   }
-  // rowsum(S0 * dSC) of channel ch0 + tid % HC over the value range of part
-  // tid / HC (the states are stored transposed: channel k of row v at v * KD + k,
-  // so a wave reads consecutive channels)
-  constexpr int PARTS = NT / HC;
-  float rs = 0.f;
-  {
-    const int cr = ch0 + tid % HC, part = tid / HC;
-    const float* S0 = p.S + (int64_t)u * KK + cr;
-    const float* dSC = p.dS + (int64_t)u * KK + cr;
-#pragma unroll
-    for (int vv = 0; vv < KD / PARTS; ++vv) {
-      const int v = (KD / PARTS) * part + vv;
-      rs += S0[v * KD] * dSC[v * KD];
-    }
-  }
+  // rowsum(S0 * dSC) of the thread's channel, formed by k_bw_grads
+  const float rsum = p.RS[(int64_t)u * KD + ch0 + tid % HC];
   if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
 #pragma unroll
   for (int it = 0; it < BC * HC / 4 / NT; ++it) {
@@ -1290,7 +1289,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   }
   lds_barrier();
 
-  sRS[tid / HC][tid % HC] = rs;
   const float glast = sG[BC - 1][rl];
   float rdg[NB][4], rpp[NB][4];   // dG and P of this lane's rows
 #pragma unroll
@@ -1401,9 +1399,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     }
     sSegP[sg][ch] = ps;
     sSegG[sg][ch] = gs;
-    float rsum = 0.f;
-#pragma unroll
-    for (int pp = 0; pp < NSG; ++pp) rsum += sRS[pp][ch];
     lds_barrier();
     float fwd = 0.f, acc = scar[BC - 1] ? ex2(sG[BC - 1][ch]) * rsum : 0.f;
 #pragma unroll
@@ -1705,7 +1700,7 @@ using namespace dn;
 
 namespace {
 
-constexpr size_t kUnitFloats = 9 * (size_t)CK + 4 * (size_t)CC + KD + 3 * (size_t)KK;
+constexpr size_t kUnitFloats = 9 * (size_t)CK + 4 * (size_t)CC + 2 * KD + 3 * (size_t)KK;
 
 // Chunks per token block: the whole sequence, or with recompute_states the
 // smallest number of chunks that still gives kRecomputeUnits (batch, head,
@@ -1773,7 +1768,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   auto take = [&](size_t per) { float* r = ws; ws += units * per; return r; };
   p.G = take(CK); p.Wm = take(CK); p.WT = take(CK); p.Kc = take(CK); p.KcT = take(CK);
   p.PT = take(KK); p.U0T = take(CK); p.MT = take(CC); p.TT = take(CC); p.lam = take(KD);
-  p.dMw = take(CC); p.dAw = take(CC); p.Rq = take(CK); p.Rk = take(CK); p.Rb = take(CK);
+  p.dMw = take(CC); p.dAw = take(CC); p.Rq = take(CK); p.Rk = take(CK); p.Rb = take(CK); p.RS = take(KD);
   p.S = take(KK); p.dS = take(KK);
   // the state entering block j (j >= 1), (B, H, K, V) each, then the carried
   // state gradient

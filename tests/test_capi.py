@@ -100,7 +100,7 @@ def test_invalid_args_rejected_without_gpu():
     for f in ("q", "k", "v", "g", "b", "w", "d_out", "dq", "dk", "dv", "dg", "db", "dw"):
         setattr(bw, f, 0x1000)
     need = lib.dn_prefill_bwd_workspace_size(ctypes.byref(bw))
-    assert need == 4 * 2 * 4 * (9 * 64 * 128 + 4 * 64 * 64 + 128 + 3 * 128 * 128)   # bytes: 2 chunks x 4 heads
+    assert need == 4 * 2 * 4 * (9 * 64 * 128 + 4 * 64 * 64 + 2 * 128 + 3 * 128 * 128)   # bytes: 2 chunks x 4 heads
     assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -2
     bw.d_init = 0x1000
     assert lib.dn_prefill_bwd(ctypes.byref(bw), None, 0, None) == -1 and b"init_state" in lib.dn_last_error()
@@ -114,7 +114,7 @@ def test_invalid_args_rejected_without_gpu():
     ra.g_heads, ra.g_chans, ra.b_heads, ra.b_chans, ra.w_heads, ra.w_chans = 2, 128, 2, 128, 4, 128
     ra.qk_dtype, ra.v_dtype = _lib.DN_BF16, _lib.DN_BF16
     need = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
-    core = 4 * 2 * 4 * (9 * 64 * 128 + 4 * 64 * 64 + 128 + 3 * 128 * 128)
+    core = 4 * 2 * 4 * (9 * 64 * 128 + 4 * 64 * 64 + 2 * 128 + 3 * 128 * 128)
     assert need == 512 + 11 * 1 * 128 * 4 * 128 * 4 + core
     fake = [0x1000] * 6 + [None]   # dq dk dv dg db dw, no d_init
     assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -2
@@ -129,7 +129,7 @@ def test_recompute_states_workspace_size():
     chunk) units) plus one (B,H,128,128) f32 state per block boundary and one
     carried state gradient; without it, every chunk of the sequence."""
     lib = _lib.load_library()
-    unit = 4 * (9 * 64 * 128 + 4 * 64 * 64 + 128 + 3 * 128 * 128)   # bytes per (batch, head, chunk)
+    unit = 4 * (9 * 64 * 128 + 4 * 64 * 64 + 2 * 128 + 3 * 128 * 128)   # bytes per (batch, head, chunk)
     kk = 4 * 128 * 128
     bw = _lib.BackwardArgs()
     bw.abi_version = _lib.DN_ABI_VERSION
