@@ -980,21 +980,87 @@ __device__ __forceinline__ void load_yT(float (&y)[4][8], const float* X, int wv
     for (int e = 0; e < 8; ++e) y[s][e] = X[(32 * s + pi_k(q, e)) * KD + 16 * wv + l16];
 }
 
-// acc[I] += X[rows 16I..][:] * Y^T with X in LDS (row pitch KP) and Y preloaded
-template <bool BF>
-__device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, const float (&y)[4][8], int q,
-                                       int l16) {
-  using O = Op<BF>;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const typename O::F b = O::make(y[s]);
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      float x[8];
-      row8(X + (16 * I + l16) * KP, s, q, x);
-      O::mac(acc[I][0], O::make(x), b);
-    }
+// A 64 x W matrix in LDS: fp32, or in bf16 mode split into high and low
+// bf16 planes (the same bytes), so that the split products read their
+// operands without converting them: each value is split once, by the thread
+// that stores it, instead of by every wave that reads it.
+template <bool BF, int W> struct LMat;
+template <int W> struct LMat<false, W> {
+  float a[BC][W + 4];
+  __device__ __forceinline__ Frag<false> row_frag(int r, int s, int q) const {
+    float x[8];
+    row8(&a[r][0], s, q, x);
+    return fr8(x);
   }
+  // column c, rows 32 s + pi_k(q, e)
+  __device__ __forceinline__ Frag<false> col_frag(int c, int s, int q) const {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = a[32 * s + pi_k(q, e)][c];
+    return fr8(x);
+  }
+  __device__ __forceinline__ void put(int r, int c, float v) { a[r][c] = v; }
+  __device__ __forceinline__ void put4(int r, int c, float4 v) { *reinterpret_cast<float4*>(&a[r][c]) = v; }
+  __device__ __forceinline__ float4 get4(int r, int c) const { return *reinterpret_cast<const float4*>(&a[r][c]); }
+};
+template <int W> struct LMat<true, W> {
+  bf16 h[BC][W + 4], lw[BC][W + 4];
+  __device__ __forceinline__ Pol<true>::F3 row_frag(int r, int s, int q) const {
+    Pol<true>::F3 f;
+    const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&h[r][32 * s + 4 * q]);
+    const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&h[r][32 * s + 16 + 4 * q]);
+    const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&lw[r][32 * s + 4 * q]);
+    const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&lw[r][32 * s + 16 + 4 * q]);
+    f.hi.v = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+    f.lo.v = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+    return f;
+  }
+  __device__ __forceinline__ Pol<true>::F3 col_frag(int c, int s, int q) const {
+    Pol<true>::F3 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      f.hi.v[e] = h[32 * s + pi_k(q, e)][c];
+      f.lo.v[e] = lw[32 * s + pi_k(q, e)][c];
+    }
+    return f;
+  }
+  __device__ __forceinline__ void put(int r, int c, float v) {
+    const bf16 x = (bf16)v;
+    h[r][c] = x;
+    lw[r][c] = (bf16)(v - (float)x);
+  }
+  __device__ __forceinline__ void put4(int r, int c, float4 v) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    bf16x4 hh, ll;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hh[e] = (bf16)x[e];
+      ll[e] = (bf16)(x[e] - (float)hh[e]);
+    }
+    *reinterpret_cast<bf16x4*>(&h[r][c]) = hh;
+    *reinterpret_cast<bf16x4*>(&lw[r][c]) = ll;
+  }
+  __device__ __forceinline__ float4 get4(int r, int c) const {
+    const bf16x4 hh = *reinterpret_cast<const bf16x4*>(&h[r][c]);
+    const bf16x4 ll = *reinterpret_cast<const bf16x4*>(&lw[r][c]);
+    return make_float4((float)hh[0] + (float)ll[0], (float)hh[1] + (float)ll[1], (float)hh[2] + (float)ll[2],
+                       (float)hh[3] + (float)ll[3]);
+  }
+};
+
+// acc[I] += X[rows 16I..][:] * Y^T with X in LDS and Y's fragments preloaded
+template <bool BF>
+__device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const LMat<BF, KD>& X,
+                                       const typename Op<BF>::F (&y)[4], int q, int l16) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int I = 0; I < 4; ++I) Op<BF>::mac(acc[I][0], X.row_frag(16 * I + l16, s, q), y[s]);
+}
+template <bool BF>
+__device__ __forceinline__ void split4(const float (&y)[4][8], typename Op<BF>::F (&f)[4]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) f[s] = Op<BF>::make(y[s]);
 }
 
 // Every operand that comes from global memory is loaded one phase ahead of
@@ -1003,11 +1069,8 @@ __device__ __forceinline__ void nt_lds(f32x4 (&acc)[4][TPW], const float* X, con
 template <bool BF>
 __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   using O = Op<BF>;
-  __shared__ float sdO[BC][KP];
-  __shared__ float sX[BC][KP];       // dU, then dX
-  __shared__ float sU[BC][KP];
-  __shared__ float sT[BC][KP];       // W, then Kc
-  __shared__ float sMT[BC][CP];      // M^T
+  __shared__ LMat<BF, KD> sdO, sX, sU, sT;   // sX: dU, then dX; sT: W, then Kc
+  __shared__ LMat<BF, BC> sMT;               // M^T
   __shared__ int sseg[BC], scar[BC], slast[BC];
   static_assert(TPW == 1, "one 16-column tile per wave");
 
@@ -1030,31 +1093,33 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int it = 0; it < BC * KD / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     const float4 v = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
-    *reinterpret_cast<float4*>(&sdO[i][4 * c4]) = v;
+    sdO.put4(i, 4 * c4, v);
   }
   // W (then Kc below) from the scan operand order: per task one lane's run pair
-  auto stage_op = [&](const float* arr, float (*dstT)[KP]) {
+  auto stage_op = [&](const float* arr, LMat<BF, KD>& dstT) {
     for (int task = tid; task < BC * KD / 8; task += NT) {
       const int ln = task & 63, pr = task >> 6, blk = pr / (KD / 32), s = pr % (KD / 32);
       const int i = 16 * blk + (ln & 15), cc = 32 * s + 4 * (ln >> 4);
       float x[8];
       op_get8<BF>(arr, i, cc, KD / 32, x);
-      *reinterpret_cast<float4*>(&dstT[i][cc]) = make_float4(x[0], x[1], x[2], x[3]);
-      *reinterpret_cast<float4*>(&dstT[i][cc + 16]) = make_float4(x[4], x[5], x[6], x[7]);
+      dstT.put4(i, cc, make_float4(x[0], x[1], x[2], x[3]));
+      dstT.put4(i, cc + 16, make_float4(x[4], x[5], x[6], x[7]));
     }
   };
   stage_op(p.Wm + (int64_t)u * CK, sT);
 #pragma unroll
   for (int it = 0; it < CC / 4 / NT; ++it) {
     const int idx = tid + NT * it, i = idx / (BC / 4), c4 = idx % (BC / 4);
-    *reinterpret_cast<float4*>(&sMT[i][4 * c4]) = ld4g(p.MT + (int64_t)u * CC + i * BC + 4 * c4);
+    sMT.put4(i, 4 * c4, ld4g(p.MT + (int64_t)u * CC + i * BC + 4 * c4));
   }
   lds_barrier();
 
   f32x4 acc[4][TPW];
   // ---- U = U0 - W S0 ---------------------------------------------------------
   zero_acc(acc);
-  nt_lds<BF>(acc, &sT[0][0], yA, q, l16);
+  typename O::F fA[4], fS0[4], fB[4];
+  split4<BF>(yA, fA);
+  nt_lds<BF>(acc, sT, fA, q, l16);
   load_yT(yB, dSC, wv, q, l16);
   // Kc: this thread's two run-pair lanes, staged once W is done
   static_assert(BC * KD / 8 == 2 * NT, "two run-pair lanes per thread");
@@ -1073,14 +1138,14 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sU[16 * I + 4 * q + e][vcol] = f4at(u0[I], e) - acc[I][0][e];
+    for (int e = 0; e < 4; ++e) sU.put(16 * I + 4 * q + e, vcol, f4at(u0[I], e) - acc[I][0][e]);
   lds_barrier();   // U complete; every wave is done with W
 #pragma unroll
   for (int t2 = 0; t2 < 2; ++t2) {
     int i, cc;
     kc_pos(t2, i, cc);
-    *reinterpret_cast<float4*>(&sT[i][cc]) = make_float4(kcx[t2][0], kcx[t2][1], kcx[t2][2], kcx[t2][3]);
-    *reinterpret_cast<float4*>(&sT[i][cc + 16]) = make_float4(kcx[t2][4], kcx[t2][5], kcx[t2][6], kcx[t2][7]);
+    sT.put4(i, cc, make_float4(kcx[t2][0], kcx[t2][1], kcx[t2][2], kcx[t2][3]));
+    sT.put4(i, cc + 16, make_float4(kcx[t2][4], kcx[t2][5], kcx[t2][6], kcx[t2][7]));
   }
 
   // rowsum over v of S0 * dSC for channel 16 wv + l16 (the lane's S0 and dSC
@@ -1097,11 +1162,13 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   }
   // ---- U dSC^T (Kc part of dk, raw) and dO S0^T (dq, raw) -------------------
   load_y(yA, dSC, wv, q, l16);
+  split4<BF>(yB, fB);
+  split4<BF>(yS0, fS0);
   zero_acc(acc);
-  nt_lds<BF>(acc, &sU[0][0], yB, q, l16);
+  nt_lds<BF>(acc, sU, fB, q, l16);
   store_frag(p.Rk + (int64_t)u * CK, wv, l, acc);
   zero_acc(acc);
-  nt_lds<BF>(acc, &sdO[0][0], yS0, q, l16);
+  nt_lds<BF>(acc, sdO, fS0, q, l16);
   store_frag(p.Rq + (int64_t)u * CK, wv, l, acc);
   // T^T rows and this lane's w, v for the dX phase
   float tt[2][4][8];
@@ -1126,32 +1193,23 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   zero_acc(acc);
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    float x[8];
+    const typename O::F bfr = sdO.col_frag(vcol, s, q);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = sdO[32 * s + pi_k(q, e)][vcol];
-    const typename O::F bfr = O::make(x);
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      float y[8];
-      row8(&sMT[16 * I + l16][0], s, q, y);
-      O::mac(acc[I][0], O::make(y), bfr);
-    }
+    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);
   }
-  nt_lds<BF>(acc, &sT[0][0], yA, q, l16);
+  split4<BF>(yA, fA);
+  nt_lds<BF>(acc, sT, fA, q, l16);
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][0][e];
+    for (int e = 0; e < 4; ++e) sX.put(16 * I + 4 * q + e, vcol, acc[I][0][e]);
   lds_barrier();
 
   // ---- dX = T^T dU ; dv = dX w ; dw = dX v ----------------------------------
   zero_acc(acc);
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = sX[32 * s + pi_k(q, e)][vcol];
-    const typename O::F bfr = O::make(x);
+    const typename O::F bfr = sX.col_frag(vcol, s, q);
 #pragma unroll
     for (int I = 0; I < 4; ++I) O::mac(acc[I][0], O::make(tt[s][I]), bfr);
   }
@@ -1159,7 +1217,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 #pragma unroll
   for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sX[16 * I + 4 * q + e][vcol] = acc[I][0][e];
+    for (int e = 0; e < 4; ++e) sX.put(16 * I + 4 * q + e, vcol, acc[I][0][e]);
   lds_barrier();
   // dv = dX w, dw = dX v, row-major and coalesced
 #pragma unroll
@@ -1167,7 +1225,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
     if (t0 + i < p.L) {
       const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
-      const float4 dx = *reinterpret_cast<const float4*>(&sX[i][4 * c4]);
+      const float4 dx = sX.get4(i, 4 * c4);
       const float4 a = wq[it], v4 = vq[it];
       const float4 dv = make_float4(dx.x * a.x, dx.y * a.y, dx.z * a.z, dx.w * a.w);
       if (p.dv_dt == DT_BF16) {
@@ -1183,7 +1241,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
 
   // ---- dX S0^T (the initial-state part of dbeta, raw) -----------------------
   zero_acc(acc);
-  nt_lds<BF>(acc, &sX[0][0], yS0, q, l16);
+  nt_lds<BF>(acc, sX, fS0, q, l16);
   store_frag(p.Rb + (int64_t)u * CK, wv, l, acc);
 
   // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
@@ -1193,14 +1251,9 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
     float* dst = (isA ? p.dAw : p.dMw) + (int64_t)u * CC;
     f32x4 a = zero4();
     if (J <= I) {
-      const float* Xs = isA ? &sX[0][0] : &sdO[0][0];
+      const LMat<BF, KD>& Xs = isA ? sX : sdO;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float xa[8], xb[8];
-        row8(Xs + (16 * I + l16) * KP, s, q, xa);
-        row8(&sU[16 * J + l16][0], s, q, xb);
-        O::mac(a, O::make(xa), O::make(xb));
-      }
+      for (int s = 0; s < 4; ++s) O::mac(a, Xs.row_frag(16 * I + l16, s, q), sU.row_frag(16 * J + l16, s, q));
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
