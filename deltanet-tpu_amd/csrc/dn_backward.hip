@@ -396,45 +396,53 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   // on the diagonal the column factor is >= 1, which is used only where the
   // block's decay span keeps it below 2^64 -- otherwise every element takes
   // e^{G_i - G_j} directly.
-  for (int task = wv; task < 20; task += NWV) {
-    const bool isM = task >= 10;
-    const int tt = task % 10;
+  // one task per lower-triangle tile (I, J) forms both A_IJ and M_IJ: they
+  // share the column operand k_j e^{G_m - G_j} and the row factor
+  // e^{G_i - G_m}
+  for (int tt = wv; tt < 10; tt += NWV) {
     const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
     const int J = tt - I * (I + 1) / 2;
     const bool diag = J == I;
-    float res[4];
+    float resA[4], resM[4];
     if (!diag || (sSafe[2 * I] & sSafe[2 * I + 1])) {
       const int m = 16 * I;
       const int i = 16 * I + l16, j = 16 * J + l16;
       const bool vi = t0 + i < p.L, vj = t0 + j < p.L;
-      const float* xi = isM ? &sQ[i][0] : &sW[i][0];
       const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
-      f32x4 acc = zero4();
+      f32x4 accA = zero4(), accM = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        float xa[8], xb[8], gi[8], gm[8], gj[8];
-        row8(xi, s, q, xa);
+        float xa[8], xq[8], xb[8], gi[8], gm[8], gj[8];
+        row8(&sW[i][0], s, q, xa);
+        row8(&sQ[i][0], s, q, xq);
         row8(kj, s, q, xb);
         row8(&sG[i][0], s, q, gi);
         row8(&sG[m][0], s, q, gm);
         row8(&sG[j][0], s, q, gj);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          xa[e] = vi ? xa[e] * ex2(gi[e] - gm[e]) : 0.f;
+          const float fi = vi ? ex2(gi[e] - gm[e]) : 0.f;
+          xa[e] *= fi;
+          xq[e] *= fi;
           const float fb = diag ? __builtin_amdgcn_exp2f(gm[e] - gj[e]) : ex2(gm[e] - gj[e]);
           xb[e] = vj ? xb[e] * fb : 0.f;
         }
-        mma(acc, fr8(xa), fr8(xb));
+        const Frag<false> fbk = fr8(xb);
+        mma(accA, fr8(xa), fbk);
+        mma(accM, fr8(xq), fbk);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) res[e] = acc[e];
+      for (int e = 0; e < 4; ++e) {
+        resA[e] = accA[e];
+        resM[e] = accM[e];
+      }
     } else {
       // diagonal block with a large decay span: e^{G_i - G_j} per element
       const int j = 16 * I + l16;
       const bool vj = t0 + j < p.L;
       const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) res[e] = 0.f;
+      for (int e = 0; e < 4; ++e) resA[e] = resM[e] = 0.f;
 #pragma unroll 8
       for (int r4 = 0; r4 < KD / 4; ++r4) {
         const float4 kv = ld4g(kj + 4 * r4);
@@ -442,18 +450,22 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 16 * I + 4 * q + e;
-          const float4 xv = *reinterpret_cast<const float4*>(isM ? &sQ[i][4 * r4] : &sW[i][4 * r4]);
+          const float4 wv4 = *reinterpret_cast<const float4*>(&sW[i][4 * r4]);
+          const float4 qv4 = *reinterpret_cast<const float4*>(&sQ[i][4 * r4]);
           const float4 giv = *reinterpret_cast<const float4*>(&sG[i][4 * r4]);
-          res[e] += xv.x * kv.x * ex2(giv.x - gjv.x) + xv.y * kv.y * ex2(giv.y - gjv.y) +
-                    xv.z * kv.z * ex2(giv.z - gjv.z) + xv.w * kv.w * ex2(giv.w - gjv.w);
+          const float f0 = kv.x * ex2(giv.x - gjv.x), f1 = kv.y * ex2(giv.y - gjv.y);
+          const float f2 = kv.z * ex2(giv.z - gjv.z), f3 = kv.w * ex2(giv.w - gjv.w);
+          resA[e] += wv4.x * f0 + wv4.y * f1 + wv4.z * f2 + wv4.w * f3;
+          resM[e] += qv4.x * f0 + qv4.y * f1 + qv4.z * f2 + qv4.w * f3;
         }
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * q + e, j = 16 * J + l16;
-      const bool ok = (isM ? j <= i : j < i) && sseg[i] == sseg[j] && t0 + i < p.L && t0 + j < p.L;
-      (isM ? sM : sA)[i][j] = ok ? res[e] : 0.f;
+      const bool same = sseg[i] == sseg[j] && t0 + i < p.L && t0 + j < p.L;
+      sA[i][j] = same && j < i ? resA[e] : 0.f;
+      sM[i][j] = same && j <= i ? resM[e] : 0.f;
     }
   }
   // w and v of this lane's W / U0 operands, loaded now and used after T
