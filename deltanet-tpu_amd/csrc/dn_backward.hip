@@ -1981,7 +1981,10 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   c.B = a->B; c.L = a->L; c.H = a->Hv; c.K = KD; c.V = KD;
   c.q = r.qe; c.k = r.ke; c.v = r.ve; c.g = r.ge; c.b = r.be; c.w = r.w_alias ? a->w : r.we;
   c.seg = r.canon; c.init_state = a->init_state; c.d_out = d_out; c.d_final = d_final;
-  c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = pre[10];
+  // without the fused prologue, w's step has derivative 1: at Hv heads and
+  // channel-wise the recurrence backward writes dw in its raw layout itself
+  const bool dw_direct = !a->fuse_prologue && a->w_heads == a->Hv && a->w_chans == KD;
+  c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = dw_direct ? (float*)dw : pre[10];
   c.d_init = d_init;
   c.recompute_states = a->recompute_states;
   rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, a->precision == 0, w, lay.core, stream);
@@ -1997,8 +2000,10 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   else hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
   if (a->b_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<1>, dim3((unsigned)((nb / KD + 7) / 8)), dim3(256), 0, st, r);
   else hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
-  if (a->w_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<2>, dim3((unsigned)((nw / KD + 7) / 8)), dim3(256), 0, st, r);
-  else hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
+  if (!dw_direct) {
+    if (a->w_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<2>, dim3((unsigned)((nw / KD + 7) / 8)), dim3(256), 0, st, r);
+    else hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
   return DN_OK;
