@@ -1544,66 +1544,94 @@ __global__ __launch_bounds__(256) void k_bw_canon(BR p) {
   }
 }
 
-// one wave per (batch, token, value head) row: the prepared inputs exactly as
-// the forward kernels form them
+// four consecutive elements of an f32 / bf16 / f16 array
+__device__ __forceinline__ void ld4_any(const void* p, int64_t i, int dt, float* x) {
+  if (dt == DT_BF16) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>((const bf16*)p + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (float)v[e];
+  } else if (dt == DT_F16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (float)((const f16*)p)[i + e];
+  } else {
+    const float4 v = ld4g((const float*)p + i);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  }
+}
+// four channels c..c+3 of a gate row (one value per head when chans == 1)
+__device__ __forceinline__ void gate4(const float* g, int64_t base, int chans, int c, float* x) {
+  if (chans == 1) {
+    x[0] = x[1] = x[2] = x[3] = g[base];
+  } else {
+    const float4 v = ld4g(g + base + c);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  }
+}
+
+// Two (batch, token, value head) rows per wave, one per 32-lane half, four
+// channels per lane (vector loads and stores): the prepared inputs as the
+// forward kernels form them (the L2 norms summed in another order, so the
+// last bit can differ).
 __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
-  const int l = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, c = 4 * (l & 31);
   const int64_t rows = (int64_t)p.B * p.L * p.Hv;
-  if (row >= rows) return;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (l >> 5);
+  const bool valid = row0 < rows;
+  const int64_t row = valid ? row0 : rows - 1;   // both halves take part in the shuffles
   const int hv = (int)(row % p.Hv);
-  const int64_t bt = row / p.Hv;                 // batch * L + token
+  const int64_t bt = row / p.Hv;
   const int hk = hv / p.G;
-  const int64_t qrow = (bt * p.Hk + hk) * KD;
-  float x[2], y[2];
+  const int64_t qrow = (bt * p.Hk + hk) * KD + c;
+  float x[4], y[4];
+  ld4_any(p.q, qrow, p.qk_dt, x);
+  ld4_any(p.k, qrow, p.qk_dt, y);
+  float sq = 0.f, sk = 0.f;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    x[e] = ld_f(p.q, qrow + l + 64 * e, p.qk_dt);
-    y[e] = ld_f(p.k, qrow + l + 64 * e, p.qk_dt);
-  }
-  float sq = x[0] * x[0] + x[1] * x[1], sk = y[0] * y[0] + y[1] * y[1];
+  for (int e = 0; e < 4; ++e) { sq += x[e] * x[e]; sk += y[e] * y[e]; }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { sq += __shfl_xor(sq, o); sk += __shfl_xor(sk, o); }
+  for (int o = 16; o > 0; o >>= 1) { sq += __shfl_xor(sq, o); sk += __shfl_xor(sk, o); }
   const bool b16 = p.qk_dt != DT_F32;
-  const int64_t orow = row * KD;
+  const int hg = gate_head(p.g_h, p.Hk, p.Hv, hv, p.G), hb = gate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
+  const int hw = gate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+  float gv[4], bv[4], wv[4] = {0.f, 0.f, 0.f, 0.f}, vv[4];
+  gate4(p.g, (bt * p.g_h + hg) * p.g_c, p.g_c, c, gv);
+  gate4(p.b, (bt * p.b_h + hb) * p.b_c, p.b_c, c, bv);
+  if (!p.w_alias) gate4(p.w, (bt * p.w_h + hw) * p.w_c, p.w_c, c, wv);
+  ld4_any(p.v, (bt * p.Hv + hv) * KD + c, p.v_dt, vv);
+  float qh[4], kh[4];
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int i = l + 64 * e;
-    float qh, kh;
+  for (int e = 0; e < 4; ++e) {
     if (p.fuse) {
-      qh = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
-      kh = y[e] * rsqrtf(sk + 1e-6f);
+      qh[e] = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
+      kh[e] = y[e] * rsqrtf(sk + 1e-6f);
     } else if (p.l2norm) {
-      qh = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
-      kh = y[e] * rsqrtf(sk + 1e-6f);
-      if (b16) { qh = p.qk_dt == DT_BF16 ? round_as<bf16>(qh) : round_as<f16>(qh);
-                 kh = p.qk_dt == DT_BF16 ? round_as<bf16>(kh) : round_as<f16>(kh); }
+      qh[e] = (x[e] * rsqrtf(sq + 1e-6f)) * p.scale;
+      kh[e] = y[e] * rsqrtf(sk + 1e-6f);
+      if (b16) { qh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(qh[e]) : round_as<f16>(qh[e]);
+                 kh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(kh[e]) : round_as<f16>(kh[e]); }
     } else {
-      qh = x[e] * p.scale;
-      kh = y[e];
-      if (b16) qh = p.qk_dt == DT_BF16 ? round_as<bf16>(qh) : round_as<f16>(qh);
+      qh[e] = x[e] * p.scale;
+      kh[e] = y[e];
+      if (b16) qh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(qh[e]) : round_as<f16>(qh[e]);
     }
-    const int hg = gate_head(p.g_h, p.Hk, p.Hv, hv, p.G), hb = gate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
-    const int hw = gate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
-    float gv = p.g[(bt * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i)];
-    float bv = p.b[(bt * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i)];
-    float wv = p.w[(bt * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i)];
     if (p.fuse) {
-      gv = -__expf(fminf(gv, 5.f));
-      bv = sigmoid_hw(bv);
-      wv = sigmoid_hw(wv);
+      gv[e] = -__expf(fminf(gv[e], 5.f));
+      bv[e] = sigmoid_hw(bv[e]);
+      wv[e] = sigmoid_hw(wv[e]);
     } else {
-      gv = fminf(gv, 0.f);
-      if (p.guard) bv = fmaxf(bv, 0.f);
+      gv[e] = fminf(gv[e], 0.f);
+      if (p.guard) bv[e] = fmaxf(bv[e], 0.f);
     }
-    if (p.guard) gv = fminf(gv, -1e-6f);
-    p.qe[orow + i] = qh;
-    p.ke[orow + i] = kh;
-    p.ge[orow + i] = gv;
-    p.be[orow + i] = bv;
-    if (!p.w_alias) p.we[orow + i] = wv;
-    p.ve[orow + i] = ld_f(p.v, (bt * p.Hv + hv) * KD + i, p.v_dt);
+    if (p.guard) gv[e] = fminf(gv[e], -1e-6f);
   }
+  if (!valid) return;
+  const int64_t o = row * KD + c;
+  *reinterpret_cast<float4*>(p.qe + o) = make_float4(qh[0], qh[1], qh[2], qh[3]);
+  *reinterpret_cast<float4*>(p.ke + o) = make_float4(kh[0], kh[1], kh[2], kh[3]);
+  *reinterpret_cast<float4*>(p.ge + o) = make_float4(gv[0], gv[1], gv[2], gv[3]);
+  *reinterpret_cast<float4*>(p.be + o) = make_float4(bv[0], bv[1], bv[2], bv[3]);
+  if (!p.w_alias) *reinterpret_cast<float4*>(p.we + o) = make_float4(wv[0], wv[1], wv[2], wv[3]);
+  *reinterpret_cast<float4*>(p.ve + o) = make_float4(vv[0], vv[1], vv[2], vv[3]);
 }
 
 // one wave per (batch, token, key head) row: dq, dk through the GQA sum and
@@ -1972,7 +2000,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_bw_canon, dim3(a->B), dim3(256), 0, st, r);
   const int64_t rows = (int64_t)a->B * a->L * a->Hv;
-  hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st, r);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
 
