@@ -1634,67 +1634,75 @@ __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
   *reinterpret_cast<float4*>(p.ve + o) = make_float4(vv[0], vv[1], vv[2], vv[3]);
 }
 
-// one wave per (batch, token, key head) row: dq, dk through the GQA sum and
-// the L2-norm / scale (a bf16 or f16 normalised q / k receives its cotangent
-// in that dtype, as the reference's cast back does)
+// two (batch, token, key head) rows per wave, one per 32-lane half, four
+// channels per lane: dq, dk through the GQA sum and the L2-norm / scale (a
+// bf16 or f16 normalised q / k receives its cotangent in that dtype, as the
+// reference's cast back does)
 __global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
-  const int l = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)p.B * p.L * p.Hk) return;
+  const int l = threadIdx.x & 63, c = 4 * (l & 31);
+  const int64_t rows = (int64_t)p.B * p.L * p.Hk;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (l >> 5);
+  const bool valid = row0 < rows;
+  const int64_t row = valid ? row0 : rows - 1;   // both halves take part in the shuffles
   const int hk = (int)(row % p.Hk);
   const int64_t bt = row / p.Hk;
-  float dqh[2] = {0.f, 0.f}, dkh[2] = {0.f, 0.f}, x[2], y[2];
+  float dqh[4] = {0.f, 0.f, 0.f, 0.f}, dkh[4] = {0.f, 0.f, 0.f, 0.f}, x[4], y[4];
   for (int g = 0; g < p.G; ++g) {
-    const int64_t er = (bt * p.Hv + hk * p.G + g) * KD;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      dqh[e] += p.dqe[er + l + 64 * e];
-      dkh[e] += p.dke[er + l + 64 * e];
-    }
+    const int64_t er = (bt * p.Hv + hk * p.G + g) * KD + c;
+    const float4 a4 = ld4g(p.dqe + er), b4 = ld4g(p.dke + er);
+    dqh[0] += a4.x; dqh[1] += a4.y; dqh[2] += a4.z; dqh[3] += a4.w;
+    dkh[0] += b4.x; dkh[1] += b4.y; dkh[2] += b4.z; dkh[3] += b4.w;
   }
   const bool b16 = p.qk_dt != DT_F32 && !p.fuse;
+  ld4_any(p.q, row * KD + c, p.qk_dt, x);
+  ld4_any(p.k, row * KD + c, p.qk_dt, y);
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    x[e] = ld_f(p.q, row * KD + l + 64 * e, p.qk_dt);
-    y[e] = ld_f(p.k, row * KD + l + 64 * e, p.qk_dt);
+  for (int e = 0; e < 4; ++e)
     if (b16) {
       dqh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(dqh[e]) : round_as<f16>(dqh[e]);
       dkh[e] = p.qk_dt == DT_BF16 ? round_as<bf16>(dkh[e]) : round_as<f16>(dkh[e]);
     }
-  }
-  float dq[2], dk[2];
+  float dq[4], dk[4];
   if (p.fuse || p.l2norm) {
-    float sq = x[0] * x[0] + x[1] * x[1], sk = y[0] * y[0] + y[1] * y[1];
-    float xq = x[0] * dqh[0] + x[1] * dqh[1], yk = y[0] * dkh[0] + y[1] * dkh[1];
+    float sq = 0.f, sk = 0.f, xq = 0.f, yk = 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
+    for (int e = 0; e < 4; ++e) {
+      sq += x[e] * x[e]; sk += y[e] * y[e];
+      xq += x[e] * dqh[e]; yk += y[e] * dkh[e];
+    }
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
       sq += __shfl_xor(sq, o); sk += __shfl_xor(sk, o);
       xq += __shfl_xor(xq, o); yk += __shfl_xor(yk, o);
     }
     // d/dx of c x / sqrt(|x|^2 + eps) = c r (dx^ - r^2 x (x . dx^))
     const float rq = rsqrtf(sq + 1e-6f), rk = rsqrtf(sk + 1e-6f);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < 4; ++e) {
       dq[e] = p.scale * rq * (dqh[e] - rq * rq * x[e] * xq);
       dk[e] = rk * (dkh[e] - rk * rk * y[e] * yk);
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) { dq[e] = p.scale * dqh[e]; dk[e] = dkh[e]; }
+    for (int e = 0; e < 4; ++e) { dq[e] = p.scale * dqh[e]; dk[e] = dkh[e]; }
   }
+  if (!valid) return;
+  const int64_t o = row * KD + c;
+  if (p.qk_dt == DT_BF16) {
+    bf16x4 hq, hk4;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int64_t o = row * KD + l + 64 * e;
-    if (p.qk_dt == DT_BF16) {
-      reinterpret_cast<bf16*>(p.dq)[o] = (bf16)dq[e];
-      reinterpret_cast<bf16*>(p.dk)[o] = (bf16)dk[e];
-    } else if (p.qk_dt == DT_F16) {
-      reinterpret_cast<f16*>(p.dq)[o] = (f16)dq[e];
-      reinterpret_cast<f16*>(p.dk)[o] = (f16)dk[e];
-    } else {
-      p.dq[o] = dq[e];
-      p.dk[o] = dk[e];
+    for (int e = 0; e < 4; ++e) { hq[e] = (bf16)dq[e]; hk4[e] = (bf16)dk[e]; }
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(p.dq) + o) = hq;
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(p.dk) + o) = hk4;
+  } else if (p.qk_dt == DT_F16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      reinterpret_cast<f16*>(p.dq)[o + e] = (f16)dq[e];
+      reinterpret_cast<f16*>(p.dk)[o + e] = (f16)dk[e];
     }
+  } else {
+    *reinterpret_cast<float4*>(p.dq + o) = make_float4(dq[0], dq[1], dq[2], dq[3]);
+    *reinterpret_cast<float4*>(p.dk + o) = make_float4(dk[0], dk[1], dk[2], dk[3]);
   }
 }
 
@@ -2019,7 +2027,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;
-  hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 3) / 4)), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 7) / 8)), dim3(256), 0, st, r);
   const int64_t ng = (int64_t)a->B * a->L * a->g_heads * a->g_chans;
   const int64_t nb = (int64_t)a->B * a->L * a->b_heads * a->b_chans;
   const int64_t nw = (int64_t)a->B * a->L * a->w_heads * a->w_chans;
