@@ -1517,15 +1517,18 @@ __device__ __forceinline__ int gate_head(int H, int Hk, int Hv, int hv, int G) {
 __device__ __forceinline__ float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094)
-__global__ __launch_bounds__(256) void k_bw_canon(BR p) {
-  __shared__ int wsum[4];
+constexpr int kCanonThreads = 1024;
+__global__ __launch_bounds__(kCanonThreads) void k_bw_canon(BR p) {
+  constexpr int NWc = kCanonThreads / 64;
+  __shared__ int wsum[NWc];
   const int bb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t base = p.seg_batched ? (int64_t)bb * p.L : 0;
   auto sid = [&](int t) -> int64_t { return p.seg ? ld_i(p.seg, base + t, p.seg_dt) : 0; };
-  // tiles of 256 tokens: thread tid flags token ts + tid as a change from the
-  // token before it; a block-wide inclusive scan of the flags gives the ids
+  // tiles of kCanonThreads tokens: thread tid flags token ts + tid as a change
+  // from the token before it; a block-wide inclusive scan of the flags gives
+  // the ids
   int run = (p.has_init && p.init_seg != nullptr) ? (sid(0) != (int64_t)p.init_seg[bb]) : 0;
-  for (int ts = 0; ts < p.L; ts += 256) {
+  for (int ts = 0; ts < p.L; ts += kCanonThreads) {
     const int t = ts + tid;
     int f = (t > 0 && t < p.L) ? (sid(t) != sid(t - 1)) : 0;
 #pragma unroll
@@ -1535,11 +1538,14 @@ __global__ __launch_bounds__(256) void k_bw_canon(BR p) {
     }
     if (lane == 63) wsum[wid] = f;
     __syncthreads();
-    int before = run;
+    int before = run, tile = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) before += w < wid ? wsum[w] : 0;
+    for (int w = 0; w < NWc; ++w) {
+      before += w < wid ? wsum[w] : 0;
+      tile += wsum[w];
+    }
     if (t < p.L) p.canon[(int64_t)bb * p.L + t] = before + f;
-    run += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    run += tile;
     __syncthreads();   // wsum is rewritten by the next tile
   }
 }
@@ -2006,7 +2012,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
 
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_bw_canon, dim3(a->B), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_canon, dim3(a->B), dim3(kCanonThreads), 0, st, r);
   const int64_t rows = (int64_t)a->B * a->L * a->Hv;
   hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st, r);
   hipError_t e = hipGetLastError();
