@@ -1,4 +1,8 @@
-// Training backward of the GDN-2 recurrence on gfx950 (fp32 throughout).
+// Training backward of the GDN-2 recurrence on gfx950.  fp32 mode runs every
+// product on v_mfma_f32_16x16x4_f32; bf16 mode runs the state scans and
+// k_bw_grads' products as split-bf16 products (hi + lo words, three
+// v_mfma_f32_16x16x32_bf16), the other kernels in fp32.  State, carries and
+// accumulations are fp32 in both.
 //
 // Reference: the custom VJP of chunk_gdn2 (maelie-labs/deltanet-tpu v0.3.0,
 // src/deltanet_tpu/gdn2.py:1446-1769) with its backward kernels
@@ -27,13 +31,14 @@
 // (the reference's strong-decay test uses g = -150 per token).
 //
 // Kernels (one launch each, in stream order):
-//   k_bw_intra   per (batch, head, chunk): A, M, T, W, U0, Xf, Kc, lam, G and
+//   k_bw_intra   per (batch, head, chunk), persistent (one workgroup per CU
+//                looping over the units): A, M, T, W, U0, Xf, Kc, lam, G and
 //                the reverse scan's state-free term Xf^T dO
-//   k_bw_chains  per (batch, head, 16-column tile) and direction, both scans in
-//                one launch: forward S_c for every chunk;
-//                reverse dS_{c+1} for every chunk, dS_0
-//   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA and the chunk-wide
-//                products of dq, dk, db
+//   k_bw_chains  per (batch, head, block of 16 or 32 state columns) and
+//                direction, both scans in one launch: forward S_c for every
+//                chunk; reverse dS_{c+1} for every chunk, dS_0
+//   k_bw_grads   per (batch, head, chunk): dv, dw, dM, dA, the chunk-wide
+//                products of dq, dk, db and rowsum(S_c * dS_{c+1})
 //   k_bw_dqk     per (batch, head, chunk, quarter of the key channels): dq, dk,
 //                db, dg
 #include "dn_common.h"
