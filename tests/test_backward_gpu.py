@@ -93,8 +93,12 @@ def test_backward_l2norm_scale_gqa():
     compare(got, ref, 1e-5, "l2norm scale=0.5 G=2")
 
 
+@pytest.mark.parametrize("precision, tol", [("fp32", 1e-5), ("bf16", 5e-5)])
 @pytest.mark.parametrize("L", [300, 384])
-def test_backward_fuse_prologue_unaligned(L):
+def test_backward_fuse_prologue_unaligned(L, precision, tol):
+    """Initial state, final-state cotangent, three documents, unaligned L; in
+    bf16 mode this drives the split-bf16 scans' state load (init / d_final)
+    and store (d_init) paths."""
     B, Hk, Hv, K, V = 1, 2, 4, 128, 128
     rng = np.random.default_rng(2026 + L)
     f = lambda *s: rng.standard_normal(s)
@@ -106,10 +110,10 @@ def test_backward_fuse_prologue_unaligned(L):
     seg = np.array([[0] * (L // 3) + [1] * (L // 3) + [2] * (L - 2 * (L // 3))], dtype=np.int32)
     do, df = f(B, L, Hv, V), f(B, Hv, K, V)
     kw = dict(qk_l2norm=True, fuse_prologue=True)
-    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision="fp32",
+    _, got = run_dev(q, k, v, g, b, w, do, df=df, init=init, precision=precision,
                      segment_ids=torch.from_numpy(seg).cuda(), **kw)
     ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, initial_state=init, segment_ids=seg, **kw)
-    compare(got, ref, 1e-5, f"fuse_prologue L={L}")
+    compare(got, ref, tol, f"fuse_prologue L={L} {precision}")
 
 
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
