@@ -1003,7 +1003,7 @@ __device__ __forceinline__ void load_yT(float (&y)[4][8], const float* X, int wv
 // that stores it, instead of by every wave that reads it.
 template <bool BF, int W> struct LMat;
 template <int W> struct LMat<false, W> {
-  float a[BC][W + 4];
+  alignas(16) float a[BC][W + 4];
   __device__ __forceinline__ Frag<false> row_frag(int r, int s, int q) const {
     float x[8];
     row8(&a[r][0], s, q, x);
@@ -1021,7 +1021,8 @@ template <int W> struct LMat<false, W> {
   __device__ __forceinline__ float4 get4(int r, int c) const { return *reinterpret_cast<const float4*>(&a[r][c]); }
 };
 template <int W> struct LMat<true, W> {
-  bf16 h[BC][W + 4], lw[BC][W + 4];
+  alignas(16) bf16 h[BC][W + 4];   // rows of (W + 4) * 2 bytes: 8-byte vector access at c % 4 == 0
+  alignas(16) bf16 lw[BC][W + 4];
   __device__ __forceinline__ Pol<true>::F3 row_frag(int r, int s, int q) const {
     Pol<true>::F3 f;
     const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&h[r][32 * s + 4 * q]);
