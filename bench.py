@@ -732,7 +732,10 @@ def main():
                  "backward_roofline": {"bound": "mfma", "dtype": "fp32", "flops": bw["flops"],
                                        "achieved": round(bw["flops"] / bw_s / 1e12, 2) if bw_s else None,
                                        "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": round(bw["flops"] / bw_s / 1e12 / PEAK_FP32_TFLOPS, 4) if bw_s else None}}
+                                       "frac": round(bw["flops"] / bw_s / 1e12 / PEAK_FP32_TFLOPS, 4) if bw_s else None,
+                                       "note": "algorithmic fp32 flops of the recurrence backward against the dense fp32 "
+                                               "MFMA peak; in bf16 mode the scans and k_bw_grads carry those products as "
+                                               "split-bf16 MFMAs (3 per product), k_bw_intra and k_bw_dqk as fp32"}}
         log(f"training step: {t_us:.1f} us; kernels per step (us): {tk_us}")
 
     copy_gbps = None
