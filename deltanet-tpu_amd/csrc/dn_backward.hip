@@ -1088,7 +1088,7 @@ template <bool BF>
 __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   using O = Op<BF>;
   __shared__ LMat<BF, KD> sdO, sX, sU, sT;   // sX: dU, then dX; sT: W, then Kc
-  __shared__ LMat<BF, BC> sMT;               // M^T
+  __shared__ LMat<BF, BC> sMT;               // M^T, then T^T
   __shared__ int sseg[BC], scar[BC], slast[BC];
   static_assert(TPW == 1, "one 16-column tile per wave");
 
@@ -1188,12 +1188,12 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   zero_acc(acc);
   nt_lds<BF>(acc, sdO, fS0, q, l16);
   store_frag(p.Rq + (int64_t)u * CK, wv, l, acc);
-  // T^T rows and this lane's w, v for the dX phase
-  float tt[2][4][8];
+  // T^T (64 x 64, row-major) for the dX phase: loaded once per workgroup
+  // (two 16-byte pieces per thread), staged into M^T's LDS once dU is done
+  static_assert(CC / 4 == 2 * NT, "two float4 of T^T per thread");
+  float4 ttq[2];
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-    for (int I = 0; I < 4; ++I) row8(p.TT + (int64_t)u * CC + (16 * I + l16) * BC, s2, q, tt[s2][I]);
+  for (int it = 0; it < 2; ++it) ttq[it] = ld4g(p.TT + (int64_t)u * CC + 4 * (tid + NT * it));
   // w, v of the coalesced dv / dw pass: float4s tid + NT it of the chunk's
   // row-major 64 x 128 tiles
   float4 wq[BC * KD / 4 / NT], vq[BC * KD / 4 / NT];
@@ -1221,6 +1221,12 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int I = 0; I < 4; ++I)
 #pragma unroll
     for (int e = 0; e < 4; ++e) sX.put(16 * I + 4 * q + e, vcol, acc[I][0][e]);
+  lds_barrier();   // dU complete; every wave is done with M^T
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int idx = tid + NT * it;
+    sMT.put4(idx / (BC / 4), 4 * (idx % (BC / 4)), ttq[it]);
+  }
   lds_barrier();
 
   // ---- dX = T^T dU ; dv = dX w ; dw = dX v ----------------------------------
@@ -1229,7 +1235,7 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int s = 0; s < 2; ++s) {
     const typename O::F bfr = sX.col_frag(vcol, s, q);
 #pragma unroll
-    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], O::make(tt[s][I]), bfr);
+    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);
   }
   lds_barrier();
 #pragma unroll
