@@ -214,7 +214,11 @@ size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
  * element type the header gives (strides are implied, never passed): a
  * channel-wise write gate at Hv heads with neither fuse_prologue nor
  * stability_guard is read in place by the recurrence kernels, every other
- * gate layout is first staged into the workspace. */
+ * gate layout is first staged into the workspace; without fuse_prologue such
+ * a gate's dw is written in place by the recurrence kernels too.  a->precision
+ * selects the arithmetic as in the forward: "bf16" (0) runs the state scans and
+ * the chunk gradient products as split-bf16 MFMA products (hi + lo words,
+ * fp32 accumulation), "fp32" (1) runs every product in fp32. */
 int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
                        void* dq, void* dk, void* dv, void* dg, void* db, void* dw, void* d_init,
                        void* workspace, size_t workspace_bytes, void* stream);
