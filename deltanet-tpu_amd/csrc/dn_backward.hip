@@ -1386,20 +1386,36 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       float xm[8], xa[8], xk[8], ym[8], ya[8], yq[8], yb[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
+        // the 16-row block of column j is known here; I is the same in the
+        // whole wave, so which side of block I it lies on is a uniform branch
+        const int jb = 2 * s + (e >> 2);
         const int j = 32 * s + pi_k(q, e);
-        const bool in = inblk && j >= m && j <= m2;
-        const bool lo = j < m || in, hi = j > m2 || in;
-        const bool self = j == 16 * I + l16;
         const float gj = sG[j][rl];
-        xm[e] = lo && !self ? sdM[16 * I + l16][j] : 0.f;
-        xa[e] = lo ? sdA[16 * I + l16][j] : 0.f;
-        const float fk = in ? __builtin_amdgcn_exp2f(gm - gj) : ex2(gm - gj);
-        xk[e] = lo ? sK[j][rl] * fk : 0.f;
-        ym[e] = hi && !self ? sdM[j][16 * I + l16] : 0.f;
-        ya[e] = hi ? sdA[j][16 * I + l16] : 0.f;
-        const float f = hi ? (in ? __builtin_amdgcn_exp2f(gj - gm2) : ex2(gj - gm2)) : 0.f;
-        yq[e] = sQ[j][rl] * f;
-        yb[e] = sB[j][rl] * sK[j][rl] * f;
+        if (jb < I) {
+          xm[e] = sdM[16 * I + l16][j];
+          xa[e] = sdA[16 * I + l16][j];
+          xk[e] = sK[j][rl] * ex2(gm - gj);
+          ym[e] = ya[e] = yq[e] = yb[e] = 0.f;
+        } else if (jb > I) {
+          xm[e] = xa[e] = xk[e] = 0.f;
+          ym[e] = sdM[j][16 * I + l16];
+          ya[e] = sdA[j][16 * I + l16];
+          const float f = ex2(gj - gm2);
+          yq[e] = sQ[j][rl] * f;
+          yb[e] = sB[j][rl] * sK[j][rl] * f;
+        } else if (inblk) {
+          const bool self = j == 16 * I + l16;
+          xm[e] = self ? 0.f : sdM[16 * I + l16][j];
+          xa[e] = sdA[16 * I + l16][j];
+          xk[e] = sK[j][rl] * __builtin_amdgcn_exp2f(gm - gj);
+          ym[e] = self ? 0.f : sdM[j][16 * I + l16];
+          ya[e] = sdA[j][16 * I + l16];
+          const float f = __builtin_amdgcn_exp2f(gj - gm2);
+          yq[e] = sQ[j][rl] * f;
+          yb[e] = sB[j][rl] * sK[j][rl] * f;
+        } else {
+          xm[e] = xa[e] = xk[e] = ym[e] = ya[e] = yq[e] = yb[e] = 0.f;
+        }
       }
       const Frag<false> fk = fr8(xk);
       mma(oq, fr8(xm), fk);
