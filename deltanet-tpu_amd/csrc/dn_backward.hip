@@ -243,7 +243,9 @@ template <> struct Op<true> {
 // ---------------------------------------------------------------------------
 // k_bw_intra
 // ---------------------------------------------------------------------------
+template <bool BF>
 __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
+  using O = Op<BF>;
   __shared__ float sG[BC][KP];
   __shared__ float sA[BC][CP];   // A, then T
   __shared__ float sM[BC][CP];
@@ -547,15 +549,27 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     }
   }
   lds_barrier();
-
-  // the chunk's dO (rows past the sequence end zero), loaded now for the P^T
-  // phase at the end
-  float4 dov[BC * KD / 4 / NT];
+  // bf16 mode: T (final, and already written out as T^T) is stored over itself
+  // as high / low bf16 planes, split once for every wave's W / U0 products
+  if constexpr (BF) {
+    float tv[CC / NT];
 #pragma unroll
-  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
-    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
-    dov[it] = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
+    for (int e = 0; e < CC / NT; ++e) {
+      const int idx = tid + NT * e;
+      tv[e] = sA[idx / BC][idx % BC];
+    }
+    lds_barrier();
+    bf16 (*th)[CP] = reinterpret_cast<bf16 (*)[CP]>(&sA[0][0]);
+#pragma unroll
+    for (int e = 0; e < CC / NT; ++e) {
+      const int idx = tid + NT * e;
+      const bf16 h = (bf16)tv[e];
+      th[idx / BC][idx % BC] = h;
+      th[BC + idx / BC][idx % BC] = (bf16)(tv[e] - (float)h);
+    }
+    lds_barrier();
   }
+
   // ---- W = T diag(carry) (b k e^G), U0 = T (w v) ---------------------------
   {
     f32x4 aw[4][TPW], au[4][TPW];
@@ -563,34 +577,42 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     for (int I = 0; I < 4; ++I)
 #pragma unroll
       for (int R2 = 0; R2 < TPW; ++R2) { aw[I][R2] = zero4(); au[I][R2] = zero4(); }
+    static_assert(TPW == 1, "one 16-column tile per wave");
+    const int r = 16 * wv + l16;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4];
+      // this lane's b k e^G and w v column fragments, then each row block's
+      // T fragment just before its two products (one T fragment live at a time)
+      float xb[8], xu[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 32 * s + pi_k(q, e);
+        xb[e] = scar[j] ? sW[j][r] * ex2(sG[j][r]) : 0.f;
+        xu[e] = wvw[s][e] * wvv[s][e];
+      }
+      const typename O::F fb = O::make(xb), fu = O::make(xu);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        float x[8];
-        const float* rp = &sA[16 * I + l16][32 * s];
-        const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
-        const float4 x1 = *reinterpret_cast<const float4*>(rp + 16 + 4 * q);
-        x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
-        a[I] = fr8(x);
-      }
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int r = 16 * (TPW * wv + R2) + l16;
-        float xb[8], xu[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = 32 * s + pi_k(q, e);
-          xb[e] = scar[j] ? sW[j][r] * ex2(sG[j][r]) : 0.f;
-          xu[e] = wvw[s][e] * wvv[s][e];
+        typename O::F a;
+        if constexpr (BF) {
+          const bf16 (*th)[CP] = reinterpret_cast<const bf16 (*)[CP]>(&sA[0][0]);
+          const int rr = 16 * I + l16;
+          const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&th[rr][32 * s + 4 * q]);
+          const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&th[rr][32 * s + 16 + 4 * q]);
+          const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&th[BC + rr][32 * s + 4 * q]);
+          const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&th[BC + rr][32 * s + 16 + 4 * q]);
+          a.hi.v = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+          a.lo.v = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        } else {
+          float x[8];
+          const float* rp = &sA[16 * I + l16][32 * s];
+          const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
+          const float4 x1 = *reinterpret_cast<const float4*>(rp + 16 + 4 * q);
+          x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+          a = fr8(x);
         }
-        const Frag<false> fb = fr8(xb), fu = fr8(xu);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          mma(aw[I][R2], a[I], fb);
-          mma(au[I][R2], a[I], fu);
-        }
+        O::mac(aw[I][0], a, fb);
+        O::mac(au[I][0], a, fu);
       }
     }
     float* WT = p.WT + (int64_t)u * CK;
@@ -612,6 +634,14 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       }
   }
   lds_barrier();
+  // the chunk's dO (rows past the sequence end zero), loaded here for the P^T
+  // phase at the end (not earlier: it would hold 16 registers through W / U0)
+  float4 dov[BC * KD / 4 / NT];
+#pragma unroll
+  for (int it = 0; it < BC * KD / 4 / NT; ++it) {
+    const int idx = tid + NT * it, i = idx / (KD / 4), c4 = idx % (KD / 4);
+    dov[it] = t0 + i < p.L ? ld4_dt(p.dout, row_of(p, bb, t0 + i, h) + 4 * c4, p.dout_dt) : zero_f4();
+  }
   // W in the scan operand order from sW: per task one lane's run pair (rows
   // of 16-row block blk, slab s)
   {
@@ -1932,7 +1962,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.init = j == 0 ? (const float*)a->init_state : boundary(j);
     p.sfin = boundary(j + 1);
     p.dfin = nullptr; p.dinit = nullptr;
-    hipLaunchKernelGGL(k_bw_intra, intra_grid(n), dim3(NT), 0, st, p);
+    if (p.bf) hipLaunchKernelGGL(k_bw_intra<true>, intra_grid(n), dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(k_bw_intra<false>, intra_grid(n), dim3(NT), 0, st, p);
     if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
     else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(chains), dim3(256), 0, st, p, chains, chains);
   }
@@ -1946,7 +1977,8 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
     p.sfin = nullptr;
     p.dfin = j == nblk - 1 ? (const float*)a->d_final : dcarry;
     p.dinit = j == 0 ? (float*)a->d_init : dcarry;
-    hipLaunchKernelGGL(k_bw_intra, intra_grid(n), dim3(NT), 0, st, p);
+    if (p.bf) hipLaunchKernelGGL(k_bw_intra<true>, intra_grid(n), dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(k_bw_intra<false>, intra_grid(n), dim3(NT), 0, st, p);
     if (p.bf) hipLaunchKernelGGL(k_bw_chains<true>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
     else hipLaunchKernelGGL(k_bw_chains<false>, chain_grid(2 * chains), dim3(256), 0, st, p, chains, 2 * chains);
     if (p.bf) hipLaunchKernelGGL(k_bw_grads<true>, dim3(n), dim3(NT), 0, st, p);
