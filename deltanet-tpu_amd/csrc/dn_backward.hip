@@ -667,7 +667,12 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       for (int R2 = 0; R2 < TPW; ++R2) ax[I][R2] = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      Frag<false> a[4];
+      // this lane's W column fragment, then each row block's M fragment just
+      // before its product
+      float xb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xb[e] = sW[32 * s + pi_k(q, e)][16 * wv + l16];
+      const typename O::F fb = O::make(xb);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         float x[8];
@@ -675,17 +680,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
         const float4 x1 = *reinterpret_cast<const float4*>(rp + 16 + 4 * q);
         x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
-        a[I] = fr8(x);
-      }
-#pragma unroll
-      for (int R2 = 0; R2 < TPW; ++R2) {
-        const int r = 16 * (TPW * wv + R2) + l16;
-        float xb[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xb[e] = sW[32 * s + pi_k(q, e)][r];
-        const Frag<false> fb = fr8(xb);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) mma(ax[I][R2], a[I], fb);
+        O::mac(ax[I][0], O::make(x), fb);
       }
     }
     float xf[4][4];
@@ -713,11 +708,14 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
     lds_barrier();
     // P^T rows v = 16 w .. 16 w + 15, all 128 k: P[k][v] = sum_i Xf[i][k] dO[i][v]
     // is the state-free term of the reverse scan's step
-    float xb[2][8];
+    typename O::F fdo[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s) {
+      float xb[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xb[s][e] = sQ[32 * s + pi_k(q, e)][16 * wv + l16];
+      for (int e = 0; e < 8; ++e) xb[e] = sQ[32 * s + pi_k(q, e)][16 * wv + l16];
+      fdo[s] = O::make(xb);
+    }
     float* PT = p.PT + (int64_t)u * KK;
 #pragma unroll
     for (int kt = 0; kt < KD / 16; ++kt) {
@@ -727,7 +725,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         float xa[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) xa[e] = sW[32 * s + pi_k(q, e)][16 * kt + l16];
-        mma(acc, fr8(xa), fr8(xb[s]));
+        O::mac(acc, O::make(xa), fdo[s]);
       }
       *reinterpret_cast<float4*>(PT + aofs(16 * wv + l16, 16 * kt + 4 * q, KD / 16)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
