@@ -1,7 +1,7 @@
 // Training backward of the GDN-2 recurrence on gfx950.  fp32 mode runs every
-// product on v_mfma_f32_16x16x4_f32; bf16 mode runs the state scans and
-// k_bw_grads' products as split-bf16 products (hi + lo words, three
-// v_mfma_f32_16x16x32_bf16), the other kernels in fp32.  State, carries and
+// product on v_mfma_f32_16x16x4_f32; bf16 mode runs the state scans,
+// k_bw_grads' products and k_bw_intra's W, U0, Xf and P products as split-bf16
+// products (hi + lo words, three v_mfma_f32_16x16x32_bf16), the rest in fp32.  State, carries and
 // accumulations are fp32 in both.
 //
 // Reference: the custom VJP of chunk_gdn2 (maelie-labs/deltanet-tpu v0.3.0,
