@@ -502,8 +502,9 @@ def rocprof_backward_summary(kt_dir):
              "summarised by:", "", "    python bench.py --rocprof-backward-summary gpurun_out/bwkt", "",
              "Workload: chunk_gdn2(is_inference=False) forward + backward under torch.autograd, B=1 L=2048 Hk=12 "
              "Hv=24 K=V=128 (bf16 q/k/v, fp32 gates, 2 segments, qk_l2norm); the backward runs at H=24 value heads, "
-             "32 chunks of 64 tokens (768 (head, chunk) units), precision bf16: k_bw_chains (state scans, 32-column blocks) and k_bw_grads run their products as split bf16 "
-             "(hi/lo words, 3 v_mfma_f32_16x16x32_bf16 per product), k_bw_intra and k_bw_dqk on v_mfma_f32_16x16x4_f32.  The "
+             "32 chunks of 64 tokens (768 (head, chunk) units), precision bf16: k_bw_chains (state scans, 32-column blocks), k_bw_grads and k_bw_intra's W / U0 / Xf / P run "
+             "their products as split bf16 (hi/lo words, 3 v_mfma_f32_16x16x32_bf16 per product), k_bw_intra's A / M and "
+             "k_bw_dqk on v_mfma_f32_16x16x4_f32.  The "
              "first four kernels are the recurrence backward (dn_prefill_bwd's kernels); the rest are the raw-input "
              "prologue recompute and the gradient sums back to the raw layouts.", "",
              "| kernel | dispatches | avg us | min us | max us |", "|---|---|---|---|---|"]
@@ -734,8 +735,9 @@ def main():
                                        "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(bw["flops"] / bw_s / 1e12 / PEAK_FP32_TFLOPS, 4) if bw_s else None,
                                        "note": "algorithmic fp32 flops of the recurrence backward against the dense fp32 "
-                                               "MFMA peak; in bf16 mode the scans and k_bw_grads carry those products as "
-                                               "split-bf16 MFMAs (3 per product), k_bw_intra and k_bw_dqk as fp32"}}
+                                               "MFMA peak; in bf16 mode the scans, k_bw_grads and most of k_bw_intra carry "
+                                               "those products as split-bf16 MFMAs (3 per product), k_bw_intra's A / M "
+                                               "and k_bw_dqk as fp32"}}
         log(f"training step: {t_us:.1f} us; kernels per step (us): {tk_us}")
 
     copy_gbps = None
