@@ -1296,23 +1296,31 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   nt_lds<BF>(acc, sX, fS0, q, l16);
   store_frag(p.Rb + (int64_t)u * CK, wv, l, acc);
 
-  // ---- dM = mask(dO U^T), dA = -mask(dX U^T): all 16 tiles, to the workspace --
-  for (int task = wv; task < 32; task += NWV) {
-    const bool isA = task >= 16;
-    const int I = (task & 15) >> 2, J = task & 3;
+  // ---- dM = mask(dO U^T), dA = -mask(dX U^T), to the workspace -------------
+  // The 10 lower-triangle 16 x 16 tiles of each (20 products, at most three
+  // per wave); the 6 tiles above the diagonal are zero.
+  for (int task = wv; task < 20; task += NWV) {
+    const bool isA = task >= 10;
+    const int tt = task % 10;
+    const int I = (tt >= 1) + (tt >= 3) + (tt >= 6);
+    const int J = tt - I * (I + 1) / 2;
     float* dst = (isA ? p.dAw : p.dMw) + (int64_t)u * CC;
     f32x4 a = zero4();
-    if (J <= I) {
-      const LMat<BF, KD>& Xs = isA ? sX : sdO;
+    const LMat<BF, KD>& Xs = isA ? sX : sdO;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) O::mac(a, Xs.row_frag(16 * I + l16, s, q), sU.row_frag(16 * J + l16, s, q));
-    }
+    for (int s = 0; s < 4; ++s) O::mac(a, Xs.row_frag(16 * I + l16, s, q), sU.row_frag(16 * J + l16, s, q));
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * I + 4 * q + e, j = 16 * J + l16;
       const bool ok = (isA ? j < i : j <= i) && sseg[i] == sseg[j];
       dst[i * BC + j] = ok ? (isA ? -a[e] : a[e]) : 0.f;
     }
+  }
+  for (int idx = tid; idx < 2 * 6 * 64; idx += NT) {   // float4s of the upper tiles
+    const int m = idx / (6 * 64), t = (idx / 64) % 6, f4 = idx % 64;
+    const int I = t < 3 ? 0 : (t < 5 ? 1 : 2), J = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+    float* dst = (m ? p.dAw : p.dMw) + (int64_t)u * CC;
+    *reinterpret_cast<float4*>(dst + (16 * I + f4 / 4) * BC + 16 * J + 4 * (f4 % 4)) = zero_f4();
   }
 }
 
