@@ -593,6 +593,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const typename O::F fb = O::make(xb), fu = O::make(xu);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
+        if (s == 1 && I < 2) continue;   // T is lower triangular: rows < 32 x columns >= 32 are zero
         typename O::F a;
         if constexpr (BF) {
           const bf16 (*th)[CP] = reinterpret_cast<const bf16 (*)[CP]>(&sA[0][0]);
@@ -675,6 +676,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const typename O::F fb = O::make(xb);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
+        if (s == 1 && I < 2) continue;   // M is lower triangular
         float x[8];
         const float* rp = &sM[16 * I + l16][32 * s];
         const float4 x0 = *reinterpret_cast<const float4*>(rp + 4 * q);
@@ -1241,7 +1243,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int s = 0; s < 2; ++s) {
     const typename O::F bfr = sdO.col_frag(vcol, s, q);
 #pragma unroll
-    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);
+    for (int I = 0; I < 4; ++I)
+      if (s == 1 || I < 2) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);   // M^T / T^T upper triangular
   }
   split4<BF>(yA, fA);
   nt_lds<BF>(acc, sT, fA, q, l16);
@@ -1263,7 +1266,8 @@ __global__ __launch_bounds__(NT) void k_bw_grads(BW p) {
   for (int s = 0; s < 2; ++s) {
     const typename O::F bfr = sX.col_frag(vcol, s, q);
 #pragma unroll
-    for (int I = 0; I < 4; ++I) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);
+    for (int I = 0; I < 4; ++I)
+      if (s == 1 || I < 2) O::mac(acc[I][0], sMT.row_frag(16 * I + l16, s, q), bfr);   // M^T / T^T upper triangular
   }
   lds_barrier();
 #pragma unroll
