@@ -1457,11 +1457,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
           xm[e] = xa[e] = xk[e] = ym[e] = ya[e] = yq[e] = yb[e] = 0.f;
         }
       }
-      const Frag<false> fk = fr8(xk);
-      mma(oq, fr8(xm), fk);
-      mma(ob, fr8(xa), fk);
-      mma(ok_, fr8(ym), fr8(yq));
-      mma(ok_, fr8(ya), fr8(yb));
+      // slab s holds row blocks 2s and 2s + 1: a side with no column in it
+      // has all-zero operands (a uniform test: I is the wave's block)
+      const bool any_lo = 2 * s < I || (inblk && I / 2 == s);
+      const bool any_hi = 2 * s + 1 > I || (inblk && I / 2 == s);
+      if (any_lo) {
+        const Frag<false> fk = fr8(xk);
+        mma(oq, fr8(xm), fk);
+        mma(ob, fr8(xa), fk);
+      }
+      if (any_hi) {
+        mma(ok_, fr8(ym), fr8(yq));
+        mma(ok_, fr8(ya), fr8(yb));
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
