@@ -239,9 +239,19 @@ def test_decode_steps_equal_chained_steps(state_dtype, guard):
     o_c = torch.stack(outs, 1)
     assert o_m.shape == (B, T, Hv, 128) and o_m.dtype == torch.bfloat16
     assert s_m.dtype == st.dtype
-    # same arithmetic in the same order: agreement to a few fp32 rounding steps
-    assert rel_l2(as_np(o_m), as_np(o_c)) < 1e-5
-    assert rel_l2(as_np(s_m), as_np(st)) < 1e-5
+    # the same arithmetic, with the column sums added in another order (the
+    # two kernels split the state rows differently over lanes and waves): the
+    # fp32 results differ by a few roundings.  A bf16-rounded output may land
+    # one bf16 step apart; a bf16 state carries such a step into the later
+    # tokens, so there the bound is bf16 rounding-level agreement.
+    ro, rs = rel_l2(as_np(o_m), as_np(o_c)), rel_l2(as_np(s_m), as_np(st))
+    print(f"multi vs chained: out {ro:.2e} state {rs:.2e}")
+    if state_dtype == "bfloat16":
+        assert ro < 2e-4 and rs < 2e-4
+    else:
+        a, c = as_np(o_m).astype(np.float64), as_np(o_c).astype(np.float64)
+        assert np.all(np.abs(a - c) <= 2.0 ** -7 * np.abs(c) + 1e-6 * np.abs(c).max())
+        assert rs < 1e-5
 
 
 @pytest.mark.parametrize("gate_heads", ["hk", "hv"])
