@@ -1720,7 +1720,7 @@ __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
 // channels per lane: dq, dk through the GQA sum and the L2-norm / scale (a
 // bf16 or f16 normalised q / k receives its cotangent in that dtype, as the
 // reference's cast back does)
-__global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
+__device__ __forceinline__ void post_qk_rows(const BR& p) {
   const int l = threadIdx.x & 63, c = 4 * (l & 31);
   const int64_t rows = (int64_t)p.B * p.L * p.Hk;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (l >> 5);
@@ -1788,6 +1788,8 @@ __global__ __launch_bounds__(256) void k_bw_post_qk(BR p) {
   }
 }
 
+__global__ __launch_bounds__(256) void k_bw_post_qk(BR p) { post_qk_rows(p); }
+
 // one thread per raw gate element: the sum of the prepared gradient over the
 // value heads and channels it was broadcast to, times the prologue derivative
 // derivative of the prologue step of gate WHICH at raw value x
@@ -1847,16 +1849,14 @@ __global__ __launch_bounds__(256) void k_bw_post_gate(BR p) {
 }
 
 // channel-wise gates (C = 128): one thread per 4 channels of one (token, head)
-// row, the row split into token and head once per thread
+// row.  Loaded: the row's prepared-gradient sum over the value heads it was
+// broadcast to, and its raw values.
+struct Gate4 { float4 s, x; };
 template <int WHICH>
-__global__ __launch_bounds__(256) void k_bw_post_gate4(BR p) {
+__device__ __forceinline__ Gate4 post_gate4_load(const BR& p, int64_t row, int c4) {
   const int H = WHICH == 0 ? p.g_h : (WHICH == 1 ? p.b_h : p.w_h);
   const float* raw = WHICH == 0 ? p.g : (WHICH == 1 ? p.b : p.w);
   const float* dpre = WHICH == 0 ? p.dge : (WHICH == 1 ? p.dbe : p.dwe);
-  float* out = WHICH == 0 ? p.dg : (WHICH == 1 ? p.db : p.dw);
-  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  const int c4 = threadIdx.x & 31;
-  if (row >= (int64_t)p.B * p.L * H) return;
   const int h = (int)(row % H);
   const int64_t bt = row / H;
   int h0, hn;
@@ -1864,15 +1864,58 @@ __global__ __launch_bounds__(256) void k_bw_post_gate4(BR p) {
   else if (H == p.Hk) { h0 = h * p.G; hn = p.G; }
   else { h0 = 0; hn = p.Hv; }
   const float* rowp = dpre + (bt * p.Hv + h0) * KD + 4 * c4;
-  float4 s = zero_f4();
+  Gate4 r{zero_f4(), ld4g(raw + row * KD + 4 * c4)};
   for (int j = 0; j < hn; ++j, rowp += KD) {
     const float4 x4 = ld4g(rowp);
-    s.x += x4.x; s.y += x4.y; s.z += x4.z; s.w += x4.w;
+    r.s.x += x4.x; r.s.y += x4.y; r.s.z += x4.z; r.s.w += x4.w;
   }
-  const float4 x = ld4g(raw + row * KD + 4 * c4);
+  return r;
+}
+template <int WHICH>
+__device__ __forceinline__ void post_gate4_store(const BR& p, int64_t row, int c4, const Gate4& r) {
+  float* out = WHICH == 0 ? p.dg : (WHICH == 1 ? p.db : p.dw);
   *reinterpret_cast<float4*>(out + row * KD + 4 * c4) =
-      make_float4(s.x * gate_deriv<WHICH>(p, x.x), s.y * gate_deriv<WHICH>(p, x.y), s.z * gate_deriv<WHICH>(p, x.z),
-                  s.w * gate_deriv<WHICH>(p, x.w));
+      make_float4(r.s.x * gate_deriv<WHICH>(p, r.x.x), r.s.y * gate_deriv<WHICH>(p, r.x.y),
+                  r.s.z * gate_deriv<WHICH>(p, r.x.z), r.s.w * gate_deriv<WHICH>(p, r.x.w));
+}
+
+template <int WHICH>
+__global__ __launch_bounds__(256) void k_bw_post_gate4(BR p) {
+  const int H = WHICH == 0 ? p.g_h : (WHICH == 1 ? p.b_h : p.w_h);
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (row >= (int64_t)p.B * p.L * H) return;
+  const int c4 = threadIdx.x & 31;
+  post_gate4_store<WHICH>(p, row, c4, post_gate4_load<WHICH>(p, row, c4));
+}
+
+// g and b together when both are channel-wise with the same head count: one
+// launch instead of two, both gates' loads issued before either store
+__global__ __launch_bounds__(256) void k_bw_post_gate4_gb(BR p) {
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (row >= (int64_t)p.B * p.L * p.g_h) return;
+  const int c4 = threadIdx.x & 31;
+  const Gate4 rg = post_gate4_load<0>(p, row, c4);
+  const Gate4 rb = post_gate4_load<1>(p, row, c4);
+  post_gate4_store<0>(p, row, c4, rg);
+  post_gate4_store<1>(p, row, c4, rb);
+}
+
+// dq, dk, dg and db in one launch when g and b are channel-wise at the key
+// heads: the same (batch, token, key head) row per 32-lane half in all four
+__global__ __launch_bounds__(256) void k_bw_post_qkgb(BR p) {
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const bool valid = row < (int64_t)p.B * p.L * p.Hk;
+  const int c4 = threadIdx.x & 31;
+  Gate4 rg{}, rb{};
+  if (valid) {
+    rg = post_gate4_load<0>(p, row, c4);
+    rb = post_gate4_load<1>(p, row, c4);
+  }
+  post_qk_rows(p);
+  if (valid) {
+    post_gate4_store<0>(p, row, c4, rg);
+    post_gate4_store<1>(p, row, c4, rb);
+  }
 }
 
 }  // namespace
@@ -2111,15 +2154,24 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;
-  hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 7) / 8)), dim3(256), 0, st, r);
   const int64_t ng = (int64_t)a->B * a->L * a->g_heads * a->g_chans;
   const int64_t nb = (int64_t)a->B * a->L * a->b_heads * a->b_chans;
   const int64_t nw = (int64_t)a->B * a->L * a->w_heads * a->w_chans;
-  // channel-wise gates take the float4 kernel (8 rows of 128 channels per block)
-  if (a->g_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<0>, dim3((unsigned)((ng / KD + 7) / 8)), dim3(256), 0, st, r);
-  else hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
-  if (a->b_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<1>, dim3((unsigned)((nb / KD + 7) / 8)), dim3(256), 0, st, r);
-  else hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
+  // channel-wise gates take the float4 kernels (8 rows of 128 channels per
+  // block); at the key heads they share the dq / dk launch
+  const bool gb4 = a->g_chans == KD && a->b_chans == KD && a->g_heads == a->b_heads;
+  if (gb4 && a->g_heads == a->Hk) {
+    hipLaunchKernelGGL(k_bw_post_qkgb, dim3((unsigned)((krows + 7) / 8)), dim3(256), 0, st, r);
+  } else if (gb4) {
+    hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 7) / 8)), dim3(256), 0, st, r);
+    hipLaunchKernelGGL(k_bw_post_gate4_gb, dim3((unsigned)((ng / KD + 7) / 8)), dim3(256), 0, st, r);
+  } else {
+    hipLaunchKernelGGL(k_bw_post_qk, dim3((unsigned)((krows + 7) / 8)), dim3(256), 0, st, r);
+    if (a->g_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<0>, dim3((unsigned)((ng / KD + 7) / 8)), dim3(256), 0, st, r);
+    else hipLaunchKernelGGL(k_bw_post_gate<0>, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, r);
+    if (a->b_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<1>, dim3((unsigned)((nb / KD + 7) / 8)), dim3(256), 0, st, r);
+    else hipLaunchKernelGGL(k_bw_post_gate<1>, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, r);
+  }
   if (!dw_direct) {
     if (a->w_chans == KD) hipLaunchKernelGGL(k_bw_post_gate4<2>, dim3((unsigned)((nw / KD + 7) / 8)), dim3(256), 0, st, r);
     else hipLaunchKernelGGL(k_bw_post_gate<2>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, r);
