@@ -1592,19 +1592,19 @@ __device__ __forceinline__ int gate_head(int H, int Hk, int Hv, int hv, int G) {
 }
 __device__ __forceinline__ float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
-// canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094)
-constexpr int kCanonThreads = 1024;
-__global__ __launch_bounds__(kCanonThreads) void k_bw_canon(BR p) {
-  constexpr int NWc = kCanonThreads / 64;
+// canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094),
+// batch row bb by one workgroup of NT threads
+template <int NT>
+__device__ __forceinline__ void canon_rows(const BR& p, int bb) {
+  constexpr int NWc = NT / 64;
   __shared__ int wsum[NWc];
-  const int bb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t base = p.seg_batched ? (int64_t)bb * p.L : 0;
   auto sid = [&](int t) -> int64_t { return p.seg ? ld_i(p.seg, base + t, p.seg_dt) : 0; };
-  // tiles of kCanonThreads tokens: thread tid flags token ts + tid as a change
-  // from the token before it; a block-wide inclusive scan of the flags gives
-  // the ids
+  // tiles of NT tokens: thread tid flags token ts + tid as a change from the
+  // token before it; a block-wide inclusive scan of the flags gives the ids
   int run = (p.has_init && p.init_seg != nullptr) ? (sid(0) != (int64_t)p.init_seg[bb]) : 0;
-  for (int ts = 0; ts < p.L; ts += kCanonThreads) {
+  for (int ts = 0; ts < p.L; ts += NT) {
     const int t = ts + tid;
     int f = (t > 0 && t < p.L) ? (sid(t) != sid(t - 1)) : 0;
 #pragma unroll
@@ -1654,10 +1654,16 @@ __device__ __forceinline__ void gate4(const float* g, int64_t base, int chans, i
 // channels per lane (vector loads and stores): the prepared inputs as the
 // forward kernels form them (the L2 norms summed in another order, so the
 // last bit can differ).
+// The first B workgroups (one per batch row, dispatched first) form the
+// canonical segment ids meanwhile.
 __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
+  if ((int)blockIdx.x < p.B) {
+    canon_rows<256>(p, (int)blockIdx.x);
+    return;
+  }
   const int l = threadIdx.x & 63, c = 4 * (l & 31);
   const int64_t rows = (int64_t)p.B * p.L * p.Hv;
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (l >> 5);
+  const int64_t row0 = ((int64_t)(blockIdx.x - p.B) * 4 + (threadIdx.x >> 6)) * 2 + (l >> 5);
   const bool valid = row0 < rows;
   const int64_t row = valid ? row0 : rows - 1;   // both halves take part in the shuffles
   const int hv = (int)(row % p.Hv);
@@ -2133,9 +2139,8 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
 
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_bw_canon, dim3(a->B), dim3(kCanonThreads), 0, st, r);
   const int64_t rows = (int64_t)a->B * a->L * a->Hv;
-  hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st, r);
+  hipLaunchKernelGGL(k_bw_prep, dim3((unsigned)((rows + 7) / 8 + a->B)), dim3(256), 0, st, r);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(DN_E_LAUNCH, hipGetErrorString(e));
 
