@@ -64,6 +64,7 @@ struct BW {
   int bf;                // precision "bf16": split-bf16 products in k_bw_grads
   int c0;                // first chunk of the block (token c0 * BC)
   const float *q, *k, *v, *g, *b, *w;
+  int qk_hd, gb_hd;      // q, k (g, b) hold H / hd heads: head h reads head h / hd
   const int32_t* seg;
   const float* init;     // state entering the block's first chunk (NULL: zero)
   float* sfin;           // NULL or: the forward scan's state leaving the block
@@ -94,6 +95,10 @@ struct BW {
 
 __device__ __forceinline__ int64_t row_of(const BW& p, int bb, int t, int h) {
   return (((int64_t)bb * p.L + t) * p.H + h) * KD;
+}
+// row of an input held at H / hd heads
+__device__ __forceinline__ int64_t row_in(const BW& p, int bb, int t, int h, int hd) {
+  return (((int64_t)bb * p.L + t) * (p.H / hd) + h / hd) * KD;
 }
 
 __device__ __forceinline__ int seg_at(const BW& p, int bb, int t) {
@@ -273,9 +278,8 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const int c4 = tid % (KD / 4), i = 4 * (tid / (KD / 4)) + it;
       nk[it] = ng[it] = zero_f4();
       if (t0 + i < p.L) {
-        const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
-        nk[it] = ld4g(p.k + ro);
-        ng[it] = ld4g(p.g + ro);
+        nk[it] = ld4g(p.k + row_in(p, bb, t0 + i, h, p.qk_hd) + 4 * c4);
+        ng[it] = ld4g(p.g + row_in(p, bb, t0 + i, h, p.gb_hd) + 4 * c4);
       }
     }
   };
@@ -299,9 +303,8 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
         make_float4(gv.x * kLog2e, gv.y * kLog2e, gv.z * kLog2e, gv.w * kLog2e);
     qst[it] = bst[it] = zero_f4();
     if (t0 + i < p.L) {
-      const int64_t ro = row_of(p, bb, t0 + i, h) + 4 * c4;
-      qst[it] = ld4g(p.q + ro);
-      bst[it] = ld4g(p.b + ro);
+      qst[it] = ld4g(p.q + row_in(p, bb, t0 + i, h, p.qk_hd) + 4 * c4);
+      bst[it] = ld4g(p.b + row_in(p, bb, t0 + i, h, p.gb_hd) + 4 * c4);
     }
   }
   lds_barrier();
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       const int m = 16 * I;
       const int i = 16 * I + l16, j = 16 * J + l16;
       const bool vi = t0 + i < p.L, vj = t0 + j < p.L;
-      const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
+      const float* kj = p.k + row_in(p, bb, vj ? t0 + j : 0, h, p.qk_hd);
       f32x4 accA = zero4(), accM = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -447,7 +450,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       // diagonal block with a large decay span: e^{G_i - G_j} per element
       const int j = 16 * I + l16;
       const bool vj = t0 + j < p.L;
-      const float* kj = p.k + row_of(p, bb, vj ? t0 + j : 0, h);
+      const float* kj = p.k + row_in(p, bb, vj ? t0 + j : 0, h, p.qk_hd);
 #pragma unroll
       for (int e = 0; e < 4; ++e) resA[e] = resM[e] = 0.f;
 #pragma unroll 8
@@ -1390,8 +1393,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const int idx = tid + NT * it, i = idx / (HC / 4), c4 = idx % (HC / 4);
     float4 qv = zero_f4(), kv = zero_f4(), bv = zero_f4();
     if (t0 + i < p.L) {
-      const int64_t ro = row_of(p, bb, t0 + i, h) + ch0 + 4 * c4;
-      qv = ld4g(p.q + ro); kv = ld4g(p.k + ro); bv = ld4g(p.b + ro);
+      const int64_t rq = row_in(p, bb, t0 + i, h, p.qk_hd) + ch0 + 4 * c4;
+      qv = ld4g(p.q + rq); kv = ld4g(p.k + rq); bv = ld4g(p.b + row_in(p, bb, t0 + i, h, p.gb_hd) + ch0 + 4 * c4);
     }
     *reinterpret_cast<float4*>(&sQ[i][4 * c4]) = qv;
     *reinterpret_cast<float4*>(&sK[i][4 * c4]) = kv;
@@ -1581,7 +1584,9 @@ struct BR {
   const int32_t* init_seg; int has_init;
   float scale; int l2norm, fuse, guard;
   int32_t* canon;                                 // (B, L)
-  float *qe, *ke, *ve, *ge, *be, *we;             // (B, L, Hv, 128) prepared inputs
+  float *qe, *ke, *ve, *ge, *be, *we;             // prepared inputs: qe, ke (B, L, Hk, 128); ge, be
+                                                  // (B, L, Hv / gb_hd, 128); ve, we (B, L, Hv, 128)
+  int gb_hd;                                      // G when g and b both sit at the key heads, else 1
   int w_alias;                                    // w's prologue step is the identity: we unused
   const float *dqe, *dke, *dge, *dbe, *dwe;       // their gradients
   float *dq, *dk, *dg, *db, *dw;                  // raw-layout gradients (dq, dk in qk_dt)
@@ -1714,10 +1719,17 @@ __global__ __launch_bounds__(256) void k_bw_prep(BR p) {
   }
   if (!valid) return;
   const int64_t o = row * KD + c;
-  *reinterpret_cast<float4*>(p.qe + o) = make_float4(qh[0], qh[1], qh[2], qh[3]);
-  *reinterpret_cast<float4*>(p.ke + o) = make_float4(kh[0], kh[1], kh[2], kh[3]);
-  *reinterpret_cast<float4*>(p.ge + o) = make_float4(gv[0], gv[1], gv[2], gv[3]);
-  *reinterpret_cast<float4*>(p.be + o) = make_float4(bv[0], bv[1], bv[2], bv[3]);
+  // q, k (and g, b at the key heads) once per key head: the first value head
+  // of the group writes them
+  if (hv % p.G == 0) {
+    *reinterpret_cast<float4*>(p.qe + qrow) = make_float4(qh[0], qh[1], qh[2], qh[3]);
+    *reinterpret_cast<float4*>(p.ke + qrow) = make_float4(kh[0], kh[1], kh[2], kh[3]);
+  }
+  if (hv % p.gb_hd == 0) {
+    const int64_t og = (bt * (p.Hv / p.gb_hd) + hv / p.gb_hd) * KD + c;
+    *reinterpret_cast<float4*>(p.ge + og) = make_float4(gv[0], gv[1], gv[2], gv[3]);
+    *reinterpret_cast<float4*>(p.be + og) = make_float4(bv[0], bv[1], bv[2], bv[3]);
+  }
   if (!p.w_alias) *reinterpret_cast<float4*>(p.we + o) = make_float4(wv[0], wv[1], wv[2], wv[3]);
   *reinterpret_cast<float4*>(p.ve + o) = make_float4(vv[0], vv[1], vv[2], vv[3]);
 }
@@ -1978,7 +1990,7 @@ extern "C" size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a) {
 
 // the recurrence backward with the element types of d_out and dv given
 static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt, bool bf, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    size_t workspace_bytes, void* stream, int qk_hd = 1, int gb_hd = 1) {
   const int rc = bw_check(a);
   if (rc != DN_OK) return rc;
   const size_t need = bw_workspace_bytes(a);
@@ -1990,6 +2002,7 @@ static int bwd_core(const dn_backward_args* a, int dout_dt, int dv_dt, int v_dt,
   p.bf = bf;
   p.q = (const float*)a->q; p.k = (const float*)a->k; p.v = (const float*)a->v;
   p.g = (const float*)a->g; p.b = (const float*)a->b; p.w = (const float*)a->w;
+  p.qk_hd = qk_hd; p.gb_hd = gb_hd;
   p.seg = a->seg;
   p.dout = a->d_out; p.dout_dt = dout_dt; p.dv_dt = dv_dt; p.v_dt = v_dt;
   p.dq = (float*)a->dq; p.dk = (float*)a->dk; p.dv = (float*)a->dv;
@@ -2136,6 +2149,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   // the recurrence kernels read w in place when its prologue step is the
   // identity on a per-value-head, channel-wise layout
   r.w_alias = !a->fuse_prologue && !a->stability_guard && a->w_heads == a->Hv && a->w_chans == KD;
+  r.gb_hd = (a->g_heads == a->Hk && a->b_heads == a->Hk) ? a->Hv / a->Hk : 1;
   r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
 
   hipStream_t st = (hipStream_t)stream;
@@ -2155,7 +2169,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   c.dq = pre[6]; c.dk = pre[7]; c.dv = dv; c.dg = pre[8]; c.db = pre[9]; c.dw = dw_direct ? (float*)dw : pre[10];
   c.d_init = d_init;
   c.recompute_states = a->recompute_states;
-  rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, a->precision == 0, w, lay.core, stream);
+  rc = bwd_core(&c, a->v_dtype, a->v_dtype, DT_F32, a->precision == 0, w, lay.core, stream, a->Hv / a->Hk, r.gb_hd);
   if (rc != DN_OK) return rc;
 
   const int64_t krows = (int64_t)a->B * a->L * a->Hk;
