@@ -369,6 +369,9 @@ class _TrainFn(torch.autograd.Function):
         _lib.check(lib.dn_prefill_fwd(ctypes.byref(a), _ptr(ws), nbytes, _stream(dev)), "dn_prefill_fwd")
         ctx.save_for_backward(q, k, v, g, b, w, init)
         ctx.meta = meta
+        # an unused output (usually the final state) reaches backward as None
+        # instead of a materialised zero tensor; the kernels take NULL for it
+        ctx.set_materialize_grads(False)
         return out, fin
 
     @staticmethod
