@@ -110,10 +110,6 @@ template <class T> struct Row8;
 template <> struct Row8<bf16> {
   bf16x8 a;
   __device__ __forceinline__ void load(const bf16* row, int cg) { a = ldg(reinterpret_cast<const bf16x8*>(row + 8 * cg)); }
-  // the single-step kernel's load: a plain (cached) load measured 1.5% faster
-  // there at config 4 than the non-temporal one, which the T-token kernel
-  // keeps (plain 7% slower there)
-  __device__ __forceinline__ void load1(const bf16* row, int cg) { a = *reinterpret_cast<const bf16x8*>(row + 8 * cg); }
   __device__ __forceinline__ void zero() { a = bf16x8{}; }
   __device__ __forceinline__ float at(int e) const { return (float)a[e]; }
   // the same value through an opaque instruction: the compiler cannot reuse
@@ -141,8 +137,6 @@ template <> struct Row8<float> {
     a = ldg(reinterpret_cast<const f32x4*>(row + 4 * cg));
     b = ldg(reinterpret_cast<const f32x4*>(row + 64 + 4 * cg));
   }
-  // non-temporal in the single-step kernel as well (plain loads 3% slower)
-  __device__ __forceinline__ void load1(const float* row, int cg) { load(row, cg); }
   __device__ __forceinline__ void zero() { a = zero4(); b = zero4(); }
   __device__ __forceinline__ float at(int e) const { return e < 4 ? a[e] : b[e - 4]; }
   __device__ __forceinline__ float at2(int e) const { return at(e); }
@@ -176,10 +170,11 @@ constexpr int kDecodeWaves = 2;
 constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel (8 measured slower)
 
 // One workgroup of NW waves per (batch row, value head).  Lane (rg, cg)
-// holds state rows rg + 4*NW*r, r < R (R = 32/NW), 8 columns per row (Row8
-// above): the 4 row groups of a wave read 4 consecutive rows per load
-// instruction (1 KB contiguous for a bf16 state; rows R*rg.. per lane
-// measured 2.5% slower at config 4).  Every global load (state, q, k, gates, v) is issued at entry so
+// holds R = 32/NW state rows, 8 columns per row (Row8 above): for a bf16
+// state rows rg + 4*NW*r, so the 4 row groups of a wave read 4 consecutive
+// rows (1 KB contiguous) per load instruction (consecutive rows per lane
+// measured 4% slower at config 4); for an fp32 state rows R*rg + r (the
+// interleaved order measured 0.5% slower there).  Every global load (state, q, k, gates, v) is issued at entry so
 // their latencies overlap; the state loads and stores are non-temporal (each
 // byte is touched once per step).  The column sums reduce inside each wave by
 // shuffles, then across the NW waves through LDS.
@@ -211,11 +206,12 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
   const bool rst = p.reset != nullptr && p.reset[bb] != 0;
   const int64_t sbase = (int64_t)bh * K * V;
 
+  auto srow = [&](int r) { return sizeof(TSin) == 2 ? 4 * NW * r + rg : R * rg + r; };
   RowIn S[R];
   const TSin* sp = (const TSin*)p.sin + sbase;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if (!rst) S[r].load1(sp + (4 * NW * r + rg) * V, cg);
+    if (!rst) S[r].load(sp + srow(r) * V, cg);
     else S[r].zero();
   }
   // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v
@@ -266,7 +262,7 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
   for (int e = 0; e < 8; ++e) { pa[e] = 0.f; pc[e] = 0.f; }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int ii = 4 * NW * r + rg;
+    const int ii = srow(r);
     const float di = dd[ii], bi = bt[ii] * di, qi = qn[ii] * di;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -315,7 +311,7 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
     float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int ii = 4 * NW * r + rg;
+      const int ii = srow(r);
       const float di = dd[ii], ki = kn[ii];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -334,12 +330,12 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
   TSout* op = (TSout*)p.sout + sbase;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int ii = 4 * NW * r + rg;
+    const int ii = srow(r);
     const float di = dd[ii], ki = kn[ii];
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = fmaf(di, S[r].at2(e), ki * vc[e]) * fac;
-    if (valid) store_row<TSin, TSout>(op + (4 * NW * r + rg) * V, cg, y);
+    if (valid) store_row<TSin, TSout>(op + srow(r) * V, cg, y);
   }
 }
 
@@ -612,7 +608,7 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
   const bool fi = a->state_in_dtype == DN_F32, fo = a->state_out_dtype == DN_F32;
   const dim3 grid((unsigned)(a->B * a->Hv));
   // the single-step kernel runs two matrices per workgroup (measured faster at
-  // config 4 than one: fp32 state 179 vs 187 us, bf16 state 93 vs 95 us)
+  // config 4 than one: fp32 state 179 vs 187 us, bf16 state 94 vs 95 us)
   const dim3 grid2((unsigned)((a->B * a->Hv + 1) / 2)), blk2(128 * kDecodeWaves);
   prof_mark(3, st, false);
   if (T == 1) {
