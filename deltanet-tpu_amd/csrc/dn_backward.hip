@@ -2077,14 +2077,21 @@ extern "C" int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t
 
 namespace {
 
+// Prepared inputs and their gradients: qe, ke at the key heads; ge, be at
+// Hv / gb_hd heads; ve, we and the five gradients at the value heads.
 struct RawLayout {
-  size_t canon, pre, core;   // bytes
+  size_t canon, pre, pre_k, pre_gb, core;   // bytes (pre*: one array)
+  int gb_hd;
+  size_t total() const { return canon + 7 * pre + 2 * pre_k + 2 * pre_gb + core; }
 };
 
 RawLayout raw_layout(const dn_prefill_args* a) {
   RawLayout r;
   r.canon = (((size_t)a->B * a->L * sizeof(int32_t)) + 255) & ~(size_t)255;
   r.pre = (size_t)a->B * a->L * a->Hv * KD * sizeof(float);
+  r.pre_k = (size_t)a->B * a->L * a->Hk * KD * sizeof(float);
+  r.gb_hd = (a->g_heads == a->Hk && a->b_heads == a->Hk) ? a->Hv / a->Hk : 1;
+  r.pre_gb = r.pre / r.gb_hd;
   dn_backward_args c{};
   c.B = a->B; c.L = a->L; c.H = a->Hv;
   c.recompute_states = a->recompute_states;
@@ -2118,8 +2125,7 @@ int raw_check(const dn_prefill_args* a) {
 
 extern "C" size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a) {
   if (raw_check(a) != DN_OK) return 0;
-  const RawLayout r = raw_layout(a);
-  return r.canon + 11 * r.pre + r.core;
+  return raw_layout(a).total();
 }
 
 extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, const void* d_final,
@@ -2130,7 +2136,7 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   if (!d_out || !dq || !dk || !dv || !dg || !db || !dw) return set_error(DN_E_INVALID, "missing gradient pointer");
   if (d_init != nullptr && a->init_state == nullptr) return set_error(DN_E_INVALID, "d_init needs init_state");
   const RawLayout lay = raw_layout(a);
-  if (workspace == nullptr || workspace_bytes < lay.canon + 11 * lay.pre + lay.core)
+  if (workspace == nullptr || workspace_bytes < lay.total())
     return set_error(DN_E_WORKSPACE, "workspace too small");
   char* w = (char*)workspace;
   BR r{};
@@ -2143,13 +2149,16 @@ extern "C" int dn_prefill_bwd_raw(const dn_prefill_args* a, const void* d_out, c
   r.scale = a->scale; r.l2norm = a->qk_l2norm; r.fuse = a->fuse_prologue; r.guard = a->stability_guard;
   r.canon = (int32_t*)w; w += lay.canon;
   float* pre[11];
-  for (int i = 0; i < 11; ++i) { pre[i] = (float*)w; w += lay.pre; }
+  for (int i = 0; i < 11; ++i) {
+    pre[i] = (float*)w;
+    w += i < 2 ? lay.pre_k : (i == 3 || i == 4) ? lay.pre_gb : lay.pre;
+  }
   r.qe = pre[0]; r.ke = pre[1]; r.ve = pre[2]; r.ge = pre[3]; r.be = pre[4]; r.we = pre[5];
   r.dqe = pre[6]; r.dke = pre[7]; r.dge = pre[8]; r.dbe = pre[9]; r.dwe = pre[10];
   // the recurrence kernels read w in place when its prologue step is the
   // identity on a per-value-head, channel-wise layout
   r.w_alias = !a->fuse_prologue && !a->stability_guard && a->w_heads == a->Hv && a->w_chans == KD;
-  r.gb_hd = (a->g_heads == a->Hk && a->b_heads == a->Hk) ? a->Hv / a->Hk : 1;
+  r.gb_hd = lay.gb_hd;
   r.dq = (float*)dq; r.dk = (float*)dk; r.dg = (float*)dg; r.db = (float*)db; r.dw = (float*)dw;
 
   hipStream_t st = (hipStream_t)stream;

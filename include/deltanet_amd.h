@@ -195,8 +195,10 @@ size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
 int dn_prefill_bwd(const dn_backward_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes dn_prefill_bwd_raw needs (0 if the arguments are invalid):
- * dn_prefill_bwd_workspace_size at H = Hv (with a->recompute_states) plus eleven
- * (B,L,Hv,128) f32 arrays. */
+ * dn_prefill_bwd_workspace_size at H = Hv (with a->recompute_states) plus the
+ * prepared inputs and their gradients as f32 arrays: seven (B,L,Hv,128), two
+ * (B,L,Hk,128) (q, k) and two for g and b, (B,L,Hk,128) when both have Hk
+ * heads and (B,L,Hv,128) otherwise. */
 size_t dn_prefill_bwd_raw_workspace_size(const dn_prefill_args* a);
 
 /* Backward of the whole training op from the forward's own arguments: the

@@ -115,7 +115,12 @@ def test_invalid_args_rejected_without_gpu():
     ra.qk_dtype, ra.v_dtype = _lib.DN_BF16, _lib.DN_BF16
     need = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
     core = 4 * 2 * 4 * (9 * 64 * 128 + 4 * 64 * 64 + 2 * 128 + 3 * 128 * 128)
-    assert need == 512 + 11 * 1 * 128 * 4 * 128 * 4 + core
+    hv_arr, hk_arr = 1 * 128 * 4 * 128 * 4, 1 * 128 * 2 * 128 * 4   # (B,L,Hv,128), (B,L,Hk,128) f32
+    # seven arrays at Hv; q, k, and g, b (both at the key heads here) at Hk
+    assert need == 512 + 7 * hv_arr + 4 * hk_arr + core
+    ra.b_heads = 4   # b at the value heads: g and b prepared at Hv
+    assert lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra)) == 512 + 9 * hv_arr + 2 * hk_arr + core
+    ra.b_heads = 2
     fake = [0x1000] * 6 + [None]   # dq dk dv dg db dw, no d_init
     assert lib.dn_prefill_bwd_raw(ctypes.byref(ra), 0x1000, None, *fake, None, 0, None) == -2
     ra.g_heads = 3
@@ -161,7 +166,7 @@ def test_recompute_states_workspace_size():
     full = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
     ra.recompute_states = 1
     rec = lib.dn_prefill_bwd_raw_workspace_size(ctypes.byref(ra))
-    pre = 11 * 4 * 8192 * 32 * 128 * 4
+    pre = (7 * 32 + 4 * 16) * 4 * 8192 * 128 * 4
     assert full - rec == (4 * 32 * 128 * unit) - (4 * 32 * 8 * unit + 16 * 4 * 32 * kk)
     assert rec > pre
 
