@@ -118,7 +118,8 @@ def chunk_gdn2(
 
     Args and returns as the reference ``chunk_gdn2``.  With ``is_inference=False``
     and inputs that require grad, the call is differentiable under torch.autograd
-    (backward: ``dn_prefill_bwd``, fp32, reference custom VJP gdn2.py:1446-1769).
+    (backward: ``dn_prefill_bwd_raw`` at the call's ``precision``, reference custom
+    VJP gdn2.py:1446-1769).
     ``recompute_states=True`` runs that backward in token blocks, keeping only
     the states at block boundaries and recomputing each block's chunk states
     (reference gdn2.py:655-695, 1614-1630): less workspace, bit-identical
