@@ -48,7 +48,6 @@ struct PF {
   void* BeF;                 // F [8][4]  bf16: be^T (rows = key channel, k = token)
   float* QeC;                // C [8][8]  f32 : qe in the accumulator layout of X^T
   void* MF;                  // F [8][4]  bf16 hi, lo: M rows (row = token)
-  void* RF;                  // F [16][4] bf16 hi, lo: R = [M; ke^T] T rows
   void* PnF;                 // F [8][4]  bf16: Pn rows (row = state row)
   float* QCw;                // C [8][nct] f32: Q tiles in the scan's state layout
   void* XF;                  // F [8][4]  bf16 hi, lo: X rows (row = token)

@@ -1322,7 +1322,7 @@ namespace {
 struct WsLayout {
   size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, sink, carry, total;
   // precision "bf16" (dn_wy.hip)
-  size_t BeF, QeC, RF, PnF, QCw, XF, OiC, SF;
+  size_t BeF, QeC, PnF, QCw, XF, OiC, SF;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1342,7 +1342,6 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
     // chunk-parallel path: M rows (k_wy only) share the X array (k_val on)
     L.BeF = take(units * sq * 2);
     L.QeC = take(units * sq * 4);
-    L.RF = take(units * sq * 8);
     L.PnF = take(units * sq * 2);
     L.QCw = take(units * KD * Vp * 4);
     L.XF = take(units * sq * 4);
@@ -1493,7 +1492,6 @@ int prefill_run(const dn_prefill_args* a, char* ws, size_t workspace_bytes, int 
   if (bf) {
     p.BeF = ws + Lw.BeF;
     p.QeC = (float*)(ws + Lw.QeC);
-    p.RF = ws + Lw.RF;
     p.PnF = ws + Lw.PnF;
     p.QCw = (float*)(ws + Lw.QCw);
     p.XF = ws + Lw.XF;

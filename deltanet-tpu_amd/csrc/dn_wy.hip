@@ -48,6 +48,22 @@ constexpr int TP = 132;                 // fp32 LDS pitch (floats) of A^T / T^T
 constexpr float kSafeNat = 68.6f;       // e^{68.6} < 2^{99}
 constexpr int SQ = CH * KD;             // elements of one 128 x 128 operand
 
+#ifdef DN_STAMPS
+// phase timestamps of one workgroup per launch (probe builds only)
+__device__ unsigned long long dn_stamp_buf[8][64];
+#define DN_STAMP(kern, k)                                                             \
+  do {                                                                                \
+    if (blockIdx.x == DN_STAMPS && threadIdx.x < 64)                                  \
+      dn_stamp_buf[kern][(k) + 32 * (threadIdx.x >> 5) * 0] = __builtin_amdgcn_s_memtime(); \
+  } while (0)
+#define DN_RSTAMP(kern, k)                                                            \
+  do {                                                                                \
+    if (blockIdx.x == DN_STAMPS && threadIdx.x < 64) dn_stamp_buf[kern][k] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define DN_STAMP(kern, k) do {} while (0)
+#define DN_RSTAMP(kern, k) do {} while (0)
+#endif
 __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float expn(float x) { return fast_exp2(x * kLog2e); }
 
@@ -149,7 +165,7 @@ __device__ __forceinline__ f32x4 tr_half(const F1& a, int half, int r16, int q) 
 //           fragments (split);
 //      smT  per-channel factor tables, then the T scratch.
 // ===========================================================================
-template <class TIn>
+template <class TIn, class TV>
 __global__ __launch_bounds__(512) void k_wy(const PF p) {
   __shared__ __align__(16) float smP[CH * TP];
   __shared__ __align__(16) bf16 smQ[2 * SQ];
@@ -158,6 +174,8 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
   __shared__ int misc[16];
   __shared__ float tokv[4 * CH];   // scalar decay: per-token loc, tail, e^Lambda, e^{Lend - Lambda}
 
+  DN_STAMP(0, 0);
+  DN_RSTAMP(0, 16);
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, r16 = l & 15, q = l >> 4;
@@ -231,6 +249,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
   asm volatile("" : "+v"(sg_t.lo), "+v"(sg_t.hi), "+v"(sg_tp.lo), "+v"(sg_tp.hi));
   asm volatile("" : "+v"(sg_0.lo), "+v"(sg_0.hi), "+v"(sg_a.lo), "+v"(sg_a.hi), "+v"(sg_b.lo), "+v"(sg_b.hi));
 
+  DN_STAMP(0, 1);
   // ---- phase 0: in-chunk document index, chunk flags ----------------------
   if (w < 2) {
     const bool chg = (p.seg != nullptr && tid > 0) ? (sg_t != sg_tp) : false;
@@ -238,7 +257,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     doc[tid] = __popcll(bal & (l == 63 ? ~0ull : ((2ull << l) - 1)));
     if (w == 0 && l == 0) misc[0] = __popcll(bal);
   }
-  __syncthreads();
+  lds_barrier();
   if (w == 1) doc[tid] += misc[0];
   if (tid == 0 && h == 0) {
     int is_new;
@@ -258,6 +277,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     p.flags[((int64_t)b * p.NCb + c) * 2 + 0] = is_new;
   }
 
+  DN_STAMP(0, 2);
   // ---- phase 1: gates, block-local decay sums ------------------------------
   // loc = sum of g over tokens (16w, i] of the row's block (<= 0), tl = sum
   // over (i, 16w+15]; the block total (tokens 16w+1 .. 16w+15) and the
@@ -268,7 +288,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     x = p.fuse ? -__expf(fminf(x, 5.f)) : fminf(x, 0.f);   // fminf(NaN, 0) = 0
     return ok ? fminf(x, gmax) : 0.f;
   };
-  float loc[32], tl[32];
+  float loc[32], gv[32];
   if (scalar_g) {
     const float gs = act_g(rw.g_sc, valid);
     const float ls = row_scan16(r16 == 0 ? 0.f : gs);
@@ -276,14 +296,12 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     if (l == 15) tbl[w] = ls;
     if (l == 0) tbl[8 + w] = gs;
   } else {
-    float gv[32];
 #pragma unroll
     for (int s = 0; s < 4; ++s) rw.g[s].to(gv + 8 * s);
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
       gv[e] = act_g(gv[e], valid);
       loc[e] = row_scan16(r16 == 0 ? 0.f : gv[e]);
-      tl[e] = row_next(row_rscan16(gv[e]));
     }
     if (r16 == 15) {
 #pragma unroll
@@ -298,9 +316,10 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
         for (int e = 0; e < 8; ++e) tbl[8 * KD + w * KD + 32 * s + pi_k(q, e)] = gv[8 * s + e];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (tid == 0 && h == 0) p.flags[((int64_t)b * p.NCb + c) * 2 + 1] = (doc[CH - 1] == 0);
 
+  DN_STAMP(0, 3);
   // ---- phase 2: per-channel (or per-token) factor tables -------------------
   // smT.  midpoint: off[8][128] (Lambda_16a - Lambda_64), eL64[128], eE64[128];
   // blockwise: F[28][128], eLa[8][128], eEa[8][128], kdf[8][128];
@@ -343,7 +362,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
       sm += tbl[8 + a];
       smT[pr] = sm;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < KD) dvec[tid] = __int_as_float(misc[4]);
   } else {
     if (tid < KD) {
@@ -373,7 +392,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
       const bool any_unsafe = __any(unsafe);
       if (l == 0) misc[2 + w] = any_unsafe;
     }
-    __syncthreads();
+    lds_barrier();
     midpoint = __builtin_amdgcn_readfirstlane(!(misc[2] | misc[3]));
     if (!midpoint) {
       if (tid < KD) {
@@ -411,11 +430,12 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
         }
         if (l == 0) misc[6 + w] = bits;
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
   const int diag_bad = (midpoint || scalar_g) ? 0 : __builtin_amdgcn_readfirstlane(misc[6] | misc[7]);
 
+  DN_STAMP(0, 4);
   // ---- phase 3: q / k normalisation (gdn2.py:2113-2122: the normalised q, k
   // are stored back in the input dtype; the fused prologue, gdn2.py:133-142,
   // keeps them in fp32) --------------------------------------------------------
@@ -474,6 +494,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
   const bool first_doc = doc[i_row] == 0;
   const bool last_doc = doc[i_row] == doc[CH - 1];
 
+  DN_STAMP(0, 5);
   // ---- phase 4: operands, one 32-channel slab at a time ---------------------
   // rowA: row operand of A (registers); row operand of M -> smQ (split);
   // column operand -> smP (split; fp32 k e^{tail} when blockwise);
@@ -485,29 +506,26 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
   float* smPf = smP;
   bf16* gBe = (bf16*)p.BeF + u * SQ;
   float* gQe = p.QeC + u * SQ;
-  bf16* gKe = reinterpret_cast<bf16*>(p.QCw + u * (int64_t)(KD * p.Vp));   // k_val rewrites it later
   F3 rowA[4], kdF[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     float qv[8], kv[8], bk[8];
     prep(rw, s, nq, nk, valid, qv, kv, bk);
-    float ra[8], rm[8], be[8], qe[8], ke[8];
+    float ra[8], rm[8], be[8], qe[8];
     if (scalar_g) {
-      const float eL = tokv[2 * CH + i_row], eE = tokv[3 * CH + i_row];
+      const float eL = tokv[2 * CH + i_row];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         ra[e] = bk[e];
         rm[e] = qv[e];
         be[e] = bk[e] * eL;
         qe[e] = qv[e] * eL;
-        ke[e] = kv[e] * eE;
       }
       stf3(smPb, w, s, l, kv);
     } else if (midpoint) {
-      float off[8], eL[8], eE[8], cc[8];
+      float off[8], eL[8], cc[8];
       row8f(t_off + w * KD + 32 * s, q, off);
       row8f(t_eL64 + 32 * s, q, eL);
-      row8f(t_eE64 + 32 * s, q, eE);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float E = expn(loc[8 * s + e] + off[e]);   // e^{Lambda_i - Lambda_64}
@@ -516,24 +534,22 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
         cc[e] = kv[e] * __builtin_amdgcn_rcpf(E);
         be[e] = ra[e] * eL[e];
         qe[e] = rm[e] * eL[e];
-        ke[e] = cc[e] * eE[e];
       }
       stf3(smPb, w, s, l, cc);
     } else {
-      float eL[8], eE[8], kf[8], kc[8], kd[8];
+      float eL[8], kf[8], kc[8], kd[8];
       row8f(t_eLa + w * KD + 32 * s, q, eL);
-      row8f(t_eEa + w * KD + 32 * s, q, eE);
       row8f(t_kdf + w * KD + 32 * s, q, kf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float E = expn(loc[8 * s + e]);            // e^{Lambda_i - Lambda_16w}
         ra[e] = bk[e] * E;
         rm[e] = qv[e] * E;
-        kc[e] = kv[e] * expn(tl[8 * s + e]);             // e^{Lambda_{16w+15} - Lambda_i}
+        const float tl = row_next(row_rscan16(gv[8 * s + e]));   // sum over (i, 16w+15]
+        kc[e] = kv[e] * expn(tl);                        // e^{Lambda_{16w+15} - Lambda_i}
         kd[e] = kc[e] * kf[e];
         be[e] = ra[e] * eL[e];
         qe[e] = rm[e] * eL[e];
-        ke[e] = kc[e] * eE[e];
       }
       kdF[s] = P::f3(kd);
       const int o = fofs(w, s, l);
@@ -546,28 +562,21 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     for (int e = 0; e < 8; ++e) {
       be[e] = first_doc ? be[e] : 0.f;
       qe[e] = first_doc ? qe[e] : 0.f;
-      ke[e] = last_doc ? ke[e] : 0.f;
     }
     const F1 fb = P::f1(be);
-    const F3 fk = P::f3(ke);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int o = fofs(2 * s + hf, w >> 1, l) + 4 * (w & 1);
       const f32x4 cb = tr_half(fb, hf, r16, q);
       const float xb[4] = {cb[0], cb[1], cb[2], cb[3]};
       SS::st4(gBe + o, xb);
-      const f32x4 ch = tr_half(fk.hi, hf, r16, q);
-      const f32x4 cl = tr_half(fk.lo, hf, r16, q);
-      const float xh[4] = {ch[0], ch[1], ch[2], ch[3]};
-      const float xl[4] = {cl[0], cl[1], cl[2], cl[3]};
-      SS::st4(gKe + o, xh);
-      SS::st4(gKe + SQ + o, xl);
       *reinterpret_cast<f32x4*>(gQe + cofs(2 * s + hf, w, 8, l)) =
           f32x4{qe[4 * hf], qe[4 * hf + 1], qe[4 * hf + 2], qe[4 * hf + 3]};
     }
   }
-  __syncthreads();
+  lds_barrier();
 
+  DN_STAMP(0, 6);
   // ---- phase 5: A and M^T tiles ----------------------------------------------
   // At[cc]: A tile (w, cc), lane (j, q) = A[16w + 4q + ii][16cc + j], cc <= w.
   // M^T tiles (cc, am), cc < am, lane (i, q) = M[16am + i][16cc + 4q + ii], are
@@ -597,21 +606,33 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     SS::st4s(gM + o, gM + SQ + o, x);
   };
   if (midpoint || scalar_g) {
+    // every column-operand fragment is read from LDS once and serves both
+    // the A tile (w, cc) and the M^T tile (cc, am)
+    F3 rq[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) rq[s] = ldf3(smQb, am, s, l);
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) {
-      if (cc <= w) {
+      if (cc <= w || cc < am) {
+        F3 cf[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) P::m33(At[cc], rowA[s], ldf3(smPb, cc, s, l));
-      }
-      if (cc < am) {
-        f32x4 m = zero4();
+        for (int s = 0; s < 4; ++s) cf[s] = ldf3(smPb, cc, s, l);
+        if (cc <= w) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) P::m33(m, ldf3(smPb, cc, s, l), ldf3(smQb, am, s, l));
-        store_mt(cc, m);
+          for (int s = 0; s < 4; ++s) P::m33(At[cc], rowA[s], cf[s]);
+        }
+        if (cc < am) {
+          f32x4 m = zero4();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) P::m33(m, cf[s], rq[s]);
+          store_mt(cc, m);
+        }
+        if (cc == w) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) P::m33(Md, cf[s], ldf3(smQb, w, s, l));
+        }
       }
     }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) P::m33(Md, ldf3(smPb, w, s, l), ldf3(smQb, w, s, l));
     if (scalar_g) {
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
@@ -654,8 +675,47 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
+  // ke = k e^{Lend - Lambda} (last document) from the column operand still in
+  // smP, transposed to ke^T fragments (rows = key channel, k = token) in smQ,
+  // which the A / M products no longer read
+  {
+    const bool lastd = last_doc;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float x[8], f[8];
+      if (!midpoint && !scalar_g) {
+        ld8f(smPf, w, s, l, x);                      // k e^{Lambda_{16w+15} - Lambda_i}
+        row8f(t_eEa + w * KD + 32 * s, q, f);
+      } else {
+        const F3 cf = ldf3(smPb, w, s, l);           // k (e^{Lambda_64 - Lambda_i})
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (float)cf.hi.v[e] + (float)cf.lo.v[e];
+        if (scalar_g) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = tokv[3 * CH + i_row];
+        } else {
+          row8f(t_eE64 + 32 * s, q, f);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = lastd ? x[e] * f[e] : 0.f;
+      const F3 fk = P::f3(x);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int o = fofs(2 * s + hf, w >> 1, l) + 4 * (w & 1);
+        const f32x4 ch = tr_half(fk.hi, hf, r16, q);
+        const f32x4 cl = tr_half(fk.lo, hf, r16, q);
+        const float xh[4] = {ch[0], ch[1], ch[2], ch[3]};
+        const float xl[4] = {cl[0], cl[1], cl[2], cl[3]};
+        SS::st4(smQb + o, xh);
+        SS::st4(smQb + SQ + o, xl);
+      }
+    }
+  }
+  lds_barrier();
+  DN_STAMP(0, 7);
   // ---- phase 6: masks; Md to the workspace, A^T into LDS --------------------
   // A strictly lower and same document; M lower and same document.
   auto mask_a = [&](f32x4& t, int rb, int cb) {   // A tile (rb, cb), lane (j, q)
@@ -691,50 +751,48 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
     const f32x4 v = (cc <= w) ? At[cc] : zero4();
     *reinterpret_cast<f32x4*>(smP + (16 * cc + r16) * TP + 16 * w + 4 * q) = v;
   }
-  __syncthreads();
+  lds_barrier();
 
+  DN_STAMP(0, 8);
   // ---- phase 6b: diagonal blocks whose span exceeds 2^99 (blockwise only) --
   // A_ij = sum_r bk_i k_j e^{loc_i - loc_j}, M_ij = sum_r q_i k_j e^{loc_i - loc_j}
   // summed per element; the owner reloads its rows, and the block's loc and
   // k are staged in smT for the column side.  The results replace the
   // block's diagonal tiles of A^T (LDS) and M (workspace).
   if (diag_bad) {
-    float* stg = reinterpret_cast<float*>(smQ);   // [4][16][128]: loc, k, q, b k of the block
-    float* res = smT;                              // [2][16][16] A, M
+    float* stg = smT;                 // [2][16][128]: loc, k of the block
+    float* res = smT + 4096;          // [2][16][16] A, M
 #pragma unroll 1
     for (int a = 0; a < 8; ++a) {
       if (!((diag_bad >> a) & 1)) continue;
+      Rows R;
+      float nq2 = 0.f, nk2 = 0.f;
       if (w == a) {
-        Rows R;
         load_rows(a, R);
-        float nq2, nk2;
         norms(R, nq2, nk2);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          float gv[8], qv[8], kv[8], bk[8];
-          R.g[s].to(gv);
+          float gv2[8], qv[8], kv[8], bk[8];
+          R.g[s].to(gv2);
           prep(R, s, nq2, nk2, valid, qv, kv, bk);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int o = r16 * KD + 32 * s + pi_k(q, e);
-            stg[o] = row_scan16(r16 == 0 ? 0.f : act_g(gv[e], valid));
+            stg[o] = row_scan16(r16 == 0 ? 0.f : act_g(gv2[e], valid));
             stg[2048 + o] = kv[e];
-            stg[4096 + o] = qv[e];
-            stg[6144 + o] = bk[e];
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
       if (w == a) {
         float sa[16], sm[16];
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) { sa[jj] = 0.f; sm[jj] = 0.f; }
 #pragma unroll 1
         for (int s = 0; s < 4; ++s) {
-          float li[8], qi[8], bi[8];
+          float li[8], qi[8], ki[8], bi[8];
           row8f(stg + r16 * KD + 32 * s, q, li);
-          row8f(stg + 4096 + r16 * KD + 32 * s, q, qi);
-          row8f(stg + 6144 + r16 * KD + 32 * s, q, bi);
+          prep(R, s, nq2, nk2, valid, qi, ki, bi);
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             float lj[8], kj[8];
@@ -772,10 +830,18 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
         store_md(a, tm);
         *reinterpret_cast<f32x4*>(smP + (16 * a + r16) * TP + 16 * a + 4 * q) = ta;
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
 
+  // M rows were written to the workspace by other waves: a full barrier
+  // (stores drained), then their loads fly during T
+  __syncthreads();
+  F3 MB[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (s <= (am >> 1)) MB[s] = SS::fa3(gM + fofs(am, s, l), gM + SQ + fofs(am, s, l));
+  DN_STAMP(0, 9);
   // ---- phase 7: T^T = (I + A^T)^-1 in place (upper unit triangular) --------
   // 16 x 16 diagonal blocks by back substitution (waves 0-1, one block per
   // 16-lane row, lane = column), then doubling Y_PQ = -Y_PP V_PQ Y_QQ for
@@ -797,7 +863,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) smP[(o + i) * TP + o + j] = y[i];
   }
-  __syncthreads();
+  lds_barrier();
   {
     // acc += X[r0 + 0..15][k0 .. k1) * Y[k0 .. k1)[c0 + 0..15] on fp32 MFMA
     // (k range in whole 16-blocks; lane (r, q) feeds k = k + 4q + e)
@@ -826,7 +892,7 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) Wp[(16 * ti + 4 * q + ii) * WP + 16 * tj + r16] = acc[ii];
       }
-      __syncthreads();
+      lds_barrier();
       for (int tau = w; tau < ntile; tau += 8) {
         const int pk = tau / (nt * nt), ti = (tau / nt) % nt, tj = tau % nt;
         const int P0 = 2 * s * pk, Q0 = P0 + s;
@@ -836,182 +902,189 @@ __global__ __launch_bounds__(512) void k_wy(const PF p) {
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) smP[(P0 + 16 * ti + 4 * q + ii) * TP + Q0 + 16 * tj + r16] = -acc[ii];
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
 
-  // ---- phase 8: R^T = T^T [M^T | ke] -> R rows (split) ----------------------
+  DN_STAMP(0, 10);
+  // ---- phase 8: R^T = T^T [M^T | ke] -> R rows (split) in LDS -------------
   // TT(t, s): lane (t, q) = T[32s + pi(q, e)][16t + t] = Y[16t + t][32s + pi].
-  // R_Q^T tiles (t, w) for every t; R_O^T tiles (t, am) for t <= am.
+  // Wave w forms R_Q^T tiles (t, w) for every t and R_O^T tiles (t, am) for
+  // t <= am; stacked in pairs of t they are the R rows of tile w (R_Q) and am
+  // (R_O), which go to LDS once T^T is no longer read: R_O over smP, R_Q over
+  // smQ, each [tile][slab][lane][8], high words then low words.
+  bf16* Ro = reinterpret_cast<bf16*>(smP);
+  bf16* Rq = smQb;
   {
-    bf16* gR = (bf16*)p.RF + u * 4 * SQ;   // 16 row tiles x 4 slabs, hi then lo
+    f32x4 aq[8], ao[8];
     auto TT = [&](int t, int s) -> F1 {
       float x[8];
       row8f(smP + (16 * t + r16) * TP + 32 * s, q, x);
       return P::f1(x);
     };
-    auto store_rt = [&](int tile, int t, const f32x4& acc) {
-      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-      const int o = fofs(tile, t >> 1, l) + 4 * (t & 1);
-      SS::st4s(gR + o, gR + 2 * SQ + o, x);
-    };
-    F3 MB[4], KeB[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s <= (am >> 1)) MB[s] = SS::fa3(gM + fofs(am, s, l), gM + SQ + fofs(am, s, l));
-      KeB[s] = SS::fa3(gKe + fofs(w, s, l), gKe + SQ + fofs(w, s, l));
-    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      f32x4 aq = zero4(), ao = zero4();
+      aq[t] = zero4();
+      ao[t] = zero4();
 #pragma unroll
       for (int s = t >> 1; s < 4; ++s) {
         const F1 tt = TT(t, s);
-        P::m13(aq, tt, KeB[s]);
-        if (t <= am && s <= (am >> 1)) P::m13(ao, tt, MB[s]);
+        P::m13(aq[t], tt, ldf3(smQb, w, s, l));
+        if (t <= am && s <= (am >> 1)) P::m13(ao[t], tt, MB[s]);
       }
-      store_rt(8 + w, t, aq);
-      if (t <= am) store_rt(am, t, ao);
     }
-    if (!(am & 1)) store_rt(am, am + 1, zero4());   // tile am+1 of R_O row block am is zero
+    lds_barrier();
+    auto put = [&](bf16* base, int tile, int t, const f32x4& acc) {
+      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+      const int o = fofs(tile, t >> 1, l) + 4 * (t & 1);
+      SS::st4s(base + o, base + SQ + o, x);
+    };
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      put(Rq, w, t, aq[t]);
+      if (t <= am) put(Ro, am, t, ao[t]);
+    }
+    if (!(am & 1)) put(Ro, am, am + 1, zero4());   // tile am+1 of R_O row block am is zero
   }
-}
+  lds_barrier();
+  DN_STAMP(0, 11);
 
-// ===========================================================================
-// k_val: X, Pn, Oi, Q from R and [-be | wv].  One 4-wave workgroup per (unit,
-// group of 128 value columns); wave j forms (w v)^T for value tiles
-// 8g + 2j, 8g + 2j + 1 (identity transposes of v rows) and computes their
-// Oi^T and Q tiles.  The 16 be "halves" (X^T rows or Pn^T rows of one key
-// channel tile) are spread over all waves of the unit.
-//   Oi^T(vt, it) = sum_s wv^T(vt, s) R_O(it, s)        split x split
-//   Q(rt, vt)    = sum_s R_Q(rt, s) wv(s, vt)          split x split
-//   X^T(t, it)   = qe^T(t, it) - sum_s be^T(t, s) R_O(it, s)   bf16
-//   Pn^T(t, rt)  = -sum_s be^T(t, s) R_Q(rt, s)               bf16
-// ===========================================================================
-template <class TV>
-__global__ __launch_bounds__(256) void k_val(const PF p) {
-  const int tid = threadIdx.x;
-  const int j = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int nwg = p.nct >> 3;
-  const int tot = p.B * p.Hx * p.NCb * nwg;
-  int id = blockIdx.x;
-  if ((tot & 7) == 0) id = (id & 7) * (tot >> 3) + (id >> 3);
-  const int g = id % nwg;
-  const int64_t u = id / nwg;
-  const int c = (int)(u % p.NCb);
-  const int h = (int)((u / p.NCb) % p.Hx);
-  const int b = (int)(u / ((int64_t)p.NCb * p.Hx));
-  const int tb = p.t0 + c * CH;
-  const int t_end = min(p.t0 + p.nt, p.L);
-  const bf16* Rh = (const bf16*)p.RF + u * 4 * SQ;
-  const bf16* Rl = Rh + 2 * SQ;
-  auto Rf3 = [&](int tile, int s) { const int o = fofs(tile, s, l); return SS::fa3(Rh + o, Rl + o); };
-
-  // ---- (w v)^T fragments of value tiles vt0, vt0 + 1 ----
-  const int vt0 = 8 * g + 2 * j;
-  const int hv = p.gates_at_hv ? h : h * p.G + (16 * vt0) / KD;
-  const int col0 = (16 * vt0) % KD;
-  const int hw = vgate_head(p, p.w_h, hv);
-  F3 Wv[2][4];
+  // ---- phase 9: value products --------------------------------------------
+  //   X^T(t, it) = qe^T(t, it) - sum_s be^T(t, s) R_O(it, s)   bf16
+  //   Pn^T(t, rt) = -sum_s be^T(t, s) R_Q(rt, s)               bf16
+  //   Oi^T(vt, it) = sum_s wv^T(vt, s) R_O(it, s)              split x split
+  //   Q(rt, vt)    = sum_s R_Q(rt, s) wv(s, vt)                split x split
+  // Wave w: key-channel tile w of be, value tiles [w nvw, (w+1) nvw)
+  // (nvw = value tiles / 8), (w v)^T by identity transposes of v rows.
   {
-    float vv[8][8], ww[8][8];
+    auto Rf3 = [&](const bf16* base, int tile, int s) {
+      const int o = fofs(tile, s, l);
+      return SS::fa3(base + o, base + SQ + o);
+    };
+    const int nvw = p.nct >> 3;
+    {
+      const bf16* Be = (const bf16*)p.BeF + u * SQ;
+      F1 be[4];
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const int t = tb + 16 * a + r16;
-      const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
-      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0, q, vv[a]);
-      if (p.w_c == 1) {
-        const float ws = ((const float*)p.w)[bt * p.w_h + hw];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ww[a][e] = ws;
-      } else {
-        row8<float>((const float*)p.w + (bt * p.w_h + hw) * p.w_c + col0, q, ww[a]);
-      }
-    }
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const bool ok = tb + 16 * a + r16 < t_end;
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float wg = p.fuse ? sigmoid_fast(ww[a][e]) : ww[a][e];
-        x[e] = ok ? wg * vv[a][e] : 0.f;
-      }
-      const F3 fx = P::f3(x);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const f32x4 ch = tr_half(fx.hi, hf, r16, q);
-        const f32x4 cl = tr_half(fx.lo, hf, r16, q);
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          Wv[hf][a >> 1].hi.v[4 * (a & 1) + ii] = (bf16)ch[ii];
-          Wv[hf][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)cl[ii];
-        }
-      }
-    }
-  }
-  float* gOi = p.OiC + u * (int64_t)(CH * p.Vp);
-  float* gQ = p.QCw + u * (int64_t)(KD * p.Vp);
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    f32x4 a0 = zero4(), a1 = zero4();
-#pragma unroll
-    for (int s = 0; s <= (it >> 1); ++s) {
-      const F3 r = Rf3(it, s);
-      P::m33(a0, Wv[0][s], r);
-      P::m33(a1, Wv[1][s], r);
-    }
-    *reinterpret_cast<f32x4*>(gOi + cofs(vt0, it, 8, l)) = a0;
-    *reinterpret_cast<f32x4*>(gOi + cofs(vt0 + 1, it, 8, l)) = a1;
-  }
-#pragma unroll
-  for (int rt = 0; rt < 8; ++rt) {
-    f32x4 a0 = zero4(), a1 = zero4();
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const F3 r = Rf3(8 + rt, s);
-      P::m33(a0, r, Wv[0][s]);
-      P::m33(a1, r, Wv[1][s]);
-    }
-    *reinterpret_cast<f32x4*>(gQ + cofs(rt, vt0, p.nct, l)) = a0;
-    *reinterpret_cast<f32x4*>(gQ + cofs(rt, vt0 + 1, p.nct, l)) = a1;
-  }
-
-  // ---- be halves ----
-  const bf16* Be = (const bf16*)p.BeF + u * SQ;
-  const float* Qe = p.QeC + u * SQ;
-  bf16* Xh = (bf16*)p.XF + u * 2 * SQ;
-  bf16* Xl = Xh + SQ;
-  bf16* Pn = (bf16*)p.PnF + u * SQ;
-  const int nw = 4 * nwg;
-  for (int hh = 4 * g + j; hh < 16; hh += nw) {
-    const int t = hh >> 1;
-    F1 be[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) be[s] = SS::fa(Be + fofs(t, s, l));
-    if (!(hh & 1)) {
+      for (int s = 0; s < 4; ++s) be[s] = SS::fa(Be + fofs(w, s, l));
+      const float* Qe = p.QeC + u * SQ;
+      bf16* Xh = (bf16*)p.XF + u * 2 * SQ;
+      bf16* Xl = Xh + SQ;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int s = 0; s <= (it >> 1); ++s) P::m11(acc, be[s], SS::fa(Rh + fofs(it, s, l)));
-        const f32x4 qe = *reinterpret_cast<const f32x4*>(Qe + cofs(t, it, 8, l));
+        for (int s = 0; s <= (it >> 1); ++s) P::m11(acc, be[s], SS::fa(Ro + fofs(it, s, l)));
+        const f32x4 qe = *reinterpret_cast<const f32x4*>(Qe + cofs(w, it, 8, l));
         const float x[4] = {qe[0] - acc[0], qe[1] - acc[1], qe[2] - acc[2], qe[3] - acc[3]};
-        const int o = fofs(it, t >> 1, l) + 4 * (t & 1);
+        const int o = fofs(it, w >> 1, l) + 4 * (w & 1);
         SS::st4s(Xh + o, Xl + o, x);
       }
-    } else {
+      bf16* Pn = (bf16*)p.PnF + u * SQ;
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) P::m11(acc, be[s], SS::fa(Rh + fofs(8 + rt, s, l)));
+        for (int s = 0; s < 4; ++s) P::m11(acc, be[s], SS::fa(Rq + fofs(rt, s, l)));
         const float x[4] = {-acc[0], -acc[1], -acc[2], -acc[3]};
-        SS::st4(Pn + fofs(rt, t >> 1, l) + 4 * (t & 1), x);
+        SS::st4(Pn + fofs(rt, w >> 1, l) + 4 * (w & 1), x);
+      }
+    }
+    float* gOi = p.OiC + u * (int64_t)(CH * p.Vp);
+    float* gQ = p.QCw + u * (int64_t)(KD * p.Vp);
+    int vstep = 1;
+#pragma unroll 1
+    for (int vp = 0; vp < nvw; vp += vstep) {
+      const int vt0 = w * nvw + vp;
+      const bool two = vp + 1 < nvw && !(vt0 & 1);   // vt0, vt0 + 1 share one 32-column slab
+      vstep = two ? 2 : 1;
+      const int hv = p.gates_at_hv ? h : h * p.G + (16 * vt0) / KD;
+      const int col0 = (16 * vt0) & ~31 & (KD - 1);   // 32-column slab holding vt0
+      const int half0 = vt0 & 1;                       // vt0's half of that slab
+      const int hw = vgate_head(p, p.w_h, hv);
+      // an offset the compiler cannot prove zero keeps the R fragment reads
+      // inside the loop (hoisted, all 52 would not fit in registers)
+      const int zo = __builtin_amdgcn_readfirstlane(vp) & 0x40000000;
+      const bf16* RoL = Ro + zo;
+      const bf16* RqL = Rq + zo;
+      F3 Wv[2][4];
+      {
+        // v and w rows of the 8 token tiles, loaded raw (converted at use)
+        Raw8<TV> rv[8];
+        Raw8<float> rwv[8];
+        float wsc[8];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+          const int t = tb + 16 * a + r16;
+          const int64_t bt = (int64_t)b * p.L + min(t, t_end - 1);
+          rv[a].load((const TV*)p.v + (bt * p.Hv + hv) * KD + col0, q);
+          if (p.w_c == 1) {
+            wsc[a] = ((const float*)p.w)[bt * p.w_h + hw];
+          } else {
+            rwv[a].load((const float*)p.w + (bt * p.w_h + hw) * p.w_c + col0, q);
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+          const bool ok = tb + 16 * a + r16 < t_end;
+          float vv[8], ww[8];
+          rv[a].to(vv);
+          if (p.w_c == 1) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ww[e] = wsc[a];
+          } else {
+            rwv[a].to(ww);
+          }
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float wg = p.fuse ? sigmoid_fast(ww[e]) : ww[e];
+            x[e] = ok ? wg * vv[e] : 0.f;
+          }
+          const F3 fx = P::f3(x);
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            // Wv[0] = vt0 (half half0 of the slab), Wv[1] = vt0 + 1 (the other half)
+            if (hf == 1 && !two) break;
+            const int hsel = two ? hf : half0;
+            const f32x4 ch = tr_half(fx.hi, hsel, r16, q);
+            const f32x4 cl = tr_half(fx.lo, hsel, r16, q);
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              Wv[hf][a >> 1].hi.v[4 * (a & 1) + ii] = (bf16)ch[ii];
+              Wv[hf][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)cl[ii];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        f32x4 a0 = zero4(), a1 = zero4();
+#pragma unroll
+        for (int s = 0; s <= (it >> 1); ++s) {
+          const F3 r = Rf3(RoL, it, s);
+          P::m33(a0, Wv[0][s], r);
+          if (two) P::m33(a1, Wv[1][s], r);
+        }
+        *reinterpret_cast<f32x4*>(gOi + cofs(vt0, it, 8, l)) = a0;
+        if (two) *reinterpret_cast<f32x4*>(gOi + cofs(vt0 + 1, it, 8, l)) = a1;
+      }
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        f32x4 a0 = zero4(), a1 = zero4();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const F3 r = Rf3(RqL, rt, s);
+          P::m33(a0, r, Wv[0][s]);
+          if (two) P::m33(a1, r, Wv[1][s]);
+        }
+        *reinterpret_cast<f32x4*>(gQ + cofs(rt, vt0, p.nct, l)) = a0;
+        if (two) *reinterpret_cast<f32x4*>(gQ + cofs(rt, vt0 + 1, p.nct, l)) = a1;
       }
     }
   }
+  DN_STAMP(0, 15);
+  DN_RSTAMP(0, 17);
 }
 
 // ===========================================================================
@@ -1019,11 +1092,11 @@ __global__ __launch_bounds__(256) void k_val(const PF p) {
 // chunks of one token block.  One 4-wave workgroup per (16 state columns,
 // exec head, batch); wave w holds state rows 32w .. 32w+31 in fp32 VGPRs.
 // Each chunk: the entering state S_c is stored (split) for k_out, its slab is
-// exchanged through LDS, and Pn S (bf16 x split) + Q + D S forms S_{c+1}.
-// Operands are prefetched two chunks ahead.
+// exchanged through LDS (high words), and Pn S (bf16) + Q + D S forms S_{c+1}.
+// Operands are prefetched three chunks ahead.
 // ===========================================================================
 __global__ __launch_bounds__(256) void k_scan(const PF p) {
-  __shared__ __align__(16) bf16 Sx[2][2][4 * 64 * 8];   // [buffer][hi, lo][slab][lane][8]
+  __shared__ __align__(16) bf16 Sx[2][4 * 64 * 8];   // [buffer][slab][lane][8] high words
   __shared__ int flg[2 * 1024];
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1064,28 +1137,34 @@ __global__ __launch_bounds__(256) void k_scan(const PF p) {
     if (is_new) { S[0] = zero4(); S[1] = zero4(); }
     const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
     const int fo = (w * 64 + l) * 8;
-    bf16* bh = &Sx[cc & 1][0][0];
-    bf16* bl = &Sx[cc & 1][1][0];
-    SS::st8s(bh + fo, bl + fo, x);
+    bf16* bh = &Sx[cc & 1][0];
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hi[e] = (bf16)x[e];
+      lo[e] = (bf16)(x[e] - (float)hi[e]);
+    }
+    *reinterpret_cast<bf16x8*>(bh + fo) = hi;
     {
       bf16* gS = (bf16*)p.SF + (ubase + cc) * 2 * sfstride;
       const int o = fofs(ct, w, l);
-      SS::st8s(gS + o, gS + sfstride + o, x);
+      *reinterpret_cast<bf16x8*>(gS + o) = hi;
+      *reinterpret_cast<bf16x8*>(gS + sfstride + o) = lo;
     }
     lds_barrier();
-    F3 Sf[4];
+    F1 Sf[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) Sf[s] = SS::fa3(bh + (s * 64 + l) * 8, bl + (s * 64 + l) * 8);
+    for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(bh + (s * 64 + l) * 8);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       f32x4 acc = o.qc[r];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) P::m13(acc, o.pn[r][s], Sf[s]);
+      for (int s = 0; s < 4; ++s) P::m11(acc, o.pn[r][s], Sf[s]);
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][ii] : 0.f);
     }
   };
-  constexpr int RS = 3;
+  constexpr int RS = 4;
   Ops o[RS];
 #pragma unroll
   for (int jj = 0; jj + 1 < RS; ++jj) load_ops(jj, o[jj]);
@@ -1110,54 +1189,64 @@ __global__ __launch_bounds__(256) void k_scan(const PF p) {
 
 // ===========================================================================
 // k_out: O^T(vt, it) = Oi^T(vt, it) + sum_s S_c^T(vt, s) X^T(s, it), chunk
-// parallel.  One 4-wave workgroup per (unit, 64 value columns); the unit's X
-// (split, 64 KB) is staged in LDS once; wave j owns value tile 4g + j.
-// Lane (i, q) holds O[token 16it + i][column 16vt + 4q + ii].
+// parallel.  One 8-wave workgroup per unit: the unit's X (split, 64 KB) is
+// staged in LDS once, and wave w owns value tiles [w nvw, (w+1) nvw) with
+// their S_c^T fragments in registers.  Every global load is issued before the
+// first product.  Lane (i, q) holds O[token 16it + i][column 16vt + 4q + ii].
 // ===========================================================================
 template <class TO>
-__global__ __launch_bounds__(256) void k_out(const PF p) {
+__global__ __launch_bounds__(512) void k_out(const PF p) {
   __shared__ __align__(16) bf16 Xs[2 * SQ];
   const int tid = threadIdx.x;
-  const int j = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, r16 = l & 15, q = l >> 4;
-  const int nwg = p.nct >> 2;
-  const int tot = p.B * p.Hx * p.NCb * nwg;
+  const int tot = p.B * p.Hx * p.NCb;
   int id = blockIdx.x;
   if ((tot & 7) == 0) id = (id & 7) * (tot >> 3) + (id >> 3);
-  const int g = id % nwg;
-  const int64_t u = id / nwg;
+  const int64_t u = id;
   const int c = (int)(u % p.NCb);
   const int h = (int)((u / p.NCb) % p.Hx);
   const int b = (int)(u / ((int64_t)p.NCb * p.Hx));
   const int tb = p.t0 + c * CH;
   const int t_end = min(p.t0 + p.nt, p.L);
-  const int vt = 4 * g + j;
-  const int hv = p.gates_at_hv ? h : h * p.G + (16 * vt) / KD;
-  const int vc = (16 * vt) % KD;
+  const int nvw = p.nct >> 3;
   const int64_t sfstride = (int64_t)KD * p.Vp;
-  const bf16* gS = (const bf16*)p.SF + u * 2 * sfstride;
-  F3 Sf[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) Sf[s] = SS::fa3(gS + fofs(vt, s, l), gS + sfstride + fofs(vt, s, l));
   {
     const uint4* src = reinterpret_cast<const uint4*>((const bf16*)p.XF + u * 2 * SQ);
     uint4* dst = reinterpret_cast<uint4*>(Xs);
+    uint4 t[8];
 #pragma unroll
-    for (int k = 0; k < (2 * SQ * 2) / (16 * 256); ++k) dst[k * 256 + tid] = src[k * 256 + tid];
+    for (int k = 0; k < 8; ++k) t[k] = src[k * 512 + tid];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[k * 512 + tid] = t[k];
   }
-  __syncthreads();
+  const bf16* gS = (const bf16*)p.SF + u * 2 * sfstride;
   const float* gOi = p.OiC + u * (int64_t)(CH * p.Vp);
+#pragma unroll 1
+  for (int vi = 0; vi < nvw; ++vi) {
+    const int vt = w * nvw + vi;
+    F3 sf[4];
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    f32x4 acc = *reinterpret_cast<const f32x4*>(gOi + cofs(vt, it, 8, l));
+    for (int s = 0; s < 4; ++s) sf[s] = SS::fa3(gS + fofs(vt, s, l), gS + sfstride + fofs(vt, s, l));
+    f32x4 acc[8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) P::m33(acc, Sf[s], ldf3(Xs, it, s, l));
-    const int t = tb + 16 * it + r16;
-    const bool tv = t < t_end;
-    const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hv) * KD + vc + 4 * q;
-    TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
-    const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-    st4<TO>(dst, x);
+    for (int it = 0; it < 8; ++it) acc[it] = *reinterpret_cast<const f32x4*>(gOi + cofs(vt, it, 8, l));
+    if (vi == 0) __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int it = 0; it < 8; ++it) P::m33(acc[it], sf[s], ldf3(Xs, it, s, l));
+    const int hv = p.gates_at_hv ? h : h * p.G + (16 * vt) / KD;
+    const int vc = (16 * vt) % KD;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int t = tb + 16 * it + r16;
+      const bool tv = t < t_end;
+      const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hv) * KD + vc + 4 * q;
+      TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
+      const float x[4] = {acc[it][0], acc[it][1], acc[it][2], acc[it][3]};
+      st4<TO>(dst, x);
+    }
   }
 }
 
@@ -1168,25 +1257,27 @@ template <class TIn, class TV>
 hipError_t launch_t(const PF& p, hipStream_t st) {
   const int units = p.B * p.Hx * p.NCb;
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_wy<TIn>), dim3(units), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((k_wy<TIn, TV>), dim3(units), dim3(512), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  prof_mark(1, st, false);
-  hipLaunchKernelGGL((k_val<TV>), dim3(units * (p.nct >> 3)), dim3(256), 0, st, p);
-  prof_mark(1, st, true);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
   prof_mark(2, st, false);
   hipLaunchKernelGGL(k_scan, dim3(p.nct, p.Hx, p.B), dim3(256), 0, st, p);
   prof_mark(2, st, true);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   prof_mark(5, st, false);
-  hipLaunchKernelGGL((k_out<TV>), dim3(units * (p.nct >> 2)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((k_out<TV>), dim3(units), dim3(512), 0, st, p);
   prof_mark(5, st, true);
   return hipGetLastError();
 }
 
 }  // namespace wy
+
+#ifdef DN_STAMPS
+extern "C" int dn_debug_stamps(unsigned long long* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(wy::dn_stamp_buf), sizeof(wy::dn_stamp_buf)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 hipError_t launch_wy(const PF& p, hipStream_t st, int qk_dt, bool v_bf16) {
   if (qk_dt == DN_BF16) return v_bf16 ? wy::launch_t<bf16, bf16>(p, st) : wy::launch_t<bf16, float>(p, st);
