@@ -44,15 +44,6 @@ struct PF {
   void *MAh, *MAl;           // F  [8][4]      ST : M, rows = token
   float* QeA;                // F  [8][4]      f32: q e^Lambda, first document
   void* sink;                // 1 KB the chain's output lanes past the last token store into
-  // Workspace of the chunk-parallel bf16 path (dn_wy.hip), per unit:
-  void* BeF;                 // F [8][4]  bf16: be^T (rows = key channel, k = token)
-  float* QeC;                // C [8][8]  f32 : qe in the accumulator layout of X^T
-  void* MF;                  // F [8][4]  bf16 hi, lo: M rows (row = token)
-  void* PnF;                 // F [8][4]  bf16: Pn rows (row = state row)
-  float* QCw;                // C [8][nct] f32: Q tiles in the scan's state layout
-  void* XF;                  // F [8][4]  bf16 hi, lo: X rows (row = token)
-  float* OiC;                // C [nct][8] f32: (Oi)^T tiles, rows = value column
-  void* SF;                  // F [nct][4] bf16 hi, lo: entering state S_c^T (row = value column)
 };
 
 // Records the message for dn_last_error() and returns `code`.
@@ -63,8 +54,5 @@ int set_error(int code, const char* msg);
 // (call it once before and once after each launch).
 bool profiling();
 void prof_mark(int kind, hipStream_t st, bool after);
-
-// The chunk-parallel prefill of one token block (precision "bf16", dn_wy.hip).
-hipError_t launch_wy(const PF& p, hipStream_t st, int qk_dt, bool v_bf16);
 
 }  // namespace dn

@@ -1321,8 +1321,6 @@ namespace {
 
 struct WsLayout {
   size_t flags, dvec, PnA, QC, XAh, XAl, OiT, BeB, KeBh, KeBl, MAh, MAl, QeA, sink, carry, total;
-  // precision "bf16" (dn_wy.hip)
-  size_t BeF, QeC, PnF, QCw, XF, OiC, SF;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1338,20 +1336,6 @@ WsLayout ws_layout(const dn_prefill_args* a, int Hx, int Vp, int NCb, bool bf) {
   auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
   L.flags = take((size_t)a->B * NCb * 2 * 4);
   L.dvec = take(units * KD * 4);
-  if (bf) {
-    // chunk-parallel path: M rows (k_wy only) share the X array (k_val on)
-    L.BeF = take(units * sq * 2);
-    L.QeC = take(units * sq * 4);
-    L.PnF = take(units * sq * 2);
-    L.QCw = take(units * KD * Vp * 4);
-    L.XF = take(units * sq * 4);
-    L.OiC = take(units * CH * Vp * 4);
-    L.SF = take(units * KD * Vp * 4);
-    L.sink = take(64 * 16);
-    L.carry = take((size_t)a->B * a->Hv * KD * KD * 4);
-    L.total = off;
-    return L;
-  }
   L.PnA = take(units * sq * es);
   L.QC = take(units * KD * Vp * 4);
   L.XAh = take(units * sq * es);
@@ -1447,7 +1431,7 @@ hipError_t dispatch_qk(const PF& p, hipStream_t st, int qk_dt, bool v_bf16) {
 }
 
 hipError_t dispatch(const PF& p, hipStream_t st, bool bf, int qk_dt, bool v_bf16) {
-  return bf ? launch_wy(p, st, qk_dt, v_bf16) : dispatch_qk<false>(p, st, qk_dt, v_bf16);
+  return bf ? dispatch_qk<true>(p, st, qk_dt, v_bf16) : dispatch_qk<false>(p, st, qk_dt, v_bf16);
 }
 
 }  // namespace
@@ -1489,16 +1473,6 @@ int prefill_run(const dn_prefill_args* a, char* ws, size_t workspace_bytes, int 
   p.flags = (int32_t*)(ws + Lw.flags);
   p.dvec = (float*)(ws + Lw.dvec);
   p.nct = Vp / 16;
-  if (bf) {
-    p.BeF = ws + Lw.BeF;
-    p.QeC = (float*)(ws + Lw.QeC);
-    p.PnF = ws + Lw.PnF;
-    p.QCw = (float*)(ws + Lw.QCw);
-    p.XF = ws + Lw.XF;
-    p.MF = ws + Lw.XF;
-    p.OiC = (float*)(ws + Lw.OiC);
-    p.SF = ws + Lw.SF;
-  }
   p.PnA = ws + Lw.PnA;
   p.QC = (float*)(ws + Lw.QC);
   p.XAh = ws + Lw.XAh;

@@ -11,7 +11,7 @@ PKG_ROOT = os.path.dirname(HERE)                      # deltanet-tpu_amd/
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 INCLUDE = os.path.join(REPO_ROOT, "include")
-SOURCES = ("dn_prefill.hip", "dn_wy.hip", "dn_decode.hip", "dn_backward.hip")
+SOURCES = ("dn_prefill.hip", "dn_decode.hip", "dn_backward.hip")
 OUT = os.path.join(HERE, "libdeltanet_amd.so")
 
 

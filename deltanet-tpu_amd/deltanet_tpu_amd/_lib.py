@@ -99,7 +99,7 @@ EXPORTED_SYMBOLS = (
     "dn_profile_begin",
     "dn_profile_end",
 )
-PROFILE_KINDS = ("prepass", "value", "chain", "decode", "backward", "output")
+PROFILE_KINDS = ("prepass", "value", "chain", "decode", "backward")
 
 _lock = threading.Lock()
 _lib = None

@@ -233,14 +233,13 @@ int dn_state_frob_cap(float* state, int64_t nmat, int32_t rows, int32_t cols, fl
 /* Kernel timing instrumentation (no counterpart in the reference; for
  * benchmarks and profilers).  Between dn_profile_begin() and dn_profile_end()
  * every dn_prefill_fwd call (from any thread of the process) records HIP events on its
- * stream around each of its kernels (precision "bf16": chunk operators, value
- * products, recurrence, output; "fp32": prepass as kind 0, chain as kind 2) and every
+ * stream around each of its kernels (prepass, chain; kind 1 is no longer
+ * recorded: the value products run inside the prepass) and every
  * dn_decode_step / dn_decode_steps call around its kernel, and every
  * dn_prefill_bwd call around its four kernels together.  dn_profile_end() waits for those
  * events and writes, per kernel kind, the summed duration in milliseconds
  * and the number of launches (arrays of DN_PROFILE_KINDS entries). */
-#define DN_PROFILE_KINDS 6   /* 0 chunk operators, 1 value products, 2 recurrence,
-                                3 decode, 4 backward, 5 output (precision "bf16") */
+#define DN_PROFILE_KINDS 5   /* 0 prepass, 1 (unused), 2 chain, 3 decode, 4 backward */
 int dn_profile_begin(void);
 int dn_profile_end(double* ms_sum, int64_t* launches);
 
