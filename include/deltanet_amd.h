@@ -183,9 +183,11 @@ typedef struct dn_backward_args {
 
 /* Workspace bytes dn_prefill_bwd needs (0 if the arguments are invalid):
  * about 545 KB per (batch, head, 64-token chunk); with recompute_states, 545 KB
- * per (batch, head, chunk of one token block) plus 64 KB per (batch, head,
- * interior block boundary).  The block is the smallest whole number of chunks
- * giving at least 1024 (batch, head, chunk) units per launch. */
+ * per (batch, head, chunk of one token block) plus 64 KB per (batch, head) for
+ * each token block when there is more than one: the states entering the
+ * interior blocks, and the state gradient carried from one block to the one
+ * before it.  The block is the smallest whole number of chunks giving at least
+ * 1024 (batch, head, chunk) units per launch. */
 size_t dn_prefill_bwd_workspace_size(const dn_backward_args* a);
 
 /* Backward of the chunked recurrence: replaces the reference's custom-VJP

@@ -361,9 +361,12 @@ def test_backward_fuse_prologue_with_guard(saturate, tol):
     assert np.abs(got["dg"][(g > -3) & (g < 0)]).max() > 0
 
 
-@pytest.mark.parametrize("with_init, shape", [(False, (2, 3000, 16, 32)), (True, (2, 3000, 16, 32)),
-                                               (True, (1, 3000, 11, 33))])
-def test_backward_recompute_states_bit_identical(with_init, shape):
+@pytest.mark.parametrize("with_init, shape, precision, fuse", [
+    (False, (2, 3000, 16, 32), "bf16", False), (True, (2, 3000, 16, 32), "bf16", False),
+    (True, (1, 3000, 11, 33), "bf16", False),
+    # the fp32 chain kernels (fp32 LDS state) and the fused prologue, in blocks
+    (True, (2, 3000, 16, 32), "fp32", False), (False, (2, 3000, 16, 32), "bf16", True)])
+def test_backward_recompute_states_bit_identical(with_init, shape, precision, fuse):
     """recompute_states=True (token blocks, only block-boundary states kept,
     chunk states recomputed per block: reference gdn2.py:655-695, 1614-1630)
     gives gradients bit-identical to the single-pass backward.  B * Hv = 64
@@ -378,8 +381,11 @@ def test_backward_recompute_states_bit_identical(with_init, shape):
     rng = np.random.default_rng(77)
     f = lambda *s: rng.standard_normal(s).astype(np.float32)
     q, k, v = f(B, L, Hk, 128), f(B, L, Hk, 128), f(B, L, Hv, 128)
-    g = -np.exp(0.39 * f(B, L, Hk, 128) - 1.0)
-    b, w = sig(0.39 * f(B, L, Hk, 128)), sig(0.39 * f(B, L, Hv, 128))
+    if fuse:   # raw pre-activation gates; w channel-wise at the value heads
+        g, b, w = f(B, L, Hk, 128), f(B, L, Hk, 128), f(B, L, Hv, 128)
+    else:
+        g = -np.exp(0.39 * f(B, L, Hk, 128) - 1.0)
+        b, w = sig(0.39 * f(B, L, Hk, 128)), sig(0.39 * f(B, L, Hv, 128))
     seg = np.zeros((B, L), np.int32)
     seg[0, 1000:] = 1
     seg[0, 1024:] = 2        # a document starting exactly at the first block edge
@@ -393,8 +399,8 @@ def test_backward_recompute_states_bit_identical(with_init, shape):
               for i, x in enumerate((q, k, v, g, b, w))]
         ti = to_dev(init).requires_grad_(True) if with_init else None
         out, fin = chunk_gdn2(*ts, initial_state=ti, output_final_state=True, is_inference=False,
-                              segment_ids=torch.from_numpy(seg).cuda(), qk_l2norm=True, precision="bf16",
-                              recompute_states=rc)
+                              segment_ids=torch.from_numpy(seg).cuda(), qk_l2norm=True, precision=precision,
+                              fuse_prologue=fuse, recompute_states=rc)
         ((out.float() * to_dev(do)).sum() + (fin * to_dev(df)).sum()).backward()
         torch.cuda.synchronize()
         res[rc] = {n: as_np(t.grad) for n, t in zip(NAMES, ts)}

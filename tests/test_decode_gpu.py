@@ -283,3 +283,70 @@ def test_decode_steps_in_place_and_single_token():
     o2, s2 = gdn2_decode_steps(*args, st, qk_l2norm=True, out_state=st)
     assert s2.data_ptr() == st.data_ptr()
     assert torch.equal(o1, o2[:, 0]) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("B,Hk,Hv", [(3, 1, 1), (1, 1, 3), (5, 1, 3)])
+def test_decode_odd_matrix_count(state_dtype, B, Hk, Hv):
+    # an odd number of (batch, value head) state matrices: the last workgroup
+    # of the two-matrices-per-workgroup fp32 kernel has an idle second half;
+    # every matrix (the last one included) must match the oracle, and the
+    # in-place call (out_state = state) must give the same bits
+    q, k, v, g, b, w = dec_inputs(90 + B * Hv, B, Hk, Hv)
+    S = 0.1 * np.random.default_rng(91).standard_normal((B, Hv, 128, 128))
+    reset = np.zeros(B, bool)
+    reset[-1] = B > 1
+    T = lambda x: to_dev(x)
+    sdt = torch.float32 if state_dtype == "float32" else torch.bfloat16
+    S_in = to_dev(S, sdt)
+    S_ref = as_np(S_in)   # the oracle starts from the stored (possibly bf16) state
+    kw = dict(reset=torch.tensor(reset), qk_l2norm=True, state_dtype=state_dtype)
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), S_in, **kw)
+    ro, rs = O.decode_step(q, k, v, g, b, w, S_ref, reset=reset, qk_l2norm=True)
+    if state_dtype == "float32":
+        check(o.reshape(B, Hv, 128), ro, s, rs, "fp32", "fp32", f"odd decode B={B} Hv={Hv}")
+    else:
+        assert rel_l2(as_np(o).reshape(B, Hv, 128), ro) < 1e-2
+        assert rel_l2(as_np(s), rs) < 1e-2
+        # every matrix, the last one included, is written
+        for i in range(B):
+            assert rel_l2(as_np(s)[i], rs[i]) < 1e-2
+    st = S_in.clone()
+    o2, s2 = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), st, out_state=st, **kw)
+    assert s2.data_ptr() == st.data_ptr()
+    assert torch.equal(o, o2) and torch.equal(s, s2)
+
+
+@pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("B,Hk,Hv", [(3, 1, 1), (1, 1, 3)])
+def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv):
+    # T tokens in one launch with an odd number of state matrices: equal to
+    # T chained single steps up to the summation order (the two kernels split
+    # the state rows differently over lanes), and the fp32 run to the oracle
+    Tn = 4
+    q, k, v, g, b, w = steps_inputs(92 + B, B, Tn, Hk, Hv)
+    S0 = 0.3 * np.random.default_rng(93).standard_normal((B, Hv, 128, 128))
+    reset = np.zeros((B, Tn), bool)
+    reset[-1, 2] = True
+    sdt = torch.float32 if state_dtype == "float32" else torch.bfloat16
+    args = [to_dev(x) for x in (q, k, v, g, b, w)]
+    kw = dict(qk_l2norm=True, state_dtype=state_dtype)
+    o_m, s_m = gdn2_decode_steps(*args, to_dev(S0, sdt), reset=torch.tensor(reset), **kw)
+    st = to_dev(S0, sdt)
+    outs = []
+    for t in range(Tn):
+        o1, st = gdn2_decode_step(*[x[:, t] for x in args], st, reset=torch.tensor(reset[:, t]), **kw)
+        outs.append(o1)
+    ro, rs = rel_l2(as_np(o_m), as_np(torch.stack(outs, 1))), rel_l2(as_np(s_m), as_np(st))
+    print(f"odd multi vs chained: out {ro:.2e} state {rs:.2e}")
+    assert ro < (2e-4 if state_dtype == "bfloat16" else 1e-6)
+    assert rs < (2e-4 if state_dtype == "bfloat16" else 1e-6)
+    # every matrix, the last one included, carries its own state
+    for i in range(B):
+        assert rel_l2(as_np(s_m)[i], as_np(st)[i]) < (2e-4 if state_dtype == "bfloat16" else 1e-6)
+    if state_dtype == "float32":
+        ref_s = S0
+        for t in range(Tn):
+            o1, ref_s = O.decode_step(q[:, t], k[:, t], v[:, t], g[:, t], b[:, t], w[:, t], ref_s,
+                                      reset=reset[:, t], qk_l2norm=True)
+        check(o_m[:, -1].reshape(B, Hv, 128), o1, s_m, ref_s, "fp32", "fp32", f"odd decode_steps B={B} Hv={Hv}")
