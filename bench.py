@@ -657,13 +657,19 @@ def main():
     # ---- decode (config 4) ------------------------------------------------
     dq, dk, dv, dg, db, dw, st = decode_inputs(torch, dev)
     dec = {}
-    for sd, elt in (("float32", 4), ("bfloat16", 2)) if args.decode_steps > 0 else ():
+    # every state dtype with and without a reset vector (a device bool tensor,
+    # all False, as a serving loop passes it: read in place by the kernel)
+    no_reset = torch.zeros(dq.shape[0], dtype=torch.bool, device=dev)
+    cases = [(sd, elt, rs) for sd, elt in (("float32", 4), ("bfloat16", 2)) for rs in (None, no_reset)]
+    for sd, elt, rs in cases if args.decode_steps > 0 else ():
         s_in = st if sd == "float32" else st.to(torch.bfloat16)
         s_out = torch.empty_like(s_in)
         n = args.decode_steps
+        tag = sd if rs is None else sd + "_reset"
 
         def dstep(a, bb):
-            return gdn2_decode_step(dq, dk, dv, dg, db, dw, a, qk_l2norm=True, state_dtype=sd, out_state=bb)
+            return gdn2_decode_step(dq, dk, dv, dg, db, dw, a, qk_l2norm=True, state_dtype=sd, out_state=bb,
+                                    reset=rs)
 
         pair = [s_in, s_out]
 
@@ -682,10 +688,10 @@ def main():
             dprof = _lib.profile_end()
             kus = dprof["decode"][0] * 1e3 / max(dprof["decode"][1], 1)
         sbytes = 2 * st.numel() * elt
-        dec[sd] = {"us_per_step": round(us, 2), "kernel_us": round(kus, 2),
-                   "state_GBps": round(sbytes / (kus * 1e-6) / 1e9, 1),
-                   "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
-        log(f"decode {sd}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[sd]['state_GBps']} GB/s)")
+        dec[tag] = {"us_per_step": round(us, 2), "kernel_us": round(kus, 2),
+                    "state_GBps": round(sbytes / (kus * 1e-6) / 1e9, 1),
+                    "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"decode {tag}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[tag]['state_GBps']} GB/s)")
 
     # ---- training step (forward + backward) at the config-2 shape ----------
     train = None

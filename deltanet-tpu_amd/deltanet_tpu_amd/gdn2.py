@@ -495,10 +495,14 @@ def gdn2_decode_step(
         r = r.reshape(-1) if r.ndim > 0 else r.reshape(1)
         if r.numel() != 1 and r.numel() != B:
             raise ValueError(f"reset batch dimension ({r.shape[0]}) must match input batch dimension ({B}).")
-        reset_t = torch.broadcast_to(r.to(torch.bool), (B,)).to(torch.uint8)
+        if r.numel() == B and r.dtype in (torch.bool, torch.uint8) and r.is_cuda and r.is_contiguous():
+            # one byte per row, nonzero = reset: read in place (no conversion copy per step)
+            reset_t = r
+        else:
+            reset_t = torch.broadcast_to(r.to(torch.bool), (B,)).to(torch.uint8)
 
     dev = _require_gpu(q, k, v, g, b, w, state)
-    if reset_t is not None:
+    if reset_t is not None and (reset_t.device != dev or not reset_t.is_contiguous()):
         reset_t = reset_t.to(dev).contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(K)
@@ -602,7 +606,11 @@ def gdn2_decode_steps(
             dim = "K" if name != "w" else "V"
             raise ValueError(f"{name} shape {tuple(t.shape)} invalid for batch={B}, T={T}, Hk={Hk}, Hv={Hv}, {dim}={last}.")
     reset_t = None
-    if reset is not None:
+    if (isinstance(reset, torch.Tensor) and tuple(reset.shape) == (B, T) and reset.dtype in (torch.bool, torch.uint8)
+            and reset.is_cuda and reset.is_contiguous()):
+        # one byte per (row, token), nonzero = reset: read in place
+        reset_t = reset
+    elif reset is not None:
         r = reset if isinstance(reset, torch.Tensor) else torch.as_tensor(np.asarray(reset))
         r = r.to(torch.bool)
         if r.ndim == 0:
@@ -618,7 +626,7 @@ def gdn2_decode_steps(
         reset_t = r.to(torch.uint8)
 
     dev = _require_gpu(q, k, v, g, b, w, state)
-    if reset_t is not None:
+    if reset_t is not None and (reset_t.device != dev or not reset_t.is_contiguous()):
         reset_t = reset_t.to(dev).contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(K)
