@@ -448,11 +448,24 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
 CFG_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --kernel-trace --output-format csv "
            "-d gpurun_out/ktc -o run -- python3 bench.py --no-cpu-baseline --steps 2 --warmup 1 --decode-steps 0 "
            "--train-steps 0 --config-steps 4 --no-kernel-trace")
+CFG_PMC_CMD = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && rocprofv3 --pmc {ctr} --output-format csv "
+               "-d gpurun_out/{d} -o run -- python3 bench.py --no-cpu-baseline --steps 1 --warmup 1 --decode-steps 0 "
+               "--train-steps 0 --config-steps 2 --no-kernel-trace --copy-calibration")
 
 
-def rocprof_configs_summary(kt_dir):
+def _grid(r):
+    return tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"])) for a in "XYZ")
+
+
+def _nwg(r):
+    """Workgroups of a dispatch in the counter CSV (one flattened grid size)."""
+    return int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"]))
+
+
+def rocprof_configs_summary(kt_dir, f_dir=None, w_dir=None):
     """profiles/prefill_cfg3_cfg5_rocprof.md from the CFG_CMD kernel trace: the
-    library kernels of configs 3 and 5, told apart by their launch grids."""
+    library kernels of configs 3 and 5, told apart by their launch grids; with
+    the two CFG_PMC_CMD counter runs, the HBM traffic of each grid too."""
     import csv
     import collections
 
@@ -461,17 +474,57 @@ def rocprof_configs_summary(kt_dir):
         k = _kname(r["Kernel_Name"])
         if not k or k.startswith("copy"):
             continue
-        grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"])) for a in "XYZ")
-        rows[(k, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        rows[(k, _grid(r))].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    ctr = {}
+    if f_dir and w_dir:
+        for d, name in ((f_dir, "FETCH_SIZE"), (w_dir, "WRITE_SIZE")):
+            acc = collections.defaultdict(list)
+            for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
+                k = _kname(r["Kernel_Name"])
+                if k and r["Counter_Name"] == name:
+                    acc[k if k.startswith("copy") else (k, _nwg(r))].append(float(r["Counter_Value"]) * 1024.0)
+            cp = acc.pop("copy (calibration)")
+            cp = [x for x in cp if x > 0.5 * max(cp)]
+            scale = COPY_BYTES / (sum(cp) / len(cp))
+            ctr[name] = ({key: sum(v) / len(v) * scale for key, v in acc.items()}, scale)
+    # algorithmic bytes per dispatch: config 3 in one launch, config 5 per 8192-token block
+    w3 = prefill_work(B=4, L=8192, Hk=16, Hv=32, gates="scalar")
+    w5 = prefill_work(B=1, L=8192, Hk=16, Hv=32)
+    alg = {("k_prepass", (8192, 1, 1)): w3["prepass"]["bytes"], ("k_chain", (8, 32, 4)): w3["chain"]["bytes"],
+           ("k_prepass", (1024, 1, 1)): w5["prepass"]["bytes"], ("k_chain", (16, 16, 1)): w5["chain"]["bytes"]}
     # config 2's grids (B=1, Hk=12, 16 chunks) are the few dispatches of the warm-up and timed cfg-2 calls
     lines = ["# rocprofv3 kernel trace, configs 3 and 5 (bench.py other_configs)", "",
-             "Command:", "    " + CFG_CMD, "summarised by:", "    python bench.py --rocprof-configs-summary gpurun_out/ktc", "",
-             "Dispatches are grouped by kernel and launch grid (workgroups).  Config 3 (chunk_gdn, B=4, L=8192, "
-             "Hv=32 exec heads) and config 5 (L=65536 streamed in 8192-token blocks, Hk=16) launch distinct grids; "
-             "the config-2 calls of the same run are the 12-head grids.", "",
-             "| kernel | grid (workgroups) | dispatches | avg us | total us |", "|---|---|---|---|---|"]
+             "Command:", "    " + CFG_CMD]
+    if ctr:
+        lines += ["HBM traffic per dispatch from two counter runs:",
+                  "    " + CFG_PMC_CMD.format(ctr="FETCH_SIZE", d="pmc_cf"),
+                  "    " + CFG_PMC_CMD.format(ctr="WRITE_SIZE", d="pmc_cw"),
+                  "summarised by:", "    python bench.py --rocprof-configs-summary gpurun_out/ktc gpurun_out/pmc_cf "
+                  "gpurun_out/pmc_cw", "",
+                  f"Calibration: a plain {COPY_BYTES >> 20} MiB device copy reads FETCH_SIZE x "
+                  f"{ctr['FETCH_SIZE'][1]:.3f} and writes WRITE_SIZE x {ctr['WRITE_SIZE'][1]:.3f} bytes; both "
+                  "factors are applied below."]
+    else:
+        lines += ["summarised by:", "    python bench.py --rocprof-configs-summary gpurun_out/ktc"]
+    lines += ["", "Dispatches are grouped by kernel and launch grid (workgroups).  Config 3 (chunk_gdn, B=4, L=8192, "
+              "Hv=32 exec heads) and config 5 (L=65536 streamed in 8192-token blocks, Hk=16) launch distinct grids; "
+              "the config-2 calls of the same run are the 12-head grids.  Algorithmic bytes: inputs read once and "
+              "outputs written once (config 5: per 8192-token block).", ""]
+    if ctr:
+        lines += ["| kernel | grid (workgroups) | dispatches | avg us | total us | fetch MB | write MB | "
+                  "algorithmic MB | traffic / algorithmic |", "|---|---|---|---|---|---|---|---|---|"]
+    else:
+        lines += ["| kernel | grid (workgroups) | dispatches | avg us | total us |", "|---|---|---|---|---|"]
     for (k, grid), v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"| {k} | {grid[0]} x {grid[1]} x {grid[2]} | {len(v)} | {sum(v) / len(v):.1f} | {sum(v):.0f} |")
+        line = f"| {k} | {grid[0]} x {grid[1]} x {grid[2]} | {len(v)} | {sum(v) / len(v):.1f} | {sum(v):.0f} |"
+        if ctr:
+            nwg = grid[0] * grid[1] * grid[2]
+            fb = ctr["FETCH_SIZE"][0].get((k, nwg), float("nan"))
+            wb = ctr["WRITE_SIZE"][0].get((k, nwg), float("nan"))
+            a = alg.get((k, grid))
+            line += (f" {fb / 1e6:.1f} | {wb / 1e6:.1f} | " + (f"{a / 1e6:.1f} | {(fb + wb) / a:.2f} |" if a else
+                                                               "- | - |"))
+        lines.append(line)
     with open(os.path.join(PROFILE_DIR, "prefill_cfg3_cfg5_rocprof.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
@@ -541,8 +594,8 @@ def main():
     if len(sys.argv) == 5 and sys.argv[1] == "--rocprof-summary":
         rocprof_summary(*sys.argv[2:5])
         return
-    if len(sys.argv) == 3 and sys.argv[1] == "--rocprof-configs-summary":
-        rocprof_configs_summary(sys.argv[2])
+    if sys.argv[1:2] == ["--rocprof-configs-summary"] and len(sys.argv) in (3, 5):
+        rocprof_configs_summary(*sys.argv[2:])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)

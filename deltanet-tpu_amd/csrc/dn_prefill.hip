@@ -77,13 +77,51 @@ __device__ __forceinline__ SegId seg_raw(const PF& p, int b, int t) {
   return SegId{s32[0], w64 ? hi : 0};
 }
 
-// (w*v)^T fragments of 32 value columns of execution head h, chunk c, from
+// v rows of one 32-column slab of execution head h, chunk c (row 16a + r16 of
+// block a, fragment order, as loaded) and the write gate of those rows when it
+// has one channel.  Issued apart from their use so a caller can put them in
+// flight ahead of other work: vmcnt counts loads and stores in issue order, so
+// the wait for these rows covers only what was issued before them.
+template <class TV> struct VRows {
+  Raw8<TV> v[8];
+  float ws[8];
+};
+
+template <class TV>
+__device__ __forceinline__ void v_rows_issue(const PF& p, int b, int h, int c, int col0, int l, VRows<TV>& r) {
+  const int r16 = l & 15, q = l >> 4;
+  const int tb = p.t0 + c * CH;
+  const int t_end = min(p.t0 + p.nt, p.L);
+  const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
+  const int hw = vgate_head(p, p.w_h, hv);
+  const int cs = (col0 & ~31) % KD;
+  auto row_bt = [&](int a) { return (int64_t)b * p.L + min(tb + 16 * a + r16, t_end - 1); };
+  // (the w layout test sits outside the row loops: a branch between the
+  // loads would make each row wait for the one before)
+  if (p.w_c == 1) {
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      const int64_t bt = row_bt(a);
+      r.v[a].load((const TV*)p.v + (bt * p.Hv + hv) * KD + cs, q);
+      r.ws[a] = ((const float*)p.w)[bt * p.w_h + hw];
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      r.v[a].load((const TV*)p.v + (row_bt(a) * p.Hv + hv) * KD + cs, q);
+      r.ws[a] = 0.f;
+    }
+  }
+}
+
+// (w*v)^T fragments of 16 NT value columns of execution head h, chunk c, from
 // column col0 (rows = value column, k = token): Bwv[nt][s] covers columns
-// col0 + 16nt .. + 15 and token slab s.  Each 16-token block is loaded
-// row-wise and transposed by an identity product into half of a slab (exact).
-template <bool BF, class TV>
-__device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int col0, int l,
-                                         typename Pol<BF>::F3 (&Bwv)[2][4]) {
+// col0 + 16nt .. + 15 and token slab s, from the rows r (v_rows_issue of the
+// same columns).  Each 16-token block is transposed by an identity product
+// into half of a slab (exact).
+template <bool BF, class TV, int NT>
+__device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int col0, int l, const VRows<TV>& r,
+                                         typename Pol<BF>::F3 (&Bwv)[NT][4]) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
   using F3 = typename P::F3;
@@ -92,43 +130,38 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
   const int t_end = min(p.t0 + p.nt, p.L);
   const int hv = p.gates_at_hv ? h : h * p.G + col0 / KD;
   const int hw = vgate_head(p, p.w_h, hv);
-  // all 16 row loads are issued before any is used (the w layout test sits
-  // outside the row loops: a branch between them would make each row wait
-  // for the one before)
-  float vv[8][8], ww[8][8];
-  auto row_bt = [&](int a) { return (int64_t)b * p.L + min(tb + 16 * a + r16, t_end - 1); };
+  const int h0 = NT == 2 ? 0 : (col0 >> 4) & 1;   // first 16-column half of the slab
+  const int cs = (col0 & ~31) % KD;
+  float ww[8][8];
   if (p.w_c == 1) {
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const int64_t bt = row_bt(a);
-      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
-      const float ws = ((const float*)p.w)[bt * p.w_h + hw];
+    for (int a = 0; a < 8; ++a)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ww[a][e] = ws;
-    }
+      for (int e = 0; e < 8; ++e) ww[a][e] = r.ws[a];
   } else {
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
-      const int64_t bt = row_bt(a);
-      row8<TV>((const TV*)p.v + (bt * p.Hv + hv) * KD + col0 % KD, q, vv[a]);
-      row8<float>((const float*)p.w + (bt * p.w_h + hw) * p.w_c + col0 % KD, q, ww[a]);
+      const int64_t bt = (int64_t)b * p.L + min(tb + 16 * a + r16, t_end - 1);
+      row8<float>((const float*)p.w + (bt * p.w_h + hw) * p.w_c + cs, q, ww[a]);
     }
   }
   const F1 id0 = ident_frag<BF>(0, r16, q), id1 = ident_frag<BF>(1, r16, q);
 #pragma unroll
   for (int a = 0; a < 8; ++a) {
     const bool valid = tb + 16 * a + r16 < t_end;
-    float x[8];
+    float vv[8], x[8];
+    r.v[a].to(vv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float wg = p.fuse ? sigmoid_fast(ww[a][e]) : ww[a][e];
-      x[e] = valid ? wg * vv[a][e] : 0.f;
+      x[e] = valid ? wg * vv[e] : 0.f;
     }
     const F3 fx = P::f3(x);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
+      const bool second = nt + h0 == 1;
       f32x4 chi = zero4();
-      mma(chi, P::hi(fx), nt ? id1 : id0);
+      mma(chi, P::hi(fx), second ? id1 : id0);
       // lane (c, q): column 16nt + c, tokens 16a + 4q + ii -> slab a/2, half a&1
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
@@ -140,12 +173,235 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
       }
       if constexpr (BF) {
         f32x4 clo = zero4();
-        mma(clo, fx.lo, nt ? id1 : id0);
+        mma(clo, fx.lo, second ? id1 : id0);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) Bwv[nt][a >> 1].lo.v[4 * (a & 1) + ii] = (bf16)clo[ii];
       }
     }
   }
+}
+
+// q, k and b * k of one token row in fragment order (slab s: elements
+// 8s..8s+7), after the prologue: L2 normalisation (gdn2.py:1990-1996, the
+// normalised q and k rounded back to the input type), the q scale, the b
+// activation or clamp, and zeros for tokens past the end.
+template <class TIn>
+__device__ __forceinline__ void row_inputs(const PF& p, const Raw8<TIn> (&rq)[4], const Raw8<TIn> (&rk)[4],
+                                           const Raw8<float> (&rb)[4], float b_scalar, bool valid, float (&qv)[32],
+                                           float (&kv)[32], float (&bet)[32]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    rq[s].to(qv + 8 * s);
+    rk[s].to(kv + 8 * s);
+  }
+  if (p.b_c == 1) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) bet[e] = b_scalar;
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) rb[s].to(bet + 8 * s);
+  }
+  float ssq = 0.f, ssk = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) { ssq += qv[e] * qv[e]; ssk += kv[e] * kv[e]; }
+  ssq += __shfl_xor(ssq, 16); ssq += __shfl_xor(ssq, 32);
+  ssk += __shfl_xor(ssk, 16); ssk += __shfl_xor(ssk, 32);
+  if (p.fuse) {
+    const float rq = rsqrtf(ssq + 1e-6f) , rk = rsqrtf(ssk + 1e-6f);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      qv[e] = (qv[e] * rq) * p.scale;
+      kv[e] = kv[e] * rk;
+      bet[e] = sigmoid_fast(bet[e]);
+    }
+  } else if (p.l2norm) {
+    const float rq = rsqrtf(ssq + 1e-6f), rk = rsqrtf(ssk + 1e-6f);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) { qv[e] = round_as<TIn>((qv[e] * rq) * p.scale); kv[e] = round_as<TIn>(kv[e] * rk); }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) qv[e] = round_as<TIn>(qv[e] * p.scale);
+  }
+  if (p.guard && !p.fuse) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) bet[e] = fmaxf(bet[e], 0.f);
+  }
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    qv[e] = valid ? qv[e] : 0.f;
+    kv[e] = valid ? kv[e] : 0.f;
+    bet[e] = valid ? bet[e] * kv[e] : 0.f;
+  }
+}
+
+// ===========================================================================
+// Phases 1-3 of k_prepass for one decay and one b per (token, head) (the
+// Gated DeltaNet form, chunk_gdn: gdn.py:66-110 broadcasts them over the key
+// channels), precision "bf16" with bf16 q and k.  The per-channel machinery of
+// the general phases collapses:
+//   * Lambda is one cumulative sum per token (double-float, log2 units);
+//   * with the normalised q and k exactly bf16 (they are rounded back to the
+//     input type), the Gram matrices k k^T and q k^T are single bf16 MFMAs
+//     with fp32 accumulation, and
+//       A[i][j] = b_i e^{Lambda_i - Lambda_j} (k k^T)[i][j]   (i > j),
+//       M[i][j] =     e^{Lambda_i - Lambda_j} (q k^T)[i][j]   (i >= j),
+//     one exponential per pair, whose exponent is <= 0 for every unmasked
+//     pair (no factorisation, no overflow path);
+//   * (b k e^Lambda)^T, ke^T, qe and e^{Lambda_end} are per-row scalars times
+//     the row.
+// Results land where the general phases put them: A (fp32, row-major) in X,
+// M (split, fragment-native) and the transposed row operands in the
+// workspace; Y holds the q and k fragments until phase 4 takes it over.
+// Barriers inside wait for LDS only, so the per-row stores drain behind the
+// Gram products; the last one (a full __syncthreads) drains them before any
+// wave reads another's rows back.
+// ===========================================================================
+template <class TIn>
+__device__ __forceinline__ void prepass_scalar_gates(const PF& p, int b, int tb, int t_end, float g_tok,
+                                                     const Raw8<TIn> (&rq)[4], const Raw8<TIn> (&rk)[4],
+                                                     const Raw8<float> (&rb)[4], float b_scalar, const int* doc,
+                                                     float* X, float* Y, bf16* g_Mh, bf16* g_Ml, bf16* g_be,
+                                                     bf16* g_keh, bf16* g_kel, float* g_qe, float* g_dv) {
+  using P = Pol<true>;
+  using F1 = P::F1;
+  using F3 = P::F3;
+  using SS = Store<true>;
+  __shared__ float lam_h[CH], lam_l[CH];   // Lambda (log2 units), double-float
+  __shared__ float bet_s[CH];              // b per token (0 past the end)
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+
+  // ---- Lambda: inclusive scan of g over the chunk (waves 0 and 1) ----------
+  float hi = 0.f, lo = 0.f;
+  if (tid < CH) {
+    float gv = fminf(g_tok, 0.f);   // _nonpositive (NaN -> 0)
+    gv = fminf(gv, p.guard ? -1e-6f : 0.f);
+    hi = (tb + tid < t_end) ? gv : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float h2 = __shfl_up(hi, off), l2 = __shfl_up(lo, off);
+      if (l >= off) {
+        // error-free hi + h2 (TwoSum), the rounding error joins the low words
+        const float sum = hi + h2;
+        const float bb = sum - hi;
+        lo += l2 + ((hi - (sum - bb)) + (h2 - bb));
+        hi = sum;
+      }
+    }
+    if (w == 0 && l == 63) { lam_h[63] = hi; lam_l[63] = lo; }
+  }
+  lds_barrier();
+  if (tid < CH) {
+    if (w == 1) {
+      const float h2 = lam_h[63], l2 = lam_l[63];
+      const float sum = hi + h2;
+      const float bb = sum - hi;
+      lo += l2 + ((hi - (sum - bb)) + (h2 - bb));
+      hi = sum;
+    }
+  }
+  lds_barrier();
+  if (tid < CH) {
+    const float ph = hi * kLog2e;
+    lam_h[tid] = ph;
+    lam_l[tid] = fmaf(hi, kLog2e, -ph) + lo * kLog2e;
+  }
+  lds_barrier();
+  const float le_h = lam_h[CH - 1], le_l = lam_l[CH - 1];
+  if (tid < KD) g_dv[tid] = fast_exp2(le_h + le_l);   // e^{Lambda_end}
+
+  // ---- per-row operands of token block a = w --------------------------------
+  bf16* Kf = reinterpret_cast<bf16*>(Y);   // k fragments [block][slab][lane][8]
+  bf16* Qf = Kf + CH * KD;                 // q fragments
+  {
+    const int a = w;
+    const int i = 16 * a + r16;
+    const bool valid = tb + i < t_end;
+    float qv[32], kv[32], bet[32];
+    row_inputs<TIn>(p, rq, rk, rb, b_scalar, valid, qv, kv, bet);
+    // b alone: b * k / k is not recoverable where k = 0, so take it again
+    float bsc = p.b_c == 1 ? b_scalar : 0.f;
+    if (p.guard) bsc = fmaxf(bsc, 0.f);
+    if (q == 0) bet_s[i] = valid ? bsc : 0.f;
+    const bool first = doc[i] == 0;
+    const bool last = doc[i] == doc[CH - 1];
+    const float li_h = lam_h[i], li_l = lam_l[i];
+    const float eL = fast_exp2(li_h + li_l);                    // e^{Lambda_i} <= 1
+    const float eK = fast_exp2((le_h - li_h) + (le_l - li_l));  // e^{Lambda_end - Lambda_i} <= 1
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float bt[8], kt[8], qe[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bt[e] = first ? bet[8 * s + e] * eL : 0.f;
+        kt[e] = last ? kv[8 * s + e] * eK : 0.f;
+        qe[e] = first ? qv[8 * s + e] * eL : 0.f;
+      }
+      Store<false>::st8(g_qe + fofs(a, s, l), qe);
+      // (b k e^Lambda)^T and ke^T in fragment layout (row = key, k = token)
+      const F1 fbt = P::f1(bt);
+      const F3 fkt = P::f3(kt);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const F1 id = ident_frag<true>(hf, r16, q);
+        f32x4 cb = zero4(), chi = zero4(), clo = zero4();
+        mma(cb, fbt, id);
+        mma(chi, fkt.hi, id);
+        mma(clo, fkt.lo, id);
+        const int o = fofs(2 * s + hf, a >> 1, l) + 4 * (a & 1);
+        const float xb[4] = {cb[0], cb[1], cb[2], cb[3]};
+        const float xh[4] = {chi[0], chi[1], chi[2], chi[3]};
+        const float xl[4] = {clo[0], clo[1], clo[2], clo[3]};
+        SS::st4(g_be + o, xb);
+        SS::st4(g_keh + o, xh);
+        SS::st4(g_kel + o, xl);
+      }
+      // the normalised rows are bf16 values: their fragments are exact
+      SS::st8(Kf + fofs(a, s, l), kv + 8 * s);
+      SS::st8(Qf + fofs(a, s, l), qv + 8 * s);
+    }
+  }
+  lds_barrier();
+
+  // ---- A and M tiles (a, bb), bb <= a: 36 tiles dealt round-robin ------------
+  for (int t = w; t < 36; t += 8) {
+    int a = 0;
+    while ((a + 1) * (a + 2) / 2 <= t) ++a;
+    const int bb = t - a * (a + 1) / 2;
+    f32x4 gk = zero4(), gq = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const F1 ka = SS::fa(Kf + fofs(a, s, l));
+      const F1 kb = SS::fa(Kf + fofs(bb, s, l));
+      const F1 qa = SS::fa(Qf + fofs(a, s, l));
+      mma(gk, ka, kb);   // (k k^T)[16a + 4q + ii][16bb + r16]
+      mma(gq, kb, qa);   // (q k^T)[16a + r16][16bb + 4q + ii]
+    }
+    float mv[4];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      {
+        const int i = 16 * a + 4 * q + ii, j = 16 * bb + r16;
+        const float d = (lam_h[i] - lam_h[j]) + (lam_l[i] - lam_l[j]);
+        const bool on = i > j && doc[i] == doc[j];
+        X[i * XP + j] = on ? bet_s[i] * fast_exp2(fminf(d, 0.f)) * gk[ii] : 0.f;
+        if (bb == a && (a & 1) == 0) X[i * XP + j + 16] = 0.f;
+      }
+      {
+        const int i = 16 * a + r16, j = 16 * bb + 4 * q + ii;
+        const float d = (lam_h[i] - lam_h[j]) + (lam_l[i] - lam_l[j]);
+        const bool on = i >= j && doc[i] == doc[j];
+        mv[ii] = on ? fast_exp2(fminf(d, 0.f)) * gq[ii] : 0.f;
+      }
+    }
+    const int mo = fofs(a, bb >> 1, l) + 4 * (bb & 1);
+    SS::st4s(g_Mh + mo, g_Ml + mo, mv);
+    if (bb == a && (a & 1) == 0) {
+      const float z[4] = {0.f, 0.f, 0.f, 0.f};
+      SS::st4s(g_Mh + mo + 4, g_Ml + mo + 4, z);
+    }
+  }
+  __syncthreads();
 }
 
 // ===========================================================================
@@ -166,13 +422,13 @@ __device__ __forceinline__ void wv_frags(const PF& p, int b, int h, int c, int c
 // that puts the result directly in its consumer's fragment layout (M^T, Pn^T,
 // X^T); (b k e^Lambda)^T and ke^T are transposed by an identity product.
 // ===========================================================================
-template <bool BF, class TV>
-__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
+template <bool BF, class TV, int NT>
+__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l, const VRows<TV>& vr,
                                            const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
                                            const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
                                            const typename Store<BF>::ST* g_Ml);
 
-template <bool BF, class TIn, class TV>
+template <bool BF, class TIn, class TV, bool SC>
 __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
@@ -242,8 +498,15 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   }
   if (p.init_seg != nullptr) iseg = p.init_seg[b];
   const int g_part = tid >> 7;   // phase 1: 4 parts of 32 tokens, channel tid & 127
-  float gl[32];
-  {
+  float gl[SC ? 1 : 32];
+  if constexpr (SC) {
+    // one decay per token: thread t < 128 loads token t's (clamped to the last valid)
+    gl[0] = 0.f;
+    if (tid < CH) {
+      const int hg = kgate_head(p, p.g_h, h);
+      gl[0] = ((const float*)p.g)[((int64_t)b * p.L + min(tb + tid, t_end - 1)) * p.g_h + hg];
+    }
+  } else {
     const int kap = tid & 127;
     const int hg = kgate_head(p, p.g_h, h);
     const int tload = min(tb + 32 * g_part, t_end - 1);
@@ -313,6 +576,10 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     p.flags[((int64_t)b * p.NCb + c) * 2 + 1] = (doc[CH - 1] == 0);
   }
 
+  if constexpr (SC) {
+    prepass_scalar_gates<TIn>(p, b, tb, t_end, gl[0], rq, rk, rb, b_scalar, doc, X, Y, g_Mh, g_Ml, g_be, g_keh,
+                              g_kel, g_qe, g_dv);
+  } else {
   // ---- phase 1: block-local Lambda (double-float: X = hi, Y = lo), totals --
   {
     const int kap = tid & 127, part = g_part;
@@ -400,51 +667,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     const int t = tb + i;
     const bool valid = t < t_end;
     float qv[32], kv[32], bet[32];
-    {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        rq[s].to(qv + 8 * s);
-        rk[s].to(kv + 8 * s);
-      }
-      if (p.b_c == 1) {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) bet[e] = b_scalar;
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) rb[s].to(bet + 8 * s);
-      }
-      float ssq = 0.f, ssk = 0.f;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) { ssq += qv[e] * qv[e]; ssk += kv[e] * kv[e]; }
-      ssq += __shfl_xor(ssq, 16); ssq += __shfl_xor(ssq, 32);
-      ssk += __shfl_xor(ssk, 16); ssk += __shfl_xor(ssk, 32);
-      if (p.fuse) {
-        const float rq = rsqrtf(ssq + 1e-6f) , rk = rsqrtf(ssk + 1e-6f);
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-          qv[e] = (qv[e] * rq) * p.scale;
-          kv[e] = kv[e] * rk;
-          bet[e] = sigmoid_fast(bet[e]);
-        }
-      } else if (p.l2norm) {
-        const float rq = rsqrtf(ssq + 1e-6f), rk = rsqrtf(ssk + 1e-6f);
-#pragma unroll
-        for (int e = 0; e < 32; ++e) { qv[e] = round_as<TIn>((qv[e] * rq) * p.scale); kv[e] = round_as<TIn>(kv[e] * rk); }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) qv[e] = round_as<TIn>(qv[e] * p.scale);
-      }
-      if (p.guard && !p.fuse) {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) bet[e] = fmaxf(bet[e], 0.f);
-      }
-#pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        qv[e] = valid ? qv[e] : 0.f;
-        kv[e] = valid ? kv[e] : 0.f;
-        bet[e] = valid ? bet[e] * kv[e] : 0.f;
-      }
-    }
+    row_inputs<TIn>(p, rq, rk, rb, b_scalar, valid, qv, kv, bet);
     const bool first = doc[i] == 0;
     const bool last = doc[i] == doc[CH - 1];
     const bool blk_unsafe = unsafe_part[0][a] | unsafe_part[1][a];
@@ -790,6 +1013,8 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   }
   __syncthreads();
 
+  }
+
   // M (and, in bf16 mode, the high words of ke^T) are staged into LDS for
   // phase 5 once T no longer needs it; their loads are issued here so they
   // overlap the substitution.  16 bytes per load, 4 per array and thread.
@@ -909,6 +1134,13 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   }
   __syncthreads();
 
+  // The v rows of this wave's first value tile (16-column tiles, bf16 v) are
+  // issued now, ahead of phase 5's loads and stores: they arrive while W, Pn
+  // and X are formed.
+  constexpr bool kPreV = std::is_same<TV, bf16>::value;
+  VRows<TV> vpre;
+  if (kPreV && p.Vp < 256 && w < p.Vp / 16) v_rows_issue<TV>(p, b, h, c, 16 * w, l, vpre);
+
   // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tile w) -----------
   f32x4 Wc[8];
   {
@@ -1001,18 +1233,31 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   // One workgroup holding T, ke and M on chip replaces a separate launch
   // that reloaded them once per 32 columns (config 2: 91 vs 94 µs per step,
   // config 5: 3.7 vs 4.2 ms).
-  for (int g = w; g < p.Vp / 32; g += 8) value_cols<BF, TV>(p, b, h, c, 32 * g, l, Ts, keA, g_kel, Mh_s, Ml_s);
+  // 32 columns per wave when every wave gets some, else 16 (value heads of 128
+  // columns: all 8 waves instead of 4)
+  if (p.Vp >= 256) {
+    for (int g = w; g < p.Vp / 32; g += 8) {
+      VRows<TV> vr;
+      v_rows_issue<TV>(p, b, h, c, 32 * g, l, vr);
+      value_cols<BF, TV, 2>(p, b, h, c, 32 * g, l, vr, Ts, keA, g_kel, Mh_s, Ml_s);
+    }
+  } else {
+    for (int g = w; g < p.Vp / 16; g += 8) {
+      if (!(kPreV && g == w)) v_rows_issue<TV>(p, b, h, c, 16 * g, l, vpre);
+      value_cols<BF, TV, 1>(p, b, h, c, 16 * g, l, vpre, Ts, keA, g_kel, Mh_s, Ml_s);
+    }
+  }
 }
 
 // ===========================================================================
 // value_cols: U = T (w*v), Q = ke^T U and (M U)^T for value columns
-// [col0, col0 + 32) of one chunk unit -- one wave's share, the last phase of
+// [col0, col0 + 16 NT) of one chunk unit -- one wave's share, the last phase of
 // k_prepass.  The (w*v)^T fragments are formed here from v and w; T, ke^T
 // (high / low words) and M (high / low words) are the unit's fragment-native
 // arrays (LDS or workspace pointers).
 // ===========================================================================
-template <bool BF, class TV>
-__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l,
+template <bool BF, class TV, int NT>
+__device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int col0, int l, const VRows<TV>& vr,
                                            const typename Store<BF>::ST* g_T, const typename Store<BF>::ST* g_keh,
                                            const typename Store<BF>::ST* g_kel, const typename Store<BF>::ST* g_Mh,
                                            const typename Store<BF>::ST* g_Ml) {
@@ -1025,12 +1270,12 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
   float* g_Q = p.QC + u * (int64_t)(KD * p.Vp);
   float* g_Oi = p.OiT + u * (int64_t)(CH * p.Vp);
 
-  // (w*v)^T fragments of this wave's 32 value columns (rows = column, k = token)
-  F3 Bwv[2][4];
-  wv_frags<BF, TV>(p, b, h, c, col0, l, Bwv);
-  f32x4 Uc[2][8];
+  // (w*v)^T fragments of this wave's value columns (rows = column, k = token)
+  F3 Bwv[NT][4];
+  wv_frags<BF, TV, NT>(p, b, h, c, col0, l, vr, Bwv);
+  f32x4 Uc[NT][8];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) Uc[nt][rt] = zero4();
 #pragma unroll
@@ -1038,17 +1283,17 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
 #pragma unroll
     for (int s = 0; s <= rt / 2; ++s) {
       const F1 t = SS::fa(g_T + fofs(rt, s, l));
-      P::m13(Uc[0][rt], t, Bwv[0][s]);
-      P::m13(Uc[1][rt], t, Bwv[1][s]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) P::m13(Uc[nt][rt], t, Bwv[nt][s]);
     }
     // T read where it is used: keep the scheduler from hoisting every row's
     // fragment reads ahead (that would need them all live at once)
     __builtin_amdgcn_sched_barrier(0);
   }
   // U^T fragments (rows = value column, k = token)
-  F3 U3[2][4];
+  F3 U3[NT][4];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float x[8] = {Uc[nt][2 * s][0], Uc[nt][2 * s][1], Uc[nt][2 * s][2], Uc[nt][2 * s][3],
@@ -1058,14 +1303,15 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
   const int ct0 = col0 / 16;   // value tile of nt = 0 within the execution head
   // Q tiles (rows = key, columns = value), the chain's accumulator layout
   auto q_tile = [&](int m, const F3 (&ka)[4]) {
-    f32x4 Q0 = zero4(), Q1 = zero4();
+    f32x4 Qa[NT];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      P::m33(Q0, ka[s], U3[0][s]);
-      P::m33(Q1, ka[s], U3[1][s]);
-    }
-    *reinterpret_cast<f32x4*>(g_Q + cofs(m, ct0, p.nct, l)) = Q0;
-    *reinterpret_cast<f32x4*>(g_Q + cofs(m, ct0 + 1, p.nct, l)) = Q1;
+    for (int nt = 0; nt < NT; ++nt) Qa[nt] = zero4();
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) P::m33(Qa[nt], ka[s], U3[nt][s]);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(g_Q + cofs(m, ct0 + nt, p.nct, l)) = Qa[nt];
   };
   auto ld_ke = [&](int m, F3 (&ka)[4]) {
 #pragma unroll
@@ -1092,16 +1338,18 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
       if (s <= rt / 2) o.m[s] = SS::fa3(g_Mh + fofs(rt, s, l), g_Ml + fofs(rt, s, l));
   };
   auto oi_tile = [&](int rt, const MOps& o) {
-    f32x4 O0 = zero4(), O1 = zero4();
+    f32x4 Oa[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) Oa[nt] = zero4();
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s <= rt / 2) {
-        P::m33(O0, U3[0][s], o.m[s]);
-        P::m33(O1, U3[1][s], o.m[s]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) P::m33(Oa[nt], U3[nt][s], o.m[s]);
       }
     }
-    *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0, p.nct, l)) = O0;
-    *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0 + 1, p.nct, l)) = O1;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(g_Oi + cofs(rt, ct0 + nt, p.nct, l)) = Oa[nt];
   };
   {
     MOps ma, mb;
@@ -1405,10 +1653,27 @@ int check_args(const dn_prefill_args* a) {
   return DN_OK;
 }
 
+int g_prepass_scalar = -1;   // -1: unread; 0: general path forced (DN_PREPASS_SCALAR=0, measurements)
+
+// One decay and one b per (token, head) with bf16 q / k in precision "bf16"
+// (the Gated DeltaNet form) runs the scalar-gate prepass.
+bool scalar_gates(const PF& p) {
+  if (g_prepass_scalar < 0) {
+    const char* e = getenv("DN_PREPASS_SCALAR");
+    g_prepass_scalar = (e && atoi(e) == 0) ? 0 : 1;
+  }
+  return g_prepass_scalar == 1 && p.g_c == 1 && p.b_c == 1 && !p.fuse;
+}
+
 template <bool BF, class TIn, class TV>
 hipError_t launch_all(const PF& p, hipStream_t st) {
   prof_mark(0, st, false);
-  hipLaunchKernelGGL((k_prepass<BF, TIn, TV>), dim3(p.B * p.Hx * p.NCb), dim3(512), 0, st, p);
+  bool sc = false;
+  if constexpr (BF && std::is_same<TIn, bf16>::value) {
+    sc = scalar_gates(p);
+    if (sc) hipLaunchKernelGGL((k_prepass<BF, TIn, TV, true>), dim3(p.B * p.Hx * p.NCb), dim3(512), 0, st, p);
+  }
+  if (!sc) hipLaunchKernelGGL((k_prepass<BF, TIn, TV, false>), dim3(p.B * p.Hx * p.NCb), dim3(512), 0, st, p);
   prof_mark(0, st, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -67,6 +67,48 @@ def test_matrix_gate_layouts(layout, Hk, Hv, precision):
     check(out, ro, st, rs, precision, "fp32", f"{layout} Hk={Hk} Hv={Hv} {precision}")
 
 
+# One decay and one b per (token, head) with bf16 q / k in precision "bf16"
+# takes the scalar-gate prepass (Gram products on the normalised bf16 rows,
+# one exponential per token pair): its edge cases against the oracle.
+SCALAR_CASES = {
+    "hv_docs_init": dict(L=300, layout=("rank3_hv", "rank3_hv", "rank3_hv"), docs=True, init=True),
+    "hk_gates": dict(L=384, layout=("rank3_hk", "rank3_hk", "channel_hv"), docs=True),
+    "scalar4d_one": dict(L=129, layout=("scalar_hv", "scalar_one", "rank3_hv")),
+    "one_token": dict(L=1, layout=("rank3_hv", "rank3_hv", "rank3_hv"), init=True),
+    "no_l2norm": dict(L=256, layout=("rank3_hv", "rank3_hv", "rank3_hv"), l2norm=False, scale=0.3, qscale=0.1),
+    "guard": dict(L=520, layout=("rank3_hv", "rank3_hv", "rank3_hv"), docs=True, init=True, guard=True),
+    "strong_decay": dict(L=640, layout=("rank3_hv", "rank3_hv", "rank3_hv"), docs=True, strong=True),
+    "weak_decay": dict(L=512, layout=("rank3_hk", "rank3_hk", "rank3_hk"), init=True, g_shift=-7.0),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SCALAR_CASES))
+def test_scalar_gate_prefill_bf16(case):
+    c = SCALAR_CASES[case]
+    B, Hk, Hv, L = 2, 2, 4, c["L"]
+    seed = sorted(SCALAR_CASES).index(case) + 900
+    q, k, v, g, b, w = make_inputs(seed, B, L, Hk, Hv, g_layout=c["layout"][0], b_layout=c["layout"][1],
+                                   w_layout=c["layout"][2], qscale=c.get("qscale", 1.0),
+                                   g_shift=c.get("g_shift", -1.0))
+    rng = np.random.default_rng(seed)
+    if c.get("strong"):
+        # Qwen3-Next decay: -exp(A_log) softplus(a), A_log up to log(64)
+        A_log = rng.uniform(0.0, np.log(64.0), g.shape[2])
+        g = -np.exp(A_log) * np.log1p(np.exp(rng.standard_normal(g.shape[:3])))
+    seg = None
+    if c.get("docs"):
+        cuts = np.sort(rng.choice(np.arange(1, L), size=(B, 3), replace=False), axis=1)
+        seg = np.stack([np.searchsorted(cuts[i], np.arange(L), side="right") + 5 * i for i in range(B)])
+    init = 0.1 * rng.standard_normal((B, Hv, 128, 128)) if c.get("init") else None
+    kw = dict(qk_l2norm=c.get("l2norm", True))
+    if "scale" in c:
+        kw["scale"] = c["scale"]
+    if c.get("guard"):
+        kw["stability_guard"] = True
+    out, st, ro, rs = run_pair(q, k, v, g, b, w, dt="bf16", precision="bf16", seg=seg, init=init, **kw)
+    check(out, ro, st, rs, "bf16", "bf16", f"scalar gates {case}")
+
+
 @pytest.mark.parametrize("L", [300, 384])
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_fused_prologue_docs_init(L, precision):
