@@ -168,6 +168,10 @@ __device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
 // measured 3% faster than 4 and 10% faster than 8 at config 4 (bf16 state)
 constexpr int kDecodeWaves = 2;
 constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel (8 measured slower)
+// launches of at least this many tokens (and no stability guard) run the
+// chunked kernel: at config 4 it is faster from 8 tokens (bf16 state: 295 vs
+// 385 us at T = 8, 307 vs 728 us at T = 16), slower below (299 vs 219 us at T = 4)
+constexpr int kChunkMinTokens = 8;
 
 // One workgroup of NW waves per (batch row, value head).  Lane (rg, cg)
 // holds R = 32/NW state rows, 8 columns per row (Row8 above): for a bf16
@@ -343,13 +347,15 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
 }
 
 // T consecutive decode steps in one launch: the state stays in registers
-// (fp32) across the tokens and is read and written once.  Every step is the
-// single-step computation above (its column sums added in another order: 4
-// waves of 8 consecutive rows per lane); with a bf16 output state
-// the state is rounded to bf16 after every token, as T chained single steps
-// would store it.  The per-token LDS vectors are double-buffered by token
-// parity, so a token's writes never race the previous token's reads (every
-// wave has passed the previous token's barriers before it writes).
+// (fp32) across the tokens and is read and written once (a bf16 state is
+// rounded once, when it is stored).  Every step is the single-step
+// computation above (its column sums added in another order: 4 waves of 8
+// consecutive rows per lane).  It serves launches with the stability guard
+// (the cap applies after every token) and launches of fewer than
+// kChunkMinTokens tokens; the others run k_decode_chunk.  The per-token LDS
+// vectors are double-buffered by token parity, so a token's writes never race
+// the previous token's reads (every wave has passed the previous token's
+// barriers before it writes).
 template <class TSin, class TSout, int NW>
 __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
   constexpr int K = 128, V = 128, R = K / (4 * NW);   // rows per lane
@@ -507,17 +513,553 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) S[r][e] *= fac;
     }
-    if constexpr (sizeof(TSout) == 2) {
-      // the state a bf16 single step would store and the next one load
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) S[r][e] = (float)(bf16)S[r][e];
-    }
   }
   TSout* op = (TSout*)p.sout + sbase;
 #pragma unroll
   for (int r = 0; r < R; ++r) store_row<TSin, TSout>(op + (R * rg + r) * V, cg, S[r]);
+}
+
+// ---------------------------------------------------------------------------
+// T consecutive decode steps as chunks of 16 tokens in the chunked WY form
+// (the prefill's decomposition with 16-token chunks, the caller's state as
+// the state entering the first chunk), for launches without the stability
+// guard.  Per chunk of one (batch row, value head), with L the per-channel
+// cumulative log-decay inside the chunk and the documents that the reset
+// flags start (a reset at token t clears the state before token t):
+//   A[t][s] = sum_c b_tc k_tc k_sc e^{L_tc - L_sc}   (t > s, same document)
+//   M[t][s] = sum_c q_tc k_sc e^{L_tc - L_sc}        (t >= s, same document)
+//   Tm = (I + A)^-1,  W = Tm (b k e^L)_first,  U = Tm (w v)
+//   Vn = U - W S,  O = (q e^L)_first S + M Vn,  S <- D S + (k e^{L_end - L})_last^T Vn
+// (D = e^{L_end}, or 0 when the chunk holds a reset), which is the
+// token-by-token recurrence (gdn2.py:2471-2478) in exact arithmetic.  The
+// 16-row products run on MFMA in split bf16 (hi / lo words, 3 products), so
+// the state is read and written once per launch and a token costs a share of
+// a few 16-row products instead of three passes over the state.  The state
+// stays fp32 (MFMA accumulators) across the T tokens and is rounded to the
+// output state type once, at the end.
+// Layout: 4 waves; wave w owns state columns 32w..32w+31 as accumulator tiles
+// S[rt][ct] (lane (c, q): rows 16rt + 4q + ii of column 32w + 16ct + c), and
+// two stacked row tiles are the B operand of one 32-row slab, so no
+// reduction crosses waves.  The chunk's 16 x 128 operands are formed in LDS
+// by all 256 threads.  The state moves between row-major memory and the
+// accumulator layout through identity products (exact), never through LDS.
+// ---------------------------------------------------------------------------
+// An element of a run-time-typed tensor as raw bits (f32: the word; bf16 and
+// f16: the half word), converted after every load of a batch is issued: a
+// conversion inside the type branch would wait for each load in turn.
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
+  if (dt == DT_F32) return ((const uint32_t*)p)[i];
+  return ((const uint16_t*)p)[i];
+}
+__device__ __forceinline__ float bits_f(uint32_t r, int dt) {
+  if (dt == DT_F32) return __builtin_bit_cast(float, r);
+  if (dt == DT_BF16) return __builtin_bit_cast(float, r << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)r);
+}
+
+// Sum over the 16 lanes of a DPP row, every lane receiving the same value:
+// quad swaps, then rotations by 8 and by 4, an order in which all 16 lanes
+// add the same pairs (bit-identical totals).
+template <int C> __device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), C, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<0xB1>(x);    // quad_perm [1, 0, 3, 2]
+  x += dpp<0x4E>(x);    // quad_perm [2, 3, 0, 1]
+  x += dpp<0x128>(x);   // row_ror:8
+  x += dpp<0x124>(x);   // row_ror:4
+  return x;
+}
+
+// 8 consecutive elements of a run-time-typed tensor as raw 16-byte words (f32:
+// two, 16-bit types: one), converted after every load of a batch is issued.
+struct Raw8w { uint4 a, b; };
+__device__ __forceinline__ void ld8_bits(const void* p, int64_t i, int dt, Raw8w& r) {
+  if (dt == DT_F32) {
+    r.a = *reinterpret_cast<const uint4*>((const float*)p + i);
+    r.b = *reinterpret_cast<const uint4*>((const float*)p + i + 4);
+  } else {
+    r.a = *reinterpret_cast<const uint4*>((const uint16_t*)p + i);
+    r.b = r.a;
+  }
+}
+__device__ __forceinline__ void bits8_f(const Raw8w& r, int dt, float* x) {
+  const uint32_t wa[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, wb[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { x[e] = __builtin_bit_cast(float, wa[e]); x[4 + e] = __builtin_bit_cast(float, wb[e]); }
+  } else if (dt == DT_BF16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __builtin_bit_cast(float, wa[e] << 16);
+      x[2 * e + 1] = __builtin_bit_cast(float, wa[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = (float)__builtin_bit_cast(f16, (uint16_t)(wa[e] & 0xffffu));
+      x[2 * e + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(wa[e] >> 16));
+    }
+  }
+}
+
+constexpr int DC = 16;      // tokens per chunk
+constexpr int DCP = 132;    // fp32 pitch of the [token][channel] LDS arrays
+
+// An fp32 fragment as three bf16 fragments whose sum is exactly x (8
+// significant bits each: the remainders after each rounding are exact in
+// fp32 and the last fits a bf16), so identity products on the bf16 MFMA
+// move fp32 values between layouts exactly.
+__device__ __forceinline__ void split3(const float* x, Frag<true>& a, Frag<true>& b, Frag<true>& c) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bf16 h = (bf16)x[e];
+    const float r1 = x[e] - (float)h;
+    const bf16 m = (bf16)r1;
+    a.v[e] = h;
+    b.v[e] = m;
+    c.v[e] = (bf16)(r1 - (float)m);
+  }
+}
+
+// decay span (nats) up to which a chunk's A and M are formed as products of
+// per-token factors e^{L_t - L_8}, e^{L_8 - L_s} (each within e^{+-80}, far
+// inside the fp32 range); wider chunks take one exponential per pair
+constexpr float kChunkSpan = 80.f;
+
+template <class TSin, class TSout, bool BF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_decode_chunk(const DP p) {
+  constexpr int K = 128, V = 128;
+  using P = Pol<BF>;
+  using F3 = typename P::F3;
+  __shared__ __align__(16) float lds[6 * DC * DCP + 3 * DC * (DC + 1) + K + 3 * DC];
+  float* sQ = lds;                  // q -> q e^L (first document)     [DC][DCP]
+  float* sK = sQ + DC * DCP;        // k -> k e^{L_end - L} (last document)
+  float* sB = sK + DC * DCP;        // b k -> (b k e^L)_first
+  float* sL = sB + DC * DCP;        // g -> L (high word) -> W
+  float* sLl = sL + DC * DCP;       // L (low word) -> U
+  float* sV = sLl + DC * DCP;       // w v
+  float* sA = sV + DC * DCP;        // A   [DC][DC + 1]
+  float* sM = sA + DC * (DC + 1);   // M
+  float* sT = sM + DC * (DC + 1);   // (I + A)^-1
+  float* sD = sT + DC * (DC + 1);   // state row factor of the chunk
+  int* sDoc = reinterpret_cast<int*>(sD + K);   // [0, DC): document of token t; [DC, 2DC): reset flags
+  int* sWide = sDoc + 2 * DC;                    // a channel's decay span exceeds kChunkSpan
+
+  const int tid = threadIdx.x;
+  const int l = tid & 63, w = tid >> 6, r16 = l & 15, q = l >> 4;
+  const int bh = blockIdx.x;
+  const int bb = bh / p.Hv, hv = bh % p.Hv;
+  const int hk = hv / p.G;
+  const int T = p.T;
+  const int64_t sbase = (int64_t)bh * K * V;
+  const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
+  const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
+  const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
+
+  // token rows of a chunk as raw words: thread (t = tid >> 4, channels
+  // 8 (tid & 15) ..+7) loads token t's segment of q, k, v and the gates
+  // (tokens past the end read the last one; zeroed later)
+  struct Tok { Raw8w q, k, v, g, b, w; int rst; };
+  const int tr_t = tid >> 4, c8 = 8 * (tid & 15);
+  auto issue_tok = [&](int tb, Tok& r) {
+    const int tt = min(tb + tr_t, T - 1);
+    const int64_t bt_ = (int64_t)bb * T + tt;
+    ld8_bits(p.q, (bt_ * p.Hk + hk) * K + c8, p.qk_dt, r.q);
+    ld8_bits(p.k, (bt_ * p.Hk + hk) * K + c8, p.qk_dt, r.k);
+    ld8_bits(p.v, (bt_ * p.Hv + hv) * V + c8, p.v_dt, r.v);
+    auto gate = [&](const void* g, int H, int C, int dt, int hh, Raw8w& o) {
+      if (C == 1) {
+        o.a.x = ld_bits(g, bt_ * H + hh, dt);
+        o.b = o.a;
+      } else {
+        ld8_bits(g, (bt_ * H + hh) * C + c8, dt, o);
+      }
+    };
+    gate(p.g, p.g_h, p.g_c, p.g_dt, hg, r.g);
+    gate(p.b, p.b_h, p.b_c, p.b_dt, hb, r.b);
+    gate(p.w, p.w_h, p.w_c, p.w_dt, hw, r.w);
+    r.rst = 0;
+    if (p.reset != nullptr && (tid & 15) == 0) r.rst = p.reset[(int64_t)bb * T + tt];
+  };
+  Tok tok;
+  // ---- state in, without LDS: each 16-row tile of the wave's 32 columns is
+  // loaded as an A fragment (lane (r16, q): row 16rt + r16, columns
+  // 32w + pi(q, 0..7)); its products with the two halves of a 32 x 32 identity
+  // are the accumulator tiles S[rt][0], S[rt][1] (exact; an fp32 state as
+  // three bf16 parts)
+  f32x4 S[8][2];
+  {
+    const TSin* sp = (const TSin*)p.sin + sbase + 32 * w + 4 * q;
+    if constexpr (sizeof(TSin) == 2) {
+      bf16x4 ra[8], rb[8];
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const TSin* rp = sp + (int64_t)(16 * rt + r16) * V;
+        ra[rt] = *reinterpret_cast<const bf16x4*>(rp);
+        rb[rt] = *reinterpret_cast<const bf16x4*>(rp + 16);
+      }
+      issue_tok(0, tok);   // chunk 0's rows load beside the state
+      const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        Frag<true> f;
+        f.v = bf16x8{ra[rt][0], ra[rt][1], ra[rt][2], ra[rt][3], rb[rt][0], rb[rt][1], rb[rt][2], rb[rt][3]};
+        S[rt][0] = zero4();
+        S[rt][1] = zero4();
+        mma(S[rt][0], f, id0);
+        mma(S[rt][1], f, id1);
+      }
+    } else {
+      f32x4 ra[8], rb[8];
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const TSin* rp = sp + (int64_t)(16 * rt + r16) * V;
+        ra[rt] = *reinterpret_cast<const f32x4*>(rp);
+        rb[rt] = *reinterpret_cast<const f32x4*>(rp + 16);
+      }
+      issue_tok(0, tok);
+      const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const float x[8] = {ra[rt][0], ra[rt][1], ra[rt][2], ra[rt][3], rb[rt][0], rb[rt][1], rb[rt][2], rb[rt][3]};
+        Frag<true> fa, fb, fc;
+        split3(x, fa, fb, fc);
+        S[rt][0] = zero4();
+        S[rt][1] = zero4();
+        mma(S[rt][0], fa, id0);
+        mma(S[rt][1], fa, id1);
+        mma(S[rt][0], fb, id0);
+        mma(S[rt][1], fb, id1);
+        mma(S[rt][0], fc, id0);
+        mma(S[rt][1], fc, id1);
+      }
+    }
+  }
+
+  const int nchunk = (T + DC - 1) / DC;
+#pragma unroll 1
+  for (int c0 = 0; c0 < nchunk; ++c0) {
+    const int tb = c0 * DC;
+    // ---- token rows: prologue (gdn2.py:2393-2438) into LDS
+    {
+      const bool ok = tb + tr_t < T;
+      float xq[8], xk[8], xv[8], xg[8], xb[8], xw[8];
+      bits8_f(tok.q, p.qk_dt, xq);
+      bits8_f(tok.k, p.qk_dt, xk);
+      bits8_f(tok.v, p.v_dt, xv);
+      auto gate = [&](const Raw8w& r, int C, int dt, float* x) {
+        if (C == 1) {
+          const float s1 = bits_f(r.a.x, dt);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = s1;
+        } else {
+          bits8_f(r, dt, x);
+        }
+      };
+      gate(tok.g, p.g_c, p.g_dt, xg);
+      gate(tok.b, p.b_c, p.b_dt, xb);
+      gate(tok.w, p.w_c, p.w_dt, xw);
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { sq = fmaf(xq[e], xq[e], sq); sk = fmaf(xk[e], xk[e], sk); }
+      sq = row16_sum(sq);
+      sk = row16_sum(sk);
+      float yq[8], yk[8], yb[8], yg[8], yv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (p.l2norm) {
+          yq[e] = xq[e] / sqrtf(sq + 1e-6f) * p.scale;
+          yk[e] = xk[e] / sqrtf(sk + 1e-6f);
+        } else {
+          yq[e] = xq[e] * p.scale;
+          yk[e] = xk[e];
+        }
+        yq[e] = ok ? yq[e] : 0.f;
+        yk[e] = ok ? yk[e] : 0.f;
+        yb[e] = ok ? xb[e] * yk[e] : 0.f;
+        yg[e] = ok ? fminf(xg[e], 0.f) : 0.f;   // _nonpositive (NaN -> 0)
+        yv[e] = ok ? xw[e] * xv[e] : 0.f;
+      }
+      const int o = tr_t * DCP + c8;
+      st4<float>(&sQ[o], yq); st4<float>(&sQ[o + 4], yq + 4);
+      st4<float>(&sK[o], yk); st4<float>(&sK[o + 4], yk + 4);
+      st4<float>(&sB[o], yb); st4<float>(&sB[o + 4], yb + 4);
+      st4<float>(&sL[o], yg); st4<float>(&sL[o + 4], yg + 4);
+      st4<float>(&sV[o], yv); st4<float>(&sV[o + 4], yv + 4);
+      if ((tid & 15) == 0) sDoc[DC + tr_t] = (ok && tok.rst != 0) ? 1 : 0;
+      if (tid == 0) sWide[0] = 0;
+    }
+    __syncthreads();
+    // ---- L per channel (double-float running sum), documents per token
+    if (tid < K) {
+      float gv[DC];
+#pragma unroll
+      for (int t = 0; t < DC; ++t) gv[t] = sL[t * DCP + tid];
+      float hi = 0.f, lo = 0.f;
+#pragma unroll
+      for (int t = 0; t < DC; ++t) {
+        const float sum = hi + gv[t];
+        const float bbv = sum - hi;
+        lo += (hi - (sum - bbv)) + (gv[t] - bbv);
+        hi = sum;
+        sL[t * DCP + tid] = hi;
+        sLl[t * DCP + tid] = lo;
+      }
+      // L_0 - L_15 >= 0 (g <= 0): the chunk's decay span on this channel
+      if (-(hi + lo) + gv[0] > kChunkSpan) sWide[0] = 1;
+    } else if (tid < K + DC) {
+      const int t = tid - K;
+      int d = 0;
+      for (int u = 0; u <= t; ++u) d += sDoc[DC + u];
+      sDoc[t] = d;
+    }
+    __syncthreads();
+    // ---- A and M
+    if (!sWide[0]) {
+      // factored: A = (b k e^{L - L_8}) (k e^{L_8 - L})^T, M = (q e^{L - L_8}) (k e^{L_8 - L})^T
+      // on MFMA, wave 0 for A and wave 1 for M (lane (t | s = r16, q), 32-channel slabs)
+      if (w < 2) {
+        const float* X = w == 0 ? sB : sQ;
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+          float xr[8], kc[8], lr[8], lrl[8], lt[8], ltl[8];
+          row8<float>(&X[r16 * DCP + 32 * s2], q, xr);
+          row8<float>(&sK[r16 * DCP + 32 * s2], q, kc);
+          row8<float>(&sL[8 * DCP + 32 * s2], q, lr);
+          row8<float>(&sLl[8 * DCP + 32 * s2], q, lrl);
+          row8<float>(&sL[r16 * DCP + 32 * s2], q, lt);
+          row8<float>(&sLl[r16 * DCP + 32 * s2], q, ltl);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = (lt[e] - lr[e]) + (ltl[e] - lrl[e]);   // row r16: L - L_8
+            xr[e] *= __expf(d);
+            kc[e] *= __expf(-d);
+          }
+          P::m33(acc, P::f3(xr), P::f3(kc));   // acc[ii] = (row 4q + ii) . (column r16)
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int t = 4 * q + ii, s2 = r16;
+          const bool same = sDoc[t] == sDoc[s2];
+          if (w == 0) sA[t * (DC + 1) + s2] = (s2 < t && same) ? acc[ii] : 0.f;
+          else sM[t * (DC + 1) + s2] = (s2 <= t && same) ? acc[ii] : 0.f;
+        }
+      }
+    } else {
+      // one exponential per pair: thread (t = tid & 15, s = tid >> 4)
+      const int t = tid & 15, s2 = tid >> 4;
+      float a = 0.f, m = 0.f;
+      if (s2 <= t && sDoc[t] == sDoc[s2]) {
+#pragma unroll 1
+        for (int c = 0; c < K; c += 4) {
+          const f32x4 lt = *reinterpret_cast<const f32x4*>(&sL[t * DCP + c]);
+          const f32x4 ls = *reinterpret_cast<const f32x4*>(&sL[s2 * DCP + c]);
+          const f32x4 ltl = *reinterpret_cast<const f32x4*>(&sLl[t * DCP + c]);
+          const f32x4 lsl = *reinterpret_cast<const f32x4*>(&sLl[s2 * DCP + c]);
+          const f32x4 bt = *reinterpret_cast<const f32x4*>(&sB[t * DCP + c]);
+          const f32x4 qt = *reinterpret_cast<const f32x4*>(&sQ[t * DCP + c]);
+          const f32x4 ks = *reinterpret_cast<const f32x4*>(&sK[s2 * DCP + c]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float ex = __expf((lt[e] - ls[e]) + (ltl[e] - lsl[e]));   // <= 1
+            const float kx = ks[e] * ex;
+            a = fmaf(bt[e], kx, a);
+            m = fmaf(qt[e], kx, m);
+          }
+        }
+      }
+      sA[t * (DC + 1) + s2] = s2 < t ? a : 0.f;
+      sM[t * (DC + 1) + s2] = m;   // 0 above the diagonal and across documents
+    }
+    __syncthreads();
+    // ---- Tm = (I + A)^-1 by forward substitution (lane j: column j)
+    if (tid < DC) {
+      const int j = tid;
+      float tc[DC];
+#pragma unroll
+      for (int i = 0; i < DC; ++i) tc[i] = i == j ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 1; i < DC; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < i; ++m) acc = fmaf(sA[i * (DC + 1) + m], tc[m], acc);
+        if (i > j) tc[i] = -acc;
+      }
+#pragma unroll
+      for (int i = 0; i < DC; ++i) sT[i * (DC + 1) + j] = tc[i];
+    }
+    // ---- row factors in place (thread: token s, channels 8cg..8cg+7):
+    // be = (b k e^L)_first, q e^L (first), k e^{L_end - L} (last); D
+    // (reads L, sB, sQ, sK only: runs beside the substitution)
+    {
+      const int sr = tid >> 4, c8 = 8 * (tid & 15);
+      const int dl = sDoc[DC - 1];
+      const bool first = sDoc[sr] == 0, last = sDoc[sr] == dl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int o = sr * DCP + c8 + e;
+        const float lt = sL[o], ltl = sLl[o];
+        const float le = sL[(DC - 1) * DCP + c8 + e], lel = sLl[(DC - 1) * DCP + c8 + e];
+        const float eL = __expf(lt + ltl);
+        sB[o] = first ? sB[o] * eL : 0.f;
+        sQ[o] = first ? sQ[o] * eL : 0.f;
+        sK[o] = last ? sK[o] * __expf((le - lt) + (lel - ltl)) : 0.f;
+        if (sr == 0) sD[c8 + e] = dl == 0 ? __expf(le + lel) : 0.f;
+      }
+    }
+    __syncthreads();
+    // ---- W = Tm be -> sL, U = Tm (w v) -> sLl (thread: token t, channels 8cg..8cg+7)
+    {
+      const int t = tid >> 4, c8 = 8 * (tid & 15);
+      float tr[DC];
+#pragma unroll
+      for (int s2 = 0; s2 < DC; ++s2) tr[s2] = sT[t * (DC + 1) + s2];
+      float aw[8], au[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { aw[e] = 0.f; au[e] = 0.f; }
+#pragma unroll
+      for (int s2 = 0; s2 < DC; ++s2) {
+        float be[8], wv[8];
+        ld4<float>(&sB[s2 * DCP + c8], be);
+        ld4<float>(&sB[s2 * DCP + c8 + 4], be + 4);
+        ld4<float>(&sV[s2 * DCP + c8], wv);
+        ld4<float>(&sV[s2 * DCP + c8 + 4], wv + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          aw[e] = fmaf(tr[s2], be[e], aw[e]);   // Tm is 0 above the diagonal
+          au[e] = fmaf(tr[s2], wv[e], au[e]);
+        }
+      }
+      __syncthreads();   // every thread has read L before W and U replace it
+      st4<float>(&sL[t * DCP + c8], aw);
+      st4<float>(&sL[t * DCP + c8 + 4], aw + 4);
+      st4<float>(&sLl[t * DCP + c8], au);
+      st4<float>(&sLl[t * DCP + c8 + 4], au + 4);
+    }
+    __syncthreads();
+    // ---- the wave's 32 state columns: Vn, O, state update
+    {
+      f32x4 vn[2], o[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        o[ct] = zero4();
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) vn[ct][ii] = sLl[(4 * q + ii) * DCP + 32 * w + 16 * ct + r16];
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        F3 Sf[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const float x[8] = {S[2 * s2][ct][0], S[2 * s2][ct][1], S[2 * s2][ct][2], S[2 * s2][ct][3],
+                              S[2 * s2 + 1][ct][0], S[2 * s2 + 1][ct][1], S[2 * s2 + 1][ct][2], S[2 * s2 + 1][ct][3]};
+          Sf[ct] = P::f3(x);
+        }
+        float xw[8], xq[8];
+        row8<float>(&sL[r16 * DCP + 32 * s2], q, xw);
+        row8<float>(&sQ[r16 * DCP + 32 * s2], q, xq);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xw[e] = -xw[e];
+        const F3 Wf = P::f3(xw), Qf = P::f3(xq);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          P::m33(vn[ct], Wf, Sf[ct]);   // Vn[4q + ii][col] = U - W S
+          P::m33(o[ct], Qf, Sf[ct]);    // (q e^L) S
+        }
+      }
+      // Vn as the B operand (k = token): tokens 4q..4q+3 from the accumulator, 16..31 zero
+      F3 Vf[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const float x[8] = {vn[ct][0], vn[ct][1], vn[ct][2], vn[ct][3], 0.f, 0.f, 0.f, 0.f};
+        Vf[ct] = P::f3(x);
+      }
+      {
+        const float xm[8] = {sM[r16 * (DC + 1) + 4 * q], sM[r16 * (DC + 1) + 4 * q + 1],
+                             sM[r16 * (DC + 1) + 4 * q + 2], sM[r16 * (DC + 1) + 4 * q + 3], 0.f, 0.f, 0.f, 0.f};
+        const F3 Mf = P::f3(xm);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) P::m33(o[ct], Mf, Vf[ct]);
+      }
+      // outputs: lane (c, q) holds tokens 4q..4q+3 of column 32w + 16ct + c
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int tt = tb + 4 * q + ii;
+          if (tt < T) {
+            const int64_t oi = (((int64_t)bb * T + tt) * p.Hv + hv) * V + 32 * w + 16 * ct + r16;
+            if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)o[ct][ii];
+            else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)o[ct][ii];
+            else ((float*)p.out)[oi] = o[ct][ii];
+          }
+        }
+      }
+      // S <- D S + Ke^T Vn
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sD[16 * rt + 4 * q]);
+        const float xk[8] = {sK[(4 * q) * DCP + 16 * rt + r16], sK[(4 * q + 1) * DCP + 16 * rt + r16],
+                             sK[(4 * q + 2) * DCP + 16 * rt + r16], sK[(4 * q + 3) * DCP + 16 * rt + r16],
+                             0.f, 0.f, 0.f, 0.f};
+        const F3 Kf = P::f3(xk);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) S[rt][ct][ii] *= d4[ii];
+          P::m33(S[rt][ct], Kf, Vf[ct]);
+        }
+      }
+    }
+    // the next chunk's rows load across the barrier (chunk 0's were issued at entry)
+    __builtin_amdgcn_sched_barrier(0);   // (not hoisted into the products above)
+    if (c0 + 1 < nchunk) issue_tok(tb + DC, tok);
+    __syncthreads();
+  }
+
+  // ---- state out, without LDS: the accumulator pair of slab s2 read as an A
+  // operand is S^T (row = state column, k = state row); its products with the
+  // identity halves give lane (c, q) state row 32 s2 + 16 hf + c, columns
+  // 32w + 16ct + 4q .. +3 (a bf16 state is rounded first, an fp32 one moves as
+  // three bf16 parts: exact either way).  Plain (cached) loads and stores:
+  // each instruction covers 32-byte pieces of 16 rows, which the L2 merges
+  // (non-temporal ones measured 20 % slower here).
+  {
+    TSout* op = (TSout*)p.sout + sbase + 32 * w + 4 * q;
+    const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const float x[8] = {S[2 * s2][ct][0], S[2 * s2][ct][1], S[2 * s2][ct][2], S[2 * s2][ct][3],
+                            S[2 * s2 + 1][ct][0], S[2 * s2 + 1][ct][1], S[2 * s2 + 1][ct][2], S[2 * s2 + 1][ct][3]};
+        Frag<true> fa, fb, fc;
+        if constexpr (sizeof(TSout) == 2) {
+          fa = make_frag<true>(x);   // the stored bf16 state
+        } else {
+          split3(x, fa, fb, fc);
+        }
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          f32x4 y = zero4();
+          mma(y, fa, hf ? id1 : id0);
+          if constexpr (sizeof(TSout) == 4) {
+            mma(y, fb, hf ? id1 : id0);
+            mma(y, fc, hf ? id1 : id0);
+          }
+          TSout* rp = op + (int64_t)(32 * s2 + 16 * hf + r16) * V + 16 * ct;
+          if constexpr (sizeof(TSout) == 2) {
+            const bf16x4 h{(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+            *reinterpret_cast<bf16x4*>(rp) = h;
+          } else {
+            *reinterpret_cast<f32x4*>(rp) = y;
+          }
+        }
+      }
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void k_frob_cap(float* S, int64_t per, float tau) {
@@ -579,6 +1121,15 @@ extern "C" int dn_profile_end(double* ms_sum, int64_t* launches) {
 extern "C" int dn_abi_version(void) { return DN_ABI_VERSION; }
 
 namespace {
+int g_decode_chunk = -1;   // -1: unread; 0: per-token kernel forced (DN_DECODE_CHUNK=0, measurements)
+bool decode_chunked() {
+  if (g_decode_chunk < 0) {
+    const char* e = getenv("DN_DECODE_CHUNK");
+    g_decode_chunk = (e && atoi(e) == 0) ? 0 : 1;
+  }
+  return g_decode_chunk == 1;
+}
+
 int decode_launch(const dn_decode_args* a, int T, void* stream) {
   if (a == nullptr) return set_error(DN_E_INVALID, "null args");
   if (a->abi_version != DN_ABI_VERSION) return set_error(DN_E_ABI, "dn_decode_args built for another ABI version");
@@ -619,6 +1170,13 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
     else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
     else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
     else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
+  } else if (!p.guard && T >= kChunkMinTokens && decode_chunked()) {
+    // products on the fp32 MFMA when either side of the state is fp32, in
+    // split bf16 for a bf16 state (its rounding dominates)
+    if (fi && fo) hipLaunchKernelGGL((k_decode_chunk<float, float, false>), grid, dim3(256), 0, st, p);
+    else if (fi && !fo) hipLaunchKernelGGL((k_decode_chunk<float, bf16, false>), grid, dim3(256), 0, st, p);
+    else if (fo) hipLaunchKernelGGL((k_decode_chunk<bf16, float, false>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((k_decode_chunk<bf16, bf16, true>), grid, dim3(256), 0, st, p);
   } else {
     if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
     else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);

@@ -567,10 +567,12 @@ def gdn2_decode_steps(
     and w: (B, T, Hx) or (B, T, Hx, V) with Hx in {1, Hk, Hv}; state
     (B, Hv, K, V).  ``reset`` is None, (B,) (clear the state before the first
     token) or (B, T) (clear it before each marked token).  Returns
-    ``(output (B, T, Hv, V), new_state)``, equal to T chained
-    ``gdn2_decode_step`` calls: the state is read and written once, and with
-    ``state_dtype`` bfloat16 it is rounded to bf16 after every token as the
-    chained calls would store it.
+    ``(output (B, T, Hv, V), new_state)``: the recurrence of T chained
+    ``gdn2_decode_step`` calls, with the state read once, carried in fp32
+    across the T tokens and stored once (a bfloat16 ``state_dtype`` is rounded
+    once, at the end, where chained calls round after every token).  From 8
+    tokens without the stability guard the launch runs the tokens as 16-token
+    chunks in the WY form on matrix cores.
     """
     if stability_guard and isinstance(stability_tau, (int, float)) and not stability_tau > 0:
         raise ValueError(f"stability_tau must be positive, got {stability_tau}.")

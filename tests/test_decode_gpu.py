@@ -213,16 +213,31 @@ def steps_inputs(seed, B, T, Hk, Hv, gate_heads="hk"):
     return q, k, v, g, b, w
 
 
+def chain_oracle(q, k, v, g, b, w, S0, reset, **kw):
+    """T chained oracle steps (float64, no rounding between tokens)."""
+    ref_s, ro = S0, []
+    for t in range(q.shape[1]):
+        o1, ref_s = O.decode_step(q[:, t], k[:, t], v[:, t], g[:, t], b[:, t], w[:, t], ref_s,
+                                  reset=reset[:, t], **kw)
+        ro.append(o1)
+    return np.stack(ro, 1), ref_s
+
+
 @pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
 @pytest.mark.parametrize("guard", [False, True])
-def test_decode_steps_equal_chained_steps(state_dtype, guard):
+@pytest.mark.parametrize("T", [6, 20])
+def test_decode_steps_equal_chained_steps(state_dtype, guard, T):
     # one launch over T tokens == T chained single steps (per-token resets,
-    # stability cap after every token, bf16 state rounded after every token)
-    B, T, Hk, Hv = 3, 6, 2, 4
+    # stability cap after every token).  T = 6 and launches with the guard run
+    # the per-token kernel; T = 20 without it runs two 16-token chunks in the
+    # WY form, a reset inside each.
+    B, Hk, Hv = 3, 2, 4
     q, k, v, g, b, w = steps_inputs(31, B, T, Hk, Hv)
     S0 = 0.3 * np.random.default_rng(32).standard_normal((B, Hv, 128, 128))
     reset = np.zeros((B, T), bool)
     reset[1, 0] = reset[2, 3] = True
+    if T > 16:
+        reset[0, 17] = True
     tb = lambda x: to_dev(x, torch.bfloat16)
     st0 = to_dev(S0)
     if state_dtype == "bfloat16":
@@ -239,16 +254,23 @@ def test_decode_steps_equal_chained_steps(state_dtype, guard):
     o_c = torch.stack(outs, 1)
     assert o_m.shape == (B, T, Hv, 128) and o_m.dtype == torch.bfloat16
     assert s_m.dtype == st.dtype
-    # the same arithmetic, with the column sums added in another order (the
-    # two kernels split the state rows differently over lanes and waves): the
-    # fp32 results differ by a few roundings.  A bf16-rounded output may land
-    # one bf16 step apart; a bf16 state carries such a step into the later
-    # tokens, so there the bound is bf16 rounding-level agreement.
     ro, rs = rel_l2(as_np(o_m), as_np(o_c)), rel_l2(as_np(s_m), as_np(st))
-    print(f"multi vs chained: out {ro:.2e} state {rs:.2e}")
+    print(f"multi vs chained T={T}: out {ro:.2e} state {rs:.2e}")
     if state_dtype == "bfloat16":
-        assert ro < 2e-4 and rs < 2e-4
+        # the launch rounds the state once, the chained steps after every
+        # token: they agree at the bf16 rounding level, and the launch is
+        # within one final rounding of the unrounded recurrence
+        assert ro < 1e-2 and rs < 1e-2
+        bfr = lambda x: O.bf16_round(x).astype(np.float64)
+        ref_o, ref_s = chain_oracle(bfr(q), bfr(k), bfr(v), g, b, w, as_np(st0).astype(np.float64), reset,
+                                    qk_l2norm=True, stability_guard=guard, stability_tau=20.0)
+        eo, es = rel_l2(as_np(o_m), ref_o), rel_l2(as_np(s_m), ref_s)
+        print(f"multi vs unrounded oracle: out {eo:.2e} state {es:.2e}")
+        assert eo < 4e-3 and es < 4e-3
     else:
+        # the same recurrence, the sums in another order (and, for the chunked
+        # form, another association): fp32 results a few roundings apart; a
+        # bf16-rounded output may land one bf16 step apart
         a, c = as_np(o_m).astype(np.float64), as_np(o_c).astype(np.float64)
         assert np.all(np.abs(a - c) <= 2.0 ** -7 * np.abs(c) + 1e-6 * np.abs(c).max())
         assert rs < 1e-5
@@ -319,11 +341,12 @@ def test_decode_odd_matrix_count(state_dtype, B, Hk, Hv):
 
 @pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
 @pytest.mark.parametrize("B,Hk,Hv", [(3, 1, 1), (1, 1, 3)])
-def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv):
+@pytest.mark.parametrize("Tn", [4, 12])
+def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv, Tn):
     # T tokens in one launch with an odd number of state matrices: equal to
-    # T chained single steps up to the summation order (the two kernels split
-    # the state rows differently over lanes), and the fp32 run to the oracle
-    Tn = 4
+    # T chained single steps up to the summation order (the kernels split the
+    # state rows differently over lanes; Tn = 12 runs the chunked form) and
+    # the bf16 state's single rounding, and the fp32 run to the oracle
     q, k, v, g, b, w = steps_inputs(92 + B, B, Tn, Hk, Hv)
     S0 = 0.3 * np.random.default_rng(93).standard_normal((B, Hv, 128, 128))
     reset = np.zeros((B, Tn), bool)
@@ -339,14 +362,62 @@ def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv):
         outs.append(o1)
     ro, rs = rel_l2(as_np(o_m), as_np(torch.stack(outs, 1))), rel_l2(as_np(s_m), as_np(st))
     print(f"odd multi vs chained: out {ro:.2e} state {rs:.2e}")
-    assert ro < (2e-4 if state_dtype == "bfloat16" else 1e-6)
-    assert rs < (2e-4 if state_dtype == "bfloat16" else 1e-6)
+    bound = 1e-2 if state_dtype == "bfloat16" else (1e-6 if Tn < 8 else 1e-5)
+    assert ro < bound and rs < bound
     # every matrix, the last one included, carries its own state
     for i in range(B):
-        assert rel_l2(as_np(s_m)[i], as_np(st)[i]) < (2e-4 if state_dtype == "bfloat16" else 1e-6)
+        assert rel_l2(as_np(s_m)[i], as_np(st)[i]) < bound
     if state_dtype == "float32":
         ref_s = S0
         for t in range(Tn):
             o1, ref_s = O.decode_step(q[:, t], k[:, t], v[:, t], g[:, t], b[:, t], w[:, t], ref_s,
                                       reset=reset[:, t], qk_l2norm=True)
         check(o_m[:, -1].reshape(B, Hv, 128), o1, s_m, ref_s, "fp32", "fp32", f"odd decode_steps B={B} Hv={Hv}")
+
+
+# Launches of 8 or more tokens without the stability guard run 16-token chunks
+# in the WY form: parity with the float64 token-by-token oracle across ragged
+# chunk counts, resets at and inside chunk boundaries, gate layouts and dtypes,
+# no L2 norm, and a decay strong enough to take the one-exponential-per-pair
+# path for A and M (a chunk's decay span above 80 nats).
+CHUNK_CASES = {
+    "T8_hk": dict(T=8, gates="hk"),
+    "T16_hv_resets": dict(T=16, gates="hv", resets=[(0, 0), (1, 7), (1, 15)]),
+    "T37_scalar": dict(T=37, gates="scalar", resets=[(0, 16), (1, 20), (1, 21)]),
+    "T24_no_l2norm_f16_gates": dict(T=24, gates="hk", l2norm=False, scale=0.2, gate_dtype="f16"),
+    "T19_strong_decay": dict(T=19, gates="hv", strong=True, resets=[(1, 9)]),
+}
+
+
+@pytest.mark.parametrize("state_dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("case", sorted(CHUNK_CASES))
+def test_decode_steps_chunked_vs_oracle(case, state_dtype):
+    c = CHUNK_CASES[case]
+    B, Hk, Hv, T = 2, 2, 4, c["T"]
+    seed = 500 + sorted(CHUNK_CASES).index(case)
+    rng = np.random.default_rng(seed)
+    q, k, v, g, b, w = steps_inputs(seed, B, T, Hk, Hv, "hv" if c["gates"] == "hv" else "hk")
+    if c["gates"] == "scalar":
+        g = -np.exp(0.39 * rng.standard_normal((B, T, Hv)) - 1)
+        b = sig(0.39 * rng.standard_normal((B, T, Hv)))
+        w = sig(0.39 * rng.standard_normal((B, T, Hv)))
+    if c.get("strong"):
+        g = -np.exp(rng.uniform(0, np.log(40.0), g.shape))   # up to 40 nats per token
+    reset = np.zeros((B, T), bool)
+    for bi, ti in c.get("resets", []):
+        reset[bi, ti] = True
+    S0 = 0.2 * rng.standard_normal((B, Hv, 128, 128))
+    sdt = torch.float32 if state_dtype == "float32" else torch.bfloat16
+    gdt = torch.float16 if c.get("gate_dtype") == "f16" else torch.float32
+    if gdt == torch.float16:
+        g, b, w = (x.astype(np.float16).astype(np.float64) for x in (g, b, w))
+    kw = dict(qk_l2norm=c.get("l2norm", True))
+    if "scale" in c:
+        kw["scale"] = c["scale"]
+    st0 = to_dev(S0, sdt)
+    o, s = gdn2_decode_steps(to_dev(q), to_dev(k), to_dev(v), to_dev(g, gdt), to_dev(b, gdt), to_dev(w, gdt),
+                             st0, reset=torch.tensor(reset), state_dtype=state_dtype, **kw)
+    ro, rs = chain_oracle(q, k, v, g, b, w, as_np(st0).astype(np.float64), reset, **kw)
+    prec = "fp32" if state_dtype == "float32" else "bf16"
+    check(o.reshape(B, T * Hv, 128), ro.reshape(B, T * Hv, 128), s, rs, prec, "fp32",
+          f"decode_steps chunked {case} {state_dtype}")
