@@ -347,9 +347,9 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
 }
 
 // T consecutive decode steps in one launch: the state stays in registers
-// (fp32) across the tokens and is read and written once (a bf16 state is
-// rounded once, when it is stored).  Every step is the single-step
-// computation above (its column sums added in another order: 4 waves of 8
+// across the tokens and is read and written once; with a bf16 output state it
+// is rounded to bf16 after every token, as T chained single steps would store
+// it.  Every step is the single-step computation above (its column sums added in another order: 4 waves of 8
 // consecutive rows per lane).  It serves launches with the stability guard
 // (the cap applies after every token) and launches of fewer than
 // kChunkMinTokens tokens; the others run k_decode_chunk.  The per-token LDS
@@ -513,6 +513,15 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) S[r][e] *= fac;
     }
+    if constexpr (sizeof(TSout) == 2) {
+      // the state a bf16 single step would store and the next one load (the
+      // compiler then keeps it packed: T = 16, bf16 state 728 us against
+      // 922 us with an fp32 carry)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) S[r][e] = (float)(bf16)S[r][e];
+    }
   }
   TSout* op = (TSout*)p.sout + sbase;
 #pragma unroll
@@ -632,17 +641,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int K = 128, V = 128;
   using P = Pol<BF>;
   using F3 = typename P::F3;
-  __shared__ __align__(16) float lds[6 * DC * DCP + 3 * DC * (DC + 1) + K + 3 * DC];
-  float* sQ = lds;                  // q -> q e^L (first document)     [DC][DCP]
-  float* sK = sQ + DC * DCP;        // k -> k e^{L_end - L} (last document)
-  float* sB = sK + DC * DCP;        // b k -> (b k e^L)_first
-  float* sL = sB + DC * DCP;        // g -> L (high word) -> W
+  __shared__ __align__(16) float lds[9 * DC * DCP + 2 * DC * (DC + 1) + K + 3 * DC];
+  float* sQ = lds;                  // q                                [DC][DCP]
+  float* sK = sQ + DC * DCP;        // k
+  float* sB = sK + DC * DCP;        // b k
+  float* sL = sB + DC * DCP;        // g -> L (high word) -> A / M partial sums -> W
   float* sLl = sL + DC * DCP;       // L (low word) -> U
   float* sV = sLl + DC * DCP;       // w v
-  float* sA = sV + DC * DCP;        // A   [DC][DC + 1]
+  float* sBe = sV + DC * DCP;       // (b k e^L)_first
+  float* sQe = sBe + DC * DCP;      // (q e^L)_first
+  float* sKe = sQe + DC * DCP;      // (k e^{L_end - L})_last
+  float* sA = sKe + DC * DCP;       // A   [DC][DC + 1]
   float* sM = sA + DC * (DC + 1);   // M
-  float* sT = sM + DC * (DC + 1);   // (I + A)^-1
-  float* sD = sT + DC * (DC + 1);   // state row factor of the chunk
+  float* sD = sM + DC * (DC + 1);   // state row factor of the chunk
   int* sDoc = reinterpret_cast<int*>(sD + K);   // [0, DC): document of token t; [DC, 2DC): reset flags
   int* sWide = sDoc + 2 * DC;                    // a channel's decay span exceeds kChunkSpan
 
@@ -687,46 +698,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // loaded as an A fragment (lane (r16, q): row 16rt + r16, columns
   // 32w + pi(q, 0..7)); its products with the two halves of a 32 x 32 identity
   // are the accumulator tiles S[rt][0], S[rt][1] (exact; an fp32 state as
-  // three bf16 parts)
-  f32x4 S[8][2];
+  // three bf16 parts).  The loads are issued first and consumed only after
+  // chunk 0's token phases, so their latency and the token rows' overlap.
+  typedef typename std::conditional<sizeof(TSin) == 2, bf16x4, f32x4>::type RawS;
+  RawS ra[8], rb[8];
   {
     const TSin* sp = (const TSin*)p.sin + sbase + 32 * w + 4 * q;
-    if constexpr (sizeof(TSin) == 2) {
-      bf16x4 ra[8], rb[8];
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const TSin* rp = sp + (int64_t)(16 * rt + r16) * V;
-        ra[rt] = *reinterpret_cast<const bf16x4*>(rp);
-        rb[rt] = *reinterpret_cast<const bf16x4*>(rp + 16);
-      }
-      issue_tok(0, tok);   // chunk 0's rows load beside the state
-      const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
+    for (int rt = 0; rt < 8; ++rt) {
+      const TSin* rp = sp + (int64_t)(16 * rt + r16) * V;
+      ra[rt] = *reinterpret_cast<const RawS*>(rp);
+      rb[rt] = *reinterpret_cast<const RawS*>(rp + 16);
+    }
+  }
+  issue_tok(0, tok);   // chunk 0's rows load beside the state
+  f32x4 S[8][2];
+  auto state_in = [&]() {
+    const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        Frag<true> f;
-        f.v = bf16x8{ra[rt][0], ra[rt][1], ra[rt][2], ra[rt][3], rb[rt][0], rb[rt][1], rb[rt][2], rb[rt][3]};
-        S[rt][0] = zero4();
-        S[rt][1] = zero4();
+    for (int rt = 0; rt < 8; ++rt) {
+      const float x[8] = {(float)ra[rt][0], (float)ra[rt][1], (float)ra[rt][2], (float)ra[rt][3],
+                          (float)rb[rt][0], (float)rb[rt][1], (float)rb[rt][2], (float)rb[rt][3]};
+      S[rt][0] = zero4();
+      S[rt][1] = zero4();
+      if constexpr (sizeof(TSin) == 2) {
+        const Frag<true> f = make_frag<true>(x);   // (the stored bf16 values: exact)
         mma(S[rt][0], f, id0);
         mma(S[rt][1], f, id1);
-      }
-    } else {
-      f32x4 ra[8], rb[8];
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const TSin* rp = sp + (int64_t)(16 * rt + r16) * V;
-        ra[rt] = *reinterpret_cast<const f32x4*>(rp);
-        rb[rt] = *reinterpret_cast<const f32x4*>(rp + 16);
-      }
-      issue_tok(0, tok);
-      const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const float x[8] = {ra[rt][0], ra[rt][1], ra[rt][2], ra[rt][3], rb[rt][0], rb[rt][1], rb[rt][2], rb[rt][3]};
+      } else {
         Frag<true> fa, fb, fc;
         split3(x, fa, fb, fc);
-        S[rt][0] = zero4();
-        S[rt][1] = zero4();
         mma(S[rt][0], fa, id0);
         mma(S[rt][1], fa, id1);
         mma(S[rt][0], fb, id0);
@@ -735,11 +736,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         mma(S[rt][1], fc, id1);
       }
     }
-  }
+  };
 
   const int nchunk = (T + DC - 1) / DC;
-#pragma unroll 1
-  for (int c0 = 0; c0 < nchunk; ++c0) {
+  // everything of a chunk up to W and U (LDS operands only)
+  auto chunk_operands = [&](int c0) {
     const int tb = c0 * DC;
     // ---- token rows: prologue (gdn2.py:2393-2438) into LDS
     {
@@ -791,61 +792,96 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (tid == 0) sWide[0] = 0;
     }
     __syncthreads();
-    // ---- L per channel (double-float running sum), documents per token
-    if (tid < K) {
-      float gv[DC];
-#pragma unroll
-      for (int t = 0; t < DC; ++t) gv[t] = sL[t * DCP + tid];
-      float hi = 0.f, lo = 0.f;
+    // ---- L per channel (double-float running sum), the documents, and the
+    // row factors: thread (channel c = tid & 127, tokens 8h..8h+7, h = tid >> 7);
+    // both threads of a channel form the whole sum, each writes its half
+    {
+      const int c = tid & 127, h = tid >> 7;
+      // the running sums and documents of this thread's half only (static
+      // register indices: a token belongs to the half under a predicate)
+      float Lh[8], Ll[8];
+      int doc8[8], d = 0;
+      float hi = 0.f, lo = 0.f, g0 = 0.f;
 #pragma unroll
       for (int t = 0; t < DC; ++t) {
-        const float sum = hi + gv[t];
+        const float gv = sL[t * DCP + c];
+        if (t == 0) g0 = gv;
+        d += sDoc[DC + t];
+        const float sum = hi + gv;
         const float bbv = sum - hi;
-        lo += (hi - (sum - bbv)) + (gv[t] - bbv);
+        lo += (hi - (sum - bbv)) + (gv - bbv);
         hi = sum;
-        sL[t * DCP + tid] = hi;
-        sLl[t * DCP + tid] = lo;
+        if ((t >> 3) == h) { Lh[t & 7] = hi; Ll[t & 7] = lo; doc8[t & 7] = d; }
+        if (tid == t) sDoc[t] = d;   // (read after the barrier below the factors)
       }
+      const int dl = d;
       // L_0 - L_15 >= 0 (g <= 0): the chunk's decay span on this channel
-      if (-(hi + lo) + gv[0] > kChunkSpan) sWide[0] = 1;
-    } else if (tid < K + DC) {
-      const int t = tid - K;
-      int d = 0;
-      for (int u = 0; u <= t; ++u) d += sDoc[DC + u];
-      sDoc[t] = d;
+      const bool wide = -(hi + lo) + g0 > kChunkSpan;
+      if (__any(wide) && l == 0) sWide[0] = 1;
+      if (h == 0) sD[c] = dl == 0 ? __expf(hi + lo) : 0.f;
+      __syncthreads();   // both halves have read g
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float lh = Lh[j], ll = Ll[j];
+        const int dt = doc8[j];
+        const int o = (8 * h + j) * DCP + c;
+        sL[o] = lh;
+        sLl[o] = ll;
+        const float eL = __expf(lh + ll);                     // e^{L_t} <= 1
+        const float eK = __expf((hi - lh) + (lo - ll));       // e^{L_end - L_t} <= 1
+        sBe[o] = dt == 0 ? sB[o] * eL : 0.f;
+        sQe[o] = dt == 0 ? sQ[o] * eL : 0.f;
+        sKe[o] = dt == dl ? sK[o] * eK : 0.f;
+      }
     }
     __syncthreads();
     // ---- A and M
-    if (!sWide[0]) {
+    const bool wide = sWide[0] != 0;
+    if (!wide) {
       // factored: A = (b k e^{L - L_8}) (k e^{L_8 - L})^T, M = (q e^{L - L_8}) (k e^{L_8 - L})^T
-      // on MFMA, wave 0 for A and wave 1 for M (lane (t | s = r16, q), 32-channel slabs)
-      if (w < 2) {
-        const float* X = w == 0 ? sB : sQ;
-        f32x4 acc = zero4();
+      // on MFMA: wave w sums over channel slab w (lane (t | s = r16, q)) and
+      // leaves its partial A and M in that slab's columns of L, which only it reads
+      f32x4 pa = zero4(), pm = zero4();
+      {
+        const int s2 = w;
+        float xb[8], xq[8], kc[8], lr[8], lrl[8], lt[8], ltl[8];
+        row8<float>(&sB[r16 * DCP + 32 * s2], q, xb);
+        row8<float>(&sQ[r16 * DCP + 32 * s2], q, xq);
+        row8<float>(&sK[r16 * DCP + 32 * s2], q, kc);
+        row8<float>(&sL[8 * DCP + 32 * s2], q, lr);
+        row8<float>(&sLl[8 * DCP + 32 * s2], q, lrl);
+        row8<float>(&sL[r16 * DCP + 32 * s2], q, lt);
+        row8<float>(&sLl[r16 * DCP + 32 * s2], q, ltl);
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-          float xr[8], kc[8], lr[8], lrl[8], lt[8], ltl[8];
-          row8<float>(&X[r16 * DCP + 32 * s2], q, xr);
-          row8<float>(&sK[r16 * DCP + 32 * s2], q, kc);
-          row8<float>(&sL[8 * DCP + 32 * s2], q, lr);
-          row8<float>(&sLl[8 * DCP + 32 * s2], q, lrl);
-          row8<float>(&sL[r16 * DCP + 32 * s2], q, lt);
-          row8<float>(&sLl[r16 * DCP + 32 * s2], q, ltl);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float d = (lt[e] - lr[e]) + (ltl[e] - lrl[e]);   // row r16: L - L_8
-            xr[e] *= __expf(d);
-            kc[e] *= __expf(-d);
-          }
-          P::m33(acc, P::f3(xr), P::f3(kc));   // acc[ii] = (row 4q + ii) . (column r16)
+        for (int e = 0; e < 8; ++e) {
+          const float d = (lt[e] - lr[e]) + (ltl[e] - lrl[e]);   // row r16: L - L_8
+          const float ex = __expf(d);
+          xb[e] *= ex;
+          xq[e] *= ex;
+          kc[e] *= __expf(-d);
         }
+        const F3 fk = P::f3(kc);
+        P::m33(pa, P::f3(xb), fk);   // pa[ii] = (row 4q + ii) . (column r16)
+        P::m33(pm, P::f3(xq), fk);
+      }
+      // partial tile of slab w: A at columns 32w + 0..15, M at 32w + 16..31
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int t = 4 * q + ii, s2 = r16;
-          const bool same = sDoc[t] == sDoc[s2];
-          if (w == 0) sA[t * (DC + 1) + s2] = (s2 < t && same) ? acc[ii] : 0.f;
-          else sM[t * (DC + 1) + s2] = (s2 <= t && same) ? acc[ii] : 0.f;
+      for (int ii = 0; ii < 4; ++ii) {
+        sL[(4 * q + ii) * DCP + 32 * w + r16] = pa[ii];
+        sL[(4 * q + ii) * DCP + 32 * w + 16 + r16] = pm[ii];
+      }
+      __syncthreads();
+      {
+        const int t = tid & 15, s2 = tid >> 4;
+        float a = 0.f, m = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          a += sL[t * DCP + 32 * ww + s2];
+          m += sL[t * DCP + 32 * ww + 16 + s2];
         }
+        const bool same = sDoc[t] == sDoc[s2];
+        sA[t * (DC + 1) + s2] = (s2 < t && same) ? a : 0.f;
+        sM[t * (DC + 1) + s2] = (s2 <= t && same) ? m : 0.f;
       }
     } else {
       // one exponential per pair: thread (t = tid & 15, s = tid >> 4)
@@ -874,71 +910,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       sM[t * (DC + 1) + s2] = m;   // 0 above the diagonal and across documents
     }
     __syncthreads();
-    // ---- Tm = (I + A)^-1 by forward substitution (lane j: column j)
-    if (tid < DC) {
-      const int j = tid;
-      float tc[DC];
-#pragma unroll
-      for (int i = 0; i < DC; ++i) tc[i] = i == j ? 1.f : 0.f;
-#pragma unroll
-      for (int i = 1; i < DC; ++i) {
-        float acc = 0.f;
-#pragma unroll
-        for (int m = 0; m < i; ++m) acc = fmaf(sA[i * (DC + 1) + m], tc[m], acc);
-        if (i > j) tc[i] = -acc;
-      }
-#pragma unroll
-      for (int i = 0; i < DC; ++i) sT[i * (DC + 1) + j] = tc[i];
-    }
-    // ---- row factors in place (thread: token s, channels 8cg..8cg+7):
-    // be = (b k e^L)_first, q e^L (first), k e^{L_end - L} (last); D
-    // (reads L, sB, sQ, sK only: runs beside the substitution)
+    // ---- W and U by forward substitution, (I + A) W = be and (I + A) U = w v:
+    // thread tid < 128 solves column tid of W (into sL), the others column
+    // tid - 128 of U (into sLl); every thread reads its own column only
     {
-      const int sr = tid >> 4, c8 = 8 * (tid & 15);
-      const int dl = sDoc[DC - 1];
-      const bool first = sDoc[sr] == 0, last = sDoc[sr] == dl;
+      const int c = tid & 127;
+      const float* rhs = tid < K ? sBe : sV;
+      float* dst = tid < K ? sL : sLl;
+      float x[DC];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int o = sr * DCP + c8 + e;
-        const float lt = sL[o], ltl = sLl[o];
-        const float le = sL[(DC - 1) * DCP + c8 + e], lel = sLl[(DC - 1) * DCP + c8 + e];
-        const float eL = __expf(lt + ltl);
-        sB[o] = first ? sB[o] * eL : 0.f;
-        sQ[o] = first ? sQ[o] * eL : 0.f;
-        sK[o] = last ? sK[o] * __expf((le - lt) + (lel - ltl)) : 0.f;
-        if (sr == 0) sD[c8 + e] = dl == 0 ? __expf(le + lel) : 0.f;
+      for (int t = 0; t < DC; ++t) x[t] = rhs[t * DCP + c];
+#pragma unroll
+      for (int t = 1; t < DC; ++t) {
+        // row t's reads where they are used (hoisting all 120 would hold them live)
+        __builtin_amdgcn_sched_barrier(0);
+        float acc = x[t];
+#pragma unroll
+        for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sA[t * (DC + 1) + s2], x[s2], acc);
+        x[t] = acc;
       }
+#pragma unroll
+      for (int t = 0; t < DC; ++t) dst[t * DCP + c] = x[t];
     }
     __syncthreads();
-    // ---- W = Tm be -> sL, U = Tm (w v) -> sLl (thread: token t, channels 8cg..8cg+7)
-    {
-      const int t = tid >> 4, c8 = 8 * (tid & 15);
-      float tr[DC];
-#pragma unroll
-      for (int s2 = 0; s2 < DC; ++s2) tr[s2] = sT[t * (DC + 1) + s2];
-      float aw[8], au[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { aw[e] = 0.f; au[e] = 0.f; }
-#pragma unroll
-      for (int s2 = 0; s2 < DC; ++s2) {
-        float be[8], wv[8];
-        ld4<float>(&sB[s2 * DCP + c8], be);
-        ld4<float>(&sB[s2 * DCP + c8 + 4], be + 4);
-        ld4<float>(&sV[s2 * DCP + c8], wv);
-        ld4<float>(&sV[s2 * DCP + c8 + 4], wv + 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          aw[e] = fmaf(tr[s2], be[e], aw[e]);   // Tm is 0 above the diagonal
-          au[e] = fmaf(tr[s2], wv[e], au[e]);
-        }
-      }
-      __syncthreads();   // every thread has read L before W and U replace it
-      st4<float>(&sL[t * DCP + c8], aw);
-      st4<float>(&sL[t * DCP + c8 + 4], aw + 4);
-      st4<float>(&sLl[t * DCP + c8], au);
-      st4<float>(&sLl[t * DCP + c8 + 4], au + 4);
-    }
-    __syncthreads();
+  };
+  // the wave's state columns: outputs and the state update
+  auto chunk_products = [&](int c0) {
+    const int tb = c0 * DC;
     // ---- the wave's 32 state columns: Vn, O, state update
     {
       f32x4 vn[2], o[2];
@@ -959,7 +957,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         float xw[8], xq[8];
         row8<float>(&sL[r16 * DCP + 32 * s2], q, xw);
-        row8<float>(&sQ[r16 * DCP + 32 * s2], q, xq);
+        row8<float>(&sQe[r16 * DCP + 32 * s2], q, xq);
 #pragma unroll
         for (int e = 0; e < 8; ++e) xw[e] = -xw[e];
         const F3 Wf = P::f3(xw), Qf = P::f3(xq);
@@ -1001,8 +999,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) {
         const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sD[16 * rt + 4 * q]);
-        const float xk[8] = {sK[(4 * q) * DCP + 16 * rt + r16], sK[(4 * q + 1) * DCP + 16 * rt + r16],
-                             sK[(4 * q + 2) * DCP + 16 * rt + r16], sK[(4 * q + 3) * DCP + 16 * rt + r16],
+        const float xk[8] = {sKe[(4 * q) * DCP + 16 * rt + r16], sKe[(4 * q + 1) * DCP + 16 * rt + r16],
+                             sKe[(4 * q + 2) * DCP + 16 * rt + r16], sKe[(4 * q + 3) * DCP + 16 * rt + r16],
                              0.f, 0.f, 0.f, 0.f};
         const F3 Kf = P::f3(xk);
 #pragma unroll
@@ -1017,6 +1015,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __builtin_amdgcn_sched_barrier(0);   // (not hoisted into the products above)
     if (c0 + 1 < nchunk) issue_tok(tb + DC, tok);
     __syncthreads();
+  };
+  chunk_operands(0);
+  state_in();
+  chunk_products(0);
+#pragma unroll 1
+  for (int c0 = 1; c0 < nchunk; ++c0) {
+    chunk_operands(c0);
+    chunk_products(c0);
   }
 
   // ---- state out, without LDS: the accumulator pair of slab s2 read as an A

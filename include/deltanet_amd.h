@@ -143,12 +143,14 @@ int dn_decode_step(const dn_decode_args* a, void* stream);
  * Same arguments as dn_decode_step except that every per-token tensor carries
  * a token axis after the batch axis: q, k (B,T,Hk,K); v, out (B,T,Hv,V); gates
  * (B,T,Hx,Cx); reset NULL or (B,T), clearing the state before that token.  The
- * result is the recurrence of T chained dn_decode_step calls with the state
- * carried in fp32 across the T tokens and converted to state_out_dtype once
- * (chained bf16 steps round it after every token); stability_guard caps after
- * every token.  T >= 8 without the guard runs as 16-token chunks in the
- * chunked WY form (fp32 products on the fp32 matrix cores when either state is
- * fp32, split bf16 for a bf16 state).  T == 1 is dn_decode_step. */
+ * result is the recurrence of T chained dn_decode_step calls; stability_guard
+ * caps after every token.  T >= 8 without the guard runs as 16-token chunks in
+ * the chunked WY form (fp32 products on the fp32 matrix cores when either state
+ * is fp32, split bf16 for a bf16 state) and carries the state in fp32 across
+ * the T tokens, converting it to state_out_dtype once; the other launches
+ * round a bf16 state after every token, as chained steps do.  A bf16 state
+ * therefore agrees with chained steps to bf16 rounding.  T == 1 is
+ * dn_decode_step. */
 int dn_decode_steps(const dn_decode_args* a, int32_t T, void* stream);
 
 /* Arguments of the training backward of the chunked recurrence.  All tensors

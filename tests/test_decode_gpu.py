@@ -257,10 +257,15 @@ def test_decode_steps_equal_chained_steps(state_dtype, guard, T):
     ro, rs = rel_l2(as_np(o_m), as_np(o_c)), rel_l2(as_np(s_m), as_np(st))
     print(f"multi vs chained T={T}: out {ro:.2e} state {rs:.2e}")
     if state_dtype == "bfloat16":
-        # the launch rounds the state once, the chained steps after every
-        # token: they agree at the bf16 rounding level, and the launch is
-        # within one final rounding of the unrounded recurrence
-        assert ro < 1e-2 and rs < 1e-2
+        if T < 8 or guard:
+            # the per-token kernel rounds the state after every token, as the
+            # chained steps do: the same values up to the summation order
+            assert ro < 2e-4 and rs < 2e-4
+        else:
+            # the chunked launch rounds the state once, the chained steps
+            # after every token: they agree at the bf16 rounding level
+            assert ro < 1e-2 and rs < 1e-2
+        # and either stays within bf16 rounding of the unrounded recurrence
         bfr = lambda x: O.bf16_round(x).astype(np.float64)
         ref_o, ref_s = chain_oracle(bfr(q), bfr(k), bfr(v), g, b, w, as_np(st0).astype(np.float64), reset,
                                     qk_l2norm=True, stability_guard=guard, stability_tau=20.0)
@@ -345,8 +350,9 @@ def test_decode_odd_matrix_count(state_dtype, B, Hk, Hv):
 def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv, Tn):
     # T tokens in one launch with an odd number of state matrices: equal to
     # T chained single steps up to the summation order (the kernels split the
-    # state rows differently over lanes; Tn = 12 runs the chunked form) and
-    # the bf16 state's single rounding, and the fp32 run to the oracle
+    # state rows differently over lanes; Tn = 12 runs the chunked form, which
+    # rounds a bf16 state once instead of after every token), and the fp32
+    # run to the oracle
     q, k, v, g, b, w = steps_inputs(92 + B, B, Tn, Hk, Hv)
     S0 = 0.3 * np.random.default_rng(93).standard_normal((B, Hv, 128, 128))
     reset = np.zeros((B, Tn), bool)
@@ -362,7 +368,7 @@ def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv, Tn):
         outs.append(o1)
     ro, rs = rel_l2(as_np(o_m), as_np(torch.stack(outs, 1))), rel_l2(as_np(s_m), as_np(st))
     print(f"odd multi vs chained: out {ro:.2e} state {rs:.2e}")
-    bound = 1e-2 if state_dtype == "bfloat16" else (1e-6 if Tn < 8 else 1e-5)
+    bound = (2e-4 if Tn < 8 else 1e-2) if state_dtype == "bfloat16" else (1e-6 if Tn < 8 else 1e-5)
     assert ro < bound and rs < bound
     # every matrix, the last one included, carries its own state
     for i in range(B):
