@@ -620,7 +620,7 @@ def main():
 
     import torch
 
-    from deltanet_tpu_amd import _lib, chunk_gdn, chunk_gdn2, gdn2_decode_step
+    from deltanet_tpu_amd import _lib, chunk_gdn, chunk_gdn2, gdn2_decode_step, gdn2_decode_steps
 
     _TRACE["on"] = not args.no_kernel_trace
 
@@ -746,6 +746,36 @@ def main():
                     "frac_hbm_peak": round(sbytes / (kus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"decode {tag}: {us:.1f} us/step (kernel {kus:.1f} us, {dec[tag]['state_GBps']} GB/s)")
 
+    # ---- multi-token decode (dn_decode_steps), config-4 shape, 16 tokens per launch
+    dsteps = {}
+    if args.decode_steps > 0:
+        Tm = 16
+        gm = torch.Generator(device=dev)
+        gm.manual_seed(41)
+        rn = lambda *s_: torch.randn(*s_, device=dev, generator=gm)
+        Bm, Hkm, Hvm = dq.shape[0], dq.shape[2], dv.shape[2]
+        mq, mk = rn(Bm, Tm, Hkm, 128).to(torch.bfloat16), rn(Bm, Tm, Hkm, 128).to(torch.bfloat16)
+        mv = rn(Bm, Tm, Hvm, 128).to(torch.bfloat16)
+        mg = -torch.exp(0.39 * rn(Bm, Tm, Hkm, 128) - 1.0)
+        mb, mw = torch.sigmoid(0.39 * rn(Bm, Tm, Hkm, 128)), torch.sigmoid(0.39 * rn(Bm, Tm, Hvm, 128))
+        for sd, elt in (("float32", 4), ("bfloat16", 2)):
+            s_in = st if sd == "float32" else st.to(torch.bfloat16)
+            pair = [s_in, torch.empty_like(s_in)]
+
+            def mstep():
+                gdn2_decode_steps(mq, mk, mv, mg, mb, mw, pair[0], qk_l2norm=True, state_dtype=sd, out_state=pair[1])
+                pair.reverse()
+
+            n = max(4, args.decode_steps // 4)
+            us = time_calls(torch, mstep, n, 3) * 1e3
+            kt = kernel_times(torch, mstep, n)
+            kus = next((v_ for k_, v_ in (kt or {}).items() if k_.startswith("k_decode")), us)
+            sbytes = 2 * st.numel() * elt
+            dsteps[sd] = {"tokens_per_launch": Tm, "us_per_launch": round(us, 2), "kernel_us": round(kus, 2),
+                          "kernel_us_per_token": round(kus / Tm, 2),
+                          "state_GBps": round(sbytes / (kus * 1e-6) / 1e9, 1)}
+            log(f"decode_steps {sd} T={Tm}: kernel {kus:.1f} us ({kus / Tm:.1f} us/token)")
+
     # ---- training step (forward + backward) at the config-2 shape ----------
     train = None
     if args.train_steps > 0:
@@ -857,6 +887,8 @@ def main():
         "roofline": roof,
         "decode": {"workload": "gdn2_decode_step, BASELINE config 4: B=256 Hk=16 Hv=32 K=V=128, bf16 qkv, "
                                "channel-wise fp32 gates, qk_l2norm", **dec},
+        "decode_steps": {"workload": "gdn2_decode_steps, config-4 shape, 16 tokens per launch (chunked WY form), "
+                                     "bf16 qkv, channel-wise fp32 gates, qk_l2norm", **dsteps},
         "training": train,
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,
