@@ -614,6 +614,7 @@ __device__ __forceinline__ void bits8_f(const Raw8w& r, int dt, float* x) {
 
 constexpr int DC = 16;      // tokens per chunk
 constexpr int DCP = 132;    // fp32 pitch of the [token][channel] LDS arrays
+constexpr int AP = 20;      // fp32 pitch of the 16 x 16 token-pair arrays (16-byte rows)
 
 // An fp32 fragment as three bf16 fragments whose sum is exactly x (8
 // significant bits each: the remainders after each rounding are exact in
@@ -641,7 +642,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int K = 128, V = 128;
   using P = Pol<BF>;
   using F3 = typename P::F3;
-  __shared__ __align__(16) float lds[9 * DC * DCP + 2 * DC * (DC + 1) + K + 3 * DC];
+  __shared__ __align__(16) float lds[9 * DC * DCP + 2 * DC * AP + K + 3 * DC];
   float* sQ = lds;                  // q                                [DC][DCP]
   float* sK = sQ + DC * DCP;        // k
   float* sB = sK + DC * DCP;        // b k
@@ -652,8 +653,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* sQe = sBe + DC * DCP;      // (q e^L)_first
   float* sKe = sQe + DC * DCP;      // (k e^{L_end - L})_last
   float* sA = sKe + DC * DCP;       // A   [DC][DC + 1]
-  float* sM = sA + DC * (DC + 1);   // M
-  float* sD = sM + DC * (DC + 1);   // state row factor of the chunk
+  float* sM = sA + DC * AP;   // M
+  float* sD = sM + DC * AP;   // state row factor of the chunk
   int* sDoc = reinterpret_cast<int*>(sD + K);   // [0, DC): document of token t; [DC, 2DC): reset flags
   int* sWide = sDoc + 2 * DC;                    // a channel's decay span exceeds kChunkSpan
 
@@ -767,11 +768,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       sq = row16_sum(sq);
       sk = row16_sum(sk);
       float yq[8], yk[8], yb[8], yg[8], yv[8];
+      const float iq = 1.f / sqrtf(sq + 1e-6f), ik = 1.f / sqrtf(sk + 1e-6f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (p.l2norm) {
-          yq[e] = xq[e] / sqrtf(sq + 1e-6f) * p.scale;
-          yk[e] = xk[e] / sqrtf(sk + 1e-6f);
+          yq[e] = xq[e] * iq * p.scale;
+          yk[e] = xk[e] * ik;
         } else {
           yq[e] = xq[e] * p.scale;
           yk[e] = xk[e];
@@ -880,8 +882,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           m += sL[t * DCP + 32 * ww + 16 + s2];
         }
         const bool same = sDoc[t] == sDoc[s2];
-        sA[t * (DC + 1) + s2] = (s2 < t && same) ? a : 0.f;
-        sM[t * (DC + 1) + s2] = (s2 <= t && same) ? m : 0.f;
+        sA[t * AP + s2] = (s2 < t && same) ? a : 0.f;
+        sM[t * AP + s2] = (s2 <= t && same) ? m : 0.f;
       }
     } else {
       // one exponential per pair: thread (t = tid & 15, s = tid >> 4)
@@ -906,8 +908,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
       }
-      sA[t * (DC + 1) + s2] = s2 < t ? a : 0.f;
-      sM[t * (DC + 1) + s2] = m;   // 0 above the diagonal and across documents
+      sA[t * AP + s2] = s2 < t ? a : 0.f;
+      sM[t * AP + s2] = m;   // 0 above the diagonal and across documents
     }
     __syncthreads();
     // ---- W and U by forward substitution, (I + A) W = be and (I + A) U = w v:
@@ -926,7 +928,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         __builtin_amdgcn_sched_barrier(0);
         float acc = x[t];
 #pragma unroll
-        for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sA[t * (DC + 1) + s2], x[s2], acc);
+        for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sA[t * AP + s2], x[s2], acc);
         x[t] = acc;
       }
 #pragma unroll
@@ -975,8 +977,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         Vf[ct] = P::f3(x);
       }
       {
-        const float xm[8] = {sM[r16 * (DC + 1) + 4 * q], sM[r16 * (DC + 1) + 4 * q + 1],
-                             sM[r16 * (DC + 1) + 4 * q + 2], sM[r16 * (DC + 1) + 4 * q + 3], 0.f, 0.f, 0.f, 0.f};
+        const float xm[8] = {sM[r16 * AP + 4 * q], sM[r16 * AP + 4 * q + 1],
+                             sM[r16 * AP + 4 * q + 2], sM[r16 * AP + 4 * q + 3], 0.f, 0.f, 0.f, 0.f};
         const F3 Mf = P::f3(xm);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) P::m33(o[ct], Mf, Vf[ct]);
