@@ -377,8 +377,8 @@ def _kname(n):
     if not m or "dn" not in n:
         return None
     k = m.group(1)
-    if k == "k_decode":
-        return "k_decode<bf16>" if ("DF16b" in n or "bf16" in n) else "k_decode<f32>"
+    if k in ("k_decode", "k_decode_chunk"):
+        return k + ("<bf16>" if ("DF16b" in n or "bf16" in n) else "<f32>")
     return k
 
 
@@ -410,7 +410,7 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
     work = prefill_work()
     out = {"fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
     lines = ["# rocprofv3 kernel trace + PMC traffic, bench.py workload (prefill BASELINE config 2, "
-             "decode config 4)", "",
+             "decode config 4, 16-token decode launches at the config-4 shape)", "",
              "Kernel durations from:", "    " + KT_CMD, "",
              "HBM traffic per dispatch from two counter runs:",
              "    " + PMC_CMD.format(ctr="FETCH_SIZE", d="pmc_f"),
@@ -421,11 +421,16 @@ def rocprof_summary(kt_dir, f_dir, w_dir):
              "| kernel | dispatches | avg us | min us | max us | fetch MB | write MB | algorithmic MB | "
              "traffic / algorithmic |",
              "|---|---|---|---|---|---|---|---|---|"]
+    # the 16-token decode launch: state in and out, plus q, k, v (bf16), g, b (fp32, Hk heads), w (fp32, Hv
+    # heads) and the bf16 output of its 16 tokens
+    tok16 = 256 * 16 * 128 * (2 * 16 * 2 + 32 * 2 + 2 * 16 * 4 + 32 * 4 + 32 * 2)
     alg = {"k_prepass": work["prepass"]["bytes"], "k_chain": work["chain"]["bytes"],
            "k_decode<f32>": 2 * 256 * 32 * 128 * 128 * 4, "k_decode<bf16>": 2 * 256 * 32 * 128 * 128 * 2,
+           "k_decode_chunk<f32>": 2 * 256 * 32 * 128 * 128 * 4 + tok16,
+           "k_decode_chunk<bf16>": 2 * 256 * 32 * 128 * 128 * 2 + tok16,
            "copy (calibration)": 2 * COPY_BYTES}
-    for k in ("k_prepass", "k_chain", "k_decode<f32>", "k_decode<bf16>",
-              "copy (calibration)"):
+    for k in ("k_prepass", "k_chain", "k_decode<f32>", "k_decode<bf16>", "k_decode_chunk<f32>",
+              "k_decode_chunk<bf16>", "copy (calibration)"):
         if k not in dur:
             continue
         v = dur[k]
