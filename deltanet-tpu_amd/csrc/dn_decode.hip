@@ -647,11 +647,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* sK = sQ + DC * DCP;        // k
   float* sB = sK + DC * DCP;        // b k
   float* sL = sB + DC * DCP;        // g -> L (high word) -> A / M partial sums -> W
-  float* sLl = sL + DC * DCP;       // L (low word) -> U
+  float* sLl = sL + DC * DCP;       // L (low word) -> U^T [V][DC]
   float* sV = sLl + DC * DCP;       // w v
   float* sBe = sV + DC * DCP;       // (b k e^L)_first
   float* sQe = sBe + DC * DCP;      // (q e^L)_first
-  float* sKe = sQe + DC * DCP;      // (k e^{L_end - L})_last
+  float* sKe = sQe + DC * DCP;      // (k e^{L_end - L})_last, transposed [K][DC]
   float* sA = sKe + DC * DCP;       // A   [DC][DC + 1]
   float* sM = sA + DC * AP;   // M
   float* sD = sM + DC * AP;   // state row factor of the chunk
@@ -822,6 +822,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (__any(wide) && l == 0) sWide[0] = 1;
       if (h == 0) sD[c] = dl == 0 ? __expf(hi + lo) : 0.f;
       __syncthreads();   // both halves have read g
+      float ke8[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float lh = Lh[j], ll = Ll[j];
@@ -833,8 +834,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float eK = __expf((hi - lh) + (lo - ll));       // e^{L_end - L_t} <= 1
         sBe[o] = dt == 0 ? sB[o] * eL : 0.f;
         sQe[o] = dt == 0 ? sQ[o] * eL : 0.f;
-        sKe[o] = dt == dl ? sK[o] * eK : 0.f;
+        ke8[j] = dt == dl ? sK[o] * eK : 0.f;
       }
+      // ke^T (row = channel, 16 tokens): the update's A operand is one 16-byte read
+      st4<float>(&sKe[c * DC + 8 * h], ke8);
+      st4<float>(&sKe[c * DC + 8 * h + 4], ke8 + 4);
     }
     __syncthreads();
     // ---- A and M
@@ -918,7 +922,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     {
       const int c = tid & 127;
       const float* rhs = tid < K ? sBe : sV;
-      float* dst = tid < K ? sL : sLl;
       float x[DC];
 #pragma unroll
       for (int t = 0; t < DC; ++t) x[t] = rhs[t * DCP + c];
@@ -931,8 +934,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sA[t * AP + s2], x[s2], acc);
         x[t] = acc;
       }
+      if (tid < K) {
 #pragma unroll
-      for (int t = 0; t < DC; ++t) dst[t * DCP + c] = x[t];
+        for (int t = 0; t < DC; ++t) sL[t * DCP + c] = x[t];
+      } else {
+        // U^T (row = value column, 16 tokens): the products' accumulator init is one 16-byte read
+#pragma unroll
+        for (int t4 = 0; t4 < DC; t4 += 4) st4<float>(&sLl[c * DC + t4], x + t4);
+      }
     }
     __syncthreads();
   };
@@ -945,8 +954,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         o[ct] = zero4();
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) vn[ct][ii] = sLl[(4 * q + ii) * DCP + 32 * w + 16 * ct + r16];
+        vn[ct] = *reinterpret_cast<const f32x4*>(&sLl[(32 * w + 16 * ct + r16) * DC + 4 * q]);
       }
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
@@ -977,8 +985,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         Vf[ct] = P::f3(x);
       }
       {
-        const float xm[8] = {sM[r16 * AP + 4 * q], sM[r16 * AP + 4 * q + 1],
-                             sM[r16 * AP + 4 * q + 2], sM[r16 * AP + 4 * q + 3], 0.f, 0.f, 0.f, 0.f};
+        const f32x4 m4 = *reinterpret_cast<const f32x4*>(&sM[r16 * AP + 4 * q]);
+        const float xm[8] = {m4[0], m4[1], m4[2], m4[3], 0.f, 0.f, 0.f, 0.f};
         const F3 Mf = P::f3(xm);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) P::m33(o[ct], Mf, Vf[ct]);
@@ -1001,9 +1009,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) {
         const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sD[16 * rt + 4 * q]);
-        const float xk[8] = {sKe[(4 * q) * DCP + 16 * rt + r16], sKe[(4 * q + 1) * DCP + 16 * rt + r16],
-                             sKe[(4 * q + 2) * DCP + 16 * rt + r16], sKe[(4 * q + 3) * DCP + 16 * rt + r16],
-                             0.f, 0.f, 0.f, 0.f};
+        const f32x4 k4 = *reinterpret_cast<const f32x4*>(&sKe[(16 * rt + r16) * DC + 4 * q]);
+        const float xk[8] = {k4[0], k4[1], k4[2], k4[3], 0.f, 0.f, 0.f, 0.f};
         const F3 Kf = P::f3(xk);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
