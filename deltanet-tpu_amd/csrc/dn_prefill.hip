@@ -1387,14 +1387,19 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
 // remainder runs after the loop: an exit in the middle of a trip would make
 // the loop head wait for every outstanding load, the prefetches included.
 // ===========================================================================
-template <bool BF> struct ChainSets {
-  static constexpr int rec = 4, out = 3;
+template <bool BF, int NTL> struct ChainSets {
+  static constexpr int rec = NTL == 1 ? 4 : 2, out = NTL == 1 ? 3 : 2;
 };
-template <> struct ChainSets<false> {   // fp32 fragments are twice as wide
+template <int NTL> struct ChainSets<false, NTL> {   // fp32 fragments are twice as wide
   static constexpr int rec = 2, out = 3;
 };
 
-template <bool BF, class TO>
+// NTL: 16-column tiles per workgroup.  One tile per workgroup spreads a
+// head's columns over the most CUs (config 2: 192 workgroups); when the tiles
+// outnumber the CUs, a workgroup takes NTL tiles of one value head, so each
+// chunk's Pn and X fragments are loaded once for all of them (the CU's load
+// rate bounds a step: one tile loads 112 KB per chunk, NTL tiles 48 + 64 NTL).
+template <bool BF, class TO, int NTL>
 __global__ __launch_bounds__(512) void k_chain(const PF p) {
   using P = Pol<BF>;
   using F1 = typename P::F1;
@@ -1403,36 +1408,39 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
   using ST = typename SS::ST;
   constexpr int NT = 512;
   constexpr int FR = 4 * 64 * 8;   // elements of one tile's S^T fragment
-  // S_c^T fragment, high and low words, double-buffered
-  __shared__ __align__(16) ST Sh_s[2][FR];
-  __shared__ __align__(16) ST Sl_s[2][BF ? FR : 1];
+  // S_c^T fragments of the NTL tiles, high and low words, double-buffered
+  __shared__ __align__(16) ST Sh_s[2][NTL][FR];
+  __shared__ __align__(16) ST Sl_s[2][NTL][BF ? FR : 1];
   __shared__ int flg[2 * kMaxBlockChunks];   // is_new_doc, all_same_doc per chunk
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63, r16 = l & 15, q = l >> 4;
-  int ct, h, b;
-  xcd_block(ct, h, b);
-  const int hv = p.gates_at_hv ? h : h * p.G + (16 * ct) / KD;
-  const int vc = (16 * ct) % KD;   // first column of the tile inside head hv
-  auto frag_lo = [&](int buf) -> ST* { return BF ? &Sl_s[buf][0] : &Sh_s[buf][0]; };
+  int ctg, h, b;
+  xcd_block(ctg, h, b);
+  const int ct0 = NTL * ctg;       // first tile; the NTL tiles lie in one value head
+  const int hv = p.gates_at_hv ? h : h * p.G + (16 * ct0) / KD;
+  const int vc0 = (16 * ct0) % KD;   // first column of the tiles inside head hv
+  auto frag_lo = [&](int buf, int j) -> ST* { return BF ? &Sl_s[buf][j][0] : &Sh_s[buf][j][0]; };
   // chunk flags into LDS once, so testing them never waits on vector loads
   for (int i = tid; i < 2 * p.NCb; i += NT) flg[i] = p.flags[(int64_t)b * p.NCb * 2 + i];
   __syncthreads();
 
   if (wid < 4) {
     // ---------------- recurrence: state rows 32w.. ----------------
-    constexpr int RS = ChainSets<BF>::rec;
+    constexpr int RS = ChainSets<BF, NTL>::rec;
     const int w = wid;
-    const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + vc + r16;
-    f32x4 S[2];
+    const int64_t sbase = ((int64_t)b * p.Hv + hv) * KD * KD + vc0 + r16;
+    f32x4 S[NTL][2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int j = 0; j < NTL; ++j)
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        S[r][ii] = p.has_init ? p.init[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          S[j][r][ii] = p.has_init ? p.init[sbase + 16 * j + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] : 0.f;
     struct Ops {
       F1 pf[2][4];
-      f32x4 qc[2], dv[2];
+      f32x4 qc[NTL][2], dv[2];
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
@@ -1443,57 +1451,67 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
       for (int r = 0; r < 2; ++r) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) o.pf[r][s] = SS::fa(Pn + fofs(2 * w + r, s, l));
-        o.qc[r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct, p.nct, l));
+#pragma unroll
+        for (int j = 0; j < NTL; ++j) o.qc[j][r] = *reinterpret_cast<const f32x4*>(Qc + cofs(2 * w + r, ct0 + j, p.nct, l));
         o.dv[r] = *reinterpret_cast<const f32x4*>(p.dvec + u * KD + 32 * w + 16 * r + 4 * q);
       }
     };
     auto step = [&](int c, const Ops& o) {
       const int is_new = flg[2 * c], same = flg[2 * c + 1];
-      if (is_new) { S[0] = zero4(); S[1] = zero4(); }
-      // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
-      const float x[8] = {S[0][0], S[0][1], S[0][2], S[0][3], S[1][0], S[1][1], S[1][2], S[1][3]};
       const int fo = (w * 64 + l) * 8;
-      SS::st8s(&Sh_s[c & 1][fo], frag_lo(c & 1) + fo, x);
+#pragma unroll
+      for (int j = 0; j < NTL; ++j) {
+        if (is_new) { S[j][0] = zero4(); S[j][1] = zero4(); }
+        // lane (n, q) holds rows 32w + 16r + 4q + ii = element 4r + ii of slab w
+        const float x[8] = {S[j][0][0], S[j][0][1], S[j][0][2], S[j][0][3],
+                            S[j][1][0], S[j][1][1], S[j][1][2], S[j][1][3]};
+        SS::st8s(&Sh_s[c & 1][j][fo], frag_lo(c & 1, j) + fo, x);
+      }
       lds_barrier();
-      F1 Sf[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][(s * 64 + l) * 8]);
+      for (int j = 0; j < NTL; ++j) {
+        F1 Sf[4];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        f32x4 acc = o.qc[r];
+        for (int s = 0; s < 4; ++s) Sf[s] = SS::fa(&Sh_s[c & 1][j][(s * 64 + l) * 8]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
+        for (int r = 0; r < 2; ++r) {
+          f32x4 acc = o.qc[j][r];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) S[r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[r][ii] : 0.f);
+          for (int s = 0; s < 4; ++s) P::m11(acc, o.pf[r][s], Sf[s]);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) S[j][r][ii] = acc[ii] + (same ? o.dv[r][ii] * S[j][r][ii] : 0.f);
+        }
       }
     };
     Ops o[RS];
 #pragma unroll
-    for (int j = 0; j + 1 < RS; ++j) load_ops(j, o[j]);
+    for (int jj = 0; jj + 1 < RS; ++jj) load_ops(jj, o[jj]);
     const int ntrip = p.NCb / RS;
 #pragma unroll 1
     for (int k = 0; k < ntrip; ++k) {
 #pragma unroll
-      for (int j = 0; j < RS; ++j) {
-        load_ops(RS * k + j + RS - 1, o[(j + RS - 1) % RS]);
-        step(RS * k + j, o[j]);
+      for (int jj = 0; jj < RS; ++jj) {
+        load_ops(RS * k + jj + RS - 1, o[(jj + RS - 1) % RS]);
+        step(RS * k + jj, o[jj]);
       }
     }
     const int rem = p.NCb - RS * ntrip;   // < RS; their operands are loaded
 #pragma unroll
-    for (int j = 0; j + 1 < RS; ++j)
-      if (j < rem) step(RS * ntrip + j, o[j]);
+    for (int jj = 0; jj + 1 < RS; ++jj)
+      if (jj < rem) step(RS * ntrip + jj, o[jj]);
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int j = 0; j < NTL; ++j)
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) p.fin[sbase + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[r][ii];
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) p.fin[sbase + 16 * j + (int64_t)(32 * w + 16 * r + 4 * q + ii) * KD] = S[j][r][ii];
   } else {
     // ---------------- output: token tiles 2t, 2t + 1 ----------------
-    constexpr int OS = ChainSets<BF>::out;
+    constexpr int OS = ChainSets<BF, NTL>::out;
     const int t2 = 2 * (wid - 4);
     struct Ops {
-      F3 xb[2][4];   // X fragments of the two token tiles
-      f32x4 oi[2];   // (M U)^T tiles of the two token tiles
+      F3 xb[2][4];        // X fragments of the two token tiles (all NTL column tiles use them)
+      f32x4 oi[NTL][2];   // (M U)^T tiles of the two token tiles
     };
     auto load_ops = [&](int c, Ops& o) {
       const int cc = min(c, p.NCb - 1);
@@ -1504,36 +1522,44 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
       for (int r = 0; r < 2; ++r) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) o.xb[r][s] = SS::fa3(Xh + fofs(t2 + r, s, l), Xl + fofs(t2 + r, s, l));
-        o.oi[r] = *reinterpret_cast<const f32x4*>(p.OiT + u * (int64_t)(CH * p.Vp) + cofs(t2 + r, ct, p.nct, l));
+#pragma unroll
+        for (int j = 0; j < NTL; ++j)
+          o.oi[j][r] = *reinterpret_cast<const f32x4*>(p.OiT + u * (int64_t)(CH * p.Vp) + cofs(t2 + r, ct0 + j, p.nct, l));
       }
     };
-    f32x4 res[2];
+    f32x4 res[NTL][2];
     auto step = [&](int c, const Ops& o) {
       lds_barrier();
-      res[0] = o.oi[0];
-      res[1] = o.oi[1];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int fs = (s * 64 + l) * 8;
-        const F3 sf = SS::fa3(&Sh_s[c & 1][fs], frag_lo(c & 1) + fs);
-        P::m33(res[0], sf, o.xb[0][s]);
-        P::m33(res[1], sf, o.xb[1][s]);
+      for (int j = 0; j < NTL; ++j) {
+        res[j][0] = o.oi[j][0];
+        res[j][1] = o.oi[j][1];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int fs = (s * 64 + l) * 8;
+          const F3 sf = SS::fa3(&Sh_s[c & 1][j][fs], frag_lo(c & 1, j) + fs);
+          P::m33(res[j][0], sf, o.xb[0][s]);
+          P::m33(res[j][1], sf, o.xb[1][s]);
+        }
       }
     };
-    // lane (t, q) holds O[token 16 (t2 + r) + t][column 16ct + 4q + ii].
+    // lane (t, q) holds O[token 16 (t2 + r) + t][column 16 (ct0 + j) + 4q + ii].
     // Every lane stores (tokens past the end into the workspace's sink): a
     // store skipped under a branch would leave the compiler unsure how many
     // vector-memory operations are pending at the loop head, and it would
     // then wait for all of them (the prefetches included).
     auto store = [&](int c) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int t = p.t0 + c * CH + 16 * (t2 + r) + r16;
-        const bool tv = t < min(p.t0 + p.nt, p.L);
-        const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hv) * KD + vc + 4 * q;
-        TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
-        const float x[4] = {res[r][0], res[r][1], res[r][2], res[r][3]};
-        st4<TO>(dst, x);
+      for (int j = 0; j < NTL; ++j) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int t = p.t0 + c * CH + 16 * (t2 + r) + r16;
+          const bool tv = t < min(p.t0 + p.nt, p.L);
+          const int64_t ob = (((int64_t)b * p.L + (tv ? t : 0)) * p.Hv + hv) * KD + vc0 + 16 * j + 4 * q;
+          TO* dst = tv ? (TO*)p.out + ob : (TO*)p.sink + 4 * l;
+          const float x[4] = {res[j][r][0], res[j][r][1], res[j][r][2], res[j][r][3]};
+          st4<TO>(dst, x);
+        }
       }
     };
     // Each chunk's prefetch is issued before its output store: the wait for
@@ -1541,23 +1567,23 @@ __global__ __launch_bounds__(512) void k_chain(const PF p) {
     // counter counts stores too and drains in order).
     Ops o[OS];
 #pragma unroll
-    for (int j = 0; j + 1 < OS; ++j) load_ops(j, o[j]);
+    for (int jj = 0; jj + 1 < OS; ++jj) load_ops(jj, o[jj]);
     const int ntrip = p.NCb / OS;
 #pragma unroll 1
     for (int k = 0; k < ntrip; ++k) {
 #pragma unroll
-      for (int j = 0; j < OS; ++j) {
-        step(OS * k + j, o[j]);
-        load_ops(OS * k + j + OS - 1, o[(j + OS - 1) % OS]);
-        store(OS * k + j);
+      for (int jj = 0; jj < OS; ++jj) {
+        step(OS * k + jj, o[jj]);
+        load_ops(OS * k + jj + OS - 1, o[(jj + OS - 1) % OS]);
+        store(OS * k + jj);
       }
     }
     const int rem = p.NCb - OS * ntrip;
 #pragma unroll
-    for (int j = 0; j + 1 < OS; ++j)
-      if (j < rem) {
-        step(OS * ntrip + j, o[j]);
-        store(OS * ntrip + j);
+    for (int jj = 0; jj + 1 < OS; ++jj)
+      if (jj < rem) {
+        step(OS * ntrip + jj, o[jj]);
+        store(OS * ntrip + jj);
       }
   }
 }
@@ -1653,6 +1679,16 @@ int check_args(const dn_prefill_args* a) {
   return DN_OK;
 }
 
+int g_chain_tiles = -1;   // -1: unread; 0: by grid size; 1, 2, 4: forced (DN_CHAIN_TILES, measurements)
+int chain_tiles() {
+  if (g_chain_tiles < 0) {
+    const char* e = getenv("DN_CHAIN_TILES");
+    const int v = e ? atoi(e) : 0;
+    g_chain_tiles = (v == 1 || v == 2 || v == 4) ? v : 0;
+  }
+  return g_chain_tiles;
+}
+
 int g_prepass_scalar = -1;   // -1: unread; 0: general path forced (DN_PREPASS_SCALAR=0, measurements)
 
 // One decay and one b per (token, head) with bf16 q / k in precision "bf16"
@@ -1678,7 +1714,19 @@ hipError_t launch_all(const PF& p, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   prof_mark(2, st, false);
-  hipLaunchKernelGGL((k_chain<BF, TV>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
+  // several column tiles per workgroup once the tiles outnumber the CUs
+  // (bf16 mode; config 3: 1024 tiles)
+  const int tiles = (p.Vp / 16) * p.Hx * p.B;
+  int ntl = 1;
+  if constexpr (BF) {
+    ntl = chain_tiles();
+    if (ntl == 0) ntl = tiles >= 4 * 256 ? 4 : (tiles >= 2 * 256 ? 2 : 1);
+    if (ntl == 4)
+      hipLaunchKernelGGL((k_chain<BF, TV, 4>), dim3(p.Vp / 64, p.Hx, p.B), dim3(512), 0, st, p);
+    else if (ntl == 2)
+      hipLaunchKernelGGL((k_chain<BF, TV, 2>), dim3(p.Vp / 32, p.Hx, p.B), dim3(512), 0, st, p);
+  }
+  if (ntl == 1) hipLaunchKernelGGL((k_chain<BF, TV, 1>), dim3(p.Vp / 16, p.Hx, p.B), dim3(512), 0, st, p);
   prof_mark(2, st, true);
   return hipGetLastError();
 }

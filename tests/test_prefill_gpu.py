@@ -109,6 +109,22 @@ def test_scalar_gate_prefill_bf16(case):
     check(out, ro, st, rs, "bf16", "bf16", f"scalar gates {case}")
 
 
+# With more 16-column tiles than 512 (bf16 mode), the chain runs 2 or 4 tiles
+# per workgroup: (B=2 / B=4) x 32 heads x 8 tiles, short sequences, both
+# prepass forms (channel gates; one decay and b per token and head).
+@pytest.mark.parametrize("B", [2, 4])
+@pytest.mark.parametrize("gates", ["channel_hv", "scalar"])
+def test_chain_tiles_per_workgroup(B, gates):
+    Hk, Hv, L = 16, 32, 300
+    layout = ("channel_hv", "channel_hv", "channel_hv") if gates == "channel_hv" else ("rank3_hv", "rank3_hv", "rank3_hv")
+    q, k, v, g, b, w = make_inputs(70 + B, B, L, Hk, Hv, g_layout=layout[0], b_layout=layout[1], w_layout=layout[2])
+    rng = np.random.default_rng(71 + B)
+    seg = np.stack([np.repeat([0, 1, 2], [100, 120, 80]) + 3 * i for i in range(B)])
+    init = 0.1 * rng.standard_normal((B, Hv, 128, 128))
+    out, st, ro, rs = run_pair(q, k, v, g, b, w, dt="bf16", precision="bf16", seg=seg, init=init, qk_l2norm=True)
+    check(out, ro, st, rs, "bf16", "bf16", f"chain tiles B={B} {gates}")
+
+
 @pytest.mark.parametrize("L", [300, 384])
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_fused_prologue_docs_init(L, precision):
