@@ -379,6 +379,10 @@ def _kname(n):
     k = m.group(1)
     if k in ("k_decode", "k_decode_chunk"):
         return k + ("<bf16>" if ("DF16b" in n or "bf16" in n) else "<f32>")
+    if k == "k_chain":
+        t = re.search(r"k_chainILb\dE\w+?Li(\d)E", n)   # column tiles per workgroup
+        if t and t.group(1) != "1":
+            return f"k_chain<{t.group(1)} tiles>"
     return k
 
 
@@ -496,6 +500,7 @@ def rocprof_configs_summary(kt_dir, f_dir=None, w_dir=None):
     w3 = prefill_work(B=4, L=8192, Hk=16, Hv=32, gates="scalar")
     w5 = prefill_work(B=1, L=8192, Hk=16, Hv=32)
     alg = {("k_prepass", (8192, 1, 1)): w3["prepass"]["bytes"], ("k_chain", (8, 32, 4)): w3["chain"]["bytes"],
+           ("k_chain<4 tiles>", (2, 32, 4)): w3["chain"]["bytes"],
            ("k_prepass", (1024, 1, 1)): w5["prepass"]["bytes"], ("k_chain", (16, 16, 1)): w5["chain"]["bytes"]}
     # config 2's grids (B=1, Hk=12, 16 chunks) are the few dispatches of the warm-up and timed cfg-2 calls
     lines = ["# rocprofv3 kernel trace, configs 3 and 5 (bench.py other_configs)", "",
