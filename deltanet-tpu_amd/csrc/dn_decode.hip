@@ -652,6 +652,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* sBe = sV + DC * DCP;       // (b k e^L)_first
   float* sQe = sBe + DC * DCP;      // (q e^L)_first
   float* sKe = sQe + DC * DCP;      // (k e^{L_end - L})_last, transposed [K][DC]
+  // bf16 mode keeps -W, (q e^L)_first and ke^T as split bf16 planes (high
+  // words, then low words) in the space of their fp32 arrays, split once by
+  // the thread that forms them rather than by every wave that reads them
+  bf16* sWh = reinterpret_cast<bf16*>(sL);   // -W   [DC][DCP] high, then low
+  bf16* sQh = reinterpret_cast<bf16*>(sQe);  // q e^L
+  bf16* sKh = reinterpret_cast<bf16*>(sKe);  // ke^T [K][DC]
+  constexpr int WPL = DC * DCP;              // bf16 offset of a low plane
+  constexpr int KPL = K * DC;
   float* sA = sKe + DC * DCP;       // A   [DC][DC + 1]
   float* sM = sA + DC * AP;   // M
   float* sD = sM + DC * AP;   // state row factor of the chunk
@@ -723,7 +731,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       S[rt][0] = zero4();
       S[rt][1] = zero4();
       if constexpr (sizeof(TSin) == 2) {
-        const Frag<true> f = make_frag<true>(x);   // (the stored bf16 values: exact)
+        Frag<true> f;   // the stored bf16 values as they are
+        f.v = __builtin_shufflevector(ra[rt], rb[rt], 0, 1, 2, 3, 4, 5, 6, 7);
         mma(S[rt][0], f, id0);
         mma(S[rt][1], f, id1);
       } else {
@@ -833,12 +842,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float eL = __expf(lh + ll);                     // e^{L_t} <= 1
         const float eK = __expf((hi - lh) + (lo - ll));       // e^{L_end - L_t} <= 1
         sBe[o] = dt == 0 ? sB[o] * eL : 0.f;
-        sQe[o] = dt == 0 ? sQ[o] * eL : 0.f;
+        const float qe = dt == 0 ? sQ[o] * eL : 0.f;
+        if constexpr (BF) {
+          const bf16 hh = (bf16)qe;
+          sQh[(8 * h + j) * DCP + c] = hh;
+          sQh[WPL + (8 * h + j) * DCP + c] = (bf16)(qe - (float)hh);
+        } else {
+          sQe[o] = qe;
+        }
         ke8[j] = dt == dl ? sK[o] * eK : 0.f;
       }
       // ke^T (row = channel, 16 tokens): the update's A operand is one 16-byte read
-      st4<float>(&sKe[c * DC + 8 * h], ke8);
-      st4<float>(&sKe[c * DC + 8 * h + 4], ke8 + 4);
+      if constexpr (BF) {
+        bf16x8 kh, kl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          kh[j] = (bf16)ke8[j];
+          kl[j] = (bf16)(ke8[j] - (float)kh[j]);
+        }
+        *reinterpret_cast<bf16x8*>(&sKh[c * DC + 8 * h]) = kh;
+        *reinterpret_cast<bf16x8*>(&sKh[KPL + c * DC + 8 * h]) = kl;
+      } else {
+        st4<float>(&sKe[c * DC + 8 * h], ke8);
+        st4<float>(&sKe[c * DC + 8 * h + 4], ke8 + 4);
+      }
     }
     __syncthreads();
     // ---- A and M
@@ -935,8 +962,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         x[t] = acc;
       }
       if (tid < K) {
+        if constexpr (BF) {
 #pragma unroll
-        for (int t = 0; t < DC; ++t) sL[t * DCP + c] = x[t];
+          for (int t = 0; t < DC; ++t) {
+            const bf16 hh = (bf16)(-x[t]);
+            sWh[t * DCP + c] = hh;
+            sWh[WPL + t * DCP + c] = (bf16)(-x[t] - (float)hh);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < DC; ++t) sL[t * DCP + c] = x[t];
+        }
       } else {
         // U^T (row = value column, 16 tokens): the products' accumulator init is one 16-byte read
 #pragma unroll
@@ -965,12 +1001,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                               S[2 * s2 + 1][ct][0], S[2 * s2 + 1][ct][1], S[2 * s2 + 1][ct][2], S[2 * s2 + 1][ct][3]};
           Sf[ct] = P::f3(x);
         }
-        float xw[8], xq[8];
-        row8<float>(&sL[r16 * DCP + 32 * s2], q, xw);
-        row8<float>(&sQe[r16 * DCP + 32 * s2], q, xq);
+        F3 Wf, Qf;
+        if constexpr (BF) {
+          auto plane8 = [&](const bf16* pl) {
+            const bf16* rp = pl + r16 * DCP + 32 * s2 + 4 * q;
+            Frag<true> f;
+            f.v = __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(rp), *reinterpret_cast<const bf16x4*>(rp + 16),
+                                          0, 1, 2, 3, 4, 5, 6, 7);
+            return f;
+          };
+          Wf.hi = plane8(sWh); Wf.lo = plane8(sWh + WPL);
+          Qf.hi = plane8(sQh); Qf.lo = plane8(sQh + WPL);
+        } else {
+          float xw[8], xq[8];
+          row8<float>(&sL[r16 * DCP + 32 * s2], q, xw);
+          row8<float>(&sQe[r16 * DCP + 32 * s2], q, xq);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xw[e] = -xw[e];
-        const F3 Wf = P::f3(xw), Qf = P::f3(xq);
+          for (int e = 0; e < 8; ++e) xw[e] = -xw[e];
+          Wf = P::f3(xw);
+          Qf = P::f3(xq);
+        }
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           P::m33(vn[ct], Wf, Sf[ct]);   // Vn[4q + ii][col] = U - W S
@@ -1009,9 +1059,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int rt = 0; rt < 8; ++rt) {
         const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sD[16 * rt + 4 * q]);
-        const f32x4 k4 = *reinterpret_cast<const f32x4*>(&sKe[(16 * rt + r16) * DC + 4 * q]);
-        const float xk[8] = {k4[0], k4[1], k4[2], k4[3], 0.f, 0.f, 0.f, 0.f};
-        const F3 Kf = P::f3(xk);
+        F3 Kf;
+        if constexpr (BF) {
+          const bf16x4 z4 = {};
+          const bf16* kp = sKh + (16 * rt + r16) * DC + 4 * q;
+          Kf.hi.v = __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(kp), z4, 0, 1, 2, 3, 4, 5, 6, 7);
+          Kf.lo.v = __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(kp + KPL), z4, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+          const f32x4 k4 = *reinterpret_cast<const f32x4*>(&sKe[(16 * rt + r16) * DC + 4 * q]);
+          const float xk[8] = {k4[0], k4[1], k4[2], k4[3], 0.f, 0.f, 0.f, 0.f};
+          Kf = P::f3(xk);
+        }
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
 #pragma unroll
