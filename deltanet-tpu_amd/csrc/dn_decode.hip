@@ -1042,18 +1042,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int ct = 0; ct < 2; ++ct) P::m33(o[ct], Mf, Vf[ct]);
       }
       // outputs: lane (c, q) holds tokens 4q..4q+3 of column 32w + 16ct + c
+      // (one 64-bit base per chunk; the chunk's offsets fit 32 bits)
+      {
+        const int ostr = p.Hv * V;   // elements from one token's row to the next
+        const int64_t obase = ((int64_t)bb * T + tb) * ostr + (int64_t)hv * V + 32 * w + r16;
+        auto store_out = [&](auto* op) {
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
+          for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int tt = tb + 4 * q + ii;
-          if (tt < T) {
-            const int64_t oi = (((int64_t)bb * T + tt) * p.Hv + hv) * V + 32 * w + 16 * ct + r16;
-            if (p.v_dt == DT_BF16) ((bf16*)p.out)[oi] = (bf16)o[ct][ii];
-            else if (p.v_dt == DT_F16) ((f16*)p.out)[oi] = (f16)o[ct][ii];
-            else ((float*)p.out)[oi] = o[ct][ii];
-          }
-        }
+            for (int ii = 0; ii < 4; ++ii)
+              if (tb + 4 * q + ii < T) op[(4 * q + ii) * ostr + 16 * ct] = from_f<std::remove_pointer_t<decltype(op)>>(o[ct][ii]);
+        };
+        if (p.v_dt == DT_BF16) store_out((bf16*)p.out + obase);
+        else if (p.v_dt == DT_F16) store_out((f16*)p.out + obase);
+        else store_out((float*)p.out + obase);
       }
       // S <- D S + Ke^T Vn
 #pragma unroll
