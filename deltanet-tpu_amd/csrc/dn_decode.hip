@@ -96,6 +96,42 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// One row (elems elements) of a run-time-typed tensor, base t + row * elems
+// elements, read through a buffer resource: loads are bounds-checked by the
+// hardware (bytes past the row's last whole word read as 0).  Buffer loads
+// need 4-byte-aligned addresses, so the resource starts at the word holding
+// the row's first byte (o0: the row's offset in it) and a 16-bit element is
+// the half of its aligned word that ld_row shifts down.  Loads of a run-time
+// type through typed pointers sit in branches whose joins make the compiler
+// wait for each load before issuing the next; these do not.  The row must
+// stay under 2^31 bytes.
+struct TRow {
+  __amdgpu_buffer_rsrc_t rs;
+  int o0;
+};
+__device__ __forceinline__ TRow row_rsrc(const void* t, int64_t row, int elems, int dt) {
+  const int64_t bytes = (int64_t)elems * (dt == DT_F32 ? 4 : 2);
+  const uintptr_t start = reinterpret_cast<uintptr_t>(t) + row * bytes;
+  const int o0 = (int)(start & 3);
+  // word 3: the gfx9 raw-buffer format (32-bit data, no swizzle)
+  return TRow{__builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(start - o0), (short)0,
+                                                (int)((o0 + bytes + 3) & ~(int64_t)3), 0x00020000),
+              o0};
+}
+// element idx of such a row as raw bits in the low word (f32) or half word
+// (bf16, f16), converted by bits_f once a batch of loads is issued
+__device__ __forceinline__ uint32_t ld_row(const TRow& r, int idx, int dt) {
+  const int bo = r.o0 + idx * (dt == DT_F32 ? 4 : 2);
+  return __builtin_amdgcn_raw_buffer_load_b32(r.rs, bo & ~3, 0, 0) >> (8 * (bo & 2));
+}
+
+// raw bits of an element (f32: the word; bf16 and f16: the low half word) as a float
+__device__ __forceinline__ float bits_f(uint32_t r, int dt) {
+  if (dt == DT_F32) return __builtin_bit_cast(float, r);
+  if (dt == DT_BF16) return __builtin_bit_cast(float, r << 16);
+  return (float)__builtin_bit_cast(f16, (uint16_t)r);
+}
+
 // State loads and stores are non-temporal: each byte is touched once per
 // step, so it should not displace cached lines (measured faster than plain
 // loads and stores at config 4).
@@ -207,35 +243,45 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
   const int cg = tid & 15, rg = tid >> 4;
   const int bh_raw = blockIdx.x * HPW + hs;
   const bool valid = HPW == 1 || bh_raw < p.B * p.Hv;   // an odd count leaves the last half idle
-  const int bh = valid ? bh_raw : p.B * p.Hv - 1;
+  // (wave-uniform: the row resources below live in scalar registers)
+  const int bh = __builtin_amdgcn_readfirstlane(valid ? bh_raw : p.B * p.Hv - 1);
   const int bb = bh / p.Hv, hv = bh % p.Hv;
   const int hk = hv / p.G;
-  const bool rst = p.reset != nullptr && p.reset[bb] != 0;
   const int64_t sbase = (int64_t)bh * K * V;
 
-  // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v
+  // lanes 0-127: element i = tid of q, k, g, b and column j = tid of w, v,
+  // every load issued before the first use of any (no branch between them)
   const int i = tid;
-  float xq = 0.f, xk = 0.f, gv = 0.f, bv = 0.f, wv = 0.f, vv = 0.f;
+  uint32_t xq_ = 0, xk_ = 0, gv_ = 0, bv_ = 0, wv_ = 0, vv_ = 0;
+  int rflag = 0;
+  if (p.reset != nullptr) rflag = p.reset[bb];
   if (tid < 128) {
-    const int64_t qo = ((int64_t)bb * p.Hk + hk) * K + i;
-    xq = ld_f(p.q, qo, p.qk_dt);
-    xk = ld_f(p.k, qo, p.qk_dt);
     const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
     const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
     const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
-    gv = ld_f(p.g, ((int64_t)bb * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
-    bv = ld_f(p.b, ((int64_t)bb * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
-    wv = ld_f(p.w, ((int64_t)bb * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
-    vv = ld_f(p.v, ((int64_t)bb * p.Hv + hv) * V + i, p.v_dt);
+    const auto rq = row_rsrc(p.q, bb, p.Hk * K, p.qk_dt), rk = row_rsrc(p.k, bb, p.Hk * K, p.qk_dt);
+    const auto rg_ = row_rsrc(p.g, bb, p.g_h * p.g_c, p.g_dt), rb_ = row_rsrc(p.b, bb, p.b_h * p.b_c, p.b_dt);
+    const auto rw = row_rsrc(p.w, bb, p.w_h * p.w_c, p.w_dt), rv = row_rsrc(p.v, bb, p.Hv * V, p.v_dt);
+    xq_ = ld_row(rq, hk * K + i, p.qk_dt);
+    xk_ = ld_row(rk, hk * K + i, p.qk_dt);
+    gv_ = ld_row(rg_, hg * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
+    bv_ = ld_row(rb_, hb * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
+    wv_ = ld_row(rw, hw * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
+    vv_ = ld_row(rv, hv * V + i, p.v_dt);
   }
+  // the state is loaded whatever the reset flag says (a reset row reads it
+  // for nothing) and cleared once the flag is known, so no load waits for it
   auto srow = [&](int r) { return sizeof(TSin) == 2 ? 4 * NW * r + rg : R * rg + r; };
   RowIn S[R];
   const TSin* sp = (const TSin*)p.sin + sbase;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (!rst) S[r].load(sp + srow(r) * V, cg);
-    else S[r].zero();
-  }
+  for (int r = 0; r < R; ++r) S[r].load(sp + srow(r) * V, cg);
+  // first use of the small loads: only now, after the state loads are issued
+  // (an empty asm that "updates" them keeps their conversion from moving up)
+  asm volatile("" : "+v"(xq_), "+v"(xk_), "+v"(gv_), "+v"(bv_), "+v"(wv_), "+v"(vv_), "+v"(rflag));
+  const bool rst = __builtin_amdgcn_readfirstlane(rflag) != 0;
+  const float xq = bits_f(xq_, p.qk_dt), xk = bits_f(xk_, p.qk_dt), gv = bits_f(gv_, p.g_dt),
+              bv = bits_f(bv_, p.b_dt), wv = bits_f(wv_, p.w_dt), vv = bits_f(vv_, p.v_dt);
   {
     const float sq = wave_sum(xq * xq), sk = wave_sum(xk * xk);
     if (lane == 0 && wid < 2) { rbuf[0][wid] = sq; rbuf[1][wid] = sk; }
@@ -263,6 +309,10 @@ __global__ __launch_bounds__(64 * NW * HPW) void k_decode(const DP p) {
   __syncthreads();
   const float qk = rbuf[2][0] + rbuf[2][1];
 
+  if (rst) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) S[r].zero();
+  }
   // this lane's partial column sums of b k^T (D S) and q^T (D S), D = diag(e^g)
   float pa[8], pc[8];
 #pragma unroll
@@ -380,17 +430,23 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
   const int hg = dgate_head(p.g_h, p.Hk, p.Hv, hv, p.G);
   const int hb = dgate_head(p.b_h, p.Hk, p.Hv, hv, p.G);
   const int hw = dgate_head(p.w_h, p.Hk, p.Hv, hv, p.G);
-  float xq = 0.f, xk = 0.f, gv = 0.f, bv = 0.f, wv = 0.f, vv = 0.f;
+  // a token's inputs as raw bits (and its reset flag), converted at the top
+  // of its step: no load of the batch waits for another
+  uint32_t xq_ = 0, xk_ = 0, gv_ = 0, bv_ = 0, wv_ = 0, vv_ = 0;
+  int rf_ = 0;
   auto ld_tok = [&](int t) {
+    const int64_t row = (int64_t)bb * T + t;
+    if (p.reset != nullptr) rf_ = p.reset[row];
     if (tid < 128) {
-      const int64_t bt_ = (int64_t)bb * T + t;
-      const int64_t qo = (bt_ * p.Hk + hk) * K + i;
-      xq = ld_f(p.q, qo, p.qk_dt);
-      xk = ld_f(p.k, qo, p.qk_dt);
-      gv = ld_f(p.g, (bt_ * p.g_h + hg) * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
-      bv = ld_f(p.b, (bt_ * p.b_h + hb) * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
-      wv = ld_f(p.w, (bt_ * p.w_h + hw) * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
-      vv = ld_f(p.v, (bt_ * p.Hv + hv) * V + i, p.v_dt);
+      const TRow rq = row_rsrc(p.q, row, p.Hk * K, p.qk_dt), rk = row_rsrc(p.k, row, p.Hk * K, p.qk_dt);
+      const TRow rg_ = row_rsrc(p.g, row, p.g_h * p.g_c, p.g_dt), rb_ = row_rsrc(p.b, row, p.b_h * p.b_c, p.b_dt);
+      const TRow rw = row_rsrc(p.w, row, p.w_h * p.w_c, p.w_dt), rv = row_rsrc(p.v, row, p.Hv * V, p.v_dt);
+      xq_ = ld_row(rq, hk * K + i, p.qk_dt);
+      xk_ = ld_row(rk, hk * K + i, p.qk_dt);
+      gv_ = ld_row(rg_, hg * p.g_c + (p.g_c == 1 ? 0 : i), p.g_dt);
+      bv_ = ld_row(rb_, hb * p.b_c + (p.b_c == 1 ? 0 : i), p.b_dt);
+      wv_ = ld_row(rw, hw * p.w_c + (p.w_c == 1 ? 0 : i), p.w_dt);
+      vv_ = ld_row(rv, hv * V + i, p.v_dt);
     }
   };
   ld_tok(0);   // before the state loads, as in the single step (fp32 state, T = 8: 556 to 514 us)
@@ -408,7 +464,12 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
 #pragma unroll 1
   for (int t = 0; t < T; ++t) {
     const int u = t & 1;
-    if (p.reset != nullptr && p.reset[(int64_t)bb * T + t] != 0) {
+    // (an empty asm that "updates" the raw inputs keeps their conversion, and
+    // so the wait for them, after every load issued before this point)
+    asm volatile("" : "+v"(xq_), "+v"(xk_), "+v"(gv_), "+v"(bv_), "+v"(wv_), "+v"(vv_), "+v"(rf_));
+    const float xq = bits_f(xq_, p.qk_dt), xk = bits_f(xk_, p.qk_dt), gv = bits_f(gv_, p.g_dt),
+                bv = bits_f(bv_, p.b_dt), wv = bits_f(wv_, p.w_dt), vv = bits_f(vv_, p.v_dt);
+    if (__builtin_amdgcn_readfirstlane(rf_) != 0) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -438,7 +499,6 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
       const float qk = wave_sum(yq * yk);
       if (lane == 0) rbuf[u][2][wid] = qk;
     }
-    const float wv_t = wv, vv_t = vv;
     if (t + 1 < T) ld_tok(t + 1);   // the next token's inputs load meanwhile
     __syncthreads();
     const float qk = rbuf[u][2][0] + rbuf[u][2][1];
@@ -476,7 +536,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
       float A = 0.f, Cc = 0.f;
 #pragma unroll
       for (int r = 0; r < NW; ++r) { A += red[u][0][r][j]; Cc += red[u][1][r][j]; }
-      const float nv = wv_t * vv_t - A;
+      const float nv = wv * vv - A;
       vn[u][j] = nv;
       const float o = Cc + qk * nv;
       const int64_t oi = (((int64_t)bb * T + t) * p.Hv + hv) * V + j;
@@ -559,11 +619,6 @@ __global__ __launch_bounds__(64 * NW) void k_decode_multi(const DP p) {
 __device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i, int dt) {
   if (dt == DT_F32) return ((const uint32_t*)p)[i];
   return ((const uint16_t*)p)[i];
-}
-__device__ __forceinline__ float bits_f(uint32_t r, int dt) {
-  if (dt == DT_F32) return __builtin_bit_cast(float, r);
-  if (dt == DT_BF16) return __builtin_bit_cast(float, r << 16);
-  return (float)__builtin_bit_cast(f16, (uint16_t)r);
 }
 
 // Sum over the 16 lanes of a DPP row, every lane receiving the same value:
