@@ -65,6 +65,9 @@ __device__ __forceinline__ int vgate_head(const PF& p, int H, int hv) {
 // A segment id as two 32-bit words loaded without a branch, so the loads can
 // be issued early (the value is only compared for equality).  int32 ids read
 // their word twice.
+// A segment id as its two 32-bit words; an int32 id repeats its one word in
+// hi (no select on the loaded value, so nothing waits for the load until the
+// ids are compared; equality is unchanged)
 struct SegId {
   int32_t lo, hi;
   __device__ __forceinline__ bool operator!=(const SegId& o) const { return lo != o.lo || hi != o.hi; }
@@ -73,8 +76,7 @@ __device__ __forceinline__ SegId seg_raw(const PF& p, int b, int t) {
   const int64_t i = p.seg_batched ? (int64_t)b * p.L + t : (int64_t)t;
   const bool w64 = p.seg_dt == DT_I64;
   const int32_t* s32 = (const int32_t*)p.seg + (w64 ? 2 * i : i);
-  const int32_t hi = s32[w64 ? 1 : 0];
-  return SegId{s32[0], w64 ? hi : 0};
+  return SegId{s32[0], s32[w64 ? 1 : 0]};
 }
 
 // v rows of one 32-column slab of execution head h, chunk c (row 16a + r16 of
