@@ -427,3 +427,33 @@ def test_decode_steps_chunked_vs_oracle(case, state_dtype):
     prec = "fp32" if state_dtype == "float32" else "bf16"
     check(o.reshape(B, T * Hv, 128), ro.reshape(B, T * Hv, 128), s, rs, prec, "fp32",
           f"decode_steps chunked {case} {state_dtype}")
+
+
+# 16-bit inputs: the decode kernels read a token's elements as words through
+# a bounds-checked resource per row, so this covers odd element indices (the
+# high half of a word), rows that start 2 bytes into a word (one-head,
+# one-channel 16-bit gates at odd batch rows), bf16 / f16 q, k, v and a reset
+# on an odd row, on the single-step kernel (T = 1) and the per-token kernel
+# (T = 4), against the float64 oracle.
+@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_decode_16bit_inputs_and_word_offsets(T, dt):
+    B, Hk, Hv = 3, 2, 4
+    rng = np.random.default_rng(900 + 2 * T + (dt == "f16"))
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    stored = lambda x: as_np(to_dev(x, tdt)).astype(np.float64)   # values as the device holds them
+    q = stored(rng.standard_normal((B, T, Hk, 128)))
+    k = stored(rng.standard_normal((B, T, Hk, 128)))
+    v = stored(rng.standard_normal((B, T, Hv, 128)))
+    g = stored(-np.exp(0.39 * rng.standard_normal((B, T, 1)) - 1))   # one head, one channel
+    b = stored(sig(0.39 * rng.standard_normal((B, T, Hk))))          # key heads, one channel
+    w = stored(sig(0.39 * rng.standard_normal((B, T, Hv, 128))))     # value heads, channel-wise
+    S0 = 0.2 * rng.standard_normal((B, Hv, 128, 128))
+    reset = np.zeros((B, T), bool)
+    reset[1, T - 1] = True
+    o, s = gdn2_decode_steps(*(to_dev(x, tdt) for x in (q, k, v, g, b, w)), to_dev(S0),
+                             reset=torch.tensor(reset), qk_l2norm=True)
+    assert o.dtype == tdt
+    ro, rs = chain_oracle(q, k, v, g, b, w, S0, reset, qk_l2norm=True)
+    check(o.reshape(B, T * Hv, 128), ro.reshape(B, T * Hv, 128), s, rs, "fp32", "bf16",
+          f"decode 16-bit inputs T={T} {dt}")
