@@ -758,11 +758,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (p.reset != nullptr && (tid & 15) == 0) r.rst = p.reset[(int64_t)bb * T + tt];
   };
   Tok tok;
+  issue_tok(0, tok);   // chunk 0's rows first: vmcnt retires loads in issue order
   // ---- state in, without LDS: each 16-row tile of the wave's 32 columns is
   // loaded as an A fragment (lane (r16, q): row 16rt + r16, columns
   // 32w + pi(q, 0..7)); its products with the two halves of a 32 x 32 identity
   // are the accumulator tiles S[rt][0], S[rt][1] (exact; an fp32 state as
-  // three bf16 parts).  The loads are issued first and consumed only after
+  // three bf16 parts).  The loads are issued after chunk 0's token rows
+  // (so a wait for a row does not wait for the state) and consumed only after
   // chunk 0's token phases, so their latency and the token rows' overlap.
   typedef typename std::conditional<sizeof(TSin) == 2, bf16x4, f32x4>::type RawS;
   RawS ra[8], rb[8];
@@ -775,7 +777,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       rb[rt] = *reinterpret_cast<const RawS*>(rp + 16);
     }
   }
-  issue_tok(0, tok);   // chunk 0's rows load beside the state
   f32x4 S[8][2];
   auto state_in = [&]() {
     const Frag<true> id0 = ident_frag<true>(0, r16, q), id1 = ident_frag<true>(1, r16, q);
