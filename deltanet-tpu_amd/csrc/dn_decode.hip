@@ -1008,13 +1008,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       float x[DC];
 #pragma unroll
       for (int t = 0; t < DC; ++t) x[t] = rhs[t * DCP + c];
+      // row t + 1's reads are issued before row t's products, so each row's
+      // LDS latency overlaps the row before; A is the same for every lane, so
+      // a row moves to scalar registers as it is used (no vector registers
+      // held for it)
+      float an[DC];
+      an[0] = sA[1 * AP];
 #pragma unroll
       for (int t = 1; t < DC; ++t) {
-        // row t's reads where they are used (hoisting all 120 would hold them live)
+        float ac[DC];
+#pragma unroll
+        for (int s2 = 0; s2 < t; ++s2)
+          ac[s2] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, an[s2])));
+        if (t + 1 < DC) {
+#pragma unroll
+          for (int s2 = 0; s2 <= t; ++s2) an[s2] = sA[(t + 1) * AP + s2];
+        }
         __builtin_amdgcn_sched_barrier(0);
         float acc = x[t];
 #pragma unroll
-        for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sA[t * AP + s2], x[s2], acc);
+        for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-ac[s2], x[s2], acc);
         x[t] = acc;
       }
       if (tid < K) {
