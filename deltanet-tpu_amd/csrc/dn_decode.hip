@@ -200,8 +200,10 @@ __device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
   }
 }
 
-// waves per workgroup of the single-step kernel: 2 (16 state rows per lane)
-// measured 3% faster than 4 and 10% faster than 8 at config 4 (bf16 state)
+// waves per matrix of the single-step kernel with an fp32 state on either
+// side: 2 (16 state rows per lane), two matrices per workgroup (config 4:
+// 179 us against 184-192 for 4 waves or other matrix counts).  A bf16 state
+// both ways runs 4 waves on one matrix (see the launch).
 constexpr int kDecodeWaves = 2;
 constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel (8 measured slower)
 // launches of at least this many tokens (and no stability guard) run the
@@ -1313,7 +1315,9 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
     if (fi && fo) hipLaunchKernelGGL((k_decode<float, float, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
     else if (fi && !fo) hipLaunchKernelGGL((k_decode<float, bf16, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
     else if (fo) hipLaunchKernelGGL((k_decode<bf16, float, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
-    else hipLaunchKernelGGL((k_decode<bf16, bf16, kDecodeWaves, 2>), grid2, blk2, 0, st, p);
+    // a bf16 state both ways: four waves on one matrix per workgroup (90.4-90.8
+    // vs 91.1-91.4 us at config 4; the fp32 forms measured slower so: 184 vs 179)
+    else hipLaunchKernelGGL((k_decode<bf16, bf16, 4, 1>), grid, dim3(256), 0, st, p);
   } else if (!p.guard && T >= kChunkMinTokens && decode_chunked()) {
     // products on the fp32 MFMA when either side of the state is fp32, in
     // split bf16 for a bf16 state (its rounding dominates)
