@@ -205,7 +205,7 @@ __device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
 // 179 us against 184-192 for 4 waves or other matrix counts).  A bf16 state
 // both ways runs 4 waves on one matrix (see the launch).
 constexpr int kDecodeWaves = 2;
-constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel (8 measured slower)
+constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel, fp32 state (8 measured slower)
 // launches of at least this many tokens (and no stability guard) run the
 // chunked kernel: at config 4 it is faster from 8 tokens (bf16 state: 295 vs
 // 385 us at T = 8, 307 vs 728 us at T = 16), slower below (299 vs 219 us at T = 4)
@@ -1329,7 +1329,9 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
     if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
     else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
     else if (fo) hipLaunchKernelGGL((k_decode_multi<bf16, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
-    else hipLaunchKernelGGL((k_decode_multi<bf16, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
+    // a bf16 state both ways: two waves per matrix (T = 4: 188-192 vs 216-219
+    // us at config 4; the fp32 forms measured slower so: 327 vs 292)
+    else hipLaunchKernelGGL((k_decode_multi<bf16, bf16, 2>), grid, dim3(128), 0, st, p);
   }
   prof_mark(3, st, true);
   const hipError_t e = hipGetLastError();
