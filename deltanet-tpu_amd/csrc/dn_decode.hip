@@ -694,7 +694,10 @@ __device__ __forceinline__ void split3(const float* x, Frag<true>& a, Frag<true>
 // inside the fp32 range); wider chunks take one exponential per pair
 constexpr float kChunkSpan = 80.f;
 
-template <class TSin, class TSout, bool BF>
+// GK: every gate is fp32 with one value per channel (the gate loads then
+// carry no branch on the type or the channel count, which would make the
+// compiler wait for each load in turn)
+template <class TSin, class TSout, bool BF, bool GK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_decode_chunk(const DP p) {
   constexpr int K = 128, V = 128;
   using P = Pol<BF>;
@@ -746,6 +749,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     ld8_bits(p.k, (bt_ * p.Hk + hk) * K + c8, p.qk_dt, r.k);
     ld8_bits(p.v, (bt_ * p.Hv + hv) * V + c8, p.v_dt, r.v);
     auto gate = [&](const void* g, int H, int C, int dt, int hh, Raw8w& o) {
+      if constexpr (GK) {
+        const float* gp = (const float*)g + (bt_ * H + hh) * K + c8;
+        o.a = *reinterpret_cast<const uint4*>(gp);
+        o.b = *reinterpret_cast<const uint4*>(gp + 4);
+        return;
+      }
       if (C == 1) {
         o.a.x = ld_bits(g, bt_ * H + hh, dt);
         o.b = o.a;
@@ -818,6 +827,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       bits8_f(tok.k, p.qk_dt, xk);
       bits8_f(tok.v, p.v_dt, xv);
       auto gate = [&](const Raw8w& r, int C, int dt, float* x) {
+        if constexpr (GK) {
+          bits8_f(r, DT_F32, x);
+          return;
+        }
         if (C == 1) {
           const float s1 = bits_f(r.a.x, dt);
 #pragma unroll
@@ -1321,10 +1334,21 @@ int decode_launch(const dn_decode_args* a, int T, void* stream) {
   } else if (!p.guard && T >= kChunkMinTokens && decode_chunked()) {
     // products on the fp32 MFMA when either side of the state is fp32, in
     // split bf16 for a bf16 state (its rounding dominates)
-    if (fi && fo) hipLaunchKernelGGL((k_decode_chunk<float, float, false>), grid, dim3(256), 0, st, p);
-    else if (fi && !fo) hipLaunchKernelGGL((k_decode_chunk<float, bf16, false>), grid, dim3(256), 0, st, p);
-    else if (fo) hipLaunchKernelGGL((k_decode_chunk<bf16, float, false>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((k_decode_chunk<bf16, bf16, true>), grid, dim3(256), 0, st, p);
+    const bool gk = a->g_dtype == DN_F32 && a->b_dtype == DN_F32 && a->w_dtype == DN_F32 && a->g_chans == 128 &&
+                    a->b_chans == 128 && a->w_chans == 128;
+    if (fi && fo) {
+      if (gk) hipLaunchKernelGGL((k_decode_chunk<float, float, false, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((k_decode_chunk<float, float, false, false>), grid, dim3(256), 0, st, p);
+    } else if (fi && !fo) {
+      if (gk) hipLaunchKernelGGL((k_decode_chunk<float, bf16, false, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((k_decode_chunk<float, bf16, false, false>), grid, dim3(256), 0, st, p);
+    } else if (fo) {
+      if (gk) hipLaunchKernelGGL((k_decode_chunk<bf16, float, false, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((k_decode_chunk<bf16, float, false, false>), grid, dim3(256), 0, st, p);
+    } else {
+      if (gk) hipLaunchKernelGGL((k_decode_chunk<bf16, bf16, true, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((k_decode_chunk<bf16, bf16, true, false>), grid, dim3(256), 0, st, p);
+    }
   } else {
     if (fi && fo) hipLaunchKernelGGL((k_decode_multi<float, float, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
     else if (fi && !fo) hipLaunchKernelGGL((k_decode_multi<float, bf16, kMultiWaves>), grid, dim3(64 * kMultiWaves), 0, st, p);
