@@ -207,9 +207,10 @@ __device__ __forceinline__ void store_row(TSout* row, int cg, const float* y) {
 constexpr int kDecodeWaves = 2;
 constexpr int kMultiWaves = 4;   // waves per workgroup of the T-token kernel, fp32 state (8 measured slower)
 // launches of at least this many tokens (and no stability guard) run the
-// chunked kernel: at config 4 it is faster from 8 tokens (bf16 state: 295 vs
-// 385 us at T = 8, 307 vs 728 us at T = 16), slower below (299 vs 219 us at T = 4)
-constexpr int kChunkMinTokens = 8;
+// chunked kernel: at config 4 a launch below 16 tokens costs about what one of
+// 8 does (212 us bf16 state, 354 us fp32), so it is faster from 6 tokens (per
+// token kernel at T = 6: 253 / 377 us, at T = 5: 221 / 338 us)
+constexpr int kChunkMinTokens = 6;
 
 // One workgroup of NW waves per (batch row, value head).  Lane (rg, cg)
 // holds R = 32/NW state rows, 8 columns per row (Row8 above): for a bf16

@@ -568,7 +568,7 @@ def gdn2_decode_steps(
     (B, Hv, K, V).  ``reset`` is None, (B,) (clear the state before the first
     token) or (B, T) (clear it before each marked token).  Returns
     ``(output (B, T, Hv, V), new_state)``: the recurrence of T chained
-    ``gdn2_decode_step`` calls with the state read and written once.  From 8
+    ``gdn2_decode_step`` calls with the state read and written once.  From 6
     tokens without the stability guard the launch runs the tokens as 16-token
     chunks in the WY form on matrix cores and carries the state in fp32,
     rounding a bfloat16 ``state_dtype`` once at the end; shorter launches (and

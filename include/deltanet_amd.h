@@ -144,7 +144,7 @@ int dn_decode_step(const dn_decode_args* a, void* stream);
  * a token axis after the batch axis: q, k (B,T,Hk,K); v, out (B,T,Hv,V); gates
  * (B,T,Hx,Cx); reset NULL or (B,T), clearing the state before that token.  The
  * result is the recurrence of T chained dn_decode_step calls; stability_guard
- * caps after every token.  T >= 8 without the guard runs as 16-token chunks in
+ * caps after every token.  T >= 6 without the guard runs as 16-token chunks in
  * the chunked WY form (fp32 products on the fp32 matrix cores when either state
  * is fp32, split bf16 for a bf16 state) and carries the state in fp32 across
  * the T tokens, converting it to state_out_dtype once; the other launches
