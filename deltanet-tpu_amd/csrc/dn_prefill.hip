@@ -548,13 +548,17 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   asm volatile("" : "+v"(sg_0.lo), "+v"(sg_0.hi), "+v"(sg_a.lo), "+v"(sg_a.hi), "+v"(sg_b.lo), "+v"(sg_b.hi));
 
   // ---- phase 0: in-chunk document index (segment canonicalisation) -------
-  if (tid < CH) doc[tid] = (p.seg != nullptr && tid > 0) ? (sg_t != sg_tp) : 0;
-  __syncthreads();
-  for (int off = 1; off < CH; off <<= 1) {
-    int v = 0;
-    if (tid < CH && tid >= off) v = doc[tid - off];
+  // doc[i] = number of segment starts among tokens 1..i: a wave ballot and a
+  // popcount per token (waves 0 and 1 hold tokens 0..127), wave 1 adding
+  // wave 0's total
+  {
+    __shared__ int starts0;
+    const bool st = tid < CH && tid > 0 && p.seg != nullptr && (sg_t != sg_tp);
+    const uint64_t bal = __ballot(st);
+    const int upto = __popcll(bal & ((2ull << l) - 1ull));   // lanes 0..l (l = 63: all)
+    if (tid == 0) starts0 = __popcll(bal);
     __syncthreads();
-    if (tid < CH) doc[tid] += v;
+    if (tid < CH) doc[tid] = upto + (w == 1 ? starts0 : 0);
     __syncthreads();
   }
   if (tid == 0 && h == 0) {
