@@ -1393,8 +1393,10 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
 // remainder runs after the loop: an exit in the middle of a trip would make
 // the loop head wait for every outstanding load, the prefetches included.
 // ===========================================================================
+// (several tiles per workgroup: one recurrence set, the registers two would
+// hold spilled; config 3 chain 492-502 to 434-438 us)
 template <bool BF, int NTL> struct ChainSets {
-  static constexpr int rec = NTL == 1 ? 4 : 2, out = NTL == 1 ? 3 : 2;
+  static constexpr int rec = NTL == 1 ? 4 : 1, out = NTL == 1 ? 3 : 2;
 };
 template <int NTL> struct ChainSets<false, NTL> {   // fp32 fragments are twice as wide
   static constexpr int rec = 2, out = 3;
