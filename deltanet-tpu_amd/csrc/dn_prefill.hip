@@ -1393,10 +1393,12 @@ __device__ __forceinline__ void value_cols(const PF& p, int b, int h, int c, int
 // remainder runs after the loop: an exit in the middle of a trip would make
 // the loop head wait for every outstanding load, the prefetches included.
 // ===========================================================================
-// (several tiles per workgroup: one recurrence set, the registers two would
-// hold spilled; config 3 chain 492-502 to 434-438 us)
+// (one tile: 2 and 3 sets, config 2 chain 28.4-28.8 to 27.8 us and config 5
+// 1325-1336 to 1300-1304 us against 4 and 3; several tiles per workgroup: one
+// recurrence set, the registers two would hold spilled, config 3 chain
+// 492-502 to 434-438 us)
 template <bool BF, int NTL> struct ChainSets {
-  static constexpr int rec = NTL == 1 ? 4 : 1, out = NTL == 1 ? 3 : 2;
+  static constexpr int rec = NTL == 1 ? 2 : 1, out = NTL == 1 ? 3 : 2;
 };
 template <int NTL> struct ChainSets<false, NTL> {   // fp32 fragments are twice as wide
   static constexpr int rec = 2, out = 3;
