@@ -271,7 +271,7 @@ __device__ __forceinline__ void prepass_scalar_gates(const PF& p, int b, int tb,
   __shared__ float lam_h[CH], lam_l[CH];   // Lambda (log2 units), double-float
   __shared__ float bet_s[CH];              // b per token (0 past the end)
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, q = l >> 4;
 
   // ---- Lambda: inclusive scan of g over the chunk (waves 0 and 1) ----------
   float hi = 0.f, lo = 0.f;
@@ -451,7 +451,9 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   __shared__ int wide_part[2];        // per 64-channel half: the chunk-reference path is unsafe
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r16 = l & 15, q = l >> 4;
+  // (the wave index as a scalar: loops and tile indices over waves stay in
+  // scalar registers, with no per-lane masks)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, r16 = l & 15, q = l >> 4;
   const int units = p.B * p.Hx * p.NCb;
   // chunk unit: XCD-aware remap (the hardware deals linear block ids to the 8
   // XCDs round-robin; consecutive chunks of a head share one XCD's L2)
