@@ -385,14 +385,18 @@ def test_decode_steps_odd_matrix_count(state_dtype, B, Hk, Hv, Tn):
 # in the WY form: parity with the float64 token-by-token oracle across ragged
 # chunk counts, resets at and inside chunk boundaries, gate layouts and dtypes,
 # no L2 norm, and a decay strong enough to take the one-exponential-per-pair
-# path for A and M (a chunk's decay span above 80 nats).
+# path for A and M (a chunk's decay span above 80 nats).  Seeds are fixed per
+# case: without the L2 norm the state grows to ~1e8 (each token's transition
+# has an eigenvalue near 1 - b |k|^2 ~ -63), and for some seeds a plain fp32
+# token-by-token recurrence is itself ~2e-4 max-abs/rms from float64.
 CHUNK_CASES = {
-    "T6_hk": dict(T=6, gates="hk"),
-    "T8_hk": dict(T=8, gates="hk"),
-    "T16_hv_resets": dict(T=16, gates="hv", resets=[(0, 0), (1, 7), (1, 15)]),
-    "T37_scalar": dict(T=37, gates="scalar", resets=[(0, 16), (1, 20), (1, 21)]),
-    "T24_no_l2norm_f16_gates": dict(T=24, gates="hk", l2norm=False, scale=0.2, gate_dtype="f16"),
-    "T19_strong_decay": dict(T=19, gates="hv", strong=True, resets=[(1, 9)]),
+    "T6_hk": dict(seed=504, T=6, gates="hk"),
+    "T8_hk": dict(seed=505, T=8, gates="hk"),
+    "T16_hv_resets": dict(seed=500, T=16, gates="hv", resets=[(0, 0), (1, 7), (1, 15)]),
+    "T37_scalar": dict(seed=503, T=37, gates="scalar", resets=[(0, 16), (1, 20), (1, 21)]),
+    "T24_no_l2norm_f16_gates": dict(seed=502, T=24, gates="hk", l2norm=False, scale=0.2, gate_dtype="f16"),
+    "T19_strong_decay": dict(seed=501, T=19, gates="hv", strong=True, resets=[(1, 9)]),
+    "T12_one_head_gates": dict(seed=506, T=12, gates="one", resets=[(1, 3)]),
 }
 
 
@@ -401,9 +405,13 @@ CHUNK_CASES = {
 def test_decode_steps_chunked_vs_oracle(case, state_dtype):
     c = CHUNK_CASES[case]
     B, Hk, Hv, T = 2, 2, 4, c["T"]
-    seed = 500 + sorted(CHUNK_CASES).index(case)
+    seed = c["seed"]
     rng = np.random.default_rng(seed)
     q, k, v, g, b, w = steps_inputs(seed, B, T, Hk, Hv, "hv" if c["gates"] == "hv" else "hk")
+    if c["gates"] == "one":   # one channel-wise gate head shared by every head
+        g = -np.exp(0.39 * rng.standard_normal((B, T, 1, 128)) - 1)
+        b = sig(0.39 * rng.standard_normal((B, T, 1, 128)))
+        w = sig(0.39 * rng.standard_normal((B, T, 1, 128)))
     if c["gates"] == "scalar":
         g = -np.exp(0.39 * rng.standard_normal((B, T, Hv)) - 1)
         b = sig(0.39 * rng.standard_normal((B, T, Hv)))
