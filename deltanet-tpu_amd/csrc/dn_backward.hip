@@ -10,7 +10,8 @@
 // scan).  The recurrence differentiated is reference.py:123-161:
 //   Sd = e^{g_t} S ; u = w v - Sd^T (b k) ; S' = Sd + k u^T ; o = S'^T q.
 //
-// Chunk form (C = 64 tokens, G_i = cumulative log-decay from the chunk start,
+// Chunk form (C = 64 tokens, G_i = cumulative log-decay from the start of the
+// chunk or of token i's document, whichever is later,
 // carry_i = token i continues the state entering the chunk, last_j = token j
 // is in the chunk's last document, same(i,j) = same document):
 //   A_ij = sum_r b_i k_i[r] k_j[r] e^{G_i-G_j}  (j < i, same)   T = (I + A)^-1
@@ -75,7 +76,7 @@ struct BW {
   float *dq, *dk, *dv, *dg, *db, *dw;
   float* dinit;          // NULL or: the reverse scan's gradient of the state entering the block
   // workspace, per unit u = (batch * H + head) * NC + chunk
-  float *G;    // [BC][KD] cumulative log2-decay from the chunk start
+  float *G;    // [BC][KD] cumulative log2-decay from the chunk's or the token's document start
   float *Wm;   // [BC][KD] W          (these four in gofs / bofs order)
   float *WT;   // [KD][BC] W^T
   float *Kc;   // [BC][KD]
@@ -260,6 +261,7 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   __shared__ float sX[16][17];    // one 16 x 16 block in transit (T substitution)
   __shared__ int sseg[BC], scar[BC], slast[BC];
   __shared__ int sSafe[NWV];
+  __shared__ uint64_t sStarts;   // bit i: a document starts at token i (i > 0)
 
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6, q = l >> 4, l16 = l & 15;
   // Persistent: workgroup blockIdx.x takes units blockIdx.x, + gridDim.x, ...
@@ -289,7 +291,13 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   const int t0 = (p.c0 + c) * BC;
   float* G = p.G + (int64_t)u * CK;
 
-  if (tid < BC) chunk_docs(p, bb, t0, sseg, scar, slast);
+  if (tid < BC) {   // wave 0
+    chunk_docs(p, bb, t0, sseg, scar, slast);
+    const int sg = sseg[tid];
+    const int sp = __shfl_up(sg, 1);   // every lane takes part (lane 0 gets its own value)
+    const uint64_t st = __ballot(tid > 0 && sg != sp);
+    if (tid == 0) sStarts = st;
+  }
   // stage the log2-decay (rows past the sequence end are zero); k stays in
   // registers for Kc and beta = b k; q and b arrive during the decay scan
   float4 kst[SIT], qst[SIT], bst[SIT];
@@ -309,23 +317,37 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
   }
   lds_barrier();
   // ---- cumulative decay (log2 units): channel tid % 128, quarter tid / 128 --
+  // The sum restarts at every document start inside the chunk.  Only pairs of
+  // one document use a difference G_i - G_j, and the chunk-start terms
+  // (carry, lam) only tokens of the chunk's first document, so every use is
+  // unchanged; but a later document's small decays are no longer added to
+  // an earlier document's large sum, where fp32 would absorb them
+  // (reference gdn2.py mask_lambda_by_doc, tests/test_precision_flags.py).
   {
     const int ch = tid & (KD - 1), qt = tid >> 7;
+    // wave-uniform (scalar registers): the chunk's starts, this quarter's
+    const uint64_t stm = sStarts;
+    const uint32_t slo = __builtin_amdgcn_readfirstlane((uint32_t)stm);
+    const uint32_t shi = __builtin_amdgcn_readfirstlane((uint32_t)(stm >> 32));
+    const uint32_t qm = ((qt < 2 ? slo : shi) >> (16 * (qt & 1))) & 0xffffu;
+    const int first = qm ? __builtin_ctz(qm) : BC / 4;   // BC / 4: none
     float part[BC / 4];
     float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < BC / 4; ++t) {
+      if ((qm >> t) & 1u) acc = 0.f;
       acc += sG[16 * qt + t][ch];
       part[t] = acc;
     }
-    sTot[qt][ch] = acc;
+    sTot[qt][ch] = acc;   // the sum since the quarter's last start (or its whole sum)
     lds_barrier();
     float off = 0.f;
 #pragma unroll
-    for (int s2 = 0; s2 < 3; ++s2)
-      if (s2 < qt) off += sTot[s2][ch];
+    for (int s2 = 0; s2 < 3; ++s2) {
+      if (s2 < qt) off = ((((s2 < 2 ? slo : shi) >> (16 * (s2 & 1))) & 0xffffu) ? 0.f : off) + sTot[s2][ch];
+    }
 #pragma unroll
-    for (int t = 0; t < BC / 4; ++t) sG[16 * qt + t][ch] = part[t] + off;
+    for (int t = 0; t < BC / 4; ++t) sG[16 * qt + t][ch] = part[t] + (t < first ? off : 0.f);
   }
   lds_barrier();
   // G (coalesced), lam, Kc from the staged k into LDS (channels 0..63 in sA,
@@ -346,10 +368,12 @@ __global__ __launch_bounds__(NT) void k_bw_intra(BW p) {
       *reinterpret_cast<float4*>(c4 < KD / 8 ? &sA[i][4 * c4] : &sM[i][4 * c4 - KD / 2]) = kc;
     }
     if (tid < KD) p.lam[(int64_t)u * KD + tid] = scar[BC - 1] ? ex2(sG[BC - 1][tid]) : 0.f;
-    // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128
+    // block tid / 128 spans 2^{G_m - G_{m+15}} <= 2^64 in channel tid % 128,
+    // and no document starts after its first row (G is monotone in it)
     const int ch = tid & (KD - 1), blk = tid >> 7;
     const float span = sG[16 * blk][ch] - sG[16 * blk + 15][ch];
-    const bool safe = __all(span <= 64.f);
+    const bool one_doc = sseg[16 * blk] == sseg[16 * blk + 15];   // ids are nondecreasing
+    const bool safe = one_doc && __all(span <= 64.f);
     if (l == 0) sSafe[wv] = safe;
   }
   // q and beta = b k
@@ -1423,7 +1447,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     f32x4 oq = zero4(), ob = zero4(), ok_ = zero4();
     const int m = 16 * I, m2 = 16 * I + 15;
     const float gm = sG[m][rl], gm2 = sG[m2][rl];
-    const bool inblk = __all(gm - gm2 <= 64.f);
+    // G restarts at document starts: the in-block factors need one document
+    const bool inblk = sseg[m] == sseg[m2] && __all(gm - gm2 <= 64.f);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float xm[8], xa[8], xk[8], ym[8], ya[8], yq[8], yb[8];

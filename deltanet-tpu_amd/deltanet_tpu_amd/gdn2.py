@@ -126,9 +126,11 @@ def chunk_gdn2(
     gradients.  Flags that only shape the reference's TPU fallback
     (``fallback_scan``, ``truncate_bwd_dT_bf16``) are accepted and change no
     result.  ``state_fp32_matmul=True`` runs the call at ``precision="fp32"``.
-    ``mask_lambda_by_doc`` is accepted: the kernels never form a cumulative
-    decay across a document boundary, so the flag's precision concern does
-    not arise.
+    ``mask_lambda_by_doc`` is accepted and changes no result: the forward
+    accumulates the decay in double-float and the backward restarts its
+    cumulative decay at every document start inside a chunk, so a strongly
+    decayed document never absorbs the next one's decay (the flag's
+    precision concern; checked in tests/test_precision_flags_gpu.py).
     """
     # ---- validation: same checks and messages as gdn2.py:1858-1947 ----------
     if fuse_prologue and not qk_l2norm:
