@@ -90,3 +90,17 @@ def test_truncate_bwd_dT_bf16_leaves_forward_unchanged():
     o0 = chunk_gdn2(*ts, segment_ids=sg, precision="bf16")
     o1 = chunk_gdn2(*ts, segment_ids=sg, precision="bf16", truncate_bwd_dT_bf16=True)
     assert torch.equal(o0, o1)
+
+
+def test_later_document_gradients_independent_of_earlier_decay():
+    # tests/test_precision_and_doc_lambda.py:78-116: with document 0 decaying
+    # by -2000 per token, the gradients of every later token equal, bit for
+    # bit, those with no decay in document 0 (the two documents share a chunk)
+    args, seg, do = flag_inputs(strong_first_doc=True)
+    clean = list(args)
+    clean[3] = np.where((np.arange(256) < 50)[None, :, None, None], 0.0, args[3])
+    _, g_strong = run(args, seg, do, precision="fp32")
+    _, g_clean = run(tuple(clean), seg, do, precision="fp32")
+    for n in NAMES:
+        a, b = g_strong[n][:, 50:], g_clean[n][:, 50:]
+        assert np.array_equal(a, b), (n, float(np.abs(a - b).max()))
