@@ -1621,6 +1621,14 @@ __device__ __forceinline__ int gate_head(int H, int Hk, int Hv, int hv, int G) {
   return H == Hv ? hv : (H == Hk ? hv / G : 0);
 }
 __device__ __forceinline__ float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// sigmoid'(x) = s(x) s(-x) = e s^2 with e = e^{-|x|}, s = 1 / (1 + e): no
+// 1 - s(x), which loses the low bits once s(x) nears 1 (at x = 10, 1 - s is
+// 4.5e-5 and fp32 keeps it to ~1e-3 relative)
+__device__ __forceinline__ float dsigmoid(float x) {
+  const float e = __expf(-fabsf(x));
+  const float s = __builtin_amdgcn_rcpf(1.f + e);
+  return e * s * s;
+}
 
 // canonical ids: first_new + number of changes in seg[1..t] (gdn2.py:2081-2094),
 // batch row bb by one workgroup of NT threads
@@ -1845,10 +1853,10 @@ __device__ __forceinline__ float gate_deriv(const BR& p, float x) {
     }
     return (x <= 0.f && (!p.guard || x <= -1e-6f)) ? 1.f : 0.f;
   } else if (WHICH == 1) {
-    if (p.fuse) { const float sg = sigmoid_hw(x); return sg * (1.f - sg); }
+    if (p.fuse) return dsigmoid(x);
     return (!p.guard || x >= 0.f) ? 1.f : 0.f;
   } else {
-    if (p.fuse) { const float sg = sigmoid_hw(x); return sg * (1.f - sg); }
+    if (p.fuse) return dsigmoid(x);
     return 1.f;
   }
 }

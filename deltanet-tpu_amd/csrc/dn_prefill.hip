@@ -1109,16 +1109,42 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
     }
     __syncthreads();
   }
-  // T in fragment-native layout in Y (LDS), for W and the value columns
+  // T in fragment-native layout in Y (LDS), for W and the value columns.  In
+  // bf16 mode its low words go after it, where ke^T is staged once W is formed.
   ST* Ts = reinterpret_cast<ST*>(Y);
+  ST* Tl = Ts + CH * KD;
+  F1 Bbe[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) Bbe[s] = SS::fa(g_be + fofs(w, s, l));
   for (int idx = w; idx < 32; idx += 8) {
     const int rt = idx >> 2, s = idx & 3;
     if (s > (rt >> 1)) continue;
     float x[8];
     row8<float>(&X[(16 * rt + r16) * XP + 32 * s], q, x);
-    SS::st8(Ts + fofs(rt, s, l), x);
+    if constexpr (BF) SS::st8s(Ts + fofs(rt, s, l), Tl + fofs(rt, s, l), x);
+    else SS::st8(Ts + fofs(rt, s, l), x);
   }
   __syncthreads();
+  // ---- W = T be (key tile w) -------------------------------------------------
+  // In bf16 mode T enters as high and low words: with nearly repeated keys
+  // and b near 1, T is close to I minus a unit subdiagonal and W = T be
+  // cancels to a small remainder, which a bf16-rounded T would leave with
+  // 2^-9 / (1 - b) relative error (identical keys, b = 0.993: 7e-2 of the
+  // output against 9e-3 with T split).
+  f32x4 Wc[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) Wc[rt] = zero4();
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s <= rt / 2) {
+        P::m11(Wc[rt], SS::fa(Ts + fofs(rt, s, l)), Bbe[s]);
+        if constexpr (BF) P::m11(Wc[rt], SS::fa(Tl + fofs(rt, s, l)), Bbe[s]);
+      }
+    }
+  }
+  if constexpr (BF) __syncthreads();   // T's low words are read: ke^T takes their place
   // X (T in fp32) is free now: M high / low words there, ke^T high words
   // after T in Y (bf16 mode)
   ST* Mh_s = reinterpret_cast<ST*>(X);
@@ -1149,22 +1175,7 @@ __global__ __launch_bounds__(512) void k_prepass(const PF p) {
   VRows<TV> vpre;
   if (kPreV && p.Vp < 256 && w < p.Vp / 16) v_rows_issue<TV>(p, b, h, c, 16 * w, l, vpre);
 
-  // ---- phase 5: W = T be ; Pn = -ke^T W ; X = qe - M W  (key tile w) -----------
-  f32x4 Wc[8];
-  {
-    F1 Bbe[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Bbe[s] = SS::fa(g_be + fofs(w, s, l));
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) Wc[rt] = zero4();
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s <= rt / 2) P::m11(Wc[rt], SS::fa(Ts + fofs(rt, s, l)), Bbe[s]);
-      }
-    }
-  }
+  // ---- phase 5: Pn = -ke^T W ; X = qe - M W  (key tile w; W formed above) ----
   // W^T fragments (rows = key j, k = token), and their negation
   F3 W3[4], W3n[4];
 #pragma unroll
