@@ -1444,7 +1444,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     // join the same products: their column factor e^{G_m - G_j} (dq, dbeta)
     // or row factor e^{G_i - G_m2} (dk) is then >= 1 and bounded.  The pair
     // (i, i) is left out of dq and dk (its factor is e^0).
-    f32x4 oq = zero4(), ob = zero4(), ok_ = zero4();
+    // dk's pairs inside block I are scaled from the block's first row m (<= i)
+    // in their own accumulator, okb: a factor through the last row m2 would
+    // round differently with the decays of tokens after i, and a loss on
+    // tokens before some t must give their gradients bit for bit whatever
+    // follows t (the reference's tests/test_causality.py)
+    f32x4 oq = zero4(), ob = zero4(), ok_ = zero4(), okb = zero4();
     const int m = 16 * I, m2 = 16 * I + 15;
     const float gm = sG[m][rl], gm2 = sG[m2][rl];
     // G restarts at document starts: the in-block factors need one document
@@ -1476,11 +1481,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
           xm[e] = self ? 0.f : sdM[16 * I + l16][j];
           xa[e] = sdA[16 * I + l16][j];
           xk[e] = sK[j][rl] * __builtin_amdgcn_exp2f(gm - gj);
-          ym[e] = self ? 0.f : sdM[j][16 * I + l16];
-          ya[e] = sdA[j][16 * I + l16];
-          const float f = __builtin_amdgcn_exp2f(gj - gm2);
-          yq[e] = sQ[j][rl] * f;
-          yb[e] = sB[j][rl] * sK[j][rl] * f;
+          ym[e] = ya[e] = yq[e] = yb[e] = 0.f;   // dk's in-block pairs: okb below
         } else {
           xm[e] = xa[e] = xk[e] = ym[e] = ya[e] = yq[e] = yb[e] = 0.f;
         }
@@ -1488,7 +1489,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       // slab s holds row blocks 2s and 2s + 1: a side with no column in it
       // has all-zero operands (a uniform test: I is the wave's block)
       const bool any_lo = 2 * s < I || (inblk && I / 2 == s);
-      const bool any_hi = 2 * s + 1 > I || (inblk && I / 2 == s);
+      const bool any_hi = 2 * s + 1 > I;
       if (any_lo) {
         const Frag<false> fk = fr8(xk);
         mma(oq, fr8(xm), fk);
@@ -1498,6 +1499,27 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
         mma(ok_, fr8(ym), fr8(yq));
         mma(ok_, fr8(ya), fr8(yb));
       }
+    }
+    if (inblk) {   // dk's pairs inside block I: slab I / 2, elements of block I
+      const int s = I / 2;
+      float zm[8], za[8], zq[8], zb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int jb = 2 * s + (e >> 2);
+        const int j = 32 * s + pi_k(q, e);
+        if (jb == I) {
+          const bool self = j == 16 * I + l16;
+          zm[e] = self ? 0.f : sdM[j][16 * I + l16];
+          za[e] = sdA[j][16 * I + l16];
+          const float f = __builtin_amdgcn_exp2f(sG[j][rl] - gm);   // <= 1: one document, G monotone
+          zq[e] = sQ[j][rl] * f;
+          zb[e] = sB[j][rl] * sK[j][rl] * f;
+        } else {
+          zm[e] = za[e] = zq[e] = zb[e] = 0.f;
+        }
+      }
+      mma(okb, fr8(zm), fr8(zq));
+      mma(okb, fr8(za), fr8(zb));
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1523,6 +1545,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       dq += eg * rq[Ib][e] + oq[e] * ex2(gi - gm);
       dbeta += -eg * rb[Ib][e] + ob[e] * ex2(gi - gm);
       dk += ok_[e] * ex2(gm2 - gi);
+      if (inblk) dk += okb[e] * __builtin_amdgcn_exp2f(gm - gi);   // <= 2^64 (the block's span)
       const float dkc = slast[i] ? ex2(glast - gi) * rk[Ib][e] : 0.f;
       const float kv = sK[i][rl], qv = sQ[i][rl], bv = sB[i][rl], dmii = sdM[i][i];
       rdg[Ib][e] = qv * dq + bv * kv * dbeta - kv * dk;

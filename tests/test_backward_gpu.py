@@ -540,3 +540,25 @@ def test_backward_alternating_keys_vanishing_decay():
             assert e < 1e-4, (n, e)
         else:
             assert np.abs(got[n] - ref[n]).max() < 1e-6, n
+
+
+@pytest.mark.parametrize("t_cut", [100, 128])
+def test_backward_causality(t_cut):
+    # tests/test_causality.py:27-74: with the loss on outputs before t_cut,
+    # every gradient at t >= t_cut is exactly zero, and the gradients before
+    # t_cut are bit-identical when every input from t_cut on is replaced
+    from deltanet_tpu_amd import chunk_gdn2
+    B, L, Hk, Hv = 1, 256, 2, 4
+    a1 = ref_inputs(101, B, L, Hk, Hv)
+    pert = ref_inputs(202, B, L - t_cut, Hk, Hv)
+    a2 = tuple(np.concatenate([x[:, :t_cut], p], 1) for x, p in zip(a1, pert))
+    grads = []
+    for args in (a1, a2):
+        ts = [to_dev(x).requires_grad_(True) for x in args]
+        o = chunk_gdn2(*ts, is_inference=False, precision="fp32", chunk_size=128)
+        (o[:, :t_cut] ** 2).sum().backward()
+        torch.cuda.synchronize()
+        grads.append([as_np(t.grad) for t in ts])
+    for n, g1, g2 in zip(NAMES, *grads):
+        assert np.all(g1[:, t_cut:] == 0.0), (n, float(np.abs(g1[:, t_cut:]).max()))
+        assert np.array_equal(g1[:, :t_cut], g2[:, :t_cut]), (n, float(np.abs(g1[:, :t_cut] - g2[:, :t_cut]).max()))
