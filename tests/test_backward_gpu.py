@@ -562,3 +562,33 @@ def test_backward_causality(t_cut):
     for n, g1, g2 in zip(NAMES, *grads):
         assert np.all(g1[:, t_cut:] == 0.0), (n, float(np.abs(g1[:, t_cut:]).max()))
         assert np.array_equal(g1[:, :t_cut], g2[:, :t_cut]), (n, float(np.abs(g1[:, :t_cut] - g2[:, :t_cut]).max()))
+
+
+def test_backward_gate_pass_through_at_zero():
+    # tests/test_strong_decay.py:91-109: the nonpositive gate passes the full
+    # gradient at g = 0 (not half, as min(g, 0) would) and none for g > 0;
+    # a third of g exactly 0, a third positive
+    B, L, Hk, Hv = 1, 192, 2, 4
+    q, k, v, g, b, w = ref_inputs(19, B, L, Hk, Hv)
+    sel = np.random.default_rng(20).integers(0, 3, g.shape)
+    g = np.where(sel == 0, 0.0, np.where(sel == 1, 0.05, g))
+    do = np.random.default_rng(21).standard_normal((B, L, Hv, 128))
+    _, got = run_dev(q, k, v, g, b, w, do, precision="fp32")
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+    compare(got, ref, 1e-5, "g = 0 pass-through")
+    assert np.all(got["dg"][sel == 1] == 0.0)
+    assert np.abs(got["dg"][sel == 0]).max() > 0.0   # passed through (it matches the oracle above)
+
+
+def test_scale_as_array_scalar():
+    # tests/test_parity.py:286-318: scale given as an array scalar gives the
+    # float's result bit for bit, on the default and the fused-prologue paths
+    from deltanet_tpu_amd import chunk_gdn2
+    B, L, Hk, Hv = 1, 128, 2, 4
+    q, k, v, g, b, w = ref_inputs(555, B, L, Hk, Hv)
+    ts = [to_dev(x) for x in (q, k, v, g, b, w)]
+    for fuse in (False, True):
+        kw = dict(fuse_prologue=fuse, qk_l2norm=fuse, precision="fp32", is_inference=True)
+        o_f = chunk_gdn2(*ts, scale=0.2, **kw)
+        for s in (np.float32(0.2), torch.tensor(0.2), torch.tensor(0.2, dtype=torch.float64)):
+            assert torch.equal(chunk_gdn2(*ts, scale=s, **kw), o_f), (fuse, type(s))
