@@ -592,3 +592,25 @@ def test_scale_as_array_scalar():
         o_f = chunk_gdn2(*ts, scale=0.2, **kw)
         for s in (np.float32(0.2), torch.tensor(0.2), torch.tensor(0.2, dtype=torch.float64)):
             assert torch.equal(chunk_gdn2(*ts, scale=s, **kw), o_f), (fuse, type(s))
+
+
+@pytest.mark.parametrize("pattern", ["reused", "gaps"])
+def test_backward_reused_segment_ids_weak_decay(pattern):
+    # tests/test_document_boundaries.py:136-180: ids reused after another
+    # document, and pad gaps between documents, under weak decay (g = -0.01);
+    # output and every gradient within rel L2 1e-4
+    from deltanet_tpu_amd import chunk_gdn2
+    B, L, Hk, Hv = 1, 256, 2, 4
+    seg = np.array([[0] * 40 + [1] * 40 + [0] * 176] if pattern == "reused"
+                   else [[1] * 30 + [0] * 10 + [2] * 30 + [0] * 10 + [3] * 176], np.int32)
+    q, k, v, g, b, w = ref_inputs(601, B, L, Hk, Hv)
+    g = np.full_like(g, -0.01)
+    do = np.random.default_rng(602).standard_normal((B, L, Hv, 128))
+    ts = [to_dev(x).requires_grad_(True) for x in (q, k, v, g, b, w)]
+    out = chunk_gdn2(*ts, segment_ids=to_dev(seg, torch.int32), is_inference=False, precision="fp32")
+    (out * to_dev(do)).sum().backward()
+    torch.cuda.synchronize()
+    got = {n: as_np(t.grad) for n, t in zip(NAMES, ts)}
+    o_ref, _ = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg)
+    assert rel_l2(as_np(out), o_ref) < 1e-4
+    compare(got, GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, segment_ids=seg), 1e-4, f"segment ids {pattern}")
