@@ -614,3 +614,15 @@ def test_backward_reused_segment_ids_weak_decay(pattern):
     o_ref, _ = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg)
     assert rel_l2(as_np(out), o_ref) < 1e-4
     compare(got, GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, segment_ids=seg), 1e-4, f"segment ids {pattern}")
+
+
+@pytest.mark.parametrize("L", [1, 127, 1000])
+def test_backward_arbitrary_lengths(L):
+    # tests/test_arbitrary_lengths.py:23-78: one token, one short of a chunk,
+    # and a ragged multi-chunk length, against the gradient oracle
+    B, Hk, Hv = 1, 2, 4
+    q, k, v, g, b, w = ref_inputs(1010 + L, B, L, Hk, Hv)
+    do = np.random.default_rng(2020 + L).standard_normal((B, L, Hv, 128))
+    out, got = run_dev(q, k, v, g, b, w, do, precision="fp32")
+    assert out.shape == (B, L, Hv, 128) and got["dq"].shape == (B, L, Hk, 128)
+    compare(got, GR.chunk_gdn2_vjp(q, k, v, g, b, w, do), 1e-5, f"L={L}")
