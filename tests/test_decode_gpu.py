@@ -466,3 +466,49 @@ def test_decode_16bit_inputs_and_word_offsets(T, dt):
     ro, rs = chain_oracle(q, k, v, g, b, w, S0, reset, qk_l2norm=True)
     check(o.reshape(B, T * Hv, 128), ro.reshape(B, T * Hv, 128), s, rs, "fp32", "bf16",
           f"decode 16-bit inputs T={T} {dt}")
+
+
+# tests/test_matrix.py:367-429: every decode step x batch {1, 2} x heads
+# {(2, 2), (2, 4)} x reset of the first row x decay negative / zero /
+# positive (clamped), 3-D inputs, b at key heads and w at value heads with
+# one channel; output and state within rel L2 1e-4 of the float64 oracle
+@pytest.mark.parametrize("step_name", ["gdn2", "gdn", "kda", "gla", "delta_rule"])
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("Hk,Hv", [(2, 2), (2, 4)])
+@pytest.mark.parametrize("has_reset", [False, True])
+@pytest.mark.parametrize("g_regime", ["negative", "zero", "positive"])
+def test_decode_step_matrix(step_name, B, Hk, Hv, has_reset, g_regime):
+    from deltanet_tpu_amd import gdn_decode_step, gla_decode_step, kda_decode_step
+    rng = np.random.default_rng(77)
+    q = 0.1 * rng.standard_normal((B, Hk, 128))
+    k = 0.1 * rng.standard_normal((B, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, Hv, 128))
+    S = 0.05 * rng.standard_normal((B, Hv, 128, 128))
+    reset = np.array([True] + [False] * (B - 1)) if has_reset else None
+    if g_regime == "negative":
+        g = -rng.uniform(0.1, 2.0, (B, Hk, 128))
+    elif g_regime == "zero":
+        g = np.zeros((B, Hk, 128))
+    else:
+        g = rng.uniform(0.1, 1.0, (B, Hk, 128))
+    b = sig(0.39 * rng.standard_normal((B, Hk, 1)))
+    w = sig(0.39 * rng.standard_normal((B, Hv, 1)))
+    T = lambda x: to_dev(x)
+    kw = dict(reset=torch.tensor(reset) if reset is not None else None)
+    if step_name == "gdn2":
+        o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), **kw)
+        ro, rs = O.decode_step(q, k, v, g, b, w, S, reset=reset)
+    elif step_name == "gdn":
+        o, s = gdn_decode_step(T(q), T(k), T(v), T(g[:, :, :1]), T(b), T(S), **kw)
+        ro, rs = O.gdn_decode_step(q, k, v, g[:, :, :1], b, S, reset=reset)
+    elif step_name == "kda":
+        o, s = kda_decode_step(T(q), T(k), T(v), T(g), T(b), T(S), **kw)
+        ro, rs = O.decode_step(q, k, v, g, b, b, S, reset=reset)
+    elif step_name == "gla":
+        o, s = gla_decode_step(T(q), T(k), T(v), T(g), T(S), **kw)
+        ro, rs = O.decode_step(q, k, v, g, np.zeros((B, Hk, 1)), np.ones((B, Hv, 1)), S, reset=reset)
+    else:
+        o, s = delta_rule_decode_step(T(q), T(k), T(v), T(b), T(S), **kw)
+        ro, rs = O.decode_step(q, k, v, np.zeros((B, Hk, 128)), b, b, S, reset=reset)
+    eo, es = rel_l2(as_np(o).reshape(ro.shape), ro), rel_l2(as_np(s), rs)
+    assert eo < 1e-4 and es < 1e-4, (step_name, eo, es)
