@@ -626,3 +626,55 @@ def test_backward_arbitrary_lengths(L):
     out, got = run_dev(q, k, v, g, b, w, do, precision="fp32")
     assert out.shape == (B, L, Hv, 128) and got["dq"].shape == (B, L, Hk, 128)
     compare(got, GR.chunk_gdn2_vjp(q, k, v, g, b, w, do), 1e-5, f"L={L}")
+
+
+def matrix_gates(rng, layout, regime, B, L, Hk, Hv):
+    """Gate layouts and decay regimes of tests/test_matrix.py:60-128 (gdn2)."""
+    Hg = Hv if layout == "per_value_head" else Hk
+    if regime == "negative":
+        g = -rng.uniform(0.1, 2.0, (B, L, Hg, 128))
+    elif regime == "zero":
+        g = np.zeros((B, L, Hg, 128))
+    else:
+        g = rng.uniform(0.1, 1.0, (B, L, Hg, 128))
+    s = lambda *sh: sig(0.39 * rng.standard_normal(sh))
+    if layout == "channel_wise":
+        return g, s(B, L, Hk, 128), s(B, L, Hv, 128)
+    if layout == "per_key_head":
+        return g[..., :1], s(B, L, Hk, 1), s(B, L, Hv, 128)
+    if layout == "per_value_head":
+        return g[..., :1], s(B, L, Hv, 1), s(B, L, Hv, 128)
+    if layout == "scalar":
+        return g[..., 0], s(B, L, Hk), s(B, L, Hv)
+    return g[:, :, :1], s(B, L, 1, 128), s(B, L, 1, 128)   # single_head
+
+
+# tests/test_matrix.py:156-246: every gate layout x decay regime x head
+# ratio, two documents per row, an initial state; output and final state,
+# and the gradients of every input and of the initial state for a loss on
+# both, within rel L2 1e-4 of the float64 oracle
+@pytest.mark.parametrize("Hk,Hv", [(2, 2), (2, 4)])
+@pytest.mark.parametrize("layout", ["channel_wise", "per_key_head", "per_value_head", "scalar", "single_head"])
+@pytest.mark.parametrize("regime", ["negative", "zero", "positive"])
+def test_backward_gate_matrix(Hk, Hv, layout, regime):
+    B, L = 2, 300
+    rng = np.random.default_rng(42)
+    q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+    init = 0.05 * rng.standard_normal((B, Hv, 128, 128))
+    g, b, w = matrix_gates(rng, layout, regime, B, L, Hk, Hv)
+    seg = np.broadcast_to(np.array([0] * (L // 2) + [1] * (L - L // 2), np.int32), (B, L)).copy()
+    do, df = rng.standard_normal((B, L, Hv, 128)), rng.standard_normal((B, Hv, 128, 128))
+    from deltanet_tpu_amd import chunk_gdn2
+    ts = [to_dev(x).requires_grad_(True) for x in (q, k, v, g, b, w)]
+    ti = to_dev(init).requires_grad_(True)
+    out, fin = chunk_gdn2(*ts, initial_state=ti, segment_ids=to_dev(seg, torch.int32), output_final_state=True,
+                          is_inference=False, precision="fp32")
+    ((out * to_dev(do)).sum() + (fin * to_dev(df)).sum()).backward()
+    torch.cuda.synchronize()
+    o_ref, f_ref = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg, initial_state=init, output_final_state=True)
+    assert rel_l2(as_np(out), o_ref) < 1e-4 and rel_l2(as_np(fin), f_ref) < 1e-4
+    got = {n: as_np(t.grad) for n, t in zip(NAMES, ts)}
+    got["dinit"] = as_np(ti.grad)
+    ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, segment_ids=seg, initial_state=init)
+    compare(got, ref, 1e-4, f"matrix {layout} {regime} Hk={Hk} Hv={Hv}")
