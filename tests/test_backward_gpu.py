@@ -261,38 +261,56 @@ def test_backward_cu_seqlens_batch2():
     compare(got, ref, 1e-5, "cu_seqlens B=2")
 
 
-@pytest.mark.parametrize("variant", ["kda", "gla", "delta_rule"])
-def test_backward_variants(variant):
-    """The variants are adapters over chunk_gdn2 (variants.py:91-285), so they
-    train through the same backward: KDA (channel decay, b = w = beta), GLA
-    (b = 0, w = 1), DeltaNet (g = 0, b = w = beta)."""
+@pytest.mark.parametrize("variant", ["gdn", "kda", "gla", "delta_rule"])
+@pytest.mark.parametrize("Hk,Hv", [(2, 2), (2, 4)])
+@pytest.mark.parametrize("has_init", [False, True])
+def test_backward_variants(variant, Hk, Hv, has_init):
+    """The variants are adapters over chunk_gdn2 (variants.py:17-285), so they
+    train through the same backward: GDN (one decay per key head, b = w =
+    beta), KDA (channel decay, b = w = beta), GLA (b = 0, w = 1), DeltaNet
+    (g = 0, b = w = beta).  As tests/test_matrix.py:263-336: B = 2, L = 300,
+    with and without an initial state, a loss on the output and the final
+    state; every gradient (and the initial state's) within rel L2 1e-4."""
     import deltanet_tpu_amd as D
-    B, L, Hk, Hv = 1, 200, 2, 4
-    q, k, v, g, _, _ = ref_inputs(40, B, L, Hk, Hv)
-    rng = np.random.default_rng(41)
-    beta = sig(rng.standard_normal((B, L, Hk)))
-    do = rng.standard_normal((B, L, Hv, 128))
-    ones = lambda: np.ones((B, L, 1))
+    B, L = 2, 300
+    rng = np.random.default_rng(40)
+    q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+    g = -rng.uniform(0.1, 2.0, (B, L, Hk, 1 if variant == "gdn" else 128))
+    beta = sig(0.39 * rng.standard_normal((B, L, Hk, 1)))
+    init = 0.05 * rng.standard_normal((B, Hv, 128, 128)) if has_init else None
+    do, df = rng.standard_normal((B, L, Hv, 128)), rng.standard_normal((B, Hv, 128, 128))
     qt, kt, vt = (to_dev(x).requires_grad_(True) for x in (q, k, v))
     gt, bt = to_dev(g).requires_grad_(True), to_dev(beta).requires_grad_(True)
-    if variant == "kda":
-        out = D.chunk_kda(qt, kt, vt, gt, bt, precision="fp32", is_inference=False)
-        ref = GR.chunk_gdn2_vjp(q, k, v, g, beta, beta, do)
+    it = to_dev(init).requires_grad_(True) if has_init else None
+    kw = dict(initial_state=it, output_final_state=True, precision="fp32", is_inference=False)
+    zeros, ones = np.zeros((B, L, Hk, 1)), np.ones((B, L, Hv, 1))
+    if variant == "gdn":
+        out, fin = D.chunk_gdn(qt, kt, vt, gt, bt, **kw)
+        args = (g, beta, beta)
+    elif variant == "kda":
+        out, fin = D.chunk_kda(qt, kt, vt, gt, bt, **kw)
+        args = (g, beta, beta)
     elif variant == "gla":
-        out = D.chunk_gla(qt, kt, vt, gt, precision="fp32", is_inference=False)
-        ref = GR.chunk_gdn2_vjp(q, k, v, g, 0 * ones(), ones(), do)
+        out, fin = D.chunk_gla(qt, kt, vt, gt, **kw)
+        args = (g, zeros, ones)
     else:
-        out = D.chunk_delta_rule(qt, kt, vt, bt, precision="fp32", is_inference=False)
-        ref = GR.chunk_gdn2_vjp(q, k, v, 0 * ones(), beta, beta, do)
-    (out.float() * to_dev(do)).sum().backward()
+        out, fin = D.chunk_delta_rule(qt, kt, vt, bt, **kw)
+        args = (zeros, beta, beta)
+    ((out.float() * to_dev(do)).sum() + (fin * to_dev(df)).sum()).backward()
+    torch.cuda.synchronize()
+    o_ref, f_ref = O.chunk_gdn2(q, k, v, *args, initial_state=init, output_final_state=True)
+    assert rel_l2(as_np(out), o_ref) < 1e-4 and rel_l2(as_np(fin), f_ref) < 1e-4
+    ref = GR.chunk_gdn2_vjp(q, k, v, *args, do, df, initial_state=init)
     got = {"dq": as_np(qt.grad), "dk": as_np(kt.grad), "dv": as_np(vt.grad)}
     if variant != "delta_rule":
         got["dg"] = as_np(gt.grad)
     if variant != "gla":
         got["db"] = as_np(bt.grad)
-        ref = dict(ref, db=ref["db"] + ref["dw"])
-    ref = {n: ref[n] for n in got}
-    compare(got, ref, 1e-5, f"variant {variant}")
+        ref = dict(ref, db=ref["db"] + ref["dw"])   # beta feeds both b and w
+    if has_init:
+        got["dinit"] = as_np(it.grad)
+    compare(got, {n: ref[n] for n in got}, 1e-4, f"variant {variant} Hk={Hk} Hv={Hv} init={has_init}")
 
 
 def test_backward_full_size_cfg2_vs_torch_fp32():
