@@ -696,3 +696,34 @@ def test_backward_gate_matrix(Hk, Hv, layout, regime):
     got["dinit"] = as_np(ti.grad)
     ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, df, segment_ids=seg, initial_state=init)
     compare(got, ref, 1e-4, f"matrix {layout} {regime} Hk={Hk} Hv={Hv}")
+
+
+@pytest.mark.parametrize("Hk,Hv", [(2, 2), (2, 4)])
+def test_backward_chained_calls(Hk, Hv):
+    # tests/test_matrix.py:339-360: the second call starts from the first
+    # call's final state; the gradient of a loss on the second call's output
+    # and final state reaches the first call's inputs through that state.
+    # Oracle: one call over the two sequences concatenated, with no output
+    # cotangent on the first
+    from deltanet_tpu_amd import chunk_gdn2
+    B, L = 2, 300
+    rng = np.random.default_rng(1)
+    ins = []
+    for _ in range(2):
+        q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+        v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+        g, b, w = matrix_gates(rng, "channel_wise", "negative", B, L, Hk, Hv)
+        ins.append((q, k, v, g, b, w))
+    do2, df = rng.standard_normal((B, L, Hv, 128)), rng.standard_normal((B, Hv, 128, 128))
+    kw = dict(output_final_state=True, precision="fp32", is_inference=False)
+    t1 = [to_dev(x).requires_grad_(True) for x in ins[0]]
+    t2 = [to_dev(x).requires_grad_(True) for x in ins[1]]
+    _, s1 = chunk_gdn2(*t1, **kw)
+    o2, s2 = chunk_gdn2(*t2, initial_state=s1, **kw)
+    ((o2 * to_dev(do2)).sum() + (s2 * to_dev(df)).sum()).backward()
+    torch.cuda.synchronize()
+    cat = [np.concatenate([a, b_], 1) for a, b_ in zip(*ins)]
+    do = np.concatenate([np.zeros_like(do2), do2], 1)
+    ref = GR.chunk_gdn2_vjp(*cat, do, df)
+    got = {n: np.concatenate([as_np(a.grad), as_np(b_.grad)], 1) for n, a, b_ in zip(NAMES, t1, t2)}
+    compare(got, ref, 1e-4, f"chained calls Hk={Hk} Hv={Hv}")
