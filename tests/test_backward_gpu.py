@@ -727,3 +727,47 @@ def test_backward_chained_calls(Hk, Hv):
     ref = GR.chunk_gdn2_vjp(*cat, do, df)
     got = {n: np.concatenate([as_np(a.grad), as_np(b_.grad)], 1) for n, a, b_ in zip(NAMES, t1, t2)}
     compare(got, ref, 1e-4, f"chained calls Hk={Hk} Hv={Hv}")
+
+
+@pytest.mark.parametrize("case", ["gdn2_hv_decay_hk_erase", "gdn_hk_decay_hv_beta"])
+def test_backward_mixed_gate_heads(case):
+    # tests/test_variants.py:125-236: decay and erase gates at different head
+    # counts; output and gradients within rel L2 1e-5, and the first token's
+    # decode step against the oracle
+    import deltanet_tpu_amd as D
+    B, L, Hk, Hv = 1, 128, 2, 4
+    rng = np.random.default_rng(710)
+    q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+    do = rng.standard_normal((B, L, Hv, 128))
+    S0 = np.zeros((B, Hv, 128, 128))
+    qt, kt, vt = (to_dev(x).requires_grad_(True) for x in (q, k, v))
+    if case == "gdn2_hv_decay_hk_erase":
+        g = -np.exp(0.39 * rng.standard_normal((B, L, Hv, 1)) - 1.0)
+        b = sig(0.39 * rng.standard_normal((B, L, Hk, 128)))
+        w = sig(0.39 * rng.standard_normal((B, L, Hv, 128)))
+        gt, bt, wt = (to_dev(x).requires_grad_(True) for x in (g, b, w))
+        out = D.chunk_gdn2(qt, kt, vt, gt, bt, wt, precision="fp32", is_inference=False)
+        ref = GR.chunk_gdn2_vjp(q, k, v, g, b, w, do)
+        names = NAMES
+        leaves = (qt, kt, vt, gt, bt, wt)
+        od, sd = D.gdn2_decode_step(*(to_dev(x[:, 0]) for x in (q, k, v, g, b, w)), to_dev(S0))
+        rod, rsd = O.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], S0)
+    else:
+        g = -np.exp(0.39 * rng.standard_normal((B, L, Hk, 1)) - 1.0)
+        beta = sig(0.39 * rng.standard_normal((B, L, Hv, 1)))
+        gt, bt = to_dev(g).requires_grad_(True), to_dev(beta).requires_grad_(True)
+        out = D.chunk_gdn(qt, kt, vt, gt, bt, precision="fp32", is_inference=False)
+        ref = GR.chunk_gdn2_vjp(q, k, v, g, beta, beta, do)
+        ref = dict(ref, db=ref["db"] + ref["dw"])
+        names = ("dq", "dk", "dv", "dg", "db")
+        leaves = (qt, kt, vt, gt, bt)
+        od, sd = D.gdn_decode_step(*(to_dev(x[:, 0]) for x in (q, k, v, g, beta)), to_dev(S0))
+        rod, rsd = O.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0], beta[:, 0], S0)
+    (out * to_dev(do)).sum().backward()
+    torch.cuda.synchronize()
+    o_ref, _ = O.chunk_gdn2(q, k, v, *((g, b, w) if case.startswith("gdn2") else (g, beta, beta)))
+    assert rel_l2(as_np(out), o_ref) < 1e-5
+    compare({n: as_np(t.grad) for n, t in zip(names, leaves)}, {n: ref[n] for n in names}, 1e-5, case)
+    assert tuple(od.shape) == (B, Hv, 128) and tuple(sd.shape) == (B, Hv, 128, 128)
+    assert rel_l2(as_np(od), rod) < 1e-5 and rel_l2(as_np(sd), rsd) < 1e-5
