@@ -512,3 +512,34 @@ def test_decode_step_matrix(step_name, B, Hk, Hv, has_reset, g_regime):
         ro, rs = O.decode_step(q, k, v, np.zeros((B, Hk, 128)), b, b, S, reset=reset)
     eo, es = rel_l2(as_np(o).reshape(ro.shape), ro), rel_l2(as_np(s), rs)
     assert eo < 1e-4 and es < 1e-4, (step_name, eo, es)
+
+
+@pytest.mark.parametrize("Hk,Hv", [(1, 2), (1, 1)])
+def test_decode_step_equals_one_token_prefill(Hk, Hv):
+    # tests/test_variants.py:421-481: with one key head, every decode step
+    # equals the matching one-token chunk call (decode and prefill kernels
+    # agree), output and state within rel L2 1e-5
+    import deltanet_tpu_amd as D
+    B = 1
+    rng = np.random.default_rng(980)
+    q, k = rng.standard_normal((2, B, Hk, 128))
+    v = rng.standard_normal((B, Hv, 128))
+    g = -np.exp(rng.standard_normal((B, Hk, 128)) - 1.0)
+    b = sig(0.39 * rng.standard_normal((B, Hk, 128)))
+    w = sig(0.39 * rng.standard_normal((B, Hv, 128)))
+    beta = sig(0.39 * rng.standard_normal((B, Hk, 1)))
+    S = to_dev(0.05 * rng.standard_normal((B, Hv, 128, 128)))
+    T = lambda x: to_dev(x)
+    T1 = lambda x: to_dev(x[:, None])
+    kw = dict(initial_state=S, output_final_state=True, precision="fp32")
+    pairs = [
+        (D.gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), S), D.chunk_gdn2(*(T1(x) for x in (q, k, v, g, b, w)), **kw)),
+        (D.gdn_decode_step(T(q), T(k), T(v), T(g[:, :, :1]), T(beta), S), D.chunk_gdn(*(T1(x) for x in (q, k, v, g[:, :, :1], beta)), **kw)),
+        (D.kda_decode_step(T(q), T(k), T(v), T(g), T(beta), S), D.chunk_kda(*(T1(x) for x in (q, k, v, g, beta)), **kw)),
+        (D.gla_decode_step(T(q), T(k), T(v), T(g), S), D.chunk_gla(*(T1(x) for x in (q, k, v, g)), **kw)),
+        (D.delta_rule_decode_step(T(q), T(k), T(v), T(beta), S), D.chunk_delta_rule(*(T1(x) for x in (q, k, v, beta)), **kw)),
+    ]
+    for name, ((od, sd), (oc, sc)) in zip(("gdn2", "gdn", "kda", "gla", "delta_rule"), pairs):
+        eo = rel_l2(as_np(od).reshape(B, Hv, 128), as_np(oc)[:, 0])
+        es = rel_l2(as_np(sd), as_np(sc))
+        assert eo < 1e-5 and es < 1e-5, (name, eo, es)
