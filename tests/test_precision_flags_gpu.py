@@ -104,3 +104,46 @@ def test_later_document_gradients_independent_of_earlier_decay():
     for n in NAMES:
         a, b = g_strong[n][:, 50:], g_clean[n][:, 50:]
         assert np.array_equal(a, b), (n, float(np.abs(a - b).max()))
+
+
+def test_forward_paths_after_a_strongly_decayed_document():
+    # the forward paths that accumulate decay over a chunk (general prepass in
+    # both precisions, the scalar-gate prepass, the chunked multi-token
+    # decode across a reset) on a document decaying by -2000 per token
+    # followed by ones decaying by -1e-4: each within its precision's bar
+    import deltanet_tpu_amd as D
+    from tests._util import maxabs_over_rms
+    from tests.test_decode_gpu import chain_oracle
+    rng = np.random.default_rng(3)
+    B, L, Hk, Hv = 1, 256, 1, 2
+    _, seg, _ = flag_inputs(strong_first_doc=True)
+    q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+    first = (np.arange(L) < 50)[None, :, None]
+    g = np.where(first[..., None], -2000.0, -1e-4 * np.ones((B, L, Hk, 128)))
+    b, w = sig(rng.standard_normal((B, L, Hk, 128))), sig(rng.standard_normal((B, L, Hv, 128)))
+    ro, _ = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg)
+    for prec, tol in (("fp32", 1e-5), ("bf16", 5e-3)):
+        o = D.chunk_gdn2(*(to_dev(x) for x in (q, k, v, g, b, w)), segment_ids=to_dev(seg, torch.int32),
+                         precision=prec, is_inference=True)
+        assert rel_l2(as_np(o), ro) < tol, prec
+    gs = np.where(first, -2000.0, -1e-4 * np.ones((B, L, Hv)))
+    bs = sig(rng.standard_normal((B, L, Hv)))
+    qb, kb = (O.bf16_round(x).astype(np.float64) for x in (q, k))
+    ro2, _ = O.chunk_gdn2(qb, kb, v, gs, bs, bs, segment_ids=seg, qk_l2norm=True, qk_dtype="bf16")
+    o2 = D.chunk_gdn(to_dev(qb, torch.bfloat16), to_dev(kb, torch.bfloat16), to_dev(v, torch.bfloat16), to_dev(gs),
+                     to_dev(bs), segment_ids=to_dev(seg, torch.int32), precision="bf16", is_inference=True, qk_l2norm=True)
+    assert rel_l2(as_np(o2), ro2) < 1e-2
+    T, Bd = 32, 2
+    qd, kd = rng.standard_normal((2, Bd, T, Hk, 128))
+    vd = rng.standard_normal((Bd, T, Hv, 128))
+    gd = np.where((np.arange(T) % 16 < 6)[None, :, None, None], -2000.0, -1e-4 * np.ones((Bd, T, Hk, 128)))
+    bd, wd = sig(rng.standard_normal((Bd, T, Hk, 128))), sig(rng.standard_normal((Bd, T, Hv, 128)))
+    reset = np.zeros((Bd, T), bool)
+    reset[:, 6] = reset[:, 22] = True   # inside each 16-token chunk, after the strong decay
+    S0 = to_dev(0.2 * rng.standard_normal((Bd, Hv, 128, 128)))
+    o, s = D.gdn2_decode_steps(*(to_dev(x) for x in (qd, kd, vd, gd, bd, wd)), S0, reset=torch.tensor(reset),
+                               qk_l2norm=True)
+    rod, rsd = chain_oracle(qd, kd, vd, gd, bd, wd, as_np(S0), reset, qk_l2norm=True)
+    assert maxabs_over_rms(as_np(o).reshape(Bd, T * Hv, 128), rod.reshape(Bd, T * Hv, 128)) < 1e-4
+    assert rel_l2(as_np(s), rsd) < 1e-5
