@@ -1440,15 +1440,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const int I = I0 + Ib;
     // rows i of block I against columns j < 16 I (and, for dk, rows j of the
     // block against i > 16 I + 15) through MFMA.  Where the block's decay span
-    // stays below 2^64 in this wave's channels, the pairs inside the block
-    // join the same products: their column factor e^{G_m - G_j} (dq, dbeta)
-    // or row factor e^{G_i - G_m2} (dk) is then >= 1 and bounded.  The pair
-    // (i, i) is left out of dq and dk (its factor is e^0).
+    // stays below 2^64 in this wave's channels (and it holds one document),
+    // the pairs inside the block join the dq / dbeta products: their column
+    // factor e^{G_m - G_j} is then >= 1 and bounded.  The pair (i, i) is left
+    // out of dq and dk (its factor is e^0).
     // dk's pairs inside block I are scaled from the block's first row m (<= i)
-    // in their own accumulator, okb: a factor through the last row m2 would
-    // round differently with the decays of tokens after i, and a loss on
-    // tokens before some t must give their gradients bit for bit whatever
-    // follows t (the reference's tests/test_causality.py)
+    // in their own accumulator, okb (factor e^{G_j - G_m} <= 1, then
+    // e^{G_m - G_i} <= 2^64): a factor through the last row m2 would round
+    // differently with the decays of tokens after i, and a loss on tokens
+    // before some t must give their gradients bit for bit whatever follows t
+    // (the reference's tests/test_causality.py)
     f32x4 oq = zero4(), ob = zero4(), ok_ = zero4(), okb = zero4();
     const int m = 16 * I, m2 = 16 * I + 15;
     const float gm = sG[m][rl], gm2 = sG[m2][rl];
