@@ -380,3 +380,26 @@ def test_differentiation_raises():
     out = chunk_gdn2(qt, to_dev(k), to_dev(v), to_dev(g), to_dev(b), to_dev(w), is_inference=True, qk_l2norm=True)
     with pytest.raises(ValueError, match="differentiation is not supported when is_inference=True"):
         out.sum().backward()
+
+
+def test_streaming_block_edge_boundaries_and_reused_id():
+    # test_doc_reset_and_streaming.py:61-104: documents starting exactly at the
+    # block edges 128 and 256 (id 0 reused at 256), L = 300, positive decay
+    # entries (clamped), L2-norm with scale 0.25, 1-D segment ids: streaming
+    # equals the single pass within 1e-5
+    rng = np.random.default_rng(202)
+    B, L, Hk, Hv = 1, 300, 1, 2
+    q, k = rng.standard_normal((2, B, L, Hk, 128))
+    v = rng.standard_normal((B, L, Hv, 128))
+    g = 0.5 * rng.standard_normal((B, L, Hk, 128))
+    b, w = sig(rng.standard_normal((B, L, Hk, 128))), sig(rng.standard_normal((B, L, Hv, 128)))
+    seg = np.concatenate([np.zeros(128), np.ones(128), np.zeros(44)]).astype(np.int32)
+    T = lambda x: to_dev(x)
+    kw = dict(segment_ids=to_dev(seg, torch.int32), output_final_state=True, qk_l2norm=True, scale=0.25,
+              is_inference=True, precision="fp32")
+    o1, s1 = chunk_gdn2(*(T(x) for x in (q, k, v, g, b, w)), **kw)
+    o2, s2 = chunk_gdn2(*(T(x) for x in (q, k, v, g, b, w)), streaming_prefill=True, prefill_block_size=128, **kw)
+    assert np.allclose(as_np(o2), as_np(o1), rtol=1e-5, atol=1e-5)
+    assert np.allclose(as_np(s2), as_np(s1), rtol=1e-5, atol=1e-5)
+    ro, rs = O.chunk_gdn2(q, k, v, g, b, w, segment_ids=seg[None], output_final_state=True, qk_l2norm=True, scale=0.25)
+    check(o2, ro, s2, rs, "fp32", "fp32", "streaming block-edge documents")
