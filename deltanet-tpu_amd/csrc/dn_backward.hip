@@ -1375,6 +1375,18 @@ constexpr int HC = KD / 4;      // channels per k_bw_dqk workgroup
 constexpr int NQ = KD / HC;     // k_bw_dqk workgroups per unit
 constexpr int HP = HC + 4;
 
+// fp32 product over half of a fragment's k elements (4 h .. 4 h + 3), for
+// operands whose other half is zero
+__device__ __forceinline__ void mma_half(f32x4& acc, const float* a, const float* b, int h) {
+  if (h) {
+#pragma unroll
+    for (int e = 4; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  }
+}
+
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_bw_dqk(BW p) {
   __shared__ float sQ[BC][HP], sK[BC][HP], sB[BC][HP], sG[BC][HP];
   __shared__ float sdM[BC][CP], sdA[BC][CP];
@@ -1491,14 +1503,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       // has all-zero operands (a uniform test: I is the wave's block)
       const bool any_lo = 2 * s < I || (inblk && I / 2 == s);
       const bool any_hi = 2 * s + 1 > I;
+      // in the slab of block I (2 s == I: blocks I, I + 1) only one half of
+      // the k elements is nonzero on each side
       if (any_lo) {
-        const Frag<false> fk = fr8(xk);
-        mma(oq, fr8(xm), fk);
-        mma(ob, fr8(xa), fk);
+        if (2 * s == I) {
+          mma_half(oq, xm, xk, 0);
+          mma_half(ob, xa, xk, 0);
+        } else {
+          const Frag<false> fk = fr8(xk);
+          mma(oq, fr8(xm), fk);
+          mma(ob, fr8(xa), fk);
+        }
       }
       if (any_hi) {
-        mma(ok_, fr8(ym), fr8(yq));
-        mma(ok_, fr8(ya), fr8(yb));
+        if (2 * s == I) {
+          mma_half(ok_, ym, yq, 1);
+          mma_half(ok_, ya, yb, 1);
+        } else {
+          mma(ok_, fr8(ym), fr8(yq));
+          mma(ok_, fr8(ya), fr8(yb));
+        }
       }
     }
     if (inblk) {   // dk's pairs inside block I: slab I / 2, elements of block I
@@ -1519,8 +1543,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
           zm[e] = za[e] = zq[e] = zb[e] = 0.f;
         }
       }
-      mma(okb, fr8(zm), fr8(zq));
-      mma(okb, fr8(za), fr8(zb));
+      mma_half(okb, zm, zq, I & 1);   // block I is half I & 1 of slab I / 2
+      mma_half(okb, za, zb, I & 1);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
