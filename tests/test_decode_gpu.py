@@ -71,6 +71,10 @@ def test_decode_state_dtype_contract(state_dtype):
     ro, rs = O.decode_step(q, k, v, g, b, w, S)
     tol = 1e-2 if exp == torch.bfloat16 else 1e-5
     assert rel_l2(as_np(s), rs) < tol
+    if state_dtype is None:
+        # test_inference.py:150-154: with no state_dtype a bf16 state comes back as float32
+        _, s2 = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S).to(torch.bfloat16))
+        assert s2.dtype == torch.float32
 
 
 @pytest.mark.parametrize("guard", [False, True])
