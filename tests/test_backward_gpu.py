@@ -771,3 +771,21 @@ def test_backward_mixed_gate_heads(case):
     compare({n: as_np(t.grad) for n, t in zip(names, leaves)}, {n: ref[n] for n in names}, 1e-5, case)
     assert tuple(od.shape) == (B, Hv, 128) and tuple(sd.shape) == (B, Hv, 128, 128)
     assert rel_l2(as_np(od), rod) < 1e-5 and rel_l2(as_np(sd), rsd) < 1e-5
+
+
+def test_backward_fuse_prologue_scale():
+    # tests/test_parity.py:259-274 (scale on the fused path), with gradients:
+    # raw gates, L2-norm, scale 0.2, rel L2 1e-5
+    B, L, Hk, Hv = 1, 128, 2, 4
+    rng = np.random.default_rng(333)
+    q, k = 0.1 * rng.standard_normal((2, B, L, Hk, 128))
+    v = 0.1 * rng.standard_normal((B, L, Hv, 128))
+    g = 0.39 * rng.standard_normal((B, L, Hk, 128)) - 1.0
+    b = 0.39 * rng.standard_normal((B, L, Hk, 128))
+    w = 0.39 * rng.standard_normal((B, L, Hv, 128))
+    do = rng.standard_normal((B, L, Hv, 128))
+    kw = dict(qk_l2norm=True, fuse_prologue=True, scale=0.2)
+    out, got = run_dev(q, k, v, g, b, w, do, precision="fp32", **kw)
+    o_ref, _ = O.chunk_gdn2(q, k, v, g, b, w, is_inference=False, **kw)
+    assert rel_l2(out, o_ref) < 1e-5
+    compare(got, GR.chunk_gdn2_vjp(q, k, v, g, b, w, do, **kw), 1e-5, "fuse_prologue scale=0.2")
