@@ -547,3 +547,23 @@ def test_decode_step_equals_one_token_prefill(Hk, Hv):
         eo = rel_l2(as_np(od).reshape(B, Hv, 128), as_np(oc)[:, 0])
         es = rel_l2(as_np(sd), as_np(sc))
         assert eo < 1e-5 and es < 1e-5, (name, eo, es)
+
+
+def test_decode_guard_caps_a_large_state():
+    # test_streaming_and_stability.py:65-90: negative erase gate, positive
+    # decay and a state of 100 everywhere; with the guard every head's
+    # Frobenius norm ends at most tau, and equals the oracle's
+    B, Hk, Hv = 1, 2, 2
+    rng = np.random.default_rng(1234)
+    q, k = rng.standard_normal((2, B, Hk, 128))
+    v = rng.standard_normal((B, Hv, 128))
+    b = np.full((B, Hk, 128), -0.5)
+    g = np.full((B, Hk, 128), 0.5)
+    w = np.ones((B, Hv, 128))
+    S = np.full((B, Hv, 128, 128), 100.0)
+    T = lambda x: to_dev(x)
+    o, s = gdn2_decode_step(T(q), T(k), T(v), T(g), T(b), T(w), T(S), stability_guard=True, stability_tau=50.0)
+    norms = np.linalg.norm(as_np(s), axis=(-2, -1))
+    assert norms.max() <= 50.0 + 1e-2
+    ro, rs = O.decode_step(q, k, v, g, b, w, S, stability_guard=True, stability_tau=50.0)
+    assert rel_l2(as_np(s), rs) < 1e-5 and rel_l2(as_np(o).reshape(ro.shape), ro) < 1e-5
